@@ -1,0 +1,444 @@
+#!/usr/bin/env python3
+"""Benchmark: MoE-layer decode tokens/s + achieved HBM GB/s on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload (BASELINE.json's metric, config 3 at T = 8): one step is one
+decode MoE layer over T = 8 tokens — router (f32 [64,1280]), top-6 with
+renormalised gates, 64 int8 experts (gate/up [896,1280], down [1280,896],
+per-row f32 scales), SwiGLU, slot-order combine. Inputs are resident in HBM
+before timing. To measure HBM rather than the 256 MB Infinity Cache, the
+timed steps rotate over --copies distinct layers (each with its own router
+and its own copy of the expert weights; 220 MB each), like consecutive
+decoder layers. Synthetic seeded data (no checkpoint).
+
+Other workloads (--workload): lm_head (config 2), igemm (config 1), rswa
+(config 5). Each prints ONE JSON line with `roofline` (dominant kernel,
+algorithmic bytes / HIP-event-timed average launch) and, at N = 1,
+`cpu_baseline` (the reference's x86 int8 tier restated in C, oracle/,
+timed on a bounded sample on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+H, I, E, K = 1280, 896, 64, 6
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def traffic_for(kernel: str, workload: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(f"{kernel}@{workload}")
+    except Exception:
+        return None
+
+
+# ---------------------------------------------------------------------------
+# config 3: MoE decode
+# ---------------------------------------------------------------------------
+
+def make_moe_host(seed: int):
+    from franken_ocr_amd import synth
+
+    router = synth.f32_normal(synth.seed_of(seed), E * H, 0.0, 0.02).reshape(E, H)
+    wg = synth.int8_uniform(synth.seed_of(seed + 1), E * I * H)
+    wu = synth.int8_uniform(synth.seed_of(seed + 2), E * I * H)
+    wd = synth.int8_uniform(synth.seed_of(seed + 3), E * H * I)
+    sg = synth.f32_uniform(synth.seed_of(seed + 4), E * I, 1e-3, 2e-2)
+    su = synth.f32_uniform(synth.seed_of(seed + 5), E * I, 1e-3, 2e-2)
+    sd = synth.f32_uniform(synth.seed_of(seed + 6), E * H, 1e-3, 2e-2)
+    return router, wg, sg, wu, su, wd, sd
+
+
+def bench_moe(args, ctx):
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import MoeLayer
+
+    T = args.tokens
+    log(f"moe_decode: T={T}, {args.copies} layer copies, generating weights")
+    base = make_moe_host(100)
+    layers = []
+    for c in range(args.copies):
+        router = synth.f32_normal(synth.seed_of(1000 + c), E * H, 0.0, 0.02).reshape(E, H)
+        layers.append(MoeLayer(H, I, E, K, router, *base[1:], ctx=ctx))
+    hidden = synth.f32_normal(synth.seed_of(50), T * H).reshape(T, H)
+    dx = ctx.to_device(hidden)
+    dout = ctx.empty((T, H), np.float32)
+    idx_bufs = [ctx.empty((T, K), np.uint32) for _ in layers]
+    gate_bufs = [ctx.empty((T, K), np.float32) for _ in layers]
+
+    def step(i):
+        j = i % len(layers)
+        layers[j].decode(dx, dout, idx_bufs[j], gate_bufs[j], norm_topk=True, routed_scale=1.0, check_route=False)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    # distinct experts actually routed, per copy (for algorithmic bytes)
+    U = [len(np.unique(b.numpy())) for b in idx_bufs]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    ms = el / args.steps * 1e3
+    tok_s = T * args.steps / el
+
+    # per-kernel GPU time in a separate profiled pass (events between launches)
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    nprof = max(args.copies * 4, 32)
+    for i in range(nprof):
+        step(i)
+    prof = ctx.prof_read()
+    ctx.prof_enable(False)
+
+    mean_u = float(np.mean([U[i % len(U)] for i in range(args.steps)]))
+    pairs = T * K
+    gate_up_bytes = mean_u * 2 * (I * H + I * 4) + T * H + T * 4 + pairs * I * 4
+    layer_bytes = mean_u * (3 * I * H + 2 * I * 4 + H * 4) + E * H * 4 + 2 * T * H * 4
+    gu = prof.get("moe_gate_up", {"count": 1, "ms": float("nan")})
+    gu_ms = gu["ms"] / max(gu["count"], 1)
+    achieved = gate_up_bytes / (gu_ms * 1e-3) / 1e9
+    layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
+    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
+    log(f"U per copy {U}; per-kernel avg us {kernels}")
+    return {
+        "metric": "MoE-layer decode tokens/s + achieved HBM GB/s (% of 8 TB/s peak), 1 GPU",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "int8",
+        "config": {"workload": "moe_decode", "tokens": T, "hidden": H, "inter": I, "experts": E, "top_k": K,
+                   "norm_topk": True, "layer_copies_rotated": args.copies, "distinct_experts_mean": mean_u},
+        "roofline": {"bound": "hbm", "kernel": "moe_gate_up", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("moe_gate_up", "moe_decode_t%d" % T),
+                     "algorithmic_bytes_per_launch": int(gate_up_bytes), "avg_launch_us": round(gu_ms * 1e3, 3)},
+        "layer_roofline": {"achieved": round(layer_gbs, 1), "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                           "algorithmic_bytes_per_step": int(layer_bytes)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": (hidden, layers[0], base),
+    }
+
+
+def cpu_moe(args, inputs):
+    from oracle import pyoracle
+
+    hidden, layer0, base = inputs
+    from franken_ocr_amd import synth
+
+    router = synth.f32_normal(synth.seed_of(1000), E * H, 0.0, 0.02).reshape(E, H)
+    _, wg, sg, wu, su, wd, sd = base
+    L = pyoracle.lib()
+    tier = L.cpu_detect_tier()
+    T = hidden.shape[0]
+    out = np.zeros(T * H, np.float32)
+    idx = np.zeros(T * K, np.uint32)
+    gates = np.zeros(T * K, np.float32)
+    P = pyoracle.p
+    args_c = [P(np.ascontiguousarray(hidden)), T, H, I, E, K, P(router), P(wg), P(sg), P(wu), P(su), P(wd), P(sd),
+              1, 1.0, P(out), P(idx), P(gates)]
+    L.cpu_moe_decode(tier, *args_c)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        L.cpu_moe_decode(tier, *args_c)
+        n += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds or n >= 2000:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(T * n / el, 2), "unit": "tokens/s", "cores": min(K, os.cpu_count() or 1),
+            "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+            "sample": f"{n} MoE decode steps of T={T} tokens (first layer copy), {el:.1f} s; "
+                      f"top-{K} experts as concurrent single-thread tasks, tokens sequential (decoder.rs:2231-2252)"}
+
+
+# ---------------------------------------------------------------------------
+# config 2: LM head GEMV + argmax
+# ---------------------------------------------------------------------------
+
+def bench_lm_head(args, ctx):
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import QInt8, lm_head_i8
+
+    M, N, Kd = args.tokens, 129280, 1280
+    log(f"lm_head: M={M}, {args.copies} weight copies")
+    w = synth.int8_uniform(synth.seed_of(20), N * Kd)
+    s = synth.f32_uniform(synth.seed_of(21), N, 1e-3, 2e-2)
+    heads = [QInt8(w, s, N, Kd, ctx) for _ in range(args.copies)]
+    x = synth.f32_normal(synth.seed_of(22), M * Kd).reshape(M, Kd)
+    dx = ctx.to_device(x)
+    dl = ctx.empty((M, N), np.float32)
+    da = ctx.empty((M,), np.uint32)
+
+    def step(i):
+        lm_head_i8(heads[i % len(heads)], dx, da, dl)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    ms = el / args.steps * 1e3
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    for i in range(max(args.copies * 4, 24)):
+        step(i)
+    prof = ctx.prof_read()
+    ctx.prof_enable(False)
+    g = prof.get("lm_head_gemv", {"count": 1, "ms": float("nan")})
+    g_ms = g["ms"] / max(g["count"], 1)
+    gemv_bytes = N * Kd + N * 4 + M * Kd + M * 4 + M * N * 4
+    total_bytes = gemv_bytes + M * Kd * 4 + M * 4
+    achieved = gemv_bytes / (g_ms * 1e-3) / 1e9
+    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
+    log(f"per-kernel avg us {kernels}")
+    return {
+        "metric": "LM-head int8 GEMV + argmax tokens/s (129280x1280), 1 GPU",
+        "value": round(M * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "lm_head", "rows": M, "vocab": N, "hidden": Kd, "weight_copies_rotated": args.copies},
+        "roofline": {"bound": "hbm", "kernel": "lm_head_gemv", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("lm_head_gemv", f"lm_head_m{M}"),
+                     "algorithmic_bytes_per_launch": int(gemv_bytes), "avg_launch_us": round(g_ms * 1e3, 3)},
+        "step_achieved_gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1),
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": (x, w, s),
+    }
+
+
+def cpu_lm_head(args, inputs):
+    from oracle import pyoracle
+
+    x, w, s = inputs
+    L = pyoracle.lib()
+    tier = L.cpu_detect_tier()
+    M, N, Kd = x.shape[0], 129280, 1280
+    logits = np.zeros(M * N, np.float32)
+    am = np.zeros(M, np.uint32)
+    P = pyoracle.p
+    L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am))
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < args.cpu_seconds and n < 10000:
+        L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am))
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(M * n / el, 2), "unit": "tokens/s", "cores": int(L.cpu_threads()), "kind": "port",
+            "tier": L.cpu_tier_feature(tier).decode(),
+            "sample": f"{n} LM-head GEMV+argmax calls of M={M} rows, {el:.1f} s; 64-row blocks over all threads"}
+
+
+# ---------------------------------------------------------------------------
+# config 1: single igemm at the gate-proj shape
+# ---------------------------------------------------------------------------
+
+def bench_igemm(args, ctx):
+    from franken_ocr_amd import _abi, synth
+
+    M, N, Kd = args.tokens, 896, 1280
+    copies = 64  # 64 distinct experts' gate-proj weights (73 MB), rotated
+    w = synth.int8_uniform(synth.seed_of(1), copies * N * Kd)
+    a = synth.int8_uniform(synth.seed_of(2), M * Kd)
+    dw = ctx.to_device(w)
+    da = ctx.to_device(a)
+    dout = ctx.empty((M, N), np.int32)
+    import ctypes as C
+
+    def step(i):
+        off = (i % copies) * N * Kd
+        _abi.call("focr_hip_igemm_s8s8_dev", ctx.handle, da.c_ptr, dw.offset(off), M, Kd, N, dout.c_ptr)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    for i in range(256):
+        step(i)
+    prof = ctx.prof_read()
+    ctx.prof_enable(False)
+    g = prof["igemm_i8"]
+    g_ms = g["ms"] / g["count"]
+    nbytes = N * Kd + M * Kd + 2 * M * N * 4
+    achieved = nbytes / (g_ms * 1e-3) / 1e9
+    return {
+        "metric": "int8 igemm (gate-proj 896x1280) launches/s, 1 GPU",
+        "value": round(args.steps / el, 1), "unit": "launches/s", "ms_per_step": round(el / args.steps * 1e3, 5),
+        "dtype": "int8", "config": {"workload": "igemm", "m": M, "n": N, "k": Kd, "weight_copies_rotated": copies},
+        "roofline": {"bound": "hbm", "kernel": "igemm_i8", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
+        "_cpu_inputs": (a, w[: N * Kd]),
+    }
+
+
+def cpu_igemm(args, inputs):
+    from oracle import pyoracle
+
+    a, w = inputs
+    L = pyoracle.lib()
+    tier = L.cpu_detect_tier()
+    M, N, Kd = args.tokens, 896, 1280
+    out = np.zeros(M * N, np.int32)
+    P = pyoracle.p
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < args.cpu_seconds and n < 200000:
+        L.cpu_igemm_s8s8(tier, P(a), P(w), M, Kd, N, P(out))
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(n / el, 1), "unit": "launches/s", "cores": 1, "kind": "port",
+            "tier": L.cpu_tier_feature(tier).decode(), "sample": f"{n} single-thread igemm calls, {el:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+# config 5: R-SWA decode attention
+# ---------------------------------------------------------------------------
+
+def bench_rswa(args, ctx):
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import RingCache
+
+    B, G, NH, D = 8, 1024, 10, 128
+    copies = args.copies
+    caches = []
+    rng = np.random.default_rng(7)
+    ring_lens = [int(x) for x in rng.integers(0, 129, B)]
+    for c in range(copies):
+        cache = RingCache(B, G, ctx)
+        for s in range(B):
+            k = synth.f32_normal(synth.seed_of(2000 + s), NH * G * D)
+            v = synth.f32_normal(synth.seed_of(2100 + s), NH * G * D)
+            cache.record_prefill(s, ctx.to_device(k), ctx.to_device(v), G)
+            rl = ring_lens[s]
+            cache.set_state(s, rl, rl % 128 if rl < 128 else int(rng.integers(0, 128)))
+        caches.append(cache)
+    q = ctx.to_device(synth.f32_normal(synth.seed_of(2200), B * NH * D).reshape(B, NH * D))
+    out = ctx.empty((B, NH * D), np.float32)
+
+    def step(i):
+        caches[i % copies].decode_attention(q, out)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    for i in range(max(copies * 8, 64)):
+        step(i)
+    prof = ctx.prof_read()
+    ctx.prof_enable(False)
+    g = prof["rswa_chunk"]
+    g_ms = g["ms"] / g["count"]
+    keys = sum(G + r for r in ring_lens)
+    nbytes = 2 * NH * keys * D * 4 + 2 * B * NH * D * 4
+    achieved = nbytes / (g_ms * 1e-3) / 1e9
+    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
+    return {
+        "metric": "R-SWA decode attention steps/s (B=8, G=1024, 10x128), 1 GPU",
+        "value": round(args.steps / el, 1), "unit": "steps/s", "ms_per_step": round(el / args.steps * 1e3, 5),
+        "dtype": "f32", "config": {"workload": "rswa", "streams": B, "ref_rows": G, "ring_lens": ring_lens,
+                                   "cache_copies_rotated": copies},
+        "roofline": {"bound": "hbm", "kernel": "rswa_chunk", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
+WORKLOADS = {
+    "moe_decode": (bench_moe, cpu_moe),
+    "lm_head": (bench_lm_head, cpu_lm_head),
+    "igemm": (bench_igemm, cpu_igemm),
+    "rswa": (bench_rswa, None),
+}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="moe_decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=None, help="T (moe), M (lm_head/igemm)")
+    ap.add_argument("--copies", type=int, default=None, help="distinct weight copies rotated (defeats MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
+              file=sys.stderr)
+        return 2
+    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4)}
+    dt, dc = defaults[args.workload]
+    args.tokens = args.tokens or dt
+    args.copies = args.copies or dc
+
+    from franken_ocr_amd.device import Context
+
+    ctx = Context(0)
+    log(f"device {ctx.info()}")
+    run, cpu = WORKLOADS[args.workload]
+    res = run(args, ctx)
+    cpu_inputs = res.pop("_cpu_inputs")
+    line = {
+        "metric": res.pop("metric"),
+        "value": res.pop("value"),
+        "unit": res.pop("unit"),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": res.pop("dtype"),
+        "data": "synthetic (seeded splitmix64; int8 weights uniform [-127,127], scales U(1e-3,2e-2), "
+                "activations N(0,1)); no checkpoint",
+        "config": res.pop("config"),
+    }
+    line.update(res)
+    if cpu is not None and not args.no_cpu and cpu_inputs is not None:
+        log("cpu baseline (reference x86 int8 tier restated in C) ...")
+        line["cpu_baseline"] = cpu(args, cpu_inputs)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

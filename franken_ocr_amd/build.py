@@ -1,0 +1,88 @@
+"""Build recipe for libfocr_hip.so (gfx950 only) — run in-tree.
+
+    python -m franken_ocr_amd.build        # or __graft_entry__.build()
+
+Every .hip/.cpp under csrc/ is compiled with hipcc for --offload-arch=gfx950
+and linked into franken_ocr_amd/libfocr_hip.so. Flags that matter for parity:
+
+* -ffp-contract=off   no a*b+c -> FMA contraction: every f32 op rounds on its
+                      own, as the reference's Rust code does, so dequant,
+                      int4 group sums and the MoE combine are bit-reproducible.
+* -Xclang -target-feature -Xclang -packed-fp32-ops
+                      keep the compiler from emitting packed-FP32 VALU ops.
+No -ffast-math: fp32 division and sqrt stay correctly rounded (the
+quantizer's amax/127 and 1/a_scale must match the CPU bit for bit).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OUT = PKG / "libfocr_hip.so"
+BUILD = PKG / "_build"
+
+ARCH = "gfx950"
+COMMON = [
+    "-std=c++17",
+    "-O3",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-ffp-contract=off",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-result",
+    "-Wno-unused-value",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(cand).exists():
+        raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
+    return cand
+
+
+def sources() -> list[Path]:
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel/host source for gfx950 and link the shared library."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = sources()
+    jobs = min(8, len(srcs), os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT} from {len(srcs)} sources", file=sys.stderr)
+    return OUT
+
+
+if __name__ == "__main__":
+    build(verbose=True)

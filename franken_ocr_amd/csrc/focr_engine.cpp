@@ -1,0 +1,805 @@
+// focr_engine.cpp — C ABI, layer 2: the runtime self-test, uploaded weights
+// and the device-resident engine ops (GEMV, LM head + argmax, MoE decode,
+// R-SWA), plus the GPU-timed profiling counters.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "focr_internal.hpp"
+
+using namespace focr;
+
+namespace {
+
+std::string fmt(const char* f, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(buf, sizeof(buf), f, ap);
+    va_end(ap);
+    return buf;
+}
+
+struct Guard {
+    std::lock_guard<std::mutex> lk;
+    explicit Guard(focr_hip_ctx* c) : lk(c->mu) { clear_error(); }
+};
+
+#define ENGINE_CTX(ctx)                                                   \
+    if (!(ctx)) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx"); \
+    Guard guard_(ctx);                                                    \
+    FOCR_HIP_TRY((ctx)->bind(), "hipSetDevice")
+
+// dispatch.rs:340-347 xs32
+uint32_t xs32(uint32_t& s) {
+    s ^= s << 13;
+    s ^= s >> 17;
+    s ^= s << 5;
+    return s;
+}
+
+struct Shape {
+    const char* label;
+    size_t m, k, n;
+    uint32_t seed;
+};
+
+// dispatch.rs:352-368 SELFTEST_SHAPES
+const Shape kShapes[] = {
+    {"edge:1x1x1", 1, 1, 1, 0x11111111u},
+    {"edge:1x7x3", 1, 7, 3, 0x22222222u},
+    {"edge:2x3x2", 2, 3, 2, 0x33333333u},
+    {"ktail:1x15x8", 1, 15, 8, 0x44444444u},
+    {"ktail:1x16x8", 1, 16, 8, 0x55555555u},
+    {"ktail:1x17x8", 1, 17, 8, 0x66666666u},
+    {"ktail:4x33x5", 4, 33, 5, 0x77777777u},
+    {"model:attn_proj_gemv", 1, 1280, 128, 0x0badc0deu},
+    {"model:o_proj_gemv", 1, 1280, 1280, 0x12345678u},
+    {"model:expert_down_gemv", 1, 6848, 256, 0x9abcdef0u},
+    {"model:prefill_tile", 4, 1280, 64, 0x0f0f0f0fu},
+    {"overflow:max_mag_k6848", 1, 6848, 4, 0u},
+};
+
+// The self-test's in-process check: a plain i32 dot, as scalar.rs:103-115.
+template <typename TA>
+void scalar_check(const TA* a, const int8_t* b, size_t m, size_t k, size_t n, int32_t* out) {
+    for (size_t i = 0; i < m; ++i)
+        for (size_t o = 0; o < n; ++o) {
+            uint32_t acc = 0;
+            for (size_t p = 0; p < k; ++p) acc += static_cast<uint32_t>(static_cast<int32_t>(a[i * k + p]) * b[o * k + p]);
+            out[i * n + o] = static_cast<int32_t>(static_cast<uint32_t>(out[i * n + o]) + acc);
+        }
+}
+
+void append(std::string& j, const char* f, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(buf, sizeof(buf), f, ap);
+    va_end(ap);
+    j += buf;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_selftest(focr_hip_ctx* ctx, char* json, size_t cap, int32_t* all_ok) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    bool ok_all = true;
+    std::string j = "{\"selected\":\"gfx950\",\"feature\":\"gfx950+mfma-i8\",\"available\":[\"gfx950\"],\"cases\":[";
+    bool first = true;
+    for (const Shape& sh : kShapes) {
+        for (int dom = 0; dom < 2; ++dom) {
+            const size_t mk = sh.m * sh.k, nk = sh.n * sh.k, mn = sh.m * sh.n;
+            std::vector<int8_t> as(mk), b(nk);
+            std::vector<uint8_t> au(mk);
+            if (sh.seed == 0) {
+                // worst-case magnitude (dispatch.rs:382-385, :403-404)
+                std::fill(as.begin(), as.end(), static_cast<int8_t>(127));
+                std::fill(au.begin(), au.end(), static_cast<uint8_t>(255));
+                std::fill(b.begin(), b.end(), static_cast<int8_t>(-128));
+            } else {
+                uint32_t st = dom == 0 ? (sh.seed | 1u) : (((sh.seed << 7) | (sh.seed >> 25)) | 1u);
+                for (size_t i = 0; i < mk; ++i) {
+                    const uint32_t v = xs32(st) & 0xffu;
+                    as[i] = static_cast<int8_t>(static_cast<uint8_t>(v));
+                    au[i] = static_cast<uint8_t>(v);
+                }
+                for (size_t i = 0; i < nk; ++i) b[i] = static_cast<int8_t>(static_cast<uint8_t>(xs32(st) & 0xffu));
+            }
+            std::vector<int32_t> got(mn, 0), want(mn, 0);
+            int32_t st;
+            if (dom == 0) {
+                st = focr_hip_igemm_s8s8(ctx, as.data(), mk, b.data(), nk, sh.m, sh.k, sh.n, got.data(), mn);
+                scalar_check(as.data(), b.data(), sh.m, sh.k, sh.n, want.data());
+            } else {
+                st = focr_hip_igemm_u8s8(ctx, au.data(), mk, b.data(), nk, sh.m, sh.k, sh.n, got.data(), mn);
+                scalar_check(au.data(), b.data(), sh.m, sh.k, sh.n, want.data());
+            }
+            if (st) return st;
+            size_t mism = 0, first_bad = 0;
+            for (size_t i = 0; i < mn; ++i)
+                if (got[i] != want[i]) {
+                    if (!mism) first_bad = i;
+                    ++mism;
+                }
+            ok_all = ok_all && mism == 0;
+            append(j, "%s{\"kind\":\"%s\",\"label\":\"%s\",\"m\":%zu,\"k\":%zu,\"n\":%zu,\"ok\":%s,\"mismatches\":%zu",
+                   first ? "" : ",", dom == 0 ? "s8s8" : "u8s8", sh.label, sh.m, sh.k, sh.n, mism ? "false" : "true",
+                   mism);
+            if (mism)
+                append(j, ",\"first_bad\":[%zu,%d,%d]", first_bad, got[first_bad], want[first_bad]);
+            j += "}";
+            first = false;
+        }
+    }
+    append(j, "],\"all_ok\":%s}", ok_all ? "true" : "false");
+    if (all_ok) *all_ok = ok_all ? 1 : 0;
+    if (json && cap) snprintf(json, cap, "%s", j.c_str());
+    return FOCR_HIP_OK;
+}
+
+// ---- QInt8 handles ---------------------------------------------------------
+
+int32_t focr_hip_qint8_upload(focr_hip_ctx* ctx, const int8_t* w, const float* scales, size_t n, size_t k,
+                              focr_hip_qint8** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "qint8_upload: null out");
+    *out = nullptr;
+    if (n * k && (!w || !scales)) return fail(FOCR_HIP_E_ARG, "qint8_upload: null host pointer");
+    if (k % 16 != 0 || k == 0 || n == 0 || n > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+        return fail(FOCR_HIP_E_SHAPE, fmt("QInt8: gfx950 tier needs k a positive multiple of 16 and 0 < n < 2^31 (n=%zu k=%zu)", n, k));
+    std::unique_ptr<focr_hip_qint8> q(new focr_hip_qint8());
+    q->ctx = ctx;
+    q->n = n;
+    q->k = k;
+    q->owned = true;
+    FOCR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&q->w), n * k), "hipMalloc qint8 w");
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&q->scales), n * sizeof(float));
+    if (e != hipSuccess) {
+        hipFree(q->w);
+        return hip_fail(e, "hipMalloc qint8 scales");
+    }
+    FOCR_HIP_TRY(hipMemcpyAsync(q->w, w, n * k, hipMemcpyHostToDevice, ctx->stream), "H2D qint8 w");
+    FOCR_HIP_TRY(hipMemcpyAsync(q->scales, scales, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream), "H2D scales");
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    *out = q.release();
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_qint8_from_device(focr_hip_ctx* ctx, const int8_t* w, const float* scales, size_t n, size_t k,
+                                   focr_hip_qint8** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "qint8_from_device: null out");
+    *out = nullptr;
+    if (!w || !scales) return fail(FOCR_HIP_E_ARG, "qint8_from_device: null device pointer");
+    if (k % 16 != 0 || k == 0 || n == 0 || n > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+        return fail(FOCR_HIP_E_SHAPE, fmt("QInt8: gfx950 tier needs k a positive multiple of 16 and 0 < n < 2^31 (n=%zu k=%zu)", n, k));
+    if (reinterpret_cast<uintptr_t>(w) % 16 != 0)
+        return fail(FOCR_HIP_E_ARG, "qint8_from_device: weights must be 16-byte aligned");
+    focr_hip_qint8* q = new focr_hip_qint8();
+    q->ctx = ctx;
+    q->w = const_cast<int8_t*>(w);
+    q->scales = const_cast<float*>(scales);
+    q->n = n;
+    q->k = k;
+    q->owned = false;
+    *out = q;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_qint8_free(focr_hip_qint8* w) {
+    if (!w) return FOCR_HIP_OK;
+    if (w->owned) {
+        hipSetDevice(w->ctx->device);
+        hipStreamSynchronize(w->ctx->stream);
+        hipFree(w->w);
+        hipFree(w->scales);
+    }
+    delete w;
+    return FOCR_HIP_OK;
+}
+
+// ---- GEMV / LM head ------------------------------------------------------
+
+int32_t focr_hip_quantize_rows_i8(focr_hip_ctx* ctx, const float* x, size_t m, size_t k, int8_t* xq,
+                                  float* a_scales, int32_t ties_even) {
+    ENGINE_CTX(ctx);
+    if (m == 0) return FOCR_HIP_OK;
+    if (!x || !xq || !a_scales) return fail(FOCR_HIP_E_ARG, "quantize_rows_i8: null device pointer");
+    if (m > 65535 || k > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+        return fail(FOCR_HIP_E_SHAPE, "quantize_rows_i8: too many rows");
+    ProfScope ps(ctx, "quantize_rows");
+    FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)k, xq, a_scales, ties_even != 0), "quantize launch");
+    return FOCR_HIP_OK;
+}
+
+static int32_t gemv_checks(const char* name, const focr_hip_qint8* w, size_t m) {
+    if (!w) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("%s: null weight handle", name));
+    if (m < 1 || m > 32) return fail(FOCR_HIP_E_SHAPE, fmt("%s: m %zu outside 1..=32 for one call", name, m));
+    if (m * w->k > 57344) return fail(FOCR_HIP_E_SHAPE, fmt("%s: m*k %zu exceeds the 56 KiB LDS stage", name, m * w->k));
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_gemv_i8_prequant(focr_hip_ctx* ctx, const focr_hip_qint8* w, const int8_t* xq,
+                                  const float* a_scales, size_t m, float* y, int32_t* acc) {
+    ENGINE_CTX(ctx);
+    int32_t st = gemv_checks("gemv_i8_prequant", w, m);
+    if (st) return st;
+    if (!xq || !a_scales || !y) return fail(FOCR_HIP_E_ARG, "gemv_i8_prequant: null device pointer");
+    ProfScope ps(ctx, "gemv_i8");
+    FOCR_HIP_TRY(launch_gemv_i8(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, a_scales, (int)m, y, acc,
+                                nullptr, nullptr, ctx->cu_count),
+                 "gemv launch");
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_gemv_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m, float* y) {
+    ENGINE_CTX(ctx);
+    int32_t st = gemv_checks("gemv_i8", w, m);
+    if (st) return st;
+    if (!x || !y) return fail(FOCR_HIP_E_ARG, "gemv_i8: null device pointer");
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
+    if (!xq || !xs) return FOCR_HIP_E_OOM;
+    {
+        ProfScope ps(ctx, "quantize_rows");
+        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, false), "quantize launch");
+    }
+    ProfScope ps(ctx, "gemv_i8");
+    FOCR_HIP_TRY(launch_gemv_i8(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y, nullptr,
+                                nullptr, nullptr, ctx->cu_count),
+                 "gemv launch");
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m, float* logits,
+                            uint32_t* argmax) {
+    ENGINE_CTX(ctx);
+    int32_t st = gemv_checks("lm_head_i8", w, m);
+    if (st) return st;
+    if (!x || !argmax) return fail(FOCR_HIP_E_ARG, "lm_head_i8: null device pointer");
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
+    const int nparts = gemv_i8_nparts((int)w->n, ctx->cu_count);
+    uint64_t* keys = static_cast<uint64_t*>(ctx->scratch_get(kScrArg, m * nparts * sizeof(uint64_t)));
+    float* y = logits ? logits : static_cast<float*>(ctx->scratch_get(kScrLogits, m * w->n * sizeof(float)));
+    if (!xq || !xs || !keys || !y) return FOCR_HIP_E_OOM;
+    {
+        ProfScope ps(ctx, "quantize_rows");
+        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, false), "quantize launch");
+    }
+    int np = 0;
+    {
+        ProfScope ps(ctx, "lm_head_gemv");
+        FOCR_HIP_TRY(launch_gemv_i8(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y, nullptr,
+                                    keys, &np, ctx->cu_count),
+                     "lm_head gemv launch");
+    }
+    ProfScope ps(ctx, "argmax_reduce");
+    FOCR_HIP_TRY(launch_argmax_reduce(ctx->stream, keys, (int)m, np, argmax), "argmax launch");
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_argmax_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n, uint32_t* argmax) {
+    ENGINE_CTX(ctx);
+    if (m == 0) return FOCR_HIP_OK;
+    if (n == 0) return fail(FOCR_HIP_E_SHAPE, "sampler::argmax_row: empty logits row");
+    if (!logits || !argmax) return fail(FOCR_HIP_E_ARG, "argmax_rows: null device pointer");
+    if (m > 65535 || n > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+        return fail(FOCR_HIP_E_SHAPE, "argmax_rows: shape exceeds the gfx950 tier limit");
+    const int nparts = static_cast<int>(std::min<size_t>(256, (n + 4095) / 4096));
+    uint64_t* keys = static_cast<uint64_t*>(ctx->scratch_get(kScrArg, m * nparts * sizeof(uint64_t)));
+    if (!keys) return FOCR_HIP_E_OOM;
+    ProfScope ps(ctx, "argmax_rows");
+    FOCR_HIP_TRY(launch_argmax_rows(ctx->stream, logits, (int)m, (int)n, keys, nparts, argmax), "argmax launch");
+    return FOCR_HIP_OK;
+}
+
+}  // extern "C"
+
+// ---- MoE layer ---------------------------------------------------------------
+
+namespace {
+
+template <typename T>
+int32_t upload(focr_hip_ctx* ctx, T** dst, const T* src, size_t count, bool from_device, const char* what) {
+    if (from_device) {
+        *dst = const_cast<T*>(src);
+        return FOCR_HIP_OK;
+    }
+    FOCR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(dst), std::max<size_t>(count * sizeof(T), 16)), what);
+    FOCR_HIP_TRY(hipMemcpyAsync(*dst, src, count * sizeof(T), hipMemcpyHostToDevice, ctx->stream), what);
+    return FOCR_HIP_OK;
+}
+
+void free_moe(focr_hip_moe_layer* L) {
+    if (L->owned) {
+        hipFree(L->router);
+        hipFree(L->wg);
+        hipFree(L->wu);
+        hipFree(L->wd);
+        hipFree(L->sg);
+        hipFree(L->su);
+        hipFree(L->sd);
+    }
+    if (L->shared_owned) {
+        hipFree(L->swg);
+        hipFree(L->swu);
+        hipFree(L->swd);
+        hipFree(L->ssg);
+        hipFree(L->ssu);
+        hipFree(L->ssd);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_moe_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t inter, size_t n_experts, size_t top_k,
+                                  const float* router, const int8_t* wg, const float* sg, const int8_t* wu,
+                                  const float* su, const int8_t* wd, const float* sd, int32_t from_device,
+                                  focr_hip_moe_layer** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "moe_layer_create: null out");
+    *out = nullptr;
+    if (!router || !wg || !sg || !wu || !su || !wd || !sd) return fail(FOCR_HIP_E_ARG, "moe_layer_create: null pointer");
+    if (n_experts < top_k) return fail(FOCR_HIP_E_SHAPE, fmt("moe::route: n_routed_experts %zu < top_k %zu", n_experts, top_k));
+    if (n_experts < 1 || n_experts > 64 || top_k < 1 || top_k > 8)
+        return fail(FOCR_HIP_E_SHAPE, fmt("moe_layer_create: gfx950 tier supports 1..=64 experts and top_k 1..=8 (got %zu, %zu)", n_experts, top_k));
+    if (hidden % 16 || inter % 16 || hidden == 0 || inter == 0 || hidden > 2048 || inter > 2048)
+        return fail(FOCR_HIP_E_SHAPE, fmt("moe_layer_create: hidden/inter must be multiples of 16 in 16..=2048 (got %zu, %zu)", hidden, inter));
+    std::unique_ptr<focr_hip_moe_layer> L(new focr_hip_moe_layer());
+    L->ctx = ctx;
+    L->hidden = hidden;
+    L->inter = inter;
+    L->n_experts = n_experts;
+    L->top_k = top_k;
+    L->owned = !from_device;
+    const size_t E = n_experts;
+    int32_t st = FOCR_HIP_OK;
+    if ((st = upload(ctx, &L->router, router, E * hidden, from_device, "router")) ||
+        (st = upload(ctx, &L->wg, wg, E * inter * hidden, from_device, "w_gate")) ||
+        (st = upload(ctx, &L->sg, sg, E * inter, from_device, "s_gate")) ||
+        (st = upload(ctx, &L->wu, wu, E * inter * hidden, from_device, "w_up")) ||
+        (st = upload(ctx, &L->su, su, E * inter, from_device, "s_up")) ||
+        (st = upload(ctx, &L->wd, wd, E * hidden * inter, from_device, "w_down")) ||
+        (st = upload(ctx, &L->sd, sd, E * hidden, from_device, "s_down"))) {
+        hipStreamSynchronize(ctx->stream);
+        free_moe(L.get());
+        return st;
+    }
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    *out = L.release();
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_layer_set_shared(focr_hip_moe_layer* L, size_t shared_inter, const int8_t* wg, const float* sg,
+                                      const int8_t* wu, const float* su, const int8_t* wd, const float* sd,
+                                      int32_t from_device) {
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "null moe layer");
+    focr_hip_ctx* ctx = L->ctx;
+    ENGINE_CTX(ctx);
+    if (!wg || !sg || !wu || !su || !wd || !sd) return fail(FOCR_HIP_E_ARG, "moe_layer_set_shared: null pointer");
+    if (shared_inter % 16 || shared_inter == 0 || shared_inter > 2048)
+        return fail(FOCR_HIP_E_SHAPE, fmt("moe_layer_set_shared: shared_inter must be a multiple of 16 in 16..=2048 (got %zu)", shared_inter));
+    const size_t h = L->hidden;
+    focr_hip_moe_layer tmp = *L;
+    tmp.shared_owned = !from_device;
+    int32_t st = FOCR_HIP_OK;
+    if ((st = upload(ctx, &tmp.swg, wg, shared_inter * h, from_device, "shared w_gate")) ||
+        (st = upload(ctx, &tmp.ssg, sg, shared_inter, from_device, "shared s_gate")) ||
+        (st = upload(ctx, &tmp.swu, wu, shared_inter * h, from_device, "shared w_up")) ||
+        (st = upload(ctx, &tmp.ssu, su, shared_inter, from_device, "shared s_up")) ||
+        (st = upload(ctx, &tmp.swd, wd, h * shared_inter, from_device, "shared w_down")) ||
+        (st = upload(ctx, &tmp.ssd, sd, h, from_device, "shared s_down")))
+        return st;
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (L->shared_owned) {
+        hipFree(L->swg);
+        hipFree(L->swu);
+        hipFree(L->swd);
+        hipFree(L->ssg);
+        hipFree(L->ssu);
+        hipFree(L->ssd);
+    }
+    L->shared_inter = shared_inter;
+    L->swg = tmp.swg;
+    L->ssg = tmp.ssg;
+    L->swu = tmp.swu;
+    L->ssu = tmp.ssu;
+    L->swd = tmp.swd;
+    L->ssd = tmp.ssd;
+    L->shared_owned = tmp.shared_owned;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_layer_free(focr_hip_moe_layer* L) {
+    if (!L) return FOCR_HIP_OK;
+    hipSetDevice(L->ctx->device);
+    hipStreamSynchronize(L->ctx->stream);
+    free_moe(L);
+    delete L;
+    return FOCR_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct MoeScratch {
+    float* logits;
+    int8_t* xq;
+    float* xs;
+    void* tables;
+    uint32_t* idx;
+    float* gates;
+    int* flag;
+    float* act;
+    float* ybuf;
+    float* shared_act;
+    float* shared_y;
+};
+
+int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    const size_t pairs = t * L->top_k;
+    const size_t tb = moe_route_table_bytes(d);
+    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, tb + pairs * 8 + 256));
+    s->logits = static_cast<float*>(ctx->scratch_get(kScrLogits, t * L->n_experts * sizeof(float)));
+    s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
+    s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
+    s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
+    s->ybuf = static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float)));
+    s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
+    s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, 64));
+    if (!route || !s->logits || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || (with_shared && !s->shared_y))
+        return FOCR_HIP_E_OOM;
+    s->tables = route;
+    s->idx = reinterpret_cast<uint32_t*>(route + tb);
+    s->gates = reinterpret_cast<float*>(route + tb + pairs * 4);
+    s->shared_act = with_shared ? s->act + pairs * L->inter : nullptr;
+    return FOCR_HIP_OK;
+}
+
+int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t with_shared) {
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("%s: null moe layer", name));
+    if (!hidden) return fail(FOCR_HIP_E_ARG, fmt("%s: null hidden", name));
+    if (t < 1 || t > 64) return fail(FOCR_HIP_E_SHAPE, fmt("%s: t %zu outside 1..=64 for one call", name, t));
+    if (with_shared && !L->swg) return fail(FOCR_HIP_E_ARG, fmt("%s: with_shared set but no shared expert uploaded", name));
+    return FOCR_HIP_OK;
+}
+
+int32_t check_route_flag(focr_hip_ctx* ctx, const int* dflag) {
+    int flag = 0;
+    FOCR_HIP_TRY(hipMemcpyAsync(&flag, dflag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (flag) return fail(FOCR_HIP_E_ROUTE, "moe::route: no finite router score");
+    return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                           int32_t norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs) {
+    ENGINE_CTX(ctx);
+    int32_t st = moe_checks("moe_route", L, hidden, t, 0);
+    if (st) return st;
+    MoeScratch s;
+    if ((st = moe_scratch(ctx, L, t, false, &s))) return st;
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    {
+        ProfScope ps(ctx, "moe_router");
+        FOCR_HIP_TRY(launch_moe_router(ctx->stream, d, hidden, L->router, s.logits, s.xq, s.xs), "router launch");
+    }
+    {
+        ProfScope ps(ctx, "moe_topk");
+        FOCR_HIP_TRY(launch_moe_topk(ctx->stream, d, s.logits, norm_topk, routed_scale, idx ? idx : s.idx,
+                                     gates ? gates : s.gates, probs, s.tables, s.flag),
+                     "topk launch");
+    }
+    return check_route_flag(ctx, s.flag);
+}
+
+int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                            int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
+                            float* gates, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    int32_t st = moe_checks("moe_decode", L, hidden, t, with_shared);
+    if (st) return st;
+    if (!out) return fail(FOCR_HIP_E_ARG, "moe_decode: null out");
+    MoeScratch s;
+    if ((st = moe_scratch(ctx, L, t, with_shared != 0, &s))) return st;
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    const int max_active = static_cast<int>(std::min<size_t>(L->n_experts, t * L->top_k));
+    hipStream_t str = ctx->stream;
+    {
+        ProfScope ps(ctx, "moe_router");
+        FOCR_HIP_TRY(launch_moe_router(str, d, hidden, L->router, s.logits, s.xq, s.xs), "router launch");
+    }
+    {
+        ProfScope ps(ctx, "moe_topk");
+        FOCR_HIP_TRY(launch_moe_topk(str, d, s.logits, norm_topk, routed_scale, idx ? idx : s.idx,
+                                     gates ? gates : s.gates, nullptr, s.tables, s.flag),
+                     "topk launch");
+    }
+    {
+        ProfScope ps(ctx, "moe_gate_up");
+        FOCR_HIP_TRY(launch_moe_gate_up(str, d, s.tables, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter,
+                                        max_active, false),
+                     "gate_up launch");
+    }
+    {
+        ProfScope ps(ctx, "moe_down");
+        FOCR_HIP_TRY(launch_moe_down(str, d, s.tables, s.act, L->wd, L->sd, nullptr, s.ybuf, (int)L->inter, max_active,
+                                     false),
+                     "down launch");
+    }
+    if (with_shared) {
+        {
+            ProfScope ps(ctx, "moe_shared_gate_up");
+            FOCR_HIP_TRY(launch_moe_gate_up(str, d, s.tables, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
+                                            (int)L->shared_inter, 1, true),
+                         "shared gate_up launch");
+        }
+        {
+            ProfScope ps(ctx, "moe_shared_down");
+            FOCR_HIP_TRY(launch_moe_down(str, d, s.tables, s.shared_act, L->swd, L->ssd, nullptr, s.shared_y,
+                                         (int)L->shared_inter, 1, true),
+                         "shared down launch");
+        }
+    }
+    {
+        ProfScope ps(ctx, "moe_combine");
+        FOCR_HIP_TRY(launch_moe_combine(str, d, s.tables, s.ybuf, with_shared ? s.shared_y : nullptr, out),
+                     "combine launch");
+    }
+    if (check_route) return check_route_flag(ctx, s.flag);
+    return FOCR_HIP_OK;
+}
+
+// ---- R-SWA --------------------------------------------------------------------
+
+int32_t focr_hip_rswa_create(focr_hip_ctx* ctx, size_t n_streams, size_t ref_capacity, focr_hip_rswa** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "rswa_create: null out");
+    *out = nullptr;
+    if (n_streams == 0) return fail(FOCR_HIP_E_SHAPE, "rswa: batched cache needs at least one stream");
+    if (ref_capacity > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, "rswa: ref_capacity exceeds the gfx950 tier limit");
+    std::unique_ptr<focr_hip_rswa> c(new focr_hip_rswa());
+    c->ctx = ctx;
+    c->n_streams = n_streams;
+    c->ref_capacity = ref_capacity;
+    c->prefill_len.assign(n_streams, -1);
+    c->ring_len.assign(n_streams, 0);
+    c->ring_pos.assign(n_streams, 0);
+    const size_t bytes = n_streams * c->stream_floats() * sizeof(float);
+    FOCR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&c->base), bytes), "hipMalloc rswa");
+    FOCR_HIP_TRY(hipMemsetAsync(c->base, 0, bytes, ctx->stream), "hipMemsetAsync rswa");
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    *out = c.release();
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_rswa_free(focr_hip_rswa* c) {
+    if (!c) return FOCR_HIP_OK;
+    hipSetDevice(c->ctx->device);
+    hipStreamSynchronize(c->ctx->stream);
+    hipFree(c->base);
+    delete c;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_rswa_record_prefill(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* k,
+                                     const float* v, size_t seq) {
+    ENGINE_CTX(ctx);
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    if (stream >= c->n_streams) return fail(FOCR_HIP_E_SHAPE, fmt("rswa: stream %zu >= num_streams %zu", stream, c->n_streams));
+    if (seq > c->ref_capacity)
+        return fail(FOCR_HIP_E_STATE, fmt("rswa: prefill seq %zu exceeds ref_capacity %zu", seq, c->ref_capacity));
+    if (seq && (!k || !v)) return fail(FOCR_HIP_E_ARG, "rswa_record_prefill: null device pointer");
+    // head-major [10][seq][128] -> region rows [h][0..seq)
+    const size_t row = static_cast<size_t>(kHeadDim) * sizeof(float);
+    if (seq) {
+        FOCR_HIP_TRY(hipMemcpy2DAsync(c->ref_k(stream), c->ref_capacity * row, k, seq * row, seq * row, kNumHeads,
+                                      hipMemcpyDeviceToDevice, ctx->stream),
+                     "copy prefill k");
+        FOCR_HIP_TRY(hipMemcpy2DAsync(c->ref_v(stream), c->ref_capacity * row, v, seq * row, seq * row, kNumHeads,
+                                      hipMemcpyDeviceToDevice, ctx->stream),
+                     "copy prefill v");
+    }
+    c->prefill_len[stream] = static_cast<int64_t>(seq);
+    c->ring_len[stream] = 0;
+    c->ring_pos[stream] = 0;
+    return FOCR_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// rswa.rs:467-494: slot and cursor update for one stream.
+uint32_t next_slot(focr_hip_rswa* c, size_t s) {
+    uint32_t slot;
+    if (c->ring_len[s] < static_cast<uint32_t>(kRingWindow)) {
+        slot = c->ring_len[s];
+        c->ring_len[s] += 1;
+        c->ring_pos[s] = c->ring_len[s] % kRingWindow;
+    } else {
+        slot = c->ring_pos[s];
+        c->ring_pos[s] = (c->ring_pos[s] + 1) % kRingWindow;
+    }
+    return slot;
+}
+
+int32_t rswa_write_all(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* k_steps, const float* v_steps,
+                       uint32_t* slots) {
+    for (size_t s = 0; s < c->n_streams; ++s)
+        if (c->prefill_len[s] < 0) return fail(FOCR_HIP_E_STATE, "rswa: write_decode_step before record_prefill");
+    if (!k_steps || !v_steps) return fail(FOCR_HIP_E_ARG, "rswa_write_decode_step: null device pointer");
+    for (size_t s0 = 0; s0 < c->n_streams; s0 += RswaStepArgs::kMax) {
+        RswaStepArgs a{};
+        a.n = static_cast<uint32_t>(std::min<size_t>(RswaStepArgs::kMax, c->n_streams - s0));
+        for (uint32_t i = 0; i < a.n; ++i) {
+            a.slot[i] = next_slot(c, s0 + i);
+            if (slots) slots[s0 + i] = a.slot[i];
+        }
+        const size_t off = s0 * kNumHeads * kHeadDim;
+        ProfScope ps(ctx, "rswa_write");
+        FOCR_HIP_TRY(launch_rswa_write(ctx->stream, c, s0, a, k_steps + off, v_steps + off), "ring write launch");
+    }
+    return FOCR_HIP_OK;
+}
+
+int32_t rswa_attend_all(focr_hip_ctx* ctx, const focr_hip_rswa* c, const float* q, float* out) {
+    for (size_t s = 0; s < c->n_streams; ++s) {
+        if (c->prefill_len[s] < 0) return fail(FOCR_HIP_E_STATE, "rswa: decode_attention before record_prefill");
+        if (c->prefill_len[s] + c->ring_len[s] == 0)
+            return fail(FOCR_HIP_E_STATE, "rswa: empty attention key set (prefill_len=0, ring_len=0)");
+    }
+    if (!q || !out) return fail(FOCR_HIP_E_ARG, "rswa_decode_attention: null device pointer");
+    const size_t chunk_streams = std::min<size_t>(RswaStepArgs::kMax, c->n_streams);
+    float* partials = static_cast<float*>(
+        ctx->scratch_get(kScrRswa, rswa_partials_bytes(chunk_streams, c->ref_capacity + kRingWindow)));
+    if (!partials) return FOCR_HIP_E_OOM;
+    for (size_t s0 = 0; s0 < c->n_streams; s0 += RswaStepArgs::kMax) {
+        RswaStepArgs a{};
+        a.n = static_cast<uint32_t>(std::min<size_t>(RswaStepArgs::kMax, c->n_streams - s0));
+        for (uint32_t i = 0; i < a.n; ++i) {
+            a.prefill_len[i] = static_cast<uint32_t>(c->prefill_len[s0 + i]);
+            a.ring_len[i] = c->ring_len[s0 + i];
+        }
+        const size_t off = s0 * kNumHeads * kHeadDim;
+        FOCR_HIP_TRY(launch_rswa_attention(ctx->stream, c, s0, a, q + off, out + off, partials, ctx->cu_count, ctx),
+                     "attention launch");
+    }
+    return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_rswa_write_decode_step(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* k_steps,
+                                        const float* v_steps, uint32_t* slots) {
+    ENGINE_CTX(ctx);
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    return rswa_write_all(ctx, c, k_steps, v_steps, slots);
+}
+
+int32_t focr_hip_rswa_decode_attention(focr_hip_ctx* ctx, const focr_hip_rswa* c, const float* q, float* out) {
+    ENGINE_CTX(ctx);
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    return rswa_attend_all(ctx, c, q, out);
+}
+
+int32_t focr_hip_rswa_step(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* q, const float* k_steps,
+                           const float* v_steps, float* out) {
+    ENGINE_CTX(ctx);
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    int32_t st = rswa_write_all(ctx, c, k_steps, v_steps, nullptr);
+    if (st) return st;
+    return rswa_attend_all(ctx, c, q, out);
+}
+
+int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,
+                                uint32_t* ring_pos) {
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    if (stream >= c->n_streams) return fail(FOCR_HIP_E_SHAPE, "rswa: stream out of range");
+    if (c->prefill_len[stream] < 0) return fail(FOCR_HIP_E_STATE, "rswa: prefill never recorded");
+    if (prefill_len) *prefill_len = static_cast<uint32_t>(c->prefill_len[stream]);
+    if (ring_len) *ring_len = c->ring_len[stream];
+    if (ring_pos) *ring_pos = c->ring_pos[stream];
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_rswa_set_state(focr_hip_rswa* c, size_t stream, uint32_t ring_len, uint32_t ring_pos) {
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    if (stream >= c->n_streams) return fail(FOCR_HIP_E_SHAPE, "rswa: stream out of range");
+    if (c->prefill_len[stream] < 0) return fail(FOCR_HIP_E_STATE, "rswa: prefill never recorded");
+    // A reachable cursor pair: warm-up has ring_pos == ring_len % W, steady
+    // state has ring_len == W and any ring_pos < W (rswa.rs:467-494).
+    if (ring_len > static_cast<uint32_t>(kRingWindow) || ring_pos >= static_cast<uint32_t>(kRingWindow) ||
+        (ring_len < static_cast<uint32_t>(kRingWindow) && ring_pos != ring_len % kRingWindow))
+        return fail(FOCR_HIP_E_STATE, fmt("rswa: unreachable ring state (ring_len=%u, ring_pos=%u)", ring_len, ring_pos));
+    c->ring_len[stream] = ring_len;
+    c->ring_pos[stream] = ring_pos;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_rswa_regions(const focr_hip_rswa* c, size_t stream, float** ref_k, float** ref_v, float** ring_k,
+                              float** ring_v) {
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    if (stream >= c->n_streams) return fail(FOCR_HIP_E_SHAPE, "rswa: stream out of range");
+    if (ref_k) *ref_k = c->ref_k(stream);
+    if (ref_v) *ref_v = c->ref_v(stream);
+    if (ring_k) *ring_k = c->ring_k(stream);
+    if (ring_v) *ring_v = c->ring_v(stream);
+    return FOCR_HIP_OK;
+}
+
+// ---- profiling -------------------------------------------------------------------
+
+int32_t focr_hip_prof_enable(focr_hip_ctx* ctx, int32_t on) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->prof = on != 0;
+    return FOCR_HIP_OK;
+}
+
+static void drain_prof(focr_hip_ctx* ctx) {
+    hipStreamSynchronize(ctx->stream);
+    for (auto& p : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+            auto& t = ctx->prof_totals[p.name];
+            t.first += 1;
+            t.second += ms;
+        }
+        ctx->event_pool.push_back(p.start);
+        ctx->event_pool.push_back(p.stop);
+    }
+    ctx->pending.clear();
+}
+
+int32_t focr_hip_prof_reset(focr_hip_ctx* ctx) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipSetDevice(ctx->device);
+    drain_prof(ctx);
+    ctx->prof_totals.clear();
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipSetDevice(ctx->device);
+    drain_prof(ctx);
+    std::string j = "{";
+    bool first = true;
+    for (auto& kv : ctx->prof_totals) {
+        char buf[256];
+        snprintf(buf, sizeof(buf), "%s\"%s\":{\"count\":%ld,\"ms\":%.6f}", first ? "" : ",", kv.first.c_str(),
+                 kv.second.first, kv.second.second);
+        j += buf;
+        first = false;
+    }
+    j += "}";
+    if (json && cap) snprintf(json, cap, "%s", j.c_str());
+    return FOCR_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,207 @@
+// focr_internal.hpp — internals shared by the C ABI layer and the gfx950
+// kernels: the context, status/error plumbing, scratch buffers, profiling,
+// and the host-side launch functions each kernel file exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/focr_hip.h"
+
+namespace focr {
+
+// ---- status / error ------------------------------------------------------
+// The calling thread's last error message (focr_hip_last_error).
+void set_error(const std::string& msg);
+void clear_error();
+int32_t fail(int32_t code, const std::string& msg);
+// Map a HIP error to FOCR_HIP_E_HIP with "<what>: <hipGetErrorString>".
+int32_t hip_fail(hipError_t e, const char* what);
+
+#define FOCR_HIP_TRY(expr, what)                        \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return focr::hip_fail(e_, what); \
+    } while (0)
+
+// ---- scratch buffer slots (grow-only, per context) -----------------------
+enum ScratchSlot : int {
+    kScrA = 0,  // drop-in tier operand A
+    kScrB,      // drop-in tier operand B
+    kScrOut,    // drop-in tier output
+    kScrAux,    // drop-in tier scales / extra
+    kScrXq,     // quantized activation rows
+    kScrXs,     // activation scales
+    kScrArg,    // argmax partial keys
+    kScrLogits, // router logits / probs
+    kScrRoute,  // routing indices / gates / permutation tables
+    kScrAct,    // MoE SwiGLU activations [pairs][inter]
+    kScrY,      // MoE weighted expert outputs [pairs][hidden]
+    kScrShared, // shared-expert output [t][hidden]
+    kScrRswa,   // attention split-K partials
+    kScrI4,     // int4 prefill intermediates
+    kScrI4b,
+    kScrFlag,   // device status flags
+    kScrCount
+};
+
+struct ProfPending {
+    std::string name;
+    hipEvent_t start, stop;
+};
+
+}  // namespace focr
+
+struct focr_hip_ctx {
+    int device = 0;
+    int cu_count = 0;
+    std::string arch;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    struct Buf {
+        void* p = nullptr;
+        size_t cap = 0;
+    } scratch[focr::kScrCount];
+    // profiling
+    bool prof = false;
+    std::vector<focr::ProfPending> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, std::pair<long, double>> prof_totals;
+
+    // Grow-only scratch. Returns nullptr (and sets the error) on failure.
+    void* scratch_get(int slot, size_t bytes);
+    // Make current the device this context lives on.
+    hipError_t bind() const { return hipSetDevice(device); }
+    hipEvent_t take_event();
+};
+
+struct focr_hip_qint8 {
+    focr_hip_ctx* ctx = nullptr;
+    int8_t* w = nullptr;
+    float* scales = nullptr;
+    size_t n = 0, k = 0;
+    bool owned = false;
+};
+
+struct focr_hip_moe_layer {
+    focr_hip_ctx* ctx = nullptr;
+    size_t hidden = 0, inter = 0, n_experts = 0, top_k = 0;
+    float* router = nullptr;
+    int8_t *wg = nullptr, *wu = nullptr, *wd = nullptr;
+    float *sg = nullptr, *su = nullptr, *sd = nullptr;
+    bool owned = false;
+    // shared expert (optional)
+    size_t shared_inter = 0;
+    int8_t *swg = nullptr, *swu = nullptr, *swd = nullptr;
+    float *ssg = nullptr, *ssu = nullptr, *ssd = nullptr;
+    bool shared_owned = false;
+};
+
+struct focr_hip_moe_layer_i4 {
+    focr_hip_ctx* ctx = nullptr;
+    size_t hidden = 0, inter = 0, n_experts = 0, group = 0;
+    uint8_t *wg = nullptr, *wu = nullptr, *wd = nullptr;
+    float *sg = nullptr, *su = nullptr, *sd = nullptr;
+    bool owned = false;
+};
+
+struct focr_hip_rswa {
+    focr_hip_ctx* ctx = nullptr;
+    size_t n_streams = 0, ref_capacity = 0;
+    float* base = nullptr;  // one allocation for all regions
+    // host cursors (rswa.rs:132-146)
+    std::vector<int64_t> prefill_len;  // -1 = never recorded
+    std::vector<uint32_t> ring_len, ring_pos;
+    size_t stream_floats() const;
+    float* ref_k(size_t s) const;
+    float* ref_v(size_t s) const;
+    float* ring_k(size_t s) const;
+    float* ring_v(size_t s) const;
+};
+
+namespace focr {
+
+// RAII profiling bracket around one kernel launch on ctx->stream.
+struct ProfScope {
+    focr_hip_ctx* ctx;
+    const char* name;
+    hipEvent_t start = nullptr;
+    ProfScope(focr_hip_ctx* c, const char* n);
+    ~ProfScope();
+};
+
+constexpr int kNumHeads = 10;
+constexpr int kHeadDim = 128;
+constexpr int kRingWindow = 128;
+
+// ---- launch functions (defined in the .hip kernel files) -----------------
+// k_igemm.hip: drop-in tier i32 GEMM, out[M,N] += A[M,K] . B[N,K]^T.
+hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const int8_t* b,
+                           int32_t* out, int m, int k, int n);
+
+// k_gemv.hip
+hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
+                                float* a_scales, bool ties_even);
+// y[m,n] = ((f32)acc * a_scales[m]) * ws[n]; acc (nullable) gets raw i32;
+// arg_keys (nullable) gets per-block argmax keys [m][nparts].
+hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
+                          const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
+                          uint64_t* arg_keys, int* nparts_out, int cu_count);
+int gemv_i8_nparts(int n, int cu_count);
+hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int nparts,
+                                uint32_t* argmax);
+hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
+                              int nparts, uint32_t* argmax);
+
+// k_moe.hip — decode MoE pipeline. RouteTables lives in device scratch.
+struct MoeDims {
+    int t, hidden, inter, n_experts, top_k;
+};
+size_t moe_route_table_bytes(const MoeDims& d);
+hipError_t launch_moe_router(hipStream_t s, const MoeDims& d, const float* hidden,
+                             const float* router, float* logits, int8_t* xq, float* xs);
+hipError_t launch_moe_topk(hipStream_t s, const MoeDims& d, const float* logits, int norm_topk,
+                           float routed_scale, uint32_t* idx, float* gates, float* probs,
+                           void* tables, int* flag);
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* tables,
+                              const int8_t* xq, const float* xs, const int8_t* wg,
+                              const float* sg, const int8_t* wu, const float* su, float* act,
+                              int inter, int max_active, bool shared);
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* tables, const float* act,
+                           const int8_t* wd, const float* sd, const float* gates_unused,
+                           float* ybuf, int inter, int max_active, bool shared);
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const void* tables,
+                              const float* ybuf, const float* shared_y, float* out);
+
+// k_int4.hip
+hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,
+                              const float* scales, int group, int m, int k, int n, float* out,
+                              int32_t* partials);
+hipError_t launch_unpack_i4(hipStream_t s, const uint8_t* b, size_t nbytes, int8_t* out);
+hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x,
+                                 int t, int top_k, const uint32_t* idx, const float* gates,
+                                 float* out, void* scratch_a, void* scratch_b, size_t* need_a,
+                                 size_t* need_b, focr_hip_ctx* ctx);
+
+// k_rswa.hip
+struct RswaStepArgs {
+    static constexpr int kMax = 64;
+    uint32_t n;
+    uint32_t prefill_len[kMax];
+    uint32_t ring_len[kMax];
+    uint32_t slot[kMax];
+};
+hipError_t launch_rswa_write(hipStream_t s, const focr_hip_rswa* c, size_t s0,
+                             const RswaStepArgs& a, const float* k_steps, const float* v_steps);
+size_t rswa_partials_bytes(size_t n_streams, size_t max_keys);
+hipError_t launch_rswa_attention(hipStream_t s, const focr_hip_rswa* c, size_t s0,
+                                 const RswaStepArgs& a, const float* q, float* out,
+                                 float* partials, int cu_count, focr_hip_ctx* ctx);
+
+}  // namespace focr

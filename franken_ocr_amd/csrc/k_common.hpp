@@ -1,0 +1,98 @@
+// k_common.hpp — gfx950 device helpers shared by the kernel files.
+//
+// Wavefronts are 64 lanes. The int8 GEMV family assigns 16 lanes to one
+// weight row: each lane streams 16-byte chunks of the row (global_load
+// dwordx4), so one load instruction of a wave covers four 256-byte row
+// segments, and the 16 partial i32 sums are reduced with four xor shuffles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace focr {
+
+__device__ __forceinline__ int dot4_i8(int a, int b, int c) {
+    // v_dot4_i32_i8 without clamp: four signed byte products added to c,
+    // wrapping in 32 bits exactly like the reference's release-mode i32 adds.
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__device__ __forceinline__ int dot16_i8(const int4& a, const int4& b, int c) {
+    c = dot4_i8(a.x, b.x, c);
+    c = dot4_i8(a.y, b.y, c);
+    c = dot4_i8(a.z, b.z, c);
+    c = dot4_i8(a.w, b.w, c);
+    return c;
+}
+
+// Sum across the 16 lanes of a row group (all 16 lanes end with the total).
+__device__ __forceinline__ int reduce16_add(int v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_max_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Argmax key: larger key = larger value, ties -> lower index. NaN -> 0
+// ("no candidate"); -0.0 and +0.0 compare equal, as `v <= best` does in
+// sampler.rs:180. Every non-NaN value maps to a key > 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    if (v != v) return 0ull;
+    if (v == 0.0f) v = 0.0f;
+    uint32_t u = __float_as_uint(v);
+    uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
+    return key ? 0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull) : 0u;
+}
+
+__device__ __forceinline__ float key_value(uint64_t key) {
+    uint32_t ord = static_cast<uint32_t>(key >> 32);
+    uint32_t u = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+    return __uint_as_float(u);
+}
+
+// decoder.rs:1588-1597 (half away from zero) / :1647-1656 (ties even):
+// clamp into [-127, 127], NaN -> 0 (Rust's saturating `as i8`).
+__device__ __forceinline__ int8_t quant_i8(float v, float inv, bool ties_even) {
+    float r = ties_even ? rintf(v * inv) : roundf(v * inv);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
+// decoder.rs:1079-1083 silu(x) = x / (1 + e^-x), accurate expf (no fast math).
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+}  // namespace focr

@@ -1,0 +1,197 @@
+// k_rswa.hip — R-SWA ring write and split-K decode attention
+// (rswa.rs:451-513 write_decode_step, :894-939 decode_attention_scalar,
+// :1320-1367 batched_decode_attention).
+//
+// Layout in HBM, per stream, head-major f32 (the reference's RingCache
+// regions, rswa.rs:112-119): ref K [10][cap][128], ref V, ring K
+// [10][128][128], ring V. The valid keys of a stream are
+// ref[0..prefill_len) ++ ring[0..ring_len) in physical slot order; no mask.
+//
+// Attention is flash-decoding: grid (key chunk, head, stream); a block
+// scores 64 keys (two 128-dim keys per wave step, 32 lanes x float4 each),
+// takes the chunk's max / exp / sum, accumulates p . V with float4 loads and
+// writes (m, l, acc[128]); a merge kernel combines the chunks with the
+// log-sum-exp rule. HBM-bound: every K and V byte is read once.
+#include "focr_internal.hpp"
+#include "k_common.hpp"
+
+namespace focr {
+namespace {
+
+constexpr int H = kNumHeads;
+constexpr int D = kHeadDim;
+constexpr int W = kRingWindow;
+constexpr int KC = 64;  // keys per chunk
+constexpr int kPart = D + 2;
+
+struct Geom {
+    float* base;
+    size_t stream_floats;
+    size_t cap;
+    __device__ __forceinline__ float* ref_k(size_t s) const { return base + s * stream_floats; }
+    __device__ __forceinline__ float* ref_v(size_t s) const { return ref_k(s) + static_cast<size_t>(H) * cap * D; }
+    __device__ __forceinline__ float* ring_k(size_t s) const { return ref_v(s) + static_cast<size_t>(H) * cap * D; }
+    __device__ __forceinline__ float* ring_v(size_t s) const { return ring_k(s) + static_cast<size_t>(H) * W * D; }
+};
+
+Geom geom_of(const focr_hip_rswa* c) { return Geom{c->base, c->stream_floats(), c->ref_capacity}; }
+
+__global__ __launch_bounds__(D) void rswa_write_kernel(Geom g, size_t s0, RswaStepArgs a,
+                                                       const float* __restrict__ k_steps,
+                                                       const float* __restrict__ v_steps) {
+    const int si = blockIdx.x;
+    const int kv = blockIdx.y;
+    const int h = blockIdx.z;
+    const size_t s = s0 + si;
+    const float* src = (kv ? v_steps : k_steps) + (static_cast<size_t>(si) * H + h) * D;
+    float* dst = (kv ? g.ring_v(s) : g.ring_k(s)) + (static_cast<size_t>(h) * W + a.slot[si]) * D;
+    dst[threadIdx.x] = src[threadIdx.x];
+}
+
+__global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, RswaStepArgs a,
+                                                         const float* __restrict__ q, float scale,
+                                                         float* __restrict__ partials,
+                                                         int max_chunks) {
+    __shared__ float sc[KC];
+    __shared__ float4 accs[8][D / 4];
+    __shared__ float s_ml[2];
+    const int chunk = blockIdx.x;
+    const int h = blockIdx.y;
+    const int si = blockIdx.z;
+    const size_t s = s0 + si;
+    const int P = static_cast<int>(a.prefill_len[si]);
+    const int N = P + static_cast<int>(a.ring_len[si]);
+    if (chunk * KC >= N) return;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5;
+    const int dl = lane & 31;
+    const float* qh = q + (static_cast<size_t>(si) * H + h) * D;
+    const float4 qv = reinterpret_cast<const float4*>(qh)[dl];
+    const float* rk = g.ref_k(s) + static_cast<size_t>(h) * g.cap * D;
+    const float* rv = g.ref_v(s) + static_cast<size_t>(h) * g.cap * D;
+    const float* gk = g.ring_k(s) + static_cast<size_t>(h) * W * D;
+    const float* gv = g.ring_v(s) + static_cast<size_t>(h) * W * D;
+
+    // scores: wave w covers keys [w*16, w*16+16), two keys per step
+#pragma unroll
+    for (int jj = 0; jj < 16; jj += 2) {
+        const int j = wave * 16 + jj + half;
+        const int key = chunk * KC + j;
+        float d = 0.0f;
+        if (key < N) {
+            const float* kr = key < P ? rk + static_cast<size_t>(key) * D : gk + static_cast<size_t>(key - P) * D;
+            const float4 kv = reinterpret_cast<const float4*>(kr)[dl];
+            d = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+        }
+        d += __shfl_xor(d, 16, 32);
+        d += __shfl_xor(d, 8, 32);
+        d += __shfl_xor(d, 4, 32);
+        d += __shfl_xor(d, 2, 32);
+        d += __shfl_xor(d, 1, 32);
+        if (dl == 0) sc[j] = key < N ? d * scale : -INFINITY;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float v = sc[lane];
+        const float m = wave_max_f(v);
+        const float p = v == -INFINITY ? 0.0f : expf(v - m);
+        float l = p;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        sc[lane] = p;
+        if (lane == 0) {
+            s_ml[0] = m;
+            s_ml[1] = l;
+        }
+    }
+    __syncthreads();
+    // p . V: 8 key groups x 32 lanes (float4 of the head dim each)
+    const int grp = threadIdx.x >> 5;
+    const int dq = threadIdx.x & 31;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = grp; j < KC; j += 8) {
+        const int key = chunk * KC + j;
+        if (key >= N) break;
+        const float* vr = key < P ? rv + static_cast<size_t>(key) * D : gv + static_cast<size_t>(key - P) * D;
+        const float4 vv = reinterpret_cast<const float4*>(vr)[dq];
+        const float p = sc[j];
+        acc.x += p * vv.x;
+        acc.y += p * vv.y;
+        acc.z += p * vv.z;
+        acc.w += p * vv.w;
+    }
+    accs[grp][dq] = acc;
+    __syncthreads();
+    float* part = partials + ((static_cast<size_t>(si) * H + h) * max_chunks + chunk) * kPart;
+    if (threadIdx.x < D) {
+        const int d4 = threadIdx.x >> 2, c = threadIdx.x & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int gI = 0; gI < 8; ++gI) {
+            const float4 v = accs[gI][d4];
+            sum += c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+        }
+        part[2 + threadIdx.x] = sum;
+    }
+    if (threadIdx.x == 0) {
+        part[0] = s_ml[0];
+        part[1] = s_ml[1];
+    }
+}
+
+__global__ __launch_bounds__(D) void rswa_merge_kernel(RswaStepArgs a, const float* __restrict__ partials,
+                                                       int max_chunks, float* __restrict__ out) {
+    const int h = blockIdx.x;
+    const int si = blockIdx.y;
+    const int N = static_cast<int>(a.prefill_len[si] + a.ring_len[si]);
+    const int nch = (N + KC - 1) / KC;
+    const float* base = partials + (static_cast<size_t>(si) * H + h) * max_chunks * kPart;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, base[c * kPart]);
+    float L = 0.0f, acc = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        const float f = expf(base[c * kPart] - M);
+        L += base[c * kPart + 1] * f;
+        acc += base[c * kPart + 2 + threadIdx.x] * f;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    out[(static_cast<size_t>(si) * H + h) * D + threadIdx.x] = acc * inv;
+}
+
+}  // namespace
+
+size_t rswa_partials_bytes(size_t n_streams, size_t max_keys) {
+    const size_t max_chunks = (max_keys + KC - 1) / KC;
+    return n_streams * H * max_chunks * kPart * sizeof(float);
+}
+
+hipError_t launch_rswa_write(hipStream_t s, const focr_hip_rswa* c, size_t s0,
+                             const RswaStepArgs& a, const float* k_steps, const float* v_steps) {
+    if (a.n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rswa_write_kernel, dim3(a.n, 2, H), dim3(D), 0, s, geom_of(c), s0, a,
+                       k_steps, v_steps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rswa_attention(hipStream_t s, const focr_hip_rswa* c, size_t s0,
+                                 const RswaStepArgs& a, const float* q, float* out,
+                                 float* partials, int, focr_hip_ctx* ctx) {
+    if (a.n == 0) return hipSuccess;
+    const int max_chunks = static_cast<int>((c->ref_capacity + W + KC - 1) / KC);
+    const float scale = 1.0f / sqrtf(static_cast<float>(D));  // rswa.rs:52-55
+    {
+        ProfScope ps(ctx, "rswa_chunk");
+        hipLaunchKernelGGL(rswa_chunk_kernel, dim3(max_chunks, H, a.n), dim3(256), 0, s, geom_of(c),
+                           s0, a, q, scale, partials, max_chunks);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    {
+        ProfScope ps(ctx, "rswa_merge");
+        hipLaunchKernelGGL(rswa_merge_kernel, dim3(H, a.n), dim3(D), 0, s, a, partials, max_chunks, out);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace focr

@@ -1,0 +1,220 @@
+"""Device-resident engine ops: the decoder functions one level above the tier.
+
+Mirrors, on uploaded weights and device arrays:
+
+* ``QInt8`` (tensor.rs:149-179) uploaded once (DecoderWeightCacheI8::build,
+  decoder.rs:2018-2116),
+* ``gemv_i8`` / ``gemv_i8_batched`` (decoder.rs:1607-1640, :2703-2747),
+* ``lm_head_i8`` + ``argmax_row`` (decoder.rs:2275-2296, :2943-2965;
+  sampler.rs:168-186),
+* ``MoeLayer.route`` / ``MoeLayer.decode`` (moe.rs:181-266,
+  decoder.rs:2199-2268),
+* ``RingCache`` (rswa.rs:121-152, :389-513, :894-939, :1320-1367).
+
+All work is queued on the context's stream; results come back with
+``DeviceArray.numpy()``.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _abi
+from .device import Context, DeviceArray, default_context
+
+NUM_HEADS = 10
+HEAD_DIM = 128
+RING_WINDOW = 128
+
+
+def _p(x) -> C.c_void_p:
+    if x is None:
+        return C.c_void_p()
+    if isinstance(x, DeviceArray):
+        return x.c_ptr
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data_as(C.c_void_p)
+    if isinstance(x, C.c_void_p):
+        return x
+    return C.c_void_p(int(x))
+
+
+class QInt8:
+    """Per-output-channel int8 weight ``w [n, k]`` + ``scales [n]`` in HBM."""
+
+    def __init__(self, w: np.ndarray | DeviceArray, scales: np.ndarray | DeviceArray, n: int, k: int,
+                 ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.n, self.k = int(n), int(k)
+        self._h = C.c_void_p()
+        if isinstance(w, DeviceArray):
+            self._keep = (w, scales)
+            _abi.call("focr_hip_qint8_from_device", self.ctx.handle, w.c_ptr, scales.c_ptr, self.n, self.k,
+                      C.byref(self._h))
+        else:
+            w = np.ascontiguousarray(w, dtype=np.int8).reshape(-1)
+            s = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+            if w.size != self.n * self.k or s.size != self.n:
+                raise _abi.ContractViolation(_abi.E_SHAPE, f"QInt8: w len {w.size} != n*k {self.n * self.k}"
+                                             if w.size != self.n * self.k else
+                                             f"QInt8: scales len {s.size} != n {self.n}")
+            _abi.call("focr_hip_qint8_upload", self.ctx.handle, _p(w), _p(s), self.n, self.k, C.byref(self._h))
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_qint8_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def quantize_rows_i8(x: DeviceArray, xq: DeviceArray, a_scales: DeviceArray, ties_even: bool = False) -> None:
+    m, k = x.shape
+    _abi.call("focr_hip_quantize_rows_i8", x.ctx.handle, x.c_ptr, m, k, xq.c_ptr, a_scales.c_ptr, 1 if ties_even else 0)
+
+
+def gemv_i8(w: QInt8, x: DeviceArray, y: DeviceArray) -> None:
+    """y[m, n] = dequant(quantize_row_i8(x[m]) . W^T) for m <= 32 rows."""
+    m = x.shape[0] if len(x.shape) > 1 else 1
+    _abi.call("focr_hip_gemv_i8", w.ctx.handle, w.handle, x.c_ptr, m, y.c_ptr)
+
+
+def gemv_i8_prequant(w: QInt8, xq: DeviceArray, a_scales: DeviceArray, y: DeviceArray,
+                     acc: DeviceArray | None = None) -> None:
+    m = xq.shape[0] if len(xq.shape) > 1 else 1
+    _abi.call("focr_hip_gemv_i8_prequant", w.ctx.handle, w.handle, xq.c_ptr, a_scales.c_ptr, m, y.c_ptr, _p(acc))
+
+
+def lm_head_i8(w: QInt8, x: DeviceArray, argmax: DeviceArray, logits: DeviceArray | None = None) -> None:
+    """LM head on already-normed rows: logits (optional) and argmax ids."""
+    m = x.shape[0] if len(x.shape) > 1 else 1
+    _abi.call("focr_hip_lm_head_i8", w.ctx.handle, w.handle, x.c_ptr, m, _p(logits), argmax.c_ptr)
+
+
+def argmax_rows(logits: DeviceArray, argmax: DeviceArray) -> None:
+    m, n = logits.shape
+    _abi.call("focr_hip_argmax_rows", logits.ctx.handle, logits.c_ptr, m, n, argmax.c_ptr)
+
+
+class MoeLayer:
+    """A MoE layer's router (f32) and int8 experts, uploaded once.
+
+    Host arrays: router [E, hidden] f32; wg/wu [E, inter, hidden] i8 with
+    sg/su [E, inter]; wd [E, hidden, inter] i8 with sd [E, hidden]. Passing
+    DeviceArrays borrows them instead of copying.
+    """
+
+    def __init__(self, hidden: int, inter: int, n_experts: int, top_k: int, router, wg, sg, wu, su, wd, sd,
+                 ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.hidden, self.inter, self.n_experts, self.top_k = int(hidden), int(inter), int(n_experts), int(top_k)
+        self._h = C.c_void_p()
+        arrs = [router, wg, sg, wu, su, wd, sd]
+        from_dev = isinstance(router, DeviceArray)
+        if from_dev:
+            self._keep = arrs
+            ptrs = [a.c_ptr for a in arrs]
+        else:
+            dts = [np.float32, np.int8, np.float32, np.int8, np.float32, np.int8, np.float32]
+            host = [np.ascontiguousarray(a, dtype=dt) for a, dt in zip(arrs, dts)]
+            self._host = host
+            ptrs = [_p(a) for a in host]
+        _abi.call("focr_hip_moe_layer_create", self.ctx.handle, self.hidden, self.inter, self.n_experts, self.top_k,
+                  *ptrs, 1 if from_dev else 0, C.byref(self._h))
+        if not from_dev:
+            del self._host
+
+    def set_shared(self, shared_inter: int, wg, sg, wu, su, wd, sd) -> None:
+        arrs = [wg, sg, wu, su, wd, sd]
+        from_dev = isinstance(wg, DeviceArray)
+        if from_dev:
+            self._keep_shared = arrs
+            ptrs = [a.c_ptr for a in arrs]
+        else:
+            dts = [np.int8, np.float32, np.int8, np.float32, np.int8, np.float32]
+            host = [np.ascontiguousarray(a, dtype=dt) for a, dt in zip(arrs, dts)]
+            ptrs = [_p(a) for a in host]
+        _abi.call("focr_hip_moe_layer_set_shared", self._h, int(shared_inter), *ptrs, 1 if from_dev else 0)
+
+    def route(self, hidden: DeviceArray, idx: DeviceArray, gates: DeviceArray, probs: DeviceArray | None = None,
+              norm_topk: bool = False, routed_scale: float = 1.0) -> None:
+        t = hidden.shape[0]
+        _abi.call("focr_hip_moe_route", self.ctx.handle, self._h, hidden.c_ptr, t, 1 if norm_topk else 0,
+                  float(routed_scale), idx.c_ptr, gates.c_ptr, _p(probs))
+
+    def decode(self, hidden: DeviceArray, out: DeviceArray, idx: DeviceArray | None = None,
+               gates: DeviceArray | None = None, norm_topk: bool = False, routed_scale: float = 1.0,
+               with_shared: bool = False, check_route: bool = True) -> None:
+        t = hidden.shape[0]
+        _abi.call("focr_hip_moe_decode", self.ctx.handle, self._h, hidden.c_ptr, t, 1 if norm_topk else 0,
+                  float(routed_scale), 1 if with_shared else 0, out.c_ptr, _p(idx), _p(gates),
+                  1 if check_route else 0)
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_moe_layer_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class RingCache:
+    """``n_streams`` R-SWA ring caches of one layer on the device."""
+
+    def __init__(self, n_streams: int, ref_capacity: int, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.n_streams, self.ref_capacity = int(n_streams), int(ref_capacity)
+        self._h = C.c_void_p()
+        _abi.call("focr_hip_rswa_create", self.ctx.handle, self.n_streams, self.ref_capacity, C.byref(self._h))
+
+    def record_prefill(self, stream: int, k: DeviceArray, v: DeviceArray, seq: int) -> None:
+        _abi.call("focr_hip_rswa_record_prefill", self.ctx.handle, self._h, stream, _p(k), _p(v), seq)
+
+    def write_decode_step(self, k_steps: DeviceArray, v_steps: DeviceArray) -> list:
+        slots = np.zeros(self.n_streams, dtype=np.uint32)
+        _abi.call("focr_hip_rswa_write_decode_step", self.ctx.handle, self._h, k_steps.c_ptr, v_steps.c_ptr, _p(slots))
+        return [int(s) for s in slots]
+
+    def decode_attention(self, q: DeviceArray, out: DeviceArray) -> None:
+        _abi.call("focr_hip_rswa_decode_attention", self.ctx.handle, self._h, q.c_ptr, out.c_ptr)
+
+    def step(self, q: DeviceArray, k_steps: DeviceArray, v_steps: DeviceArray, out: DeviceArray) -> None:
+        _abi.call("focr_hip_rswa_step", self.ctx.handle, self._h, q.c_ptr, k_steps.c_ptr, v_steps.c_ptr, out.c_ptr)
+
+    def state(self, stream: int) -> tuple:
+        p, rl, rp = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        _abi.call("focr_hip_rswa_get_state", self._h, stream, C.byref(p), C.byref(rl), C.byref(rp))
+        return int(p.value), int(rl.value), int(rp.value)
+
+    def set_state(self, stream: int, ring_len: int, ring_pos: int) -> None:
+        _abi.call("focr_hip_rswa_set_state", self._h, stream, int(ring_len), int(ring_pos))
+
+    def regions(self, stream: int) -> dict:
+        ptrs = [C.c_void_p() for _ in range(4)]
+        _abi.call("focr_hip_rswa_regions", self._h, stream, *[C.byref(p) for p in ptrs])
+        return dict(zip(("ref_k", "ref_v", "ring_k", "ring_v"), (int(p.value) for p in ptrs)))
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_rswa_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass

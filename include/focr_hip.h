@@ -1,0 +1,267 @@
+/*
+ * focr_hip.h — C ABI of the MI355X (gfx950) tier for franken_ocr's quantized
+ * decoder hot path.
+ *
+ * Two layers, both plain C (pointers + sizes, no framework types):
+ *
+ *  1. Drop-in kernel tier. Same contract as the reference's dispatched
+ *     `simd` entry points (host slices in, host slices out, synchronous,
+ *     `+=` for int8 / overwrite for int4). A Rust `IsaTier::Gfx950` arm calls
+ *     these exactly where it calls `x86::igemm_s8s8` today.
+ *
+ *  2. Device-resident engine ops. Weights are uploaded once into HBM
+ *     (the analogue of `DecoderWeightCacheI8::build`, decoder.rs:2018-2116)
+ *     and every per-token op works on device pointers, stream-ordered on the
+ *     context's HIP stream. These replace the engine functions one level up
+ *     (gemv_i8, lm_head_cached_i8 + argmax, decode_mlp_i8, RingCache +
+ *     decode_attention), because per-call host slices would copy the 165 MB
+ *     LM-head panel over PCIe on every token.
+ *
+ * Every function returns an int32_t status (FOCR_HIP_OK == 0). On failure the
+ * calling thread's focr_hip_last_error() holds the message; for contract
+ * violations the text is the one the reference panics with
+ * (e.g. "igemm_s8s8: a.len 2 != m*k 1"), so a Rust binding can re-raise it
+ * as the same panic. Entry points taking a context are thread-safe (one
+ * mutex per context serialises use of its stream).
+ *
+ * Citations are to Dicklesworthstone/franken_ocr v0.3.0.
+ */
+#ifndef FOCR_HIP_H
+#define FOCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define FOCR_HIP_OK 0
+#define FOCR_HIP_E_SHAPE (-1)      /* shape/length contract violation (a Rust panic) */
+#define FOCR_HIP_E_HIP (-2)        /* HIP runtime error */
+#define FOCR_HIP_E_OOM (-3)        /* device allocation failed */
+#define FOCR_HIP_E_NO_DEVICE (-4)  /* no usable gfx950 device */
+#define FOCR_HIP_E_BAD_HANDLE (-5) /* null / foreign handle */
+#define FOCR_HIP_E_ARG (-6)        /* invalid argument (null pointer, bad flag) */
+#define FOCR_HIP_E_ROUTE (-7)      /* moe.rs:261-265 "no finite router score" */
+#define FOCR_HIP_E_STATE (-8)      /* rswa.rs:452-455/869-887 state errors */
+
+typedef struct focr_hip_ctx focr_hip_ctx;
+typedef struct focr_hip_qint8 focr_hip_qint8;
+typedef struct focr_hip_moe_layer focr_hip_moe_layer;
+typedef struct focr_hip_rswa focr_hip_rswa;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* focr_hip_last_error(void);
+/* Library version string. */
+const char* focr_hip_version(void);
+
+/* ---- context ----------------------------------------------------------- */
+/* Number of visible HIP devices (0 when none). */
+int32_t focr_hip_device_count(int32_t* count);
+/* Create a context on `device`: one default-priority HIP stream plus the
+ * scratch buffers the engine ops reuse. Fails with E_NO_DEVICE when the
+ * device is absent or is not gfx950 (the library ships gfx950 code only). */
+int32_t focr_hip_ctx_create(int32_t device, focr_hip_ctx** out);
+int32_t focr_hip_ctx_destroy(focr_hip_ctx* ctx);
+/* Block until all work queued on the context's stream has finished. */
+int32_t focr_hip_ctx_synchronize(focr_hip_ctx* ctx);
+/* hipDeviceSynchronize on the context's device (whole-device barrier). */
+int32_t focr_hip_device_synchronize(focr_hip_ctx* ctx);
+/* The context's hipStream_t, for callers that order their own work on it. */
+int32_t focr_hip_ctx_stream(focr_hip_ctx* ctx, void** stream);
+/* Device name / gcnArchName / CU count of the context's device. */
+int32_t focr_hip_ctx_device_info(focr_hip_ctx* ctx, char* arch, size_t arch_cap,
+                                 int32_t* cu_count);
+
+/* ---- tier reflection (dispatch.rs:48-138 IsaTier::tag/feature_string) --- */
+/* tag "gfx950", feature "gfx950+mfma-i8" — the strings `robot backends`
+ * reports for the GPU tier beside "avx512vnni"/"x86_64+avx512vnni". */
+int32_t focr_hip_tier(char* tag, size_t tag_cap, char* feature, size_t feature_cap);
+
+/* ---- device buffers (plumbing for callers without a device allocator) ---- */
+int32_t focr_hip_dmalloc(focr_hip_ctx* ctx, size_t bytes, void** out);
+int32_t focr_hip_dfree(focr_hip_ctx* ctx, void* ptr);
+/* Synchronous copies (they also wait for the context's stream). */
+int32_t focr_hip_h2d(focr_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+int32_t focr_hip_d2h(focr_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Stream-ordered device-to-device copy. */
+int32_t focr_hip_d2d(focr_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* =========================================================================
+ * Layer 1 — drop-in kernel tier (host pointers, synchronous)
+ * ========================================================================= */
+
+/* simd::igemm_s8s8 (simd/mod.rs:30-46, scalar.rs:78-116, dispatch.rs:246-262):
+ * out[M,N] += A[M,K] (i8, row-major) . B[N,K]^T (i8, output-channel-major),
+ * i32 accumulation. Length checks and messages as scalar.rs:79-102. */
+int32_t focr_hip_igemm_s8s8(focr_hip_ctx* ctx, const int8_t* a, size_t a_len, const int8_t* b,
+                            size_t b_len, size_t m, size_t k, size_t n, int32_t* out,
+                            size_t out_len);
+/* simd::igemm_u8s8 (scalar.rs:129-166, dispatch.rs:276-289): A is u8. */
+int32_t focr_hip_igemm_u8s8(focr_hip_ctx* ctx, const uint8_t* a, size_t a_len, const int8_t* b,
+                            size_t b_len, size_t m, size_t k, size_t n, int32_t* out,
+                            size_t out_len);
+/* simd::int4::igemm_s4s8_packed (int4.rs:437-461; contract :304-343, checks
+ * :350-402): out[M,N] = sum_g scale[n,g] * (i32 dot over group g), summed in
+ * f32 in increasing g; out is overwritten. group in {16, 32}. */
+int32_t focr_hip_igemm_s4s8_packed(focr_hip_ctx* ctx, const int8_t* a, size_t a_len,
+                                   const uint8_t* b_packed, size_t b_len, const float* scales,
+                                   size_t scales_len, size_t group, size_t m, size_t k, size_t n,
+                                   float* out, size_t out_len);
+/* simd::int4::igemm_s4s8 (int4.rs:170-229): the same function under the
+ * unpack-then-int8 entry's name and messages (its result is identical). */
+int32_t focr_hip_igemm_s4s8(focr_hip_ctx* ctx, const int8_t* a, size_t a_len,
+                            const uint8_t* b_packed, size_t b_len, const float* scales,
+                            size_t scales_len, size_t group, size_t m, size_t k, size_t n,
+                            float* out, size_t out_len);
+/* simd::int4::unpack_to_i8 (int4.rs:125-142): [n, k/2] packed -> [n, k] i8. */
+int32_t focr_hip_unpack_to_i8(focr_hip_ctx* ctx, const uint8_t* b_packed, size_t b_len, size_t n,
+                              size_t k, int8_t* out, size_t out_len);
+/* Test entry with no single reference counterpart: the per-group i32
+ * partial sums inside s4s8_packed_kernel_scalar (int4.rs:322-337), written
+ * as partials[m][n][k/group], so int4 "i32 accumulators" can be checked. */
+int32_t focr_hip_debug_s4s8_group_i32(focr_hip_ctx* ctx, const int8_t* a, size_t a_len,
+                                      const uint8_t* b_packed, size_t b_len, size_t group,
+                                      size_t m, size_t k, size_t n, int32_t* partials,
+                                      size_t partials_len);
+
+/* The runtime self-test behind `focr robot selftest` (dispatch.rs:376-429,
+ * cli.rs:1955-2002): the 12-shape x {s8s8, u8s8} battery run through the
+ * gfx950 tier and compared lane by lane with an in-process scalar check.
+ * Writes a JSON report {"selected","available","all_ok","cases":[...]} into
+ * json (NUL-terminated, truncated to cap) and sets *all_ok. */
+int32_t focr_hip_selftest(focr_hip_ctx* ctx, char* json, size_t cap, int32_t* all_ok);
+
+/* Device-pointer forms of the tier (stream-ordered, no host copies). */
+int32_t focr_hip_igemm_s8s8_dev(focr_hip_ctx* ctx, const int8_t* a, const int8_t* b, size_t m,
+                                size_t k, size_t n, int32_t* out);
+int32_t focr_hip_igemm_u8s8_dev(focr_hip_ctx* ctx, const uint8_t* a, const int8_t* b, size_t m,
+                                size_t k, size_t n, int32_t* out);
+int32_t focr_hip_igemm_s4s8_packed_dev(focr_hip_ctx* ctx, const int8_t* a,
+                                       const uint8_t* b_packed, const float* scales, size_t group,
+                                       size_t m, size_t k, size_t n, float* out);
+
+/* =========================================================================
+ * Layer 2 — device-resident engine ops (device pointers, stream-ordered)
+ * ========================================================================= */
+
+/* QInt8 weight handle (tensor.rs:149-179): w [n,k] i8 output-channel-major,
+ * one f32 scale per output channel. _upload copies host arrays into HBM once;
+ * _from_device wraps caller-owned device arrays (not freed by the handle). */
+int32_t focr_hip_qint8_upload(focr_hip_ctx* ctx, const int8_t* w, const float* scales, size_t n,
+                              size_t k, focr_hip_qint8** out);
+int32_t focr_hip_qint8_from_device(focr_hip_ctx* ctx, const int8_t* w, const float* scales,
+                                   size_t n, size_t k, focr_hip_qint8** out);
+int32_t focr_hip_qint8_free(focr_hip_qint8* w);
+
+/* decoder.rs:1588-1597 quantize_row_i8 (ties_even = 0: round half away,
+ * reciprocal multiply) and :1647-1656 quantize_row_i8_te (ties_even = 1),
+ * one scale per row: x [m,k] f32 -> xq [m,k] i8, a_scales [m]. */
+int32_t focr_hip_quantize_rows_i8(focr_hip_ctx* ctx, const float* x, size_t m, size_t k,
+                                  int8_t* xq, float* a_scales, int32_t ties_even);
+
+/* decoder.rs:1607 gemv_i8 (m = 1) and :2703-2747 gemv_i8_batched (m rows):
+ * each row quantized with quantize_row_i8, y[m,n] = ((f32)acc * a_scale[m])
+ * * scale[n]. m <= 32 per call. */
+int32_t focr_hip_gemv_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+                         float* y);
+/* decoder.rs:1621-1640 gemv_i8_prequant: from already-quantized rows. acc
+ * (nullable) receives the raw i32 accumulators [m,n]. */
+int32_t focr_hip_gemv_i8_prequant(focr_hip_ctx* ctx, const focr_hip_qint8* w, const int8_t* xq,
+                                  const float* a_scales, size_t m, float* y, int32_t* acc);
+
+/* decoder.rs:2275-2296 lm_head_cached_i8 / :2943-2965 batched_lm_head_i8
+ * (input = the already final-normed rows) followed by sampler.rs:168-186
+ * argmax_row per row. logits [m,n] (nullable: skip writing them); argmax [m]
+ * u32: first index of the maximum, NaN skipped, all-NaN row -> 0. */
+int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x,
+                            size_t m, float* logits, uint32_t* argmax);
+/* sampler.rs:168-186 argmax_row over m rows of n f32 logits. */
+int32_t focr_hip_argmax_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n,
+                             uint32_t* argmax);
+
+/* ---- MoE layer (decoder.rs:1971-1982 CachedMlpI8::Moe) ------------------
+ * router f32 [E, hidden]; gate/up i8 [E][inter][hidden] with scales
+ * [E][inter]; down i8 [E][hidden][inter] with scales [E][hidden]. With
+ * from_device = 0 the arrays are host memory and are uploaded once; with 1
+ * they are caller-owned device arrays that the layer borrows. */
+int32_t focr_hip_moe_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t inter,
+                                  size_t n_experts, size_t top_k, const float* router,
+                                  const int8_t* wg, const float* sg, const int8_t* wu,
+                                  const float* su, const int8_t* wd, const float* sd,
+                                  int32_t from_device, focr_hip_moe_layer** out);
+/* The fused shared expert (moe.rs:64-66; decoder.rs:2251, :2259-2261). */
+int32_t focr_hip_moe_layer_set_shared(focr_hip_moe_layer* layer, size_t shared_inter,
+                                      const int8_t* wg, const float* sg, const int8_t* wu,
+                                      const float* su, const int8_t* wd, const float* sd,
+                                      int32_t from_device);
+int32_t focr_hip_moe_layer_free(focr_hip_moe_layer* layer);
+
+/* decoder.rs:2199-2268 decode_mlp_i8 over t rows (the batched spine calls it
+ * per stream, decoder.rs:2924-2930): route (moe.rs:181-266; router logits
+ * and softmax in f64, rounded to f32), per (token, slot) the int8 SwiGLU
+ * expert (decoder.rs:1744-1755), y *= gate, combine in slot order, plus the
+ * shared expert when with_shared. hidden/out [t, hidden] f32; idx/gates
+ * [t, top_k] (both nullable). Device pointers. t <= 64. Returns E_ROUTE when
+ * a token has no finite router score (moe.rs:261-265) — detected on the
+ * device and reported by a synchronising check only when check_route = 1. */
+int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
+                            const float* hidden, size_t t, int32_t norm_topk, float routed_scale,
+                            int32_t with_shared, float* out, uint32_t* idx, float* gates,
+                            int32_t check_route);
+/* moe.rs:181-266 route alone: idx/gates [t, top_k] device pointers; probs
+ * (nullable) receives the f32 softmax [t, E]. Synchronises to report
+ * E_ROUTE. */
+int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
+                           const float* hidden, size_t t, int32_t norm_topk, float routed_scale,
+                           uint32_t* idx, float* gates, float* probs);
+
+/* ---- R-SWA ring KV cache (rswa.rs:121-152 RingCache, :645-824 batched) ---
+ * n_streams independent caches of one layer, f32, head-major per stream:
+ * ref K/V [NUM_HEADS=10][ref_capacity][HEAD_DIM=128], ring K/V
+ * [10][RING_WINDOW=128][128]. Cursor state (prefill_len, ring_len, ring_pos)
+ * is kept on the host and follows the reference's rules exactly. */
+int32_t focr_hip_rswa_create(focr_hip_ctx* ctx, size_t n_streams, size_t ref_capacity,
+                             focr_hip_rswa** out);
+int32_t focr_hip_rswa_free(focr_hip_rswa* cache);
+/* rswa.rs:389-433 record_prefill: k/v head-major [10][seq][128] (device
+ * pointers); resets ring_len = ring_pos = 0. */
+int32_t focr_hip_rswa_record_prefill(focr_hip_ctx* ctx, focr_hip_rswa* cache, size_t stream,
+                                     const float* k, const float* v, size_t seq);
+/* rswa.rs:451-513 write_decode_step for every stream: k_steps/v_steps
+ * [n_streams][10*128] device pointers; slots (host, nullable) receives each
+ * stream's physical slot. */
+int32_t focr_hip_rswa_write_decode_step(focr_hip_ctx* ctx, focr_hip_rswa* cache,
+                                        const float* k_steps, const float* v_steps,
+                                        uint32_t* slots);
+/* rswa.rs:1320-1367 batched_decode_attention (per stream, rswa.rs:894-939
+ * semantics; no causal mask; keys ref[0..prefill_len) ++ ring[0..ring_len)):
+ * q/out [n_streams][10*128] device pointers. */
+int32_t focr_hip_rswa_decode_attention(focr_hip_ctx* ctx, const focr_hip_rswa* cache,
+                                       const float* q, float* out);
+/* rswa.rs:1184-1200 convenience step: write this token's K/V, then attend. */
+int32_t focr_hip_rswa_step(focr_hip_ctx* ctx, focr_hip_rswa* cache, const float* q,
+                           const float* k_steps, const float* v_steps, float* out);
+/* Cursor reflection / speculative roll-back (rswa.rs:219-283, :524-579). */
+int32_t focr_hip_rswa_get_state(const focr_hip_rswa* cache, size_t stream, uint32_t* prefill_len,
+                                uint32_t* ring_len, uint32_t* ring_pos);
+int32_t focr_hip_rswa_set_state(focr_hip_rswa* cache, size_t stream, uint32_t ring_len,
+                                uint32_t ring_pos);
+/* Device pointers of one stream's regions (for direct fills/readback). */
+int32_t focr_hip_rswa_regions(const focr_hip_rswa* cache, size_t stream, float** ref_k,
+                              float** ref_v, float** ring_k, float** ring_v);
+
+/* ---- profiling (decoder.rs:986-1024 prof counters, GPU-timed) -----------
+ * When enabled, the engine ops bracket each kernel with HIP events on the
+ * context stream; focr_hip_prof_read synchronises and returns, per kernel
+ * name, the launch count and total milliseconds as a JSON object. */
+int32_t focr_hip_prof_enable(focr_hip_ctx* ctx, int32_t on);
+int32_t focr_hip_prof_reset(focr_hip_ctx* ctx);
+int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FOCR_HIP_H */

@@ -1,0 +1,286 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg — never by the product package.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+
+_SIGS = {
+    "oracle_igemm_s8s8": ([_P, _P, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_igemm_u8s8": ([_P, _P, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_xs32": ([_P], C.c_uint32),
+    "oracle_selftest_n_shapes": ([], _SZ),
+    "oracle_selftest_shape": ([_SZ, _P, _P, _P, _P, _P], C.c_int),
+    "oracle_selftest_fill_s8": ([_SZ, _P, _P], C.c_int),
+    "oracle_selftest_fill_u8": ([_SZ, _P, _P], C.c_int),
+    "oracle_quantize_row_i8": ([_P, _SZ, _P], C.c_float),
+    "oracle_quantize_row_i8_te": ([_P, _SZ, _P], C.c_float),
+    "oracle_gemv_i8_batched": ([_P, _SZ, _P, _P, _SZ, _SZ, _P, _P, _P, _P], None),
+    "oracle_dequant_i8": ([_P, _SZ, _SZ, _P, _P, _P], None),
+    "oracle_argmax_row": ([_P, _SZ, _P], C.c_int),
+    "oracle_lm_head_i8": ([_P, _SZ, _P, _P, _SZ, _SZ, _P, _P], C.c_int),
+    "oracle_route": ([_P, _SZ, _SZ, _P, _SZ, _SZ, C.c_int, C.c_float, _P, _P, _P], C.c_int),
+    "oracle_silu": ([C.c_float], C.c_float),
+    "oracle_expert_i8": ([_P, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P], None),
+    "oracle_moe_decode": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_float,
+                           _P, _P, _P, _P, _P, _P, _SZ, _P, _P, _P], C.c_int),
+    "oracle_sign_extend_nibble": ([C.c_uint8], C.c_int8),
+    "oracle_unpack_byte": ([C.c_uint8, _P, _P], None),
+    "oracle_unpack_to_i8": ([_P, _SZ, _SZ, _P], C.c_int),
+    "oracle_igemm_s4s8_packed": ([_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_s4s8_group_i32": ([_P, _P, _SZ, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_moe_prefill_i4": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+                              C.c_int),
+    "oracle_quantize_int8_f32": ([_P, _SZ, _SZ, _P, _P], C.c_int),
+    "oracle_pack_int4_f32": ([_P, _SZ, _SZ, _SZ, _P, _P], C.c_int),
+    "oracle_ring_write": ([_P, _P, _P, _P, _P, _P, _P], C.c_int),
+    "oracle_decode_attention": ([_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P], C.c_int),
+    "cpu_detect_tier": ([], C.c_int),
+    "cpu_tier_tag": ([C.c_int], C.c_char_p),
+    "cpu_tier_feature": ([C.c_int], C.c_char_p),
+    "cpu_set_threads": ([C.c_int], C.c_int),
+    "cpu_threads": ([], C.c_int),
+    "cpu_igemm_s8s8": ([C.c_int, _P, _P, _SZ, _SZ, _SZ, _P], None),
+    "cpu_gemv_i8": ([C.c_int, _P, _SZ, _P, _P, _SZ, _SZ, _P], None),
+    "cpu_lm_head_i8": ([C.c_int, _P, _SZ, _P, _P, _SZ, _SZ, _P, _P], None),
+    "cpu_moe_decode": ([C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_float,
+                        _P, _P, _P], C.c_int),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile oracle/*.c into oracle/liboracle.so (gcc, via the Makefile)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        h = C.CDLL(str(LIB_PATH))
+        for name, (args, res) in _SIGS.items():
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = h
+    return _lib
+
+
+def p(a: np.ndarray | None) -> C.c_void_p:
+    if a is None:
+        return C.c_void_p()
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- numpy-friendly wrappers ------------------------------------------------
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def igemm_s8s8(a, b, m, k, n, out=None):
+    out = np.zeros(m * n, np.int32) if out is None else out
+    a, b = _c(a, np.int8), _c(b, np.int8)
+    assert lib().oracle_igemm_s8s8(p(a), p(b), m, k, n, p(out)) == 0
+    return out
+
+
+def igemm_u8s8(a, b, m, k, n, out=None):
+    out = np.zeros(m * n, np.int32) if out is None else out
+    a, b = _c(a, np.uint8), _c(b, np.int8)
+    assert lib().oracle_igemm_u8s8(p(a), p(b), m, k, n, p(out)) == 0
+    return out
+
+
+def selftest_case(i, unsigned=False):
+    m, k, n, seed = C.c_size_t(), C.c_size_t(), C.c_size_t(), C.c_uint32()
+    label = C.c_char_p()
+    assert lib().oracle_selftest_shape(i, C.byref(label), C.byref(m), C.byref(k), C.byref(n), C.byref(seed)) == 0
+    m, k, n = m.value, k.value, n.value
+    a = np.zeros(m * k, np.uint8 if unsigned else np.int8)
+    b = np.zeros(n * k, np.int8)
+    f = lib().oracle_selftest_fill_u8 if unsigned else lib().oracle_selftest_fill_s8
+    assert f(i, p(a), p(b)) == 0
+    return label.value.decode(), m, k, n, seed.value, a, b
+
+
+def quantize_row_i8(x, ties_even=False):
+    x = _c(x, np.float32)
+    q = np.zeros(x.size, np.int8)
+    f = lib().oracle_quantize_row_i8_te if ties_even else lib().oracle_quantize_row_i8
+    s = f(p(x), x.size, p(q))
+    return q, np.float32(s)
+
+
+def gemv_i8_batched(x, w, scales, n, k):
+    x = _c(x, np.float32).reshape(-1, k)
+    m = x.shape[0]
+    xq = np.zeros(m * k, np.int8)
+    a_s = np.zeros(m, np.float32)
+    acc = np.zeros(m * n, np.int32)
+    y = np.zeros(m * n, np.float32)
+    lib().oracle_gemv_i8_batched(p(x), m, p(_c(w, np.int8)), p(_c(scales, np.float32)), n, k, p(xq), p(a_s), p(acc), p(y))
+    return y.reshape(m, n), acc.reshape(m, n), xq.reshape(m, k), a_s
+
+
+def argmax_row(logits):
+    logits = _c(logits, np.float32)
+    idx = C.c_uint32()
+    st = lib().oracle_argmax_row(p(logits), logits.size, C.byref(idx))
+    return st, idx.value
+
+
+def lm_head_i8(x, w, scales, n, k):
+    x = _c(x, np.float32).reshape(-1, k)
+    m = x.shape[0]
+    logits = np.zeros(m * n, np.float32)
+    am = np.zeros(m, np.uint32)
+    assert lib().oracle_lm_head_i8(p(x), m, p(_c(w, np.int8)), p(_c(scales, np.float32)), n, k, p(logits), p(am)) == 0
+    return logits.reshape(m, n), am
+
+
+def route(hidden, gate, n_experts, top_k, norm_topk=False, routed_scale=1.0):
+    hidden = _c(hidden, np.float32)
+    t, h = hidden.shape
+    idx = np.zeros(t * top_k, np.uint32)
+    w = np.zeros(t * top_k, np.float32)
+    probs = np.zeros(t * n_experts, np.float32)
+    st = lib().oracle_route(p(hidden), t, h, p(_c(gate, np.float32)), n_experts, top_k, int(norm_topk),
+                            float(routed_scale), p(idx), p(w), p(probs))
+    return st, idx.reshape(t, top_k), w.reshape(t, top_k), probs.reshape(t, n_experts)
+
+
+def expert_i8(x, h, inter, wg, sg, wu, su, wd, sd):
+    x = _c(x, np.float32)
+    y = np.zeros(h, np.float32)
+    act = np.zeros(inter, np.float32)
+    aq = np.zeros(inter, np.int8)
+    as2 = C.c_float()
+    lib().oracle_expert_i8(p(x), h, inter, p(_c(wg, np.int8)), p(_c(sg, np.float32)), p(_c(wu, np.int8)),
+                           p(_c(su, np.float32)), p(_c(wd, np.int8)), p(_c(sd, np.float32)), p(y), p(act), p(aq),
+                           C.byref(as2))
+    return y, act, aq, np.float32(as2.value)
+
+
+def moe_decode(hidden, router, wg, sg, wu, su, wd, sd, n_experts, top_k, inter, norm_topk=False, routed_scale=1.0,
+               shared=None):
+    hidden = _c(hidden, np.float32)
+    t, h = hidden.shape
+    out = np.zeros(t * h, np.float32)
+    idx = np.zeros(t * top_k, np.uint32)
+    gates = np.zeros(t * top_k, np.float32)
+    if shared is None:
+        sh = [None] * 6
+        si = 0
+    else:
+        si = shared[0]
+        sh = [_c(shared[1], np.int8), _c(shared[2], np.float32), _c(shared[3], np.int8), _c(shared[4], np.float32),
+              _c(shared[5], np.int8), _c(shared[6], np.float32)]
+    st = lib().oracle_moe_decode(p(hidden), t, h, inter, n_experts, top_k, p(_c(router, np.float32)),
+                                 p(_c(wg, np.int8)), p(_c(sg, np.float32)), p(_c(wu, np.int8)),
+                                 p(_c(su, np.float32)), p(_c(wd, np.int8)), p(_c(sd, np.float32)), int(norm_topk),
+                                 float(routed_scale), *[p(a) for a in sh], si, p(out), p(idx), p(gates))
+    return st, out.reshape(t, h), idx.reshape(t, top_k), gates.reshape(t, top_k)
+
+
+def unpack_to_i8(packed, n, k):
+    packed = _c(packed, np.uint8)
+    out = np.zeros(n * k, np.int8)
+    st = lib().oracle_unpack_to_i8(p(packed), n, k, p(out))
+    return st, out
+
+
+def igemm_s4s8_packed(a, b_packed, scales, group, m, k, n):
+    out = np.zeros(m * n, np.float32)
+    st = lib().oracle_igemm_s4s8_packed(p(_c(a, np.int8)), p(_c(b_packed, np.uint8)), p(_c(scales, np.float32)),
+                                        group, m, k, n, p(out))
+    return st, out
+
+
+def s4s8_group_i32(a, b_packed, group, m, k, n):
+    out = np.zeros(m * n * (k // group), np.int32)
+    st = lib().oracle_s4s8_group_i32(p(_c(a, np.int8)), p(_c(b_packed, np.uint8)), group, m, k, n, p(out))
+    return st, out
+
+
+def quantize_int8_f32(w, n, k):
+    w = _c(w, np.float32)
+    q = np.zeros(n * k, np.int8)
+    s = np.zeros(n, np.float32)
+    st = lib().oracle_quantize_int8_f32(p(w), n, k, p(q), p(s))
+    return st, q, s
+
+
+def pack_int4_f32(w, n, k, group):
+    w = _c(w, np.float32)
+    packed = np.zeros(n * k // 2, np.uint8)
+    s = np.zeros(n * (k // group), np.float32)
+    st = lib().oracle_pack_int4_f32(p(w), n, k, group, p(packed), p(s))
+    return st, packed, s
+
+
+def moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, n_experts, inter):
+    x = _c(x, np.float32)
+    t, h = x.shape
+    top_k = idx.shape[1]
+    out = np.zeros(t * h, np.float32)
+    xq = np.zeros(t * h, np.int8)
+    xs = np.zeros(t, np.float32)
+    st = lib().oracle_moe_prefill_i4(p(x), t, h, inter, n_experts, top_k, p(_c(idx, np.uint32)),
+                                     p(_c(gates, np.float32)), group, p(_c(wg, np.uint8)), p(_c(sg, np.float32)),
+                                     p(_c(wu, np.uint8)), p(_c(su, np.float32)), p(_c(wd, np.uint8)),
+                                     p(_c(sd, np.float32)), p(out), p(xq), p(xs))
+    return st, out.reshape(t, h), xq.reshape(t, h), xs
+
+
+class Ring:
+    """One stream's RingCache regions in host memory (head-major f32)."""
+
+    H, D, W = 10, 128, 128
+
+    def __init__(self, ref_cap):
+        self.ref_cap = ref_cap
+        self.ref_k = np.zeros((self.H, ref_cap, self.D), np.float32)
+        self.ref_v = np.zeros((self.H, ref_cap, self.D), np.float32)
+        self.ring_k = np.zeros((self.H, self.W, self.D), np.float32)
+        self.ring_v = np.zeros((self.H, self.W, self.D), np.float32)
+        self.prefill_len = 0
+        self.ring_len = C.c_uint32(0)
+        self.ring_pos = C.c_uint32(0)
+
+    def record_prefill(self, k, v, seq):
+        self.ref_k[:, :seq] = k.reshape(self.H, seq, self.D)
+        self.ref_v[:, :seq] = v.reshape(self.H, seq, self.D)
+        self.prefill_len = seq
+        self.ring_len.value = 0
+        self.ring_pos.value = 0
+
+    def write(self, k_step, v_step):
+        slot = C.c_uint32()
+        st = lib().oracle_ring_write(p(self.ring_k), p(self.ring_v), C.byref(self.ring_len), C.byref(self.ring_pos),
+                                     p(_c(k_step, np.float32)), p(_c(v_step, np.float32)), C.byref(slot))
+        assert st == 0
+        return slot.value
+
+    def attend(self, q):
+        out = np.zeros(self.H * self.D, np.float32)
+        st = lib().oracle_decode_attention(p(self.ref_k), p(self.ref_v), self.ref_cap, self.prefill_len,
+                                           p(self.ring_k), p(self.ring_v), self.ring_len.value,
+                                           p(_c(q, np.float32)), p(out))
+        return st, out

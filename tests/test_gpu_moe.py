@@ -1,0 +1,166 @@
+"""GPU parity for the MoE decode layer (moe.rs:181-266 route;
+decoder.rs:2199-2268 decode_mlp_i8 per token): routing indices bit-exact,
+gates within rel 1e-6, layer output within rel 1e-3 (BASELINE cfg3) — the
+only f32 differences come from expf in SiLU (~1 ulp) propagating through
+the act re-quantization."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from franken_ocr_amd import synth
+from oracle import pyoracle as O
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 1280, 896, 64, 6
+
+
+def _say(msg):
+    print(f"[gpu-moe] {msg}", flush=True)
+
+
+def make_layer(seed: int, h=H, inter=I, e=E):
+    router = synth.f32_normal(synth.seed_of(seed), e * h, 0.0, 0.02).reshape(e, h)
+    wg = synth.int8_uniform(synth.seed_of(seed + 1), e * inter * h)
+    wu = synth.int8_uniform(synth.seed_of(seed + 2), e * inter * h)
+    wd = synth.int8_uniform(synth.seed_of(seed + 3), e * h * inter)
+    sg = synth.f32_uniform(synth.seed_of(seed + 4), e * inter, 1e-3, 2e-2)
+    su = synth.f32_uniform(synth.seed_of(seed + 5), e * inter, 1e-3, 2e-2)
+    sd = synth.f32_uniform(synth.seed_of(seed + 6), e * h, 1e-3, 2e-2)
+    return router, wg, sg, wu, su, wd, sd
+
+
+def assert_rel(got, want, rtol):
+    scale = np.maximum(np.abs(want), np.max(np.abs(want), axis=-1, keepdims=True) * 1e-2)
+    rel = np.abs(got.astype(np.float64) - want) / scale
+    assert rel.max() <= rtol, f"max rel err {rel.max():.3e} > {rtol}"
+
+
+@pytest.fixture(scope="module")
+def layer_w():
+    return make_layer(100)
+
+
+@pytest.fixture(scope="module")
+def gpu_layer(ctx, layer_w):
+    from franken_ocr_amd.engine import MoeLayer
+
+    return MoeLayer(H, I, E, K, *layer_w, ctx=ctx)
+
+
+@pytest.mark.parametrize("t", [1, 8, 32, 64])
+@pytest.mark.parametrize("norm_topk", [True, False])
+def test_route_bit_exact(ctx, gpu_layer, layer_w, t, norm_topk):
+    _say(f"route t={t} norm={norm_topk}")
+    x = synth.f32_normal(synth.seed_of(200 + t), t * H).reshape(t, H)
+    dx = ctx.to_device(x)
+    didx, dg, dp = ctx.empty((t, K), np.uint32), ctx.empty((t, K), np.float32), ctx.empty((t, E), np.float32)
+    gpu_layer.route(dx, didx, dg, dp, norm_topk=norm_topk)
+    st, idx, w, probs = O.route(x, layer_w[0], E, K, norm_topk=norm_topk)
+    assert st == 0
+    assert np.array_equal(didx.numpy(), idx)
+    np.testing.assert_allclose(dg.numpy(), w, rtol=1e-6, atol=0)
+    np.testing.assert_allclose(dp.numpy(), probs, rtol=1e-6, atol=1e-12)
+
+
+@pytest.mark.parametrize("t", [1, 8, 32])
+def test_moe_decode_matches_oracle(ctx, gpu_layer, layer_w, t):
+    _say(f"moe_decode t={t}")
+    x = synth.f32_normal(synth.seed_of(300 + t), t * H).reshape(t, H)
+    dx = ctx.to_device(x)
+    dout = ctx.empty((t, H), np.float32)
+    didx, dg = ctx.empty((t, K), np.uint32), ctx.empty((t, K), np.float32)
+    gpu_layer.decode(dx, dout, didx, dg, norm_topk=True)
+    st, out, idx, gates = O.moe_decode(x, *layer_w, E, K, I, norm_topk=True)
+    assert st == 0
+    assert np.array_equal(didx.numpy(), idx)
+    np.testing.assert_allclose(dg.numpy(), gates, rtol=1e-6, atol=0)
+    assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
+    # deterministic: a second run is bitwise identical
+    dout2 = ctx.empty((t, H), np.float32)
+    gpu_layer.decode(dx, dout2, norm_topk=True)
+    assert np.array_equal(dout.numpy(), dout2.numpy())
+
+
+def test_moe_decode_reference_default_config(ctx, gpu_layer, layer_w):
+    """norm_topk_prob = false, routed_scaling_factor = 1.0 (moe.rs:70-73)."""
+    t = 8
+    x = synth.f32_normal(synth.seed_of(400), t * H).reshape(t, H)
+    dout = ctx.empty((t, H), np.float32)
+    gpu_layer.decode(ctx.to_device(x), dout, norm_topk=False, routed_scale=1.0)
+    st, out, _, _ = O.moe_decode(x, *layer_w, E, K, I, norm_topk=False)
+    assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
+
+
+def test_moe_decode_all_tokens_one_expert(ctx):
+    """Every token routes to the same 6 experts (P = T pairs per expert)."""
+    from franken_ocr_amd.engine import MoeLayer
+
+    router, wg, sg, wu, su, wd, sd = make_layer(500)
+    router = np.zeros_like(router)
+    router[[3, 9, 17, 30, 41, 63], :] = 0.05  # same top-6 for every positive-sum row
+    t = 40
+    x = np.abs(synth.f32_normal(synth.seed_of(501), t * H)).reshape(t, H)
+    L = MoeLayer(H, I, E, K, router, wg, sg, wu, su, wd, sd, ctx=ctx)
+    dout, didx = ctx.empty((t, H), np.float32), ctx.empty((t, K), np.uint32)
+    L.decode(ctx.to_device(x), dout, didx, norm_topk=True)
+    st, out, idx, _ = O.moe_decode(x, router, wg, sg, wu, su, wd, sd, E, K, I, norm_topk=True)
+    assert np.array_equal(didx.numpy(), idx) and sorted(idx[0].tolist()) == [3, 9, 17, 30, 41, 63]
+    assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
+
+
+def test_moe_identity_experts_known_answer(ctx):
+    """moe.rs:938-980 with int8 identity experts: 6/64 * silu(1)."""
+    from franken_ocr_amd.engine import MoeLayer
+
+    h = inter = 16
+    eye = (np.eye(16, dtype=np.int8) * 127).reshape(-1)
+    w = np.tile(eye, E)
+    s = np.full(E * 16, np.float32(1.0) / np.float32(127.0), np.float32)
+    L = MoeLayer(h, inter, E, K, np.zeros((E, h), np.float32), w, s, w, s, w, s, ctx=ctx)
+    dout = ctx.empty((1, h), np.float32)
+    didx = ctx.empty((1, K), np.uint32)
+    L.decode(ctx.to_device(np.ones((1, h), np.float32)), dout, didx)
+    assert didx.numpy()[0].tolist() == [0, 1, 2, 3, 4, 5]
+    np.testing.assert_allclose(dout.numpy()[0], 6.0 / 64 * (1.0 / (1.0 + math.exp(-1.0))), rtol=1e-5)
+
+
+def test_moe_shared_expert(ctx, layer_w):
+    from franken_ocr_amd.engine import MoeLayer
+
+    si = 1792
+    swg = synth.int8_uniform(synth.seed_of(600), si * H)
+    swu = synth.int8_uniform(synth.seed_of(601), si * H)
+    swd = synth.int8_uniform(synth.seed_of(602), H * si)
+    ssg = synth.f32_uniform(synth.seed_of(603), si, 1e-3, 2e-2)
+    ssu = synth.f32_uniform(synth.seed_of(604), si, 1e-3, 2e-2)
+    ssd = synth.f32_uniform(synth.seed_of(605), H, 1e-3, 2e-2)
+    L = MoeLayer(H, I, E, K, *layer_w, ctx=ctx)
+    L.set_shared(si, swg, ssg, swu, ssu, swd, ssd)
+    t = 4
+    x = synth.f32_normal(synth.seed_of(606), t * H).reshape(t, H)
+    dout = ctx.empty((t, H), np.float32)
+    L.decode(ctx.to_device(x), dout, with_shared=True)
+    st, out, _, _ = O.moe_decode(x, *layer_w, E, K, I, shared=(si, swg, ssg, swu, ssu, swd, ssd))
+    assert st == 0
+    assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
+
+
+def test_route_nan_reports_error(ctx, gpu_layer):
+    from franken_ocr_amd._abi import RouteError
+
+    x = np.full((2, H), np.nan, np.float32)
+    didx, dg = ctx.empty((2, K), np.uint32), ctx.empty((2, K), np.float32)
+    with pytest.raises(RouteError, match="no finite router score"):
+        gpu_layer.route(ctx.to_device(x), didx, dg)
+
+
+def test_moe_shape_errors(ctx, gpu_layer):
+    from franken_ocr_amd._abi import ContractViolation
+
+    with pytest.raises(ContractViolation, match=r"t 65 outside"):
+        gpu_layer.decode(ctx.empty((65, H), np.float32), ctx.empty((65, H), np.float32))

@@ -1,0 +1,505 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each test checks an oracle function against something other than its own
+formula: the reference's known answers (file:line cited), integer brute
+force in numpy int64, independent numpy restatements written from the spec
+(as the reference's own int4 parity test does), closed forms, and float64
+recomputations — chosen so a plausible mistake (wrong rounding mode, a
+transposed operand, a dropped term, a wrong slot order) fails.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as O
+
+
+# ---- igemm (src/simd/scalar.rs) -------------------------------------------------
+
+def test_igemm_s8s8_hand_values():
+    # scalar.rs:176-183 and simd/mod.rs:84-94
+    out = O.igemm_s8s8([1, 2, 3, 4, 5, 6], [1, 0, 1, 0, 1, 0], 2, 3, 2)
+    assert out.tolist() == [4, 2, 10, 5]
+
+
+def test_igemm_accumulates():
+    # scalar.rs:186-195: out is +=
+    out = np.array([100], np.int32)
+    O.igemm_s8s8([1, 2, 3], [1, 1, 1], 1, 3, 1, out)
+    assert out.tolist() == [106]
+    O.igemm_s8s8([1, 2, 3], [1, 1, 1], 1, 3, 1, out)
+    assert out.tolist() == [112]
+
+
+def test_igemm_u8s8_and_negatives():
+    # scalar.rs:200-220
+    assert O.igemm_u8s8([10, 20, 30], [2, -1, 1], 1, 3, 1).tolist() == [30]
+    assert O.igemm_s8s8([-2, 3], [-1, -1, 4, -2], 1, 2, 2).tolist() == [-1, -14]
+
+
+@pytest.mark.parametrize(
+    "av,bv,unsigned,want",
+    [
+        (127, 127, False, 110_451_392),  # scalar.rs:227-236
+        (-128, -128, False, 112_197_632),  # scalar.rs:240-249
+        (255, 127, True, 221_772_480),  # scalar.rs:253-262
+        (255, -128, True, -223_518_720),  # dispatch.rs:604-618 self-test extreme
+    ],
+)
+def test_igemm_k6848_extremes(av, bv, unsigned, want):
+    K = 6848
+    a = np.full(K, av, np.uint8 if unsigned else np.int8)
+    b = np.full(K, bv, np.int8)
+    out = (O.igemm_u8s8 if unsigned else O.igemm_s8s8)(a, b, 1, K, 1)
+    assert int(out[0]) == want
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 17, 5), (4, 13, 6), (5, 64, 7), (2, 1280, 9)])
+def test_igemm_matches_i64_brute_force(m, k, n, rng):
+    # scalar.rs:268-302 pattern: an independent i64 oracle
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, n * k).astype(np.int8)
+    want = a.reshape(m, k).astype(np.int64) @ b.reshape(n, k).astype(np.int64).T
+    assert np.array_equal(O.igemm_s8s8(a, b, m, k, n).reshape(m, n).astype(np.int64), want)
+    au = rng.integers(0, 256, m * k).astype(np.uint8)
+    want_u = au.reshape(m, k).astype(np.int64) @ b.reshape(n, k).astype(np.int64).T
+    assert np.array_equal(O.igemm_u8s8(au, b, m, k, n).reshape(m, n).astype(np.int64), want_u)
+
+
+# ---- self-test battery (src/simd/dispatch.rs:340-429) ----------------------------
+
+def _xs32_stream(seed: int, count: int) -> np.ndarray:
+    out = np.empty(count, np.uint32)
+    s = seed
+    for i in range(count):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = s
+    return out
+
+
+def test_selftest_shapes_and_fills_regenerate_independently():
+    L = O.lib()
+    assert L.oracle_selftest_n_shapes() == 12  # dispatch.rs:352-368 (24 cases with both domains)
+    labels = []
+    for i in range(12):
+        label, m, k, n, seed, a, b = O.selftest_case(i)
+        labels.append(label)
+        _, _, _, _, _, au, bu = O.selftest_case(i, unsigned=True)
+        if seed == 0:
+            assert (a == 127).all() and (b == -128).all() and (au == 255).all() and (bu == -128).all()
+            continue
+        if m * k + n * k <= 200_000:
+            st = _xs32_stream(seed | 1, m * k + n * k)
+            assert np.array_equal(a.view(np.uint8), (st[: m * k] & 0xFF).astype(np.uint8))
+            assert np.array_equal(b.view(np.uint8), (st[m * k :] & 0xFF).astype(np.uint8))
+            rot = ((seed << 7) | (seed >> 25)) & 0xFFFFFFFF
+            su = _xs32_stream(rot | 1, m * k + n * k)
+            assert np.array_equal(au, (su[: m * k] & 0xFF).astype(np.uint8))
+    assert labels[0] == "edge:1x1x1" and labels[-1] == "overflow:max_mag_k6848"
+
+
+# ---- quantizers (decoder.rs:1588-1597 / :1647-1656) ---------------------------------
+
+def _np_quant(x: np.ndarray, ties_even: bool):
+    x = np.asarray(x, np.float32)
+    amax = np.float32(np.max(np.abs(x))) if x.size else np.float32(0)
+    scale = np.float32(amax / np.float32(127)) if amax > 0 else np.float32(1)
+    inv = np.float32(np.float32(1) / scale)
+    v = (x * inv).astype(np.float64)
+    r = np.rint(v) if ties_even else np.sign(v) * np.floor(np.abs(v) + 0.5)
+    return np.clip(r, -127, 127).astype(np.int8), scale
+
+
+def test_quantize_row_rounding_modes_split():
+    # scale forced to 1 by the 127; the .5 ties separate the two rules
+    row = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5]
+    q, s = O.quantize_row_i8(row)
+    assert s == 1.0 and q.tolist() == [127, 1, 2, 3, -1, -2, -3]  # f32::round: half away
+    q, s = O.quantize_row_i8(row, ties_even=True)
+    assert q.tolist() == [127, 0, 2, 2, 0, -2, -2]  # round_ties_even (nn.rs:600-628 style)
+
+
+def test_quantize_row_zero_and_scale():
+    q, s = O.quantize_row_i8([0.0, -0.0, 0.0])
+    assert s == 1.0 and q.tolist() == [0, 0, 0]  # amax == 0 -> scale 1.0 (decoder.rs:1590)
+    q, s = O.quantize_row_i8([254.0, -2.0, 100.0])
+    assert s == 2.0 and q.tolist() == [127, -1, 50]
+
+
+@pytest.mark.parametrize("ties_even", [False, True])
+def test_quantize_row_matches_numpy_restatement(ties_even, rng):
+    for k in (1, 7, 896, 1280):
+        x = (rng.standard_normal(k) * rng.uniform(0.01, 10)).astype(np.float32)
+        q, s = O.quantize_row_i8(x, ties_even)
+        wq, ws = _np_quant(x, ties_even)
+        assert s == ws and np.array_equal(q, wq)
+
+
+def test_gemv_dequant_order(rng):
+    # y = ((f32)acc * a_scale) * w_scale, left to right (decoder.rs:1636)
+    n, k = 37, 64
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    w = rng.integers(-127, 128, n * k).astype(np.int8)
+    sc = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    y, acc, xq, a_s = O.gemv_i8_batched(x, w, sc, n, k)
+    want_acc = xq.astype(np.int64) @ w.reshape(n, k).astype(np.int64).T
+    assert np.array_equal(acc.astype(np.int64), want_acc)
+    want = (acc.astype(np.float32) * a_s[:, None]).astype(np.float32) * sc[None, :]
+    assert np.array_equal(y, want.astype(np.float32))
+    # the other association order differs somewhere (so the test has teeth)
+    other = acc.astype(np.float32) * (a_s[:, None] * sc[None, :])
+    assert not np.array_equal(y, other)
+
+
+# ---- argmax (sampler.rs:168-186) ------------------------------------------------------
+
+def test_argmax_known_answers():
+    assert O.argmax_row([0.1, -2.0, 3.5, 3.4, 0.0]) == (0, 2)  # sampler.rs:618-621
+    assert O.argmax_row([0.0, 5.0, 1.0, 5.0]) == (0, 1)  # ties -> lowest index, :624-634
+    assert O.argmax_row([np.nan, -np.inf, 2.0, 1.0]) == (0, 2)  # NaN skipped, :637-645
+    assert O.argmax_row([np.nan, np.nan]) == (0, 0)  # all NaN -> 0 (sampler.rs:184)
+    assert O.argmax_row([-np.inf, -np.inf]) == (0, 0)
+    assert O.argmax_row([-0.0, 0.0]) == (0, 0)  # -0 == +0: first wins
+    assert O.argmax_row([])[0] != 0  # empty row is an error
+
+
+def test_argmax_random_vs_numpy(rng):
+    for _ in range(20):
+        v = rng.standard_normal(1000).astype(np.float32)
+        v[rng.integers(0, 1000, 5)] = np.nan
+        v[rng.integers(0, 1000, 3)] = np.nanmax(v)
+        assert O.argmax_row(v) == (0, int(np.nanargmax(v)))
+
+
+# ---- router (moe.rs:181-266) ------------------------------------------------------------
+
+def _route_gate_with_col0(logits_by_expert: dict, h: int = 1280, E: int = 64):
+    hid = np.zeros((1, h), np.float32)
+    hid[0, 0] = 1.0
+    gate = np.zeros((E, h), np.float32)
+    for e, v in logits_by_expert.items():
+        gate[e, 0] = v
+    return hid, gate
+
+
+def test_route_known_answer_greedy_top6():
+    # moe.rs:777-820: experts 10..15 with logits 10..5 -> indices [10..15]
+    hid, gate = _route_gate_with_col0({10: 10.0, 11: 9.0, 12: 8.0, 13: 7.0, 14: 6.0, 15: 5.0})
+    st, idx, w, probs = O.route(hid, gate, 64, 6)
+    assert st == 0 and idx[0].tolist() == [10, 11, 12, 13, 14, 15]
+    ex = np.exp(np.array([10, 9, 8, 7, 6, 5], np.float64) - 10.0)
+    den = ex.sum() + 58 * math.exp(-10.0)
+    np.testing.assert_allclose(w[0], ex / den, rtol=1e-6)
+    assert float(w[0].sum()) < 1.0  # raw softmax probs (norm_topk_prob = false)
+    assert np.all(np.diff(w[0]) < 0)
+
+
+def test_route_renorm_and_scaling():
+    hid, gate = _route_gate_with_col0({10: 10.0, 11: 9.0, 12: 8.0, 13: 7.0, 14: 6.0, 15: 5.0})
+    _, _, w, _ = O.route(hid, gate, 64, 6, norm_topk=True)
+    assert abs(float(w[0].astype(np.float64).sum()) - 1.0) < 1e-5 and np.all(np.diff(w[0]) < 0)
+    _, _, w1, _ = O.route(hid, gate, 64, 6)
+    _, _, w25, _ = O.route(hid, gate, 64, 6, routed_scale=2.5)
+    np.testing.assert_allclose(w25, w1 * np.float32(2.5), rtol=1e-6)
+
+
+def test_route_uniform_ties_pick_lowest_indices():
+    # all-zero gate -> uniform softmax -> experts 0..5 at 1/64 each (moe.rs:938-980)
+    hid = np.ones((1, 8), np.float32)
+    gate = np.zeros((64, 8), np.float32)
+    st, idx, w, _ = O.route(hid, gate, 64, 6)
+    assert st == 0 and idx[0].tolist() == [0, 1, 2, 3, 4, 5]
+    assert np.all(w == np.float32(1 / 64))
+
+
+def test_route_nan_is_an_error():
+    # moe.rs:261-265 "no finite router score"
+    hid = np.full((1, 8), np.nan, np.float32)
+    gate = np.ones((64, 8), np.float32)
+    st, *_ = O.route(hid, gate, 64, 6)
+    assert st == -7
+
+
+def test_route_matches_float64_restatement(rng):
+    t, h, E = 16, 1280, 64
+    hid = rng.standard_normal((t, h)).astype(np.float32)
+    gate = (rng.standard_normal((E, h)) * 0.02).astype(np.float32)
+    st, idx, w, probs = O.route(hid, gate, E, 6, norm_topk=True)
+    assert st == 0
+    logits = (hid.astype(np.float64) @ gate.astype(np.float64).T).astype(np.float32)
+    z = logits.astype(np.float64)
+    ex = np.exp(z - z.max(axis=1, keepdims=True))
+    p = (ex / ex.sum(axis=1, keepdims=True)).astype(np.float32)
+    np.testing.assert_allclose(probs, p, rtol=1e-6, atol=0)
+    for r in range(t):
+        order = sorted(range(E), key=lambda e: (-float(p[r, e]), e))[:6]
+        assert idx[r].tolist() == order
+
+
+# ---- SwiGLU expert / MoE decode (decoder.rs:1744-1755, :2199-2268) -------------------
+
+def test_silu_values():
+    L = O.lib()
+    assert abs(L.oracle_silu(2.0) - 2.0 / (1.0 + math.exp(-2.0))) < 1e-6
+    assert L.oracle_silu(0.0) == 0.0
+
+
+def test_moe_identity_experts_known_answer():
+    # moe.rs:938-980: identity SwiGLU experts, uniform gate -> 6/64 * silu(1).
+    # The int8 weights of I (2x2) quantize to 127 on the diagonal, scale 1/127.
+    h, inter, E = 2, 2, 64
+    eye = np.array([127, 0, 0, 127], np.int8)
+    wg = np.tile(eye, E)
+    s = np.full(E * 2, np.float32(1.0) / np.float32(127.0), np.float32)
+    hid = np.ones((1, h), np.float32)
+    router = np.zeros((E, h), np.float32)
+    st, out, idx, gates = O.moe_decode(hid, router, wg, s, wg, s, wg, s, E, 6, inter)
+    assert st == 0 and idx[0].tolist() == [0, 1, 2, 3, 4, 5]
+    silu1 = 1.0 / (1.0 + math.exp(-1.0))
+    np.testing.assert_allclose(out[0], 6.0 / 64 * silu1, rtol=1e-5)
+
+
+def test_expert_i32_accumulators_and_float64_check(rng):
+    h, inter = 64, 48
+    x = rng.standard_normal(h).astype(np.float32)
+    wg = rng.integers(-127, 128, inter * h).astype(np.int8)
+    wu = rng.integers(-127, 128, inter * h).astype(np.int8)
+    wd = rng.integers(-127, 128, h * inter).astype(np.int8)
+    sg = rng.uniform(1e-3, 2e-2, inter).astype(np.float32)
+    su = rng.uniform(1e-3, 2e-2, inter).astype(np.float32)
+    sd = rng.uniform(1e-3, 2e-2, h).astype(np.float32)
+    y, act, aq, as2 = O.expert_i8(x, h, inter, wg, sg, wu, su, wd, sd)
+    xq, xs = _np_quant(x, False)
+    g = xq.astype(np.int64) @ wg.reshape(inter, h).astype(np.int64).T
+    u = xq.astype(np.int64) @ wu.reshape(inter, h).astype(np.int64).T
+    g64 = g * float(xs) * sg.astype(np.float64)
+    u64 = u * float(xs) * su.astype(np.float64)
+    act64 = g64 / (1 + np.exp(-g64)) * u64
+    np.testing.assert_allclose(act, act64, rtol=1e-5, atol=1e-7)
+    wq, ws = _np_quant(act, False)
+    assert np.array_equal(aq, wq) and as2 == ws
+    d = aq.astype(np.int64) @ wd.reshape(h, inter).astype(np.int64).T
+    np.testing.assert_allclose(y, d * float(as2) * sd.astype(np.float64), rtol=1e-6)
+
+
+def test_moe_decode_combine_slot_order(rng):
+    # out = ((0 + y0*w0) + y1*w1) ... in slot order; check vs float64 sum and
+    # that every token's output is the gate-weighted sum of its experts.
+    h, inter, E, t = 32, 32, 8, 3
+    router = (rng.standard_normal((E, h)) * 0.5).astype(np.float32)
+    wg = rng.integers(-127, 128, E * inter * h).astype(np.int8)
+    wu = rng.integers(-127, 128, E * inter * h).astype(np.int8)
+    wd = rng.integers(-127, 128, E * h * inter).astype(np.int8)
+    sg = rng.uniform(1e-3, 2e-2, E * inter).astype(np.float32)
+    su = rng.uniform(1e-3, 2e-2, E * inter).astype(np.float32)
+    sd = rng.uniform(1e-3, 2e-2, E * h).astype(np.float32)
+    hid = rng.standard_normal((t, h)).astype(np.float32)
+    st, out, idx, gates = O.moe_decode(hid, router, wg, sg, wu, su, wd, sd, E, 4, inter, norm_topk=True)
+    assert st == 0
+    for r in range(t):
+        acc32 = np.zeros(h, np.float32)
+        acc64 = np.zeros(h, np.float64)
+        for j in range(4):
+            e = int(idx[r, j])
+            y, *_ = O.expert_i8(hid[r], h, inter, wg[e * inter * h:(e + 1) * inter * h], sg[e * inter:(e + 1) * inter],
+                                wu[e * inter * h:(e + 1) * inter * h], su[e * inter:(e + 1) * inter],
+                                wd[e * h * inter:(e + 1) * h * inter], sd[e * h:(e + 1) * h])
+            acc32 = (acc32 + (y * gates[r, j]).astype(np.float32)).astype(np.float32)
+            acc64 += y.astype(np.float64) * float(gates[r, j])
+        assert np.array_equal(out[r], acc32)
+        np.testing.assert_allclose(out[r], acc64, rtol=1e-5, atol=1e-7)
+
+
+# ---- int4 (src/simd/int4.rs) -------------------------------------------------------------
+
+def test_int4_sign_extension_table():
+    # int4.rs:660-670
+    L = O.lib()
+    want = [0, 1, 2, 3, 4, 5, 6, 7, -8, -7, -6, -5, -4, -3, -2, -1]
+    assert [L.oracle_sign_extend_nibble(n) for n in range(16)] == want
+
+
+def test_int4_unpack_fixtures():
+    # int4.rs:676-696
+    for byte, lo_hi in [(0x21, [1, 2]), (0x43, [3, 4]), (0x87, [7, -8]), (0xF0, [0, -1]), (0x00, [0, 0]),
+                        (0x88, [-8, -8])]:
+        assert O.unpack_to_i8([byte], 1, 2)[1].tolist() == lo_hi
+    assert O.unpack_to_i8([0x21, 0x43, 0x65, 0x87], 2, 4)[1].tolist() == [1, 2, 3, 4, 5, 6, 7, -8]
+    assert O.unpack_to_i8([0x21], 1, 3)[0] != 0  # odd k rejected
+
+
+def _spec_s4s8(a, packed, scales, group, m, k, n):
+    """Independent restatement from the packing spec (int4.rs:775-810 pattern)."""
+    b = np.zeros((n, k), np.int64)
+    pk = packed.reshape(n, k // 2).astype(np.int64)
+    lo = pk & 0xF
+    hi = pk >> 4
+    b[:, 0::2] = np.where(lo >= 8, lo - 16, lo)
+    b[:, 1::2] = np.where(hi >= 8, hi - 16, hi)
+    A = a.reshape(m, k).astype(np.int64)
+    G = k // group
+    parts = np.einsum("mgk,ngk->mng", A.reshape(m, G, group), b.reshape(n, G, group))
+    out = np.zeros((m, n), np.float32)
+    sc = scales.reshape(n, G)
+    for g in range(G):
+        out = (out + (sc[None, :, g] * parts[:, :, g].astype(np.float32)).astype(np.float32)).astype(np.float32)
+    return out.reshape(-1), parts.reshape(-1)
+
+
+@pytest.mark.parametrize("m,k,n,group", [(1, 16, 1, 16), (2, 32, 3, 16), (4, 64, 5, 32), (3, 96, 2, 16),
+                                         (2, 128, 7, 32), (5, 1280, 9, 32)])
+def test_int4_matches_spec_oracle(m, k, n, group, rng):
+    a = rng.integers(-127, 128, m * k).astype(np.int8)
+    packed = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+    scales = rng.uniform(-1, 1, n * (k // group)).astype(np.float32)
+    st, out = O.igemm_s4s8_packed(a, packed, scales, group, m, k, n)
+    want, parts = _spec_s4s8(a, packed, scales, group, m, k, n)
+    assert st == 0 and np.array_equal(out, want)
+    st, got_parts = O.s4s8_group_i32(a, packed, group, m, k, n)
+    assert st == 0 and np.array_equal(got_parts.astype(np.int64), parts)
+
+
+def test_int4_adversarial_known_answers():
+    # int4.rs:853-892: all -8 weights; +/-127 alternating -> 0.0; all -127 -> 32,512 per cell
+    m, k, n, g = 2, 32, 3, 16
+    packed = np.full(n * k // 2, 0x88, np.uint8)
+    scales = np.ones(n * (k // g), np.float32)
+    alt = np.array([127 if i % 2 == 0 else -127 for i in range(m * k)], np.int8)
+    assert np.all(O.igemm_s4s8_packed(alt, packed, scales, g, m, k, n)[1] == 0.0)
+    assert np.all(O.igemm_s4s8_packed(np.full(m * k, -127, np.int8), packed, scales, g, m, k, n)[1] == 32512.0)
+
+
+def test_int4_single_group_equals_int8_per_channel(rng):
+    # int4.rs:901-925: group == k == 16 collapses to per-channel int8
+    m, k, n = 3, 16, 4
+    a = rng.integers(-127, 128, m * k).astype(np.int8)
+    packed = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+    scales = np.array([0.0625 + i * 0.03125 for i in range(n)], np.float32)
+    _, out = O.igemm_s4s8_packed(a, packed, scales, 16, m, k, n)
+    _, b = O.unpack_to_i8(packed, n, k)
+    acc = O.igemm_s8s8(a, b, m, k, n).reshape(m, n)
+    assert np.array_equal(out.reshape(m, n), (scales[None, :] * acc.astype(np.float32)).astype(np.float32))
+
+
+def test_int4_shape_rejections():
+    a = np.ones(32, np.int8)
+    assert O.igemm_s4s8_packed(a, np.zeros(16, np.uint8), np.ones(4, np.float32), 8, 1, 32, 1)[0] != 0  # int4.rs:928
+    assert O.igemm_s4s8_packed(np.ones(24, np.int8), np.zeros(12, np.uint8), np.ones(2, np.float32), 16, 1, 24, 1)[0] != 0
+
+
+# ---- weight quantizers (src/quant) ---------------------------------------------------------
+
+def test_quantize_int8_known_answers():
+    # quant/int8.rs:300-366
+    assert O.quantize_int8_f32([127.0, -127.0, 0.0, 64.0], 1, 4)[1:] and True
+    st, q, s = O.quantize_int8_f32([127.0, -127.0, 0.0, 64.0], 1, 4)
+    assert s.tolist() == [1.0] and q.tolist() == [127, -127, 0, 64]
+    st, q, s = O.quantize_int8_f32([254.0, -2.0, 100.0], 1, 3)
+    assert s.tolist() == [2.0] and q.tolist() == [127, -1, 50]
+    st, q, s = O.quantize_int8_f32([127.0, 0.0, -64.0, 254.0, -254.0, 0.0], 2, 3)
+    assert s.tolist() == [1.0, 2.0] and q.tolist() == [127, 0, -64, 127, -127, 0]
+    st, q, s = O.quantize_int8_f32([0.0, 0.0, -0.0, 0.0], 1, 4)
+    assert s.tolist() == [1.0] and q.tolist() == [0, 0, 0, 0]
+    st, q, s = O.quantize_int8_f32([127.0, 0.5, 1.5, 2.5], 1, 4)
+    assert q.tolist() == [127, 0, 2, 2]
+    st, q, s = O.quantize_int8_f32([-127.0, -2.5, -1.5, -0.5, 0.5, 1.5, 2.5, 127.0], 1, 8)
+    assert q.tolist() == [-127, -2, -2, 0, 0, 2, 2, 127]
+    st, q, s = O.quantize_int8_f32([-1000.0, 1000.0], 1, 2)
+    assert q.tolist() == [-127, 127]
+
+
+def test_pack_int4_roundtrip(rng):
+    n, k, g = 3, 64, 32
+    w = rng.standard_normal(n * k).astype(np.float32)
+    st, packed, s = O.pack_int4_f32(w, n, k, g)
+    assert st == 0
+    _, q = O.unpack_to_i8(packed, n, k)
+    assert q.min() >= -8 and q.max() <= 7
+    deq = q.reshape(n, k // g, g).astype(np.float32) * s.reshape(n, k // g, 1)
+    err = np.abs(deq.reshape(-1) - w)
+    assert np.all(err <= np.repeat(s, g) * 0.5 + 1e-6)
+
+
+# ---- R-SWA ring + attention (src/native_engine/rswa.rs) ------------------------------------
+
+H, D, W = 10, 128, 128
+
+
+def test_attention_single_key_returns_value():
+    # rswa.rs:1475-1488
+    r = O.Ring(8)
+    k = np.zeros((H, 1, D), np.float32)
+    k[:, :, 0] = 1.0
+    r.record_prefill(k, np.full((H, 1, D), 7.0, np.float32), 1)
+    q = np.zeros((H, D), np.float32)
+    q[:, 0] = 5.0
+    st, out = r.attend(q)
+    assert st == 0 and np.allclose(out, 7.0, atol=1e-5)
+
+
+def test_attention_equal_scores_average():
+    # rswa.rs:1493-1507
+    r = O.Ring(8)
+    k = np.zeros((H, 2, D), np.float32)
+    k[:, :, 0] = 1.0
+    v = np.zeros((H, 2, D), np.float32)
+    v[:, 0] = 2.0
+    v[:, 1] = 4.0
+    r.record_prefill(k, v, 2)
+    q = np.zeros((H, D), np.float32)
+    q[:, 0] = 3.0
+    st, out = r.attend(q)
+    assert np.allclose(out, 3.0, atol=1e-5)
+
+
+def test_attention_online_matches_float64_softmax(rng):
+    # rswa.rs:1511-1553 (online == naive) at a ring-wrapped random state
+    cap, seq = 64, 50
+    r = O.Ring(cap)
+    k = rng.standard_normal((H, seq, D)).astype(np.float32)
+    v = rng.standard_normal((H, seq, D)).astype(np.float32)
+    r.record_prefill(k, v, seq)
+    steps = 150  # wraps past W = 128
+    for _ in range(steps):
+        r.write(rng.standard_normal(H * D).astype(np.float32), rng.standard_normal(H * D).astype(np.float32))
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    st, out = r.attend(q)
+    assert st == 0
+    keys = np.concatenate([r.ref_k[:, :seq], r.ring_k[:, : r.ring_len.value]], axis=1).astype(np.float64)
+    vals = np.concatenate([r.ref_v[:, :seq], r.ring_v[:, : r.ring_len.value]], axis=1).astype(np.float64)
+    sc = np.einsum("hd,hkd->hk", q.astype(np.float64), keys) / math.sqrt(128.0)
+    p = np.exp(sc - sc.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    want = np.einsum("hk,hkd->hd", p, vals).reshape(-1)
+    np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+
+
+def test_ring_write_regimes():
+    # rswa.rs:1557-1613: warm-up appends in order, ring_pos tracks ring_len and
+    # wraps to 0 when full; steady state overwrites slots 0, 1, ... modulo W
+    r = O.Ring(4)
+    r.record_prefill(np.zeros((H, 2, D), np.float32), np.zeros((H, 2, D), np.float32), 2)
+    z = np.zeros(H * D, np.float32)
+    for step in range(W):
+        assert r.write(z, z) == step
+        assert r.ring_len.value == step + 1
+    assert r.ring_pos.value == 0
+    kt = np.full(H * D, 99.0, np.float32)
+    assert r.write(kt, kt) == 0 and r.ring_pos.value == 1
+    assert r.write(kt, kt) == 1 and r.ring_pos.value == 2
+    assert r.ring_len.value == W and r.ring_k[0, 0, 0] == 99.0
+    for expected in range(2, W + 3):
+        assert r.write(z, z) == expected % W
+
+
+def test_attention_empty_key_set_is_error():
+    r = O.Ring(4)
+    r.record_prefill(np.zeros((H, 0, D), np.float32), np.zeros((H, 0, D), np.float32), 0)
+    st, _ = r.attend(np.zeros(H * D, np.float32))
+    assert st != 0
