@@ -84,8 +84,11 @@ def unpack_to_i8(b_packed, n: int, k: int, ctx: Context | None = None) -> np.nda
     """int4.rs:125-142: ``[n, k/2]`` packed -> ``[n, k]`` i8 in [-8, 7]."""
     ctx = ctx or default_context()
     b8 = _as(b_packed, np.uint8)
-    out = np.zeros(n * k if k % 2 == 0 else 0, dtype=np.int8)
-    _abi.call("focr_hip_unpack_to_i8", ctx.handle, _ptr(b8), b8.size, n, k, _ptr(out), out.size)
+    # Only allocate for a shape the contract can accept; otherwise let the
+    # library report the reference's panic text (odd k, n*k/2 overflow, ...).
+    ok = k % 2 == 0 and n * (k // 2) == b8.size and n * k < 2**48
+    out = np.zeros(n * k if ok else 0, dtype=np.int8)
+    _abi.call("focr_hip_unpack_to_i8", ctx.handle, _ptr(b8), b8.size, n, k, _ptr(out), n * k if ok else 0)
     return out
 
 
