@@ -438,10 +438,8 @@ int32_t focr_hip_moe_layer_free(focr_hip_moe_layer* L) {
 namespace {
 
 struct MoeScratch {
-    float* logits;
     int8_t* xq;
     float* xs;
-    void* tables;
     uint32_t* idx;
     float* gates;
     int* flag;
@@ -449,25 +447,23 @@ struct MoeScratch {
     float* ybuf;
     float* shared_act;
     float* shared_y;
+    void* plan;
 };
 
 int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
-    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     const size_t pairs = t * L->top_k;
-    const size_t tb = moe_route_table_bytes(d);
-    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, tb + pairs * 8 + 256));
-    s->logits = static_cast<float*>(ctx->scratch_get(kScrLogits, t * L->n_experts * sizeof(float)));
+    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, pairs * 8 + 256));
     s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
     s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
     s->ybuf = static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float)));
     s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
-    s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, 64));
-    if (!route || !s->logits || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || (with_shared && !s->shared_y))
+    s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
+    s->plan = ctx->scratch_get_zeroed(kScrPlan, moe_plan_bytes());
+    if (!route || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || !s->plan || (with_shared && !s->shared_y))
         return FOCR_HIP_E_OOM;
-    s->tables = route;
-    s->idx = reinterpret_cast<uint32_t*>(route + tb);
-    s->gates = reinterpret_cast<float*>(route + tb + pairs * 4);
+    s->idx = reinterpret_cast<uint32_t*>(route);
+    s->gates = reinterpret_cast<float*>(route + pairs * 4);
     s->shared_act = with_shared ? s->act + pairs * L->inter : nullptr;
     return FOCR_HIP_OK;
 }
@@ -480,12 +476,31 @@ int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* h
     return FOCR_HIP_OK;
 }
 
-int32_t check_route_flag(focr_hip_ctx* ctx, const int* dflag) {
-    int flag = 0;
-    FOCR_HIP_TRY(hipMemcpyAsync(&flag, dflag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
+// The route kernel writes flag[t] = 1 for a token with fewer than top_k
+// finite router scores (moe.rs:261-265). Reading it synchronises.
+int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
+    std::vector<int> flags(t, 0);
+    FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
     FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (flag) return fail(FOCR_HIP_E_ROUTE, "moe::route: no finite router score");
+    for (size_t i = 0; i < t; ++i)
+        if (flags[i]) return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", i));
     return FOCR_HIP_OK;
+}
+
+int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t norm_topk,
+                     float routed_scale, const MoeScratch& s, uint32_t* idx, float* gates, float* probs, void* plan) {
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    ProfScope ps(ctx, "moe_route");
+    FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
+                                  probs, s.flag, plan),
+                 "route launch");
+    return FOCR_HIP_OK;
+}
+
+// A step that stopped between route and combine leaves the plan filled;
+// clear it so the next step starts from an empty plan.
+void reset_plan(focr_hip_ctx* ctx, void* plan) {
+    hipMemsetAsync(plan, 0, moe_plan_bytes(), ctx->stream);
 }
 
 }  // namespace
@@ -499,18 +514,10 @@ int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const
     if (st) return st;
     MoeScratch s;
     if ((st = moe_scratch(ctx, L, t, false, &s))) return st;
-    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
-    {
-        ProfScope ps(ctx, "moe_router");
-        FOCR_HIP_TRY(launch_moe_router(ctx->stream, d, hidden, L->router, s.logits, s.xq, s.xs), "router launch");
-    }
-    {
-        ProfScope ps(ctx, "moe_topk");
-        FOCR_HIP_TRY(launch_moe_topk(ctx->stream, d, s.logits, norm_topk, routed_scale, idx ? idx : s.idx,
-                                     gates ? gates : s.gates, probs, s.tables, s.flag),
-                     "topk launch");
-    }
-    return check_route_flag(ctx, s.flag);
+    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, idx ? idx : s.idx, gates ? gates : s.gates,
+                           probs, nullptr)))
+        return st;
+    return check_route_flags(ctx, s.flag, t);
 }
 
 int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
@@ -523,50 +530,42 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
     MoeScratch s;
     if ((st = moe_scratch(ctx, L, t, with_shared != 0, &s))) return st;
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
-    const int max_active = static_cast<int>(std::min<size_t>(L->n_experts, t * L->top_k));
+    uint32_t* di = idx ? idx : s.idx;
+    float* dg = gates ? gates : s.gates;
     hipStream_t str = ctx->stream;
-    {
-        ProfScope ps(ctx, "moe_router");
-        FOCR_HIP_TRY(launch_moe_router(str, d, hidden, L->router, s.logits, s.xq, s.xs), "router launch");
+    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.plan))) {
+        reset_plan(ctx, s.plan);
+        return st;
     }
-    {
-        ProfScope ps(ctx, "moe_topk");
-        FOCR_HIP_TRY(launch_moe_topk(str, d, s.logits, norm_topk, routed_scale, idx ? idx : s.idx,
-                                     gates ? gates : s.gates, nullptr, s.tables, s.flag),
-                     "topk launch");
-    }
+    hipError_t e = hipSuccess;
     {
         ProfScope ps(ctx, "moe_gate_up");
-        FOCR_HIP_TRY(launch_moe_gate_up(str, d, s.tables, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter,
-                                        max_active, false),
-                     "gate_up launch");
+        e = launch_moe_gate_up(str, d, s.plan, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false);
     }
-    {
+    if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_down");
-        FOCR_HIP_TRY(launch_moe_down(str, d, s.tables, s.act, L->wd, L->sd, nullptr, s.ybuf, (int)L->inter, max_active,
-                                     false),
-                     "down launch");
+        e = launch_moe_down(str, d, s.plan, dg, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
     }
-    if (with_shared) {
+    if (e == hipSuccess && with_shared) {
         {
             ProfScope ps(ctx, "moe_shared_gate_up");
-            FOCR_HIP_TRY(launch_moe_gate_up(str, d, s.tables, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
-                                            (int)L->shared_inter, 1, true),
-                         "shared gate_up launch");
+            e = launch_moe_gate_up(str, d, s.plan, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
+                                   (int)L->shared_inter, true);
         }
-        {
+        if (e == hipSuccess) {
             ProfScope ps(ctx, "moe_shared_down");
-            FOCR_HIP_TRY(launch_moe_down(str, d, s.tables, s.shared_act, L->swd, L->ssd, nullptr, s.shared_y,
-                                         (int)L->shared_inter, 1, true),
-                         "shared down launch");
+            e = launch_moe_down(str, d, s.plan, dg, s.shared_act, L->swd, L->ssd, s.shared_y, (int)L->shared_inter, true);
         }
     }
-    {
+    if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_combine");
-        FOCR_HIP_TRY(launch_moe_combine(str, d, s.tables, s.ybuf, with_shared ? s.shared_y : nullptr, out),
-                     "combine launch");
+        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, out, s.plan);
     }
-    if (check_route) return check_route_flag(ctx, s.flag);
+    if (e != hipSuccess) {
+        reset_plan(ctx, s.plan);
+        return hip_fail(e, "moe_decode launch");
+    }
+    if (check_route) return check_route_flags(ctx, s.flag, t);
     return FOCR_HIP_OK;
 }
 

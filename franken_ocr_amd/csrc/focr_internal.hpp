@@ -48,6 +48,7 @@ enum ScratchSlot : int {
     kScrI4,     // int4 prefill intermediates
     kScrI4b,
     kScrFlag,   // device status flags
+    kScrPlan,   // MoE step plan (zeroed on allocation)
     kScrCount
 };
 
@@ -76,6 +77,8 @@ struct focr_hip_ctx {
 
     // Grow-only scratch. Returns nullptr (and sets the error) on failure.
     void* scratch_get(int slot, size_t bytes);
+    // As scratch_get, but a fresh allocation is zero-filled (stream-ordered).
+    void* scratch_get_zeroed(int slot, size_t bytes);
     // Make current the device this context lives on.
     hipError_t bind() const { return hipSetDevice(device); }
     hipEvent_t take_event();
@@ -159,25 +162,28 @@ hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int 
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
                               int nparts, uint32_t* argmax);
 
-// k_moe.hip — decode MoE pipeline. RouteTables lives in device scratch.
+// k_moe.hip — decode MoE pipeline (route, gate_up, down, combine).
 struct MoeDims {
     int t, hidden, inter, n_experts, top_k;
 };
-size_t moe_route_table_bytes(const MoeDims& d);
-hipError_t launch_moe_router(hipStream_t s, const MoeDims& d, const float* hidden,
-                             const float* router, float* logits, int8_t* xq, float* xs);
-hipError_t launch_moe_topk(hipStream_t s, const MoeDims& d, const float* logits, int norm_topk,
-                           float routed_scale, uint32_t* idx, float* gates, float* probs,
-                           void* tables, int* flag);
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* tables,
+// The step plan (active-expert mask + per-expert pair lists) lives in zeroed
+// device scratch; route fills it, combine clears it.
+size_t moe_plan_bytes();
+// flag[t] = 1 when token t has fewer than top_k finite router scores. plan
+// may be null (route only).
+hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden,
+                            const float* router, int norm_topk, float routed_scale, int8_t* xq,
+                            float* xs, uint32_t* idx, float* gates, float* probs, int* flag,
+                            void* plan);
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan,
                               const int8_t* xq, const float* xs, const int8_t* wg,
                               const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, int max_active, bool shared);
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* tables, const float* act,
-                           const int8_t* wd, const float* sd, const float* gates_unused,
-                           float* ybuf, int inter, int max_active, bool shared);
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const void* tables,
-                              const float* ybuf, const float* shared_y, float* out);
+                              int inter, bool shared);
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* plan,
+                           const float* gates, const float* act, const int8_t* wd,
+                           const float* sd, float* ybuf, int inter, bool shared);
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf,
+                              const float* shared_y, float* out, void* plan);
 
 // k_int4.hip
 hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,

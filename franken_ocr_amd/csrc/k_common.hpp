@@ -26,6 +26,15 @@ __device__ __forceinline__ int dot16_i8(const int4& a, const int4& b, int c) {
     return c;
 }
 
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// Streaming (read-once) 16-byte load: non-temporal hint so weight rows do
+// not evict reusable lines (activations, scales) from the caches.
+__device__ __forceinline__ int4 ld_stream(const int4* p) {
+    const v4i_t v = __builtin_nontemporal_load(reinterpret_cast<const v4i_t*>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
 // Sum across the 16 lanes of a row group (all 16 lanes end with the total).
 __device__ __forceinline__ int reduce16_add(int v) {
     v += __shfl_xor(v, 8, 16);

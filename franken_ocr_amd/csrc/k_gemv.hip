@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
 #pragma unroll
                 for (int j = 0; j < JB; ++j) {
                     const int c = cb + lane + 16 * j;
-                    w[j] = c < C ? wrow[c] : make_int4(0, 0, 0, 0);
+                    w[j] = c < C ? ld_stream(wrow + c) : make_int4(0, 0, 0, 0);
                 }
 #pragma unroll
                 for (int j = 0; j < JB; ++j) {

@@ -1,289 +1,325 @@
 // k_moe.hip — the MoE decode layer (decoder.rs:2199-2268 decode_mlp_i8 over
-// T tokens) as five stream-ordered kernels:
+// T tokens) as four stream-ordered kernels:
 //
-//   router   logits[t][e] = f32(f64 dot(x_t, G_e)); x rows quantized
-//            (quantize_row_i8) for the experts in the same launch.
-//   topk     per token: f64 softmax -> f32 probs, greedy top-k (strict >,
-//            lower index on ties, NaN skipped; moe.rs:209-266), optional
-//            renorm and scale (moe.rs:226-236); then the expert-major pair
-//            permutation (a counting sort over E buckets, tokens ascending
-//            inside an expert, moe.rs:421-429).
-//   gate_up  grid (active expert, row block): the expert's gate and up rows
-//            streamed once for all of its tokens; epilogue dequant and
-//            act = silu(g) * u (decoder.rs:1746-1752).
-//   down     grid (active expert, row block): prologue re-quantizes each
-//            pair's act row into LDS (quantize_row_i8), then streams the
-//            down rows; epilogue y = dequant * gate (decoder.rs:2244-2246).
-//   combine  out[t][c] = ((0 + y_slot0) + y_slot1) ... (+ shared), slot
-//            order (decoder.rs:2253-2261) — deterministic, no atomics.
+//   route    one block per token: router logits as f64 dot products rounded
+//            to f32, quantize_row_i8 of the token row, f64 softmax rounded to
+//            f32, greedy top-k (= rank by (prob desc, index asc), NaN
+//            skipped; moe.rs:209-266), optional renorm and scale
+//            (moe.rs:226-236). Writes idx/gates [t][k] and appends each
+//            (token, slot) pair to its expert's list in the step plan (an
+//            active-expert bitmask plus per-expert pair lists, built with
+//            device atomics; the next kernel launch orders the reads).
+//   gate_up  grid (active expert, row block): issues the expert's gate and
+//            up row loads first, stages the routed tokens' int8 rows in LDS
+//            meanwhile, and writes act[t*K + j][r] = silu(g) * u
+//            (decoder.rs:1746-1752).
+//   down     grid (active expert, row block): issues the down row loads,
+//            re-quantizes each pair's act row into LDS (quantize_row_i8)
+//            meanwhile, writes y[t*K + j][r] = dequant * gate
+//            (decoder.rs:2244-2246).
+//   combine  out[t][c] = ((0 + y[t,0]) + y[t,1]) ... (+ shared), slot order
+//            (decoder.rs:2253-2261); deterministic, no atomics. It also
+//            clears the plan for the next step.
 //
-// Weight bytes dominate: each routed expert's 3.44 MB is read exactly once
-// per layer step regardless of how many of the T tokens chose it.
+// Each routed expert's 3.44 MB of weights is read exactly once per step, by
+// exactly as many blocks as it has row blocks. The order of pairs inside an
+// expert's list depends on block timing, but every pair's result is computed
+// independently and stored at its own (token, slot) slot, so outputs are
+// bit-reproducible run to run. GEMV rows use LPR lanes per row (16 for K =
+// 1280 -> 5 chunks of 16 B per lane; 8 for K = 896 -> 7 chunks).
 #include "focr_internal.hpp"
 #include "k_common.hpp"
 
 namespace focr {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kGroups = kThreads / 16;
 constexpr int kMaxT = 64;
 constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
-constexpr int kMaxPairs = kMaxT * kMaxK;
 constexpr int kPairStage = 32;  // pairs staged in LDS per pass
 constexpr int kPC = 8;          // pairs accumulated in registers per pass
 
-struct RouteTables {
-    int n_active;
-    int active_e[kMaxE];
-    int offsets[kMaxE + 1];
-    int pair_tok[kMaxPairs];
-    float pair_gate[kMaxPairs];
-    int tok_pair[kMaxPairs];
-    // identity table for the shared expert: one "expert", pairs = tokens
-    int sh_n_active;
-    int sh_active_e[1];
-    int sh_offsets[2];
-    int sh_pair_tok[kMaxT];
-    float sh_pair_gate[kMaxT];
+struct MoePlan {
+    unsigned long long mask;   // bit e: expert e has pairs this step (diagnostic)
+    int cnt[kMaxE];            // pairs per expert
+    int list[kMaxE][kMaxT];    // pair ids t*K + j, per expert
 };
 
-struct TableView {
-    const int* n_active;
-    const int* active_e;
-    const int* offsets;
-    const int* pair_tok;
-    const float* pair_gate;
-};
-
-__host__ __device__ inline TableView view(const RouteTables* t, bool shared) {
-    if (shared) return {&t->sh_n_active, t->sh_active_e, t->sh_offsets, t->sh_pair_tok, t->sh_pair_gate};
-    return {&t->n_active, t->active_e, t->offsets, t->pair_tok, t->pair_gate};
+template <int LPR>
+__device__ __forceinline__ int reduce_lanes(int v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
+    return v;
 }
 
-// ---- router: logits (f64 dots rounded to f32) + x quantization ------------
-__global__ __launch_bounds__(kThreads) void moe_router_kernel(const float* __restrict__ x,
-                                                              const float* __restrict__ G,
-                                                              float* __restrict__ logits,
-                                                              int8_t* __restrict__ xq,
-                                                              float* __restrict__ xs, int T,
-                                                              int H, int E) {
-    __shared__ float red[kThreads / 64];
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * (kThreads / 64) + wave;
-    if (e < E) {
-        const float* g = G + static_cast<size_t>(e) * H;
-        for (int t = 0; t < T; ++t) {
-            const float* xr = x + static_cast<size_t>(t) * H;
-            double acc = 0.0;
-            for (int i = lane; i < H; i += 64) acc = fma(static_cast<double>(xr[i]), static_cast<double>(g[i]), acc);
-            acc = wave_sum_d(acc);
-            if (lane == 0) logits[static_cast<size_t>(t) * E + e] = static_cast<float>(acc);
-        }
-    }
-    // quantize_row_i8 of the token rows (block-strided over tokens)
-    for (int t = blockIdx.x; t < T; t += gridDim.x) {
-        const float* xr = x + static_cast<size_t>(t) * H;
-        float amax = 0.0f;
-        for (int i = threadIdx.x; i < H; i += kThreads) amax = fmaxf(amax, fabsf(xr[i]));
-        amax = wave_max_f(amax);
-        __syncthreads();
-        if (lane == 0) red[wave] = amax;
-        __syncthreads();
-        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-        const float inv = 1.0f / a_scale;
-        int8_t* q = xq + static_cast<size_t>(t) * H;
-        for (int i = threadIdx.x; i < H; i += kThreads) q[i] = quant_i8(xr[i], inv, false);
-        if (threadIdx.x == 0) xs[t] = a_scale;
-    }
+// Index of the a-th set bit of m (a is block-uniform), or -1.
+__device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
+    for (int i = 0; i < a && m; ++i) m &= m - 1ull;
+    return m ? __ffsll(static_cast<long long>(m)) - 1 : -1;
 }
 
-// ---- top-k + permutation (one block) --------------------------------------
-__global__ __launch_bounds__(kThreads) void moe_topk_kernel(const float* __restrict__ logits, int T,
-                                                            int E, int K, int norm_topk,
-                                                            float routed_scale,
-                                                            uint32_t* __restrict__ idx_out,
-                                                            float* __restrict__ gates_out,
-                                                            float* __restrict__ probs_out,
-                                                            RouteTables* __restrict__ tb,
-                                                            int* __restrict__ flag) {
-    __shared__ int s_idx[kMaxPairs];
-    __shared__ float s_w[kMaxPairs];
-    __shared__ int s_cnt[kMaxE];
-    __shared__ int s_base[kMaxE];
-    __shared__ int s_bad;
+// ---- route: one block (16 waves) per token ---------------------------------
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+
+template <int NI>  // float4 chunks of a router row per thread, in batches (H <= 64 * 4 * NI)
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+    const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
+    float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
+    float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
+    MoePlan* __restrict__ plan) {
+    __shared__ float4 s_x[512];
+    __shared__ float s_logit[kMaxE];
+    __shared__ double s_ex[kMaxE];
+    __shared__ float s_p[kMaxE];
+    __shared__ int s_sel_e[kMaxK];
+    __shared__ float s_sel_w[kMaxK];
+    __shared__ float s_red[kRouteWaves];
+    const int t = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    if (threadIdx.x == 0) s_bad = 0;
+    const float* xr = x + static_cast<size_t>(t) * H;
+    const int H4 = H >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    for (int c = threadIdx.x; c < H4; c += kRouteThreads) s_x[c] = x4[c];
     __syncthreads();
-    for (int t = wave; t < T; t += kThreads / 64) {
-        const bool valid = lane < E;
-        const float lg = valid ? logits[static_cast<size_t>(t) * E + lane] : 0.0f;
-        // softmax in f64 over the f32 logits, each probability rounded to f32
-        const double mx = wave_max_d(valid && lg == lg ? static_cast<double>(lg) : -INFINITY);
-        const double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
-        const double sum = wave_sum_d(ex);
-        const float p = valid ? static_cast<float>(ex / sum) : 0.0f;
-        if (probs_out && valid) probs_out[static_cast<size_t>(t) * E + lane] = p;
-        bool taken = false;
-        float wsel[kMaxK];
-        int esel[kMaxK];
-        for (int slot = 0; slot < K; ++slot) {
-            const uint64_t key = (valid && !taken) ? argmax_key(p, static_cast<uint32_t>(lane)) : 0ull;
-            const uint64_t best = wave_max_u64(key);
-            int e = 0;
-            float w = 0.0f;
-            if (best == 0ull) {
-                if (lane == 0) s_bad = 1;
-            } else {
-                e = static_cast<int>(argmax_key_index(best));
-                w = __shfl(p, e, 64);
-            }
-            if (lane == e && best != 0ull) taken = true;
-            wsel[slot] = w;
-            esel[slot] = e;
-        }
-        if (lane == 0) {
-            if (norm_topk) {
-                float s = 0.0f;
-                for (int j = 0; j < K; ++j) s += wsel[j];
-                const float denom = s + 1e-20f;
-                for (int j = 0; j < K; ++j) wsel[j] = wsel[j] / denom;
-            }
-            for (int j = 0; j < K; ++j) {
-                const float w = wsel[j] * routed_scale;
-                s_idx[t * K + j] = esel[j];
-                s_w[t * K + j] = w;
-                if (idx_out) idx_out[t * K + j] = static_cast<uint32_t>(esel[j]);
-                if (gates_out) gates_out[t * K + j] = w;
+
+    // 1. logits: 16 threads per expert; thread (e, l) covers float4 chunks
+    //    c = l + 16 i of the router row, NI loads in flight per batch.
+    {
+        const int e = threadIdx.x >> 4;
+        const int l = threadIdx.x & 15;
+        double acc = 0.0;
+        if (e < E) {
+            const float4* gr = reinterpret_cast<const float4*>(G + static_cast<size_t>(e) * H);
+#pragma unroll 1
+            for (int c0 = l; c0 < H4; c0 += 16 * NI) {
+                float4 g[NI];
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const int c = c0 + 16 * i;
+                    g[i] = c < H4 ? gr[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const int c = c0 + 16 * i;
+                    const float4 xv = c < H4 ? s_x[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    acc = fma(static_cast<double>(xv.x), static_cast<double>(g[i].x), acc);
+                    acc = fma(static_cast<double>(xv.y), static_cast<double>(g[i].y), acc);
+                    acc = fma(static_cast<double>(xv.z), static_cast<double>(g[i].z), acc);
+                    acc = fma(static_cast<double>(xv.w), static_cast<double>(g[i].w), acc);
+                }
             }
         }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
+        if (l == 0 && e < E) s_logit[e] = static_cast<float>(acc);
     }
+
+    // 2. quantize_row_i8 of the token row
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < H; i += kRouteThreads) amax = fmaxf(amax, fabsf(xr[i]));
+    amax = wave_max_f(amax);
+    if (lane == 0) s_red[wave] = amax;
     __syncthreads();
-    // counting sort: thread e lists its pairs in token order
-    if (threadIdx.x < E) {
-        const int e = threadIdx.x;
-        int c = 0;
-        for (int i = 0; i < T * K; ++i) c += (s_idx[i] == e);
-        s_cnt[e] = c;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int off = 0, na = 0;
+    amax = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRouteWaves; ++w) amax = fmaxf(amax, s_red[w]);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+    for (int i = threadIdx.x; i < H; i += kRouteThreads)
+        xq[static_cast<size_t>(t) * H + i] = quant_i8(xr[i], inv, false);
+    if (threadIdx.x == 0) xs[t] = a_scale;
+
+    // 3. softmax in f64 over the f32 logits: max, exp, then a sequential sum
+    //    in expert order; each probability rounded to f32.
+    const bool valid = wave == 0 && lane < E;
+    double ex = 0.0;
+    if (valid) {
+        double mx = -INFINITY;
         for (int e = 0; e < E; ++e) {
-            s_base[e] = off;
-            if (s_cnt[e] > 0) {
-                tb->active_e[na] = e;
-                tb->offsets[na] = off;
-                ++na;
-            }
-            off += s_cnt[e];
+            const double v = static_cast<double>(s_logit[e]);
+            mx = v > mx ? v : mx;
         }
-        tb->offsets[na] = off;
-        tb->n_active = na;
-        tb->sh_n_active = 1;
-        tb->sh_active_e[0] = 0;
-        tb->sh_offsets[0] = 0;
-        tb->sh_offsets[1] = T;
-        if (flag) *flag = s_bad;
+        ex = exp(static_cast<double>(s_logit[lane]) - mx);
+        s_ex[lane] = ex;
     }
     __syncthreads();
-    if (threadIdx.x < E) {
-        const int e = threadIdx.x;
-        int p = s_base[e];
-        for (int i = 0; i < T * K; ++i) {
-            if (s_idx[i] == e) {
-                tb->pair_tok[p] = i / K;
-                tb->pair_gate[p] = s_w[i];
-                tb->tok_pair[i] = p;
-                ++p;
-            }
+    float p = 0.0f;
+    if (valid) {
+        double sum = 0.0;
+        for (int e = 0; e < E; ++e) sum += s_ex[e];
+        p = static_cast<float>(ex / sum);
+        s_p[lane] = p;
+        if (probs_out) probs_out[static_cast<size_t>(t) * E + lane] = p;
+    }
+    __syncthreads();
+    // 4. greedy top-k == rank by (prob desc, index asc) among non-NaN probs
+    int n_valid = 0;
+    if (valid) {
+        int rank = 0;
+        for (int e = 0; e < E; ++e) {
+            const float q = s_p[e];
+            if (q != q) continue;
+            ++n_valid;
+            rank += (q > p || (q == p && e < lane)) ? 1 : 0;
+        }
+        if (p == p && rank < K) {
+            s_sel_e[rank] = lane;
+            s_sel_w[rank] = p;
         }
     }
-    for (int t = threadIdx.x; t < T; t += kThreads) {
-        tb->sh_pair_tok[t] = t;
-        tb->sh_pair_gate[t] = 1.0f;
+    __syncthreads();
+    // 5. renormalise (sequential f32 sum in slot order) and scale
+    __shared__ float s_denom;
+    __shared__ int s_bad;
+    if (threadIdx.x == 0) {
+        const bool bad = n_valid < K;
+        s_bad = bad ? 1 : 0;
+        flag[t] = bad ? 1 : 0;
+        float s = 0.0f;
+        for (int j = 0; j < K; ++j) s += bad ? 0.0f : s_sel_w[j];
+        s_denom = s + 1e-20f;
+    }
+    __syncthreads();
+    // 6. publish: one thread per slot (the plan's device atomics run in
+    //    parallel rather than as a serial chain of round trips)
+    if (threadIdx.x < K) {
+        const int j = threadIdx.x;
+        const bool bad = s_bad != 0;
+        const int e = bad ? 0 : s_sel_e[j];
+        float w = bad ? 0.0f : s_sel_w[j];
+        if (norm_topk) w = w / s_denom;
+        idx_out[t * K + j] = static_cast<uint32_t>(e);
+        gates_out[t * K + j] = w * routed_scale;
+        if (plan) {
+            const int pos = atomicAdd(&plan->cnt[e], 1);
+            if (pos < kMaxT) plan->list[e][pos] = t * K + j;
+        }
     }
 }
 
-// ---- gate/up: act[p][r] = silu(g) * u --------------------------------------
-// Block = (active expert a, row block). 16 lanes per row; each lane holds its
-// gate-row and up-row chunks in registers and reuses them for every pair.
-template <int JB>
-__global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
-    const RouteTables* __restrict__ tb, int shared_mode, const int8_t* __restrict__ xq,
+// Expert of this block: routed mode takes the a-th expert with pairs (one
+// 64-lane load of the plan's counts per wave, then a ballot); shared mode is
+// one expert whose pairs are the tokens.
+struct BlockExpert {
+    int e, P;
+};
+
+__device__ __forceinline__ BlockExpert block_expert(const MoePlan* __restrict__ plan, int E, int shared_T) {
+    if (shared_T > 0) return {0, shared_T};
+    const int lane = threadIdx.x & 63;
+    const int c = lane < E ? plan->cnt[lane] : 0;
+    const unsigned long long mask = __ballot(c > 0);
+    const int e = nth_set_bit(mask, blockIdx.x);
+    if (e < 0) return {-1, 0};
+    return {e, min(__shfl(c, e, 64), kMaxT)};
+}
+
+// Stage the token rows a block needs into LDS: every token row when T fits
+// (no dependence on the plan, so these loads start immediately), else the
+// rows of the block's pairs [pb, pb + n).
+__device__ __forceinline__ void stage_rows(int4* lds, const int8_t* __restrict__ xq, int H, int C, int nrows,
+                                          const int* rows) {
+    for (int i = threadIdx.x; i < nrows * C; i += 256) {
+        const int pp = i / C, c = i - pp * C;
+        const int tok = rows ? rows[pp] : pp;
+        lds[i] = reinterpret_cast<const int4*>(xq + static_cast<size_t>(tok) * H)[c];
+    }
+}
+
+constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
+
+// ---- gate/up ------------------------------------------------------------------
+// Block = 256 threads = (256 / LPR) row groups; each group owns 2 rows, so a
+// block covers 2 * 256 / LPR rows with 4 * JC 16-byte loads in flight per lane.
+template <int LPR, int JC>
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(
+    const MoePlan* __restrict__ plan, int T, int K, int E, const int8_t* __restrict__ xq,
     const float* __restrict__ xs, const int8_t* __restrict__ wg, const float* __restrict__ sg,
-    const int8_t* __restrict__ wu, const float* __restrict__ su, float* __restrict__ act, int H,
-    int I, int rows_per_block) {
-    extern __shared__ int4 lds_x[];  // [kPairStage][H/16]
-    const TableView tv = view(tb, shared_mode != 0);
-    const int a = blockIdx.x;
-    if (a >= *tv.n_active) return;
-    const int e = tv.active_e[a];
-    const int p0 = tv.offsets[a];
-    const int P = tv.offsets[a + 1] - p0;
-    const int group = threadIdx.x >> 4;
-    const int lane = threadIdx.x & 15;
+    const int8_t* __restrict__ wu, const float* __restrict__ su, float* __restrict__ act, int H, int I,
+    int shared_T) {
+    extern __shared__ int4 lds_x[];  // [rows staged][H/16]
+    __shared__ int s_pid[kMaxT];
+    __shared__ int s_tok[kMaxT];
+    __shared__ float s_xs[kMaxT];
+    constexpr int G = 256 / LPR;  // row groups per block
+    const int grp = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
     const int C = H >> 4;
-    const int r_begin = blockIdx.y * rows_per_block;
-    const int r_end = min(r_begin + rows_per_block, I);
-    const int8_t* wg_e = wg + static_cast<size_t>(e) * I * H;
-    const int8_t* wu_e = wu + static_cast<size_t>(e) * I * H;
+    const bool all_tok = T <= kAllTok;
+    if (all_tok) stage_rows(lds_x, xq, H, C, T, nullptr);
+    if (threadIdx.x < T) s_xs[threadIdx.x] = xs[threadIdx.x];
+    const BlockExpert be = block_expert(plan, E, shared_T);
+    if (be.e < 0 || be.P == 0) return;
+    const int e = be.e, P = be.P;
+    int r[2];
+    bool live[2];
+    int4 wgv[2][JC], wuv[2][JC];
+    float sgr[2], sur[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        r[q] = blockIdx.y * 2 * G + q * G + grp;
+        live[q] = r[q] < I;
+        const size_t row = static_cast<size_t>(e) * I + (live[q] ? r[q] : 0);
+        const int4* grow = reinterpret_cast<const int4*>(wg + row * H);
+        const int4* urow = reinterpret_cast<const int4*>(wu + row * H);
+#pragma unroll
+        for (int j = 0; j < JC; ++j) {
+            const int c = lane + LPR * j;
+            wgv[q][j] = (live[q] && c < C) ? ld_stream(grow + c) : make_int4(0, 0, 0, 0);
+            wuv[q][j] = (live[q] && c < C) ? ld_stream(urow + c) : make_int4(0, 0, 0, 0);
+        }
+        sgr[q] = live[q] ? sg[row] : 0.0f;
+        sur[q] = live[q] ? su[row] : 0.0f;
+    }
+    if (threadIdx.x < P) {
+        const int pid = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
+        s_pid[threadIdx.x] = pid;
+        s_tok[threadIdx.x] = shared_T > 0 ? pid : pid / K;
+    }
+    __syncthreads();
 
     for (int pb = 0; pb < P; pb += kPairStage) {
         const int pc_n = min(kPairStage, P - pb);
-        __syncthreads();
-        for (int i = threadIdx.x; i < pc_n * C; i += kThreads) {
-            const int pp = i / C, c = i - pp * C;
-            const int tok = tv.pair_tok[p0 + pb + pp];
-            lds_x[i] = reinterpret_cast<const int4*>(xq + static_cast<size_t>(tok) * H)[c];
+        if (!all_tok) {
+            __syncthreads();
+            stage_rows(lds_x, xq, H, C, pc_n, s_tok + pb);
+            __syncthreads();
         }
-        __syncthreads();
-        for (int r0 = r_begin; r0 < r_end; r0 += kGroups) {
-            const int r = r0 + group;
-            const bool live = r < r_end;
-            int4 wgv[JB], wuv[JB];
-            const int4* grow = reinterpret_cast<const int4*>(wg_e + static_cast<size_t>(live ? r : r_begin) * H);
-            const int4* urow = reinterpret_cast<const int4*>(wu_e + static_cast<size_t>(live ? r : r_begin) * H);
+        for (int q0 = 0; q0 < pc_n; q0 += kPC) {
+            int ga[2][kPC], ua[2][kPC];
 #pragma unroll
-            for (int j = 0; j < JB; ++j) {
-                const int c = lane + 16 * j;
-                wgv[j] = (live && c < C) ? grow[c] : make_int4(0, 0, 0, 0);
-                wuv[j] = (live && c < C) ? urow[c] : make_int4(0, 0, 0, 0);
-            }
-            const float sgr = live ? sg[static_cast<size_t>(e) * I + r] : 0.0f;
-            const float sur = live ? su[static_cast<size_t>(e) * I + r] : 0.0f;
-            for (int q0 = 0; q0 < pc_n; q0 += kPC) {
-                int ga[kPC], ua[kPC];
+            for (int i = 0; i < kPC; ++i) ga[0][i] = ga[1][i] = ua[0][i] = ua[1][i] = 0;
 #pragma unroll
-                for (int i = 0; i < kPC; ++i) ga[i] = ua[i] = 0;
+            for (int j = 0; j < JC; ++j) {
+                const int c = lane + LPR * j;
+                if (c < C) {
 #pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    const int c = lane + 16 * j;
-                    if (c < C) {
-#pragma unroll
-                        for (int i = 0; i < kPC; ++i) {
-                            if (q0 + i < pc_n) {
-                                const int4 xv = lds_x[(q0 + i) * C + c];
-                                ga[i] = dot16_i8(wgv[j], xv, ga[i]);
-                                ua[i] = dot16_i8(wuv[j], xv, ua[i]);
-                            }
+                    for (int i = 0; i < kPC; ++i) {
+                        if (q0 + i < pc_n) {
+                            const int srow = all_tok ? s_tok[pb + q0 + i] : q0 + i;
+                            const int4 xv = lds_x[srow * C + c];
+                            ga[0][i] = dot16_i8(wgv[0][j], xv, ga[0][i]);
+                            ua[0][i] = dot16_i8(wuv[0][j], xv, ua[0][i]);
+                            ga[1][i] = dot16_i8(wgv[1][j], xv, ga[1][i]);
+                            ua[1][i] = dot16_i8(wuv[1][j], xv, ua[1][i]);
                         }
                     }
                 }
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
 #pragma unroll
                 for (int i = 0; i < kPC; ++i) {
-                    const int gv = reduce16_add(ga[i]);
-                    const int uv = reduce16_add(ua[i]);
-                    if (live && lane == i && q0 + i < pc_n) {
-                        const int p = p0 + pb + q0 + i;
-                        const float as = xs[tv.pair_tok[p]];
-                        const float g = (static_cast<float>(gv) * as) * sgr;
-                        const float u = (static_cast<float>(uv) * as) * sur;
-                        act[static_cast<size_t>(p) * I + r] = silu_f(g) * u;
+                    const int gv = reduce_lanes<LPR>(ga[q][i]);
+                    const int uv = reduce_lanes<LPR>(ua[q][i]);
+                    if (live[q] && lane == (i % LPR) && q0 + i < pc_n) {
+                        const int pp = pb + q0 + i;
+                        const float as = s_xs[s_tok[pp]];
+                        const float g = (static_cast<float>(gv) * as) * sgr[q];
+                        const float u = (static_cast<float>(uv) * as) * sur[q];
+                        act[static_cast<size_t>(s_pid[pp]) * I + r[q]] = silu_f(g) * u;
                     }
                 }
             }
@@ -291,36 +327,51 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     }
 }
 
-// ---- down: ybuf[p][r] = dequant(Wd[e][r] . q(act[p])) * gate[p] ------------
-template <int JB>
-__global__ __launch_bounds__(kThreads) void moe_down_kernel(
-    const RouteTables* __restrict__ tb, int shared_mode, const float* __restrict__ act,
-    const int8_t* __restrict__ wd, const float* __restrict__ sd, float* __restrict__ ybuf, int H,
-    int I, int rows_per_block) {
+// ---- down ----------------------------------------------------------------------
+template <int LPR, int JC>
+__global__ __launch_bounds__(256) void moe_down_kernel(
+    const MoePlan* __restrict__ plan, int E, const float* __restrict__ gates, const float* __restrict__ act,
+    const int8_t* __restrict__ wd, const float* __restrict__ sd, float* __restrict__ ybuf, int H, int I,
+    int shared_T) {
     extern __shared__ int4 lds_a[];  // [kPairStage][I/16]
     __shared__ float lds_as[kPairStage];
-    const TableView tv = view(tb, shared_mode != 0);
-    const int a = blockIdx.x;
-    if (a >= *tv.n_active) return;
-    const int e = tv.active_e[a];
-    const int p0 = tv.offsets[a];
-    const int P = tv.offsets[a + 1] - p0;
-    const int group = threadIdx.x >> 4;
-    const int lane = threadIdx.x & 15;
+    __shared__ int s_pid[kMaxT];
+    constexpr int G = 256 / LPR;
+    const BlockExpert be = block_expert(plan, E, shared_T);
+    if (be.e < 0 || be.P == 0) return;
+    const int e = be.e, P = be.P;
+    const int grp = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
     const int wave = threadIdx.x >> 6;
     const int wl = threadIdx.x & 63;
     const int C = I >> 4;
-    const int r_begin = blockIdx.y * rows_per_block;
-    const int r_end = min(r_begin + rows_per_block, H);
-    const int8_t* wd_e = wd + static_cast<size_t>(e) * H * I;
+    int r[2];
+    bool live[2];
+    int4 wv[2][JC];
+    float sdr[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        r[q] = blockIdx.y * 2 * G + q * G + grp;
+        live[q] = r[q] < H;
+        const size_t row = static_cast<size_t>(e) * H + (live[q] ? r[q] : 0);
+        const int4* drow = reinterpret_cast<const int4*>(wd + row * I);
+#pragma unroll
+        for (int j = 0; j < JC; ++j) {
+            const int c = lane + LPR * j;
+            wv[q][j] = (live[q] && c < C) ? ld_stream(drow + c) : make_int4(0, 0, 0, 0);
+        }
+        sdr[q] = live[q] ? sd[row] : 0.0f;
+    }
+    if (threadIdx.x < P) s_pid[threadIdx.x] = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
+    __syncthreads();
     int8_t* lds_b = reinterpret_cast<int8_t*>(lds_a);
 
     for (int pb = 0; pb < P; pb += kPairStage) {
         const int pc_n = min(kPairStage, P - pb);
-        __syncthreads();
+        if (pb) __syncthreads();
         // quantize_row_i8 of each pair's act row: one wave per pair
-        for (int pp = wave; pp < pc_n; pp += kThreads / 64) {
-            const float* ar = act + static_cast<size_t>(p0 + pb + pp) * I;
+        for (int pp = wave; pp < pc_n; pp += 4) {
+            const float* ar = act + static_cast<size_t>(s_pid[pb + pp]) * I;
             float amax = 0.0f;
             for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
             amax = wave_max_f(amax);
@@ -330,37 +381,34 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(
             if (wl == 0) lds_as[pp] = a_scale;
         }
         __syncthreads();
-        for (int r0 = r_begin; r0 < r_end; r0 += kGroups) {
-            const int r = r0 + group;
-            const bool live = r < r_end;
-            int4 wv[JB];
-            const int4* drow = reinterpret_cast<const int4*>(wd_e + static_cast<size_t>(live ? r : r_begin) * I);
+        for (int q0 = 0; q0 < pc_n; q0 += kPC) {
+            int da[2][kPC];
 #pragma unroll
-            for (int j = 0; j < JB; ++j) {
-                const int c = lane + 16 * j;
-                wv[j] = (live && c < C) ? drow[c] : make_int4(0, 0, 0, 0);
-            }
-            const float sdr = live ? sd[static_cast<size_t>(e) * H + r] : 0.0f;
-            for (int q0 = 0; q0 < pc_n; q0 += kPC) {
-                int da[kPC];
+            for (int i = 0; i < kPC; ++i) da[0][i] = da[1][i] = 0;
 #pragma unroll
-                for (int i = 0; i < kPC; ++i) da[i] = 0;
+            for (int j = 0; j < JC; ++j) {
+                const int c = lane + LPR * j;
+                if (c < C) {
 #pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    const int c = lane + 16 * j;
-                    if (c < C) {
-#pragma unroll
-                        for (int i = 0; i < kPC; ++i)
-                            if (q0 + i < pc_n) da[i] = dot16_i8(wv[j], lds_a[(q0 + i) * C + c], da[i]);
+                    for (int i = 0; i < kPC; ++i) {
+                        if (q0 + i < pc_n) {
+                            const int4 av = lds_a[(q0 + i) * C + c];
+                            da[0][i] = dot16_i8(wv[0][j], av, da[0][i]);
+                            da[1][i] = dot16_i8(wv[1][j], av, da[1][i]);
+                        }
                     }
                 }
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
 #pragma unroll
                 for (int i = 0; i < kPC; ++i) {
-                    const int dv = reduce16_add(da[i]);
-                    if (live && lane == i && q0 + i < pc_n) {
-                        const int p = p0 + pb + q0 + i;
-                        const float yv = (static_cast<float>(dv) * lds_as[q0 + i]) * sdr;
-                        ybuf[static_cast<size_t>(p) * H + r] = yv * tv.pair_gate[p];
+                    const int dv = reduce_lanes<LPR>(da[q][i]);
+                    if (live[q] && lane == (i % LPR) && q0 + i < pc_n) {
+                        const int pid = s_pid[pb + q0 + i];
+                        const float yv = (static_cast<float>(dv) * lds_as[q0 + i]) * sdr[q];
+                        const float gate = shared_T > 0 ? 1.0f : gates[pid];
+                        ybuf[static_cast<size_t>(pid) * H + r[q]] = yv * gate;
                     }
                 }
             }
@@ -368,78 +416,137 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(
     }
 }
 
-// ---- combine (slot order) ---------------------------------------------------
-__global__ __launch_bounds__(kThreads) void moe_combine_kernel(const RouteTables* __restrict__ tb,
-                                                               const float* __restrict__ ybuf,
-                                                               const float* __restrict__ shared_y,
-                                                               float* __restrict__ out, int H,
-                                                               int K) {
+// ---- combine (slot order) ---------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf,
+                                                          const float* __restrict__ shared_y,
+                                                          float* __restrict__ out, int H, int K,
+                                                          MoePlan* __restrict__ plan, int E) {
     const int t = blockIdx.y;
-    const int c = blockIdx.x * kThreads + threadIdx.x;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (plan && blockIdx.x == 0 && blockIdx.y == 0) {
+        // every reader of the plan (gate_up, down) finished before this launch
+        if (threadIdx.x < E) plan->cnt[threadIdx.x] = 0;
+        if (threadIdx.x == 0) plan->mask = 0ull;
+    }
     if (c >= H) return;
+    float v[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) v[j] = j < K ? ybuf[(static_cast<size_t>(t) * K + j) * H + c] : 0.0f;
+    const float sh = shared_y ? shared_y[static_cast<size_t>(t) * H + c] : 0.0f;
     float o = 0.0f;
-    for (int j = 0; j < K; ++j) o += ybuf[static_cast<size_t>(tb->tok_pair[t * K + j]) * H + c];
-    if (shared_y) o += shared_y[static_cast<size_t>(t) * H + c];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+        if (j < K) o += v[j];
+    if (shared_y) o += sh;
     out[static_cast<size_t>(t) * H + c] = o;
 }
 
-constexpr int kGateUpRows = 32;
-constexpr int kDownRows = 64;
+template <int LPR>
+hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan, int T, int K,
+                              int E, const int8_t* xq, const float* xs, const int8_t* wg, const float* sg,
+                              const int8_t* wu, const float* su, float* act, int H, int I, int shared_T) {
+#define FOCR_GU(J)                                                                                              \
+    case J:                                                                                                     \
+        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, plan, T, K, E, xq, xs, wg, sg, \
+                           wu, su, act, H, I, shared_T);                                                        \
+        break;
+    switch (JC) {
+        FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef FOCR_GU
+    return hipGetLastError();
+}
+
+template <int LPR>
+hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan, int E,
+                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf, int H,
+                           int I, int shared_T) {
+#define FOCR_DN(J)                                                                                                \
+    case J:                                                                                                       \
+        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, plan, E, gates, act, wd, sd, ybuf, H, \
+                           I, shared_T);                                                                          \
+        break;
+    switch (JC) {
+        FOCR_DN(1) FOCR_DN(2) FOCR_DN(3) FOCR_DN(4) FOCR_DN(5) FOCR_DN(6) FOCR_DN(7) FOCR_DN(8)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef FOCR_DN
+    return hipGetLastError();
+}
+
+// Lanes per row for a K-byte row: 16 when the 16-byte chunk count is a
+// multiple of 16 or large (K = 1280: 5 per lane), else 8 (K = 896: 7 per lane).
+void pick_lpr(int K, int* lpr, int* jc) {
+    const int C = K / 16;
+    if (C % 16 == 0 || C > 64) {
+        *lpr = 16;
+        *jc = (C + 15) / 16;
+    } else {
+        *lpr = 8;
+        *jc = (C + 7) / 8;
+    }
+}
 
 }  // namespace
 
-size_t moe_route_table_bytes(const MoeDims&) { return sizeof(RouteTables); }
+size_t moe_plan_bytes() { return sizeof(MoePlan); }
 
-hipError_t launch_moe_router(hipStream_t s, const MoeDims& d, const float* hidden,
-                             const float* router, float* logits, int8_t* xq, float* xs) {
-    if (d.t < 1 || d.t > kMaxT || d.n_experts < 1 || d.n_experts > kMaxE) return hipErrorInvalidValue;
-    const int grid = (d.n_experts + 3) / 4;
-    hipLaunchKernelGGL(moe_router_kernel, dim3(grid), dim3(kThreads), 0, s, hidden, router, logits,
-                       xq, xs, d.t, d.hidden, d.n_experts);
+hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
+                            int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
+                            float* probs, int* flag, void* plan) {
+    if (d.t < 1 || d.t > kMaxT || d.n_experts < 1 || d.n_experts > kMaxE || d.top_k < 1 || d.top_k > kMaxK ||
+        d.top_k > d.n_experts || d.hidden % 4 != 0 || d.hidden > 2048)
+        return hipErrorInvalidValue;
+    MoePlan* pl = static_cast<MoePlan*>(plan);
+    hipLaunchKernelGGL((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+                       d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, pl);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_topk(hipStream_t s, const MoeDims& d, const float* logits, int norm_topk,
-                           float routed_scale, uint32_t* idx, float* gates, float* probs,
-                           void* tables, int* flag) {
-    if (d.top_k < 1 || d.top_k > kMaxK || d.top_k > d.n_experts) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(kThreads), 0, s, logits, d.t, d.n_experts,
-                       d.top_k, norm_topk, routed_scale, idx, gates, probs,
-                       static_cast<RouteTables*>(tables), flag);
-    return hipGetLastError();
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan, const int8_t* xq, const float* xs,
+                              const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
+                              int inter, bool shared) {
+    int lpr, jc;
+    pick_lpr(d.hidden, &lpr, &jc);
+    if (d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    const int rows_per_block = 2 * (256 / lpr);
+    const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
+    const dim3 grid(max_active, (inter + rows_per_block - 1) / rows_per_block);
+    const int staged = d.t <= kAllTok ? d.t : kPairStage;
+    const size_t lds = static_cast<size_t>(staged) * d.hidden;
+    const int sh = shared ? d.t : 0;
+    const MoePlan* pl = static_cast<const MoePlan*>(plan);
+    if (lpr == 16)
+        return launch_gate_up_lpr<16>(s, grid, lds, jc, pl, d.t, d.top_k, d.n_experts, xq, xs, wg, sg, wu, su, act,
+                                      d.hidden, inter, sh);
+    return launch_gate_up_lpr<8>(s, grid, lds, jc, pl, d.t, d.top_k, d.n_experts, xq, xs, wg, sg, wu, su, act,
+                                 d.hidden, inter, sh);
 }
 
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* tables,
-                              const int8_t* xq, const float* xs, const int8_t* wg,
-                              const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, int max_active, bool shared) {
-    if (d.hidden % 16 != 0 || d.hidden > 16 * 16 * 8) return hipErrorInvalidValue;
-    const dim3 grid(max_active, (inter + kGateUpRows - 1) / kGateUpRows);
-    const size_t lds = static_cast<size_t>(kPairStage) * d.hidden;
-    hipLaunchKernelGGL(moe_gate_up_kernel<8>, grid, dim3(kThreads), lds, s,
-                       static_cast<const RouteTables*>(tables), shared ? 1 : 0, xq, xs, wg, sg, wu,
-                       su, act, d.hidden, inter, kGateUpRows);
-    return hipGetLastError();
-}
-
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* tables, const float* act,
-                           const int8_t* wd, const float* sd, const float*, float* ybuf, int inter,
-                           int max_active, bool shared) {
-    if (inter % 16 != 0 || inter > 16 * 16 * 8) return hipErrorInvalidValue;
-    const dim3 grid(max_active, (d.hidden + kDownRows - 1) / kDownRows);
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* plan, const float* gates, const float* act,
+                           const int8_t* wd, const float* sd, float* ybuf, int inter, bool shared) {
+    int lpr, jc;
+    pick_lpr(inter, &lpr, &jc);
+    if (inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    const int rows_per_block = 2 * (256 / lpr);
+    const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
+    const dim3 grid(max_active, (d.hidden + rows_per_block - 1) / rows_per_block);
     const size_t lds = static_cast<size_t>(kPairStage) * inter;
-    hipLaunchKernelGGL(moe_down_kernel<8>, grid, dim3(kThreads), lds, s,
-                       static_cast<const RouteTables*>(tables), shared ? 1 : 0, act, wd, sd, ybuf,
-                       d.hidden, inter, kDownRows);
-    return hipGetLastError();
+    const int sh = shared ? d.t : 0;
+    const MoePlan* pl = static_cast<const MoePlan*>(plan);
+    if (lpr == 16)
+        return launch_down_lpr<16>(s, grid, lds, jc, pl, d.n_experts, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
+    return launch_down_lpr<8>(s, grid, lds, jc, pl, d.n_experts, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
 }
 
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const void* tables,
-                              const float* ybuf, const float* shared_y, float* out) {
-    const dim3 grid((d.hidden + kThreads - 1) / kThreads, d.t);
-    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(kThreads), 0, s,
-                       static_cast<const RouteTables*>(tables), ybuf, shared_y, out, d.hidden,
-                       d.top_k);
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out,
+                              void* plan) {
+    const dim3 grid((d.hidden + 255) / 256, d.t);
+    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k,
+                       static_cast<MoePlan*>(plan), d.n_experts);
     return hipGetLastError();
 }
 

@@ -73,23 +73,37 @@ __global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, Rswa
     const float* gk = g.ring_k(s) + static_cast<size_t>(h) * W * D;
     const float* gv = g.ring_v(s) + static_cast<size_t>(h) * W * D;
 
-    // scores: wave w covers keys [w*16, w*16+16), two keys per step
+    // scores: wave w covers keys [w*16, w*16+16), two keys per step; all
+    // eight K-row loads of a lane are in flight before the first dot
+    float4 kv[8];
 #pragma unroll
-    for (int jj = 0; jj < 16; jj += 2) {
-        const int j = wave * 16 + jj + half;
+    for (int i = 0; i < 8; ++i) {
+        const int key = chunk * KC + wave * 16 + 2 * i + half;
+        const float* kr = key < P ? rk + static_cast<size_t>(key) * D : gk + static_cast<size_t>(key - P) * D;
+        kv[i] = key < N ? reinterpret_cast<const float4*>(kr)[dl] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int j = wave * 16 + 2 * i + half;
         const int key = chunk * KC + j;
-        float d = 0.0f;
-        if (key < N) {
-            const float* kr = key < P ? rk + static_cast<size_t>(key) * D : gk + static_cast<size_t>(key - P) * D;
-            const float4 kv = reinterpret_cast<const float4*>(kr)[dl];
-            d = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
-        }
+        float d = qv.x * kv[i].x + qv.y * kv[i].y + qv.z * kv[i].z + qv.w * kv[i].w;
         d += __shfl_xor(d, 16, 32);
         d += __shfl_xor(d, 8, 32);
         d += __shfl_xor(d, 4, 32);
         d += __shfl_xor(d, 2, 32);
         d += __shfl_xor(d, 1, 32);
         if (dl == 0) sc[j] = key < N ? d * scale : -INFINITY;
+    }
+    // p . V: 8 key groups x 32 lanes (float4 of the head dim each); the V
+    // loads do not depend on the softmax, so issue them before the barrier
+    const int grp = threadIdx.x >> 5;
+    const int dq = threadIdx.x & 31;
+    float4 vv[KC / 8];
+#pragma unroll
+    for (int i = 0; i < KC / 8; ++i) {
+        const int key = chunk * KC + grp + 8 * i;
+        const float* vr = key < P ? rv + static_cast<size_t>(key) * D : gv + static_cast<size_t>(key - P) * D;
+        vv[i] = key < N ? reinterpret_cast<const float4*>(vr)[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     __syncthreads();
     if (wave == 0) {
@@ -106,20 +120,14 @@ __global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, Rswa
         }
     }
     __syncthreads();
-    // p . V: 8 key groups x 32 lanes (float4 of the head dim each)
-    const int grp = threadIdx.x >> 5;
-    const int dq = threadIdx.x & 31;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int j = grp; j < KC; j += 8) {
-        const int key = chunk * KC + j;
-        if (key >= N) break;
-        const float* vr = key < P ? rv + static_cast<size_t>(key) * D : gv + static_cast<size_t>(key - P) * D;
-        const float4 vv = reinterpret_cast<const float4*>(vr)[dq];
-        const float p = sc[j];
-        acc.x += p * vv.x;
-        acc.y += p * vv.y;
-        acc.z += p * vv.z;
-        acc.w += p * vv.w;
+#pragma unroll
+    for (int i = 0; i < KC / 8; ++i) {
+        const float p = sc[grp + 8 * i];
+        acc.x += p * vv[i].x;
+        acc.y += p * vv[i].y;
+        acc.z += p * vv[i].z;
+        acc.w += p * vv[i].w;
     }
     accs[grp][dq] = acc;
     __syncthreads();
@@ -140,20 +148,53 @@ __global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, Rswa
     }
 }
 
+// Log-sum-exp merge of a (stream, head)'s chunk partials: M = max m_c,
+// f_c = exp(m_c - M) computed once per chunk, then every head-dim lane sums
+// independent loads acc_c[d] * f_c.
 __global__ __launch_bounds__(D) void rswa_merge_kernel(RswaStepArgs a, const float* __restrict__ partials,
                                                        int max_chunks, float* __restrict__ out) {
+    __shared__ float s_f[1024];
+    __shared__ float s_red[D / 64][2];
     const int h = blockIdx.x;
     const int si = blockIdx.y;
     const int N = static_cast<int>(a.prefill_len[si] + a.ring_len[si]);
     const int nch = (N + KC - 1) / KC;
     const float* base = partials + (static_cast<size_t>(si) * H + h) * max_chunks * kPart;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, base[c * kPart]);
-    float L = 0.0f, acc = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-        const float f = expf(base[c * kPart] - M);
-        L += base[c * kPart + 1] * f;
-        acc += base[c * kPart + 2 + threadIdx.x] * f;
+    float m = -INFINITY;
+    for (int c = threadIdx.x; c < nch; c += D) m = fmaxf(m, base[c * kPart]);
+    m = wave_max_f(m);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6][0] = m;
+    __syncthreads();
+    const float M = fmaxf(s_red[0][0], s_red[1][0]);
+    float acc = 0.0f, L = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 1024) {
+        const int cn = min(1024, nch - c0);
+        __syncthreads();
+        for (int c = threadIdx.x; c < cn; c += D) s_f[c] = expf(base[(c0 + c) * kPart] - M);
+        __syncthreads();
+        int c = 0;
+        for (; c + 4 <= cn; c += 4) {
+            const float a0 = base[(c0 + c) * kPart + 2 + threadIdx.x];
+            const float a1 = base[(c0 + c + 1) * kPart + 2 + threadIdx.x];
+            const float a2 = base[(c0 + c + 2) * kPart + 2 + threadIdx.x];
+            const float a3 = base[(c0 + c + 3) * kPart + 2 + threadIdx.x];
+            const float l0 = base[(c0 + c) * kPart + 1];
+            const float l1 = base[(c0 + c + 1) * kPart + 1];
+            const float l2 = base[(c0 + c + 2) * kPart + 1];
+            const float l3 = base[(c0 + c + 3) * kPart + 1];
+            acc += a0 * s_f[c];
+            acc += a1 * s_f[c + 1];
+            acc += a2 * s_f[c + 2];
+            acc += a3 * s_f[c + 3];
+            L += l0 * s_f[c];
+            L += l1 * s_f[c + 1];
+            L += l2 * s_f[c + 2];
+            L += l3 * s_f[c + 3];
+        }
+        for (; c < cn; ++c) {
+            acc += base[(c0 + c) * kPart + 2 + threadIdx.x] * s_f[c];
+            L += base[(c0 + c) * kPart + 1] * s_f[c];
+        }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     out[(static_cast<size_t>(si) * H + h) * D + threadIdx.x] = acc * inv;
