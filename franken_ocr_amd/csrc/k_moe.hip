@@ -9,8 +9,9 @@
 //            (token, slot) pair to its expert's list in the step plan (an
 //            active-expert bitmask plus per-expert pair lists, built with
 //            device atomics; the next kernel launch orders the reads).
-//   gate_up  grid (active expert, row block): issues the expert's gate and
-//            up row loads first, stages the routed tokens' int8 rows in LDS
+//   gate_up  grid (active expert, row block): finds its expert with one
+//            scalar load of the plan's active mask, issues the expert's gate
+//            and up row loads, stages the routed tokens' int8 rows in LDS
 //            meanwhile, and writes act[t*K + j][r] = silu(g) * u
 //            (decoder.rs:1746-1752).
 //   down     grid (active expert, row block): issues the down row loads,
@@ -26,7 +27,9 @@
 // expert's list depends on block timing, but every pair's result is computed
 // independently and stored at its own (token, slot) slot, so outputs are
 // bit-reproducible run to run. GEMV rows use LPR lanes per row (16 for K =
-// 1280 -> 5 chunks of 16 B per lane; 8 for K = 896 -> 7 chunks).
+// 1280 -> 5 chunks of 16 B per lane; 8 for K = 896 -> 7 chunks) and one row
+// per lane group: with few pairs per expert the kernels are latency-bound,
+// and the smaller register footprint buys the occupancy that hides it.
 #include "focr_internal.hpp"
 #include "k_common.hpp"
 
@@ -37,10 +40,9 @@ constexpr int kMaxT = 64;
 constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
 constexpr int kPairStage = 32;  // pairs staged in LDS per pass
-constexpr int kPC = 8;          // pairs accumulated in registers per pass
 
 struct MoePlan {
-    unsigned long long mask;   // bit e: expert e has pairs this step (diagnostic)
+    unsigned long long mask;   // bit e: expert e has pairs this step
     int cnt[kMaxE];            // pairs per expert
     int list[kMaxE][kMaxT];    // pair ids t*K + j, per expert
 };
@@ -193,27 +195,23 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         idx_out[t * K + j] = static_cast<uint32_t>(e);
         gates_out[t * K + j] = w * routed_scale;
         if (plan) {
+            atomicOr(&plan->mask, 1ull << e);
             const int pos = atomicAdd(&plan->cnt[e], 1);
             if (pos < kMaxT) plan->list[e][pos] = t * K + j;
         }
     }
 }
 
-// Expert of this block: routed mode takes the a-th expert with pairs (one
-// 64-lane load of the plan's counts per wave, then a ballot); shared mode is
-// one expert whose pairs are the tokens.
-struct BlockExpert {
-    int e, P;
-};
+// Expert of this block: routed mode takes the a-th set bit of the plan's
+// active mask (one scalar load, so the weight loads can issue right after);
+// shared mode is one expert whose pairs are the tokens.
+__device__ __forceinline__ int block_expert(const MoePlan* __restrict__ plan, int shared_T) {
+    if (shared_T > 0) return 0;
+    return nth_set_bit(plan->mask, blockIdx.x);
+}
 
-__device__ __forceinline__ BlockExpert block_expert(const MoePlan* __restrict__ plan, int E, int shared_T) {
-    if (shared_T > 0) return {0, shared_T};
-    const int lane = threadIdx.x & 63;
-    const int c = lane < E ? plan->cnt[lane] : 0;
-    const unsigned long long mask = __ballot(c > 0);
-    const int e = nth_set_bit(mask, blockIdx.x);
-    if (e < 0) return {-1, 0};
-    return {e, min(__shfl(c, e, 64), kMaxT)};
+__device__ __forceinline__ int block_pairs(const MoePlan* __restrict__ plan, int e, int shared_T) {
+    return shared_T > 0 ? shared_T : min(plan->cnt[e], kMaxT);
 }
 
 // Stage the token rows a block needs into LDS: every token row when T fits
@@ -231,11 +229,12 @@ __device__ __forceinline__ void stage_rows(int4* lds, const int8_t* __restrict__
 constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
 
 // ---- gate/up ------------------------------------------------------------------
-// Block = 256 threads = (256 / LPR) row groups; each group owns 2 rows, so a
-// block covers 2 * 256 / LPR rows with 4 * JC 16-byte loads in flight per lane.
+// Block = 256 threads = (256 / LPR) row groups, one weight row per group held
+// in registers (2 * JC 16-byte loads in flight per lane); the block's routed
+// pairs are then taken one at a time against the staged token rows.
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(
-    const MoePlan* __restrict__ plan, int T, int K, int E, const int8_t* __restrict__ xq,
+    const MoePlan* __restrict__ plan, int T, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ xs, const int8_t* __restrict__ wg, const float* __restrict__ sg,
     const int8_t* __restrict__ wu, const float* __restrict__ su, float* __restrict__ act, int H, int I,
     int shared_T) {
@@ -243,36 +242,32 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     __shared__ int s_pid[kMaxT];
     __shared__ int s_tok[kMaxT];
     __shared__ float s_xs[kMaxT];
-    constexpr int G = 256 / LPR;  // row groups per block
+    constexpr int G = 256 / LPR;  // rows per block
+    const int e = block_expert(plan, shared_T);
+    if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int C = H >> 4;
-    const bool all_tok = T <= kAllTok;
-    if (all_tok) stage_rows(lds_x, xq, H, C, T, nullptr);
-    if (threadIdx.x < T) s_xs[threadIdx.x] = xs[threadIdx.x];
-    const BlockExpert be = block_expert(plan, E, shared_T);
-    if (be.e < 0 || be.P == 0) return;
-    const int e = be.e, P = be.P;
-    int r[2];
-    bool live[2];
-    int4 wgv[2][JC], wuv[2][JC];
-    float sgr[2], sur[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        r[q] = blockIdx.y * 2 * G + q * G + grp;
-        live[q] = r[q] < I;
-        const size_t row = static_cast<size_t>(e) * I + (live[q] ? r[q] : 0);
+    const int r = blockIdx.y * G + grp;
+    const bool live = r < I;
+    const size_t row = static_cast<size_t>(e) * I + (live ? r : 0);
+    int4 wgv[JC], wuv[JC];
+    {
         const int4* grow = reinterpret_cast<const int4*>(wg + row * H);
         const int4* urow = reinterpret_cast<const int4*>(wu + row * H);
 #pragma unroll
         for (int j = 0; j < JC; ++j) {
             const int c = lane + LPR * j;
-            wgv[q][j] = (live[q] && c < C) ? ld_stream(grow + c) : make_int4(0, 0, 0, 0);
-            wuv[q][j] = (live[q] && c < C) ? ld_stream(urow + c) : make_int4(0, 0, 0, 0);
+            wgv[j] = (live && c < C) ? ld_stream(grow + c) : make_int4(0, 0, 0, 0);
+            wuv[j] = (live && c < C) ? ld_stream(urow + c) : make_int4(0, 0, 0, 0);
         }
-        sgr[q] = live[q] ? sg[row] : 0.0f;
-        sur[q] = live[q] ? su[row] : 0.0f;
     }
+    const float sgr = live ? sg[row] : 0.0f;
+    const float sur = live ? su[row] : 0.0f;
+    const bool all_tok = T <= kAllTok;
+    if (all_tok) stage_rows(lds_x, xq, H, C, T, nullptr);
+    if (threadIdx.x < T) s_xs[threadIdx.x] = xs[threadIdx.x];
+    const int P = block_pairs(plan, e, shared_T);
     if (threadIdx.x < P) {
         const int pid = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
         s_pid[threadIdx.x] = pid;
@@ -283,85 +278,68 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     for (int pb = 0; pb < P; pb += kPairStage) {
         const int pc_n = min(kPairStage, P - pb);
         if (!all_tok) {
-            __syncthreads();
+            if (pb) __syncthreads();
             stage_rows(lds_x, xq, H, C, pc_n, s_tok + pb);
             __syncthreads();
         }
-        for (int q0 = 0; q0 < pc_n; q0 += kPC) {
-            int ga[2][kPC], ua[2][kPC];
-#pragma unroll
-            for (int i = 0; i < kPC; ++i) ga[0][i] = ga[1][i] = ua[0][i] = ua[1][i] = 0;
+        for (int i = 0; i < pc_n; ++i) {
+            const int pp = pb + i;
+            const int srow = all_tok ? s_tok[pp] : i;
+            int ga = 0, ua = 0;
 #pragma unroll
             for (int j = 0; j < JC; ++j) {
                 const int c = lane + LPR * j;
                 if (c < C) {
-#pragma unroll
-                    for (int i = 0; i < kPC; ++i) {
-                        if (q0 + i < pc_n) {
-                            const int srow = all_tok ? s_tok[pb + q0 + i] : q0 + i;
-                            const int4 xv = lds_x[srow * C + c];
-                            ga[0][i] = dot16_i8(wgv[0][j], xv, ga[0][i]);
-                            ua[0][i] = dot16_i8(wuv[0][j], xv, ua[0][i]);
-                            ga[1][i] = dot16_i8(wgv[1][j], xv, ga[1][i]);
-                            ua[1][i] = dot16_i8(wuv[1][j], xv, ua[1][i]);
-                        }
-                    }
+                    const int4 xv = lds_x[srow * C + c];
+                    ga = dot16_i8(wgv[j], xv, ga);
+                    ua = dot16_i8(wuv[j], xv, ua);
                 }
             }
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-#pragma unroll
-                for (int i = 0; i < kPC; ++i) {
-                    const int gv = reduce_lanes<LPR>(ga[q][i]);
-                    const int uv = reduce_lanes<LPR>(ua[q][i]);
-                    if (live[q] && lane == (i % LPR) && q0 + i < pc_n) {
-                        const int pp = pb + q0 + i;
-                        const float as = s_xs[s_tok[pp]];
-                        const float g = (static_cast<float>(gv) * as) * sgr[q];
-                        const float u = (static_cast<float>(uv) * as) * sur[q];
-                        act[static_cast<size_t>(s_pid[pp]) * I + r[q]] = silu_f(g) * u;
-                    }
-                }
+            ga = reduce_lanes<LPR>(ga);
+            ua = reduce_lanes<LPR>(ua);
+            if (live && lane == 0) {
+                const float as = s_xs[s_tok[pp]];
+                const float g = (static_cast<float>(ga) * as) * sgr;
+                const float u = (static_cast<float>(ua) * as) * sur;
+                act[static_cast<size_t>(s_pid[pp]) * I + r] = silu_f(g) * u;
             }
         }
     }
 }
 
 // ---- down ----------------------------------------------------------------------
+constexpr int NQ = 16;  // act values per lane held in registers when a wave quantizes a row
+
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_down_kernel(
-    const MoePlan* __restrict__ plan, int E, const float* __restrict__ gates, const float* __restrict__ act,
+    const MoePlan* __restrict__ plan, const float* __restrict__ gates, const float* __restrict__ act,
     const int8_t* __restrict__ wd, const float* __restrict__ sd, float* __restrict__ ybuf, int H, int I,
     int shared_T) {
     extern __shared__ int4 lds_a[];  // [kPairStage][I/16]
     __shared__ float lds_as[kPairStage];
     __shared__ int s_pid[kMaxT];
     constexpr int G = 256 / LPR;
-    const BlockExpert be = block_expert(plan, E, shared_T);
-    if (be.e < 0 || be.P == 0) return;
-    const int e = be.e, P = be.P;
+    const int e = block_expert(plan, shared_T);
+    if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int wave = threadIdx.x >> 6;
     const int wl = threadIdx.x & 63;
     const int C = I >> 4;
-    int r[2];
-    bool live[2];
-    int4 wv[2][JC];
-    float sdr[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        r[q] = blockIdx.y * 2 * G + q * G + grp;
-        live[q] = r[q] < H;
-        const size_t row = static_cast<size_t>(e) * H + (live[q] ? r[q] : 0);
+    const int r = blockIdx.y * G + grp;
+    const bool live = r < H;
+    const size_t row = static_cast<size_t>(e) * H + (live ? r : 0);
+    int4 wv[JC];
+    {
         const int4* drow = reinterpret_cast<const int4*>(wd + row * I);
 #pragma unroll
         for (int j = 0; j < JC; ++j) {
             const int c = lane + LPR * j;
-            wv[q][j] = (live[q] && c < C) ? ld_stream(drow + c) : make_int4(0, 0, 0, 0);
+            wv[j] = (live && c < C) ? ld_stream(drow + c) : make_int4(0, 0, 0, 0);
         }
-        sdr[q] = live[q] ? sd[row] : 0.0f;
     }
+    const float sdr = live ? sd[row] : 0.0f;
+    const int P = block_pairs(plan, e, shared_T);
     if (threadIdx.x < P) s_pid[threadIdx.x] = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
     __syncthreads();
     int8_t* lds_b = reinterpret_cast<int8_t*>(lds_a);
@@ -369,48 +347,48 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     for (int pb = 0; pb < P; pb += kPairStage) {
         const int pc_n = min(kPairStage, P - pb);
         if (pb) __syncthreads();
-        // quantize_row_i8 of each pair's act row: one wave per pair
+        // quantize_row_i8 of each pair's act row: one wave per pair, the
+        // row held in registers (NQ values per lane) between the two passes
         for (int pp = wave; pp < pc_n; pp += 4) {
             const float* ar = act + static_cast<size_t>(s_pid[pb + pp]) * I;
+            if (I > 64 * NQ) {  // long rows (a wide shared expert): two passes over L2
+                float amax = 0.0f;
+                for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
+                amax = wave_max_f(amax);
+                const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+                const float inv = 1.0f / a_scale;
+                for (int i = wl; i < I; i += 64) lds_b[pp * I + i] = quant_i8(ar[i], inv, false);
+                if (wl == 0) lds_as[pp] = a_scale;
+                continue;
+            }
+            float v[NQ];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) v[q] = wl + 64 * q < I ? ar[wl + 64 * q] : 0.0f;
             float amax = 0.0f;
-            for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) amax = fmaxf(amax, fabsf(v[q]));
             amax = wave_max_f(amax);
             const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const float inv = 1.0f / a_scale;
-            for (int i = wl; i < I; i += 64) lds_b[pp * I + i] = quant_i8(ar[i], inv, false);
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+                if (wl + 64 * q < I) lds_b[pp * I + wl + 64 * q] = quant_i8(v[q], inv, false);
             if (wl == 0) lds_as[pp] = a_scale;
         }
         __syncthreads();
-        for (int q0 = 0; q0 < pc_n; q0 += kPC) {
-            int da[2][kPC];
-#pragma unroll
-            for (int i = 0; i < kPC; ++i) da[0][i] = da[1][i] = 0;
+        for (int i = 0; i < pc_n; ++i) {
+            int d = 0;
 #pragma unroll
             for (int j = 0; j < JC; ++j) {
                 const int c = lane + LPR * j;
-                if (c < C) {
-#pragma unroll
-                    for (int i = 0; i < kPC; ++i) {
-                        if (q0 + i < pc_n) {
-                            const int4 av = lds_a[(q0 + i) * C + c];
-                            da[0][i] = dot16_i8(wv[0][j], av, da[0][i]);
-                            da[1][i] = dot16_i8(wv[1][j], av, da[1][i]);
-                        }
-                    }
-                }
+                if (c < C) d = dot16_i8(wv[j], lds_a[i * C + c], d);
             }
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-#pragma unroll
-                for (int i = 0; i < kPC; ++i) {
-                    const int dv = reduce_lanes<LPR>(da[q][i]);
-                    if (live[q] && lane == (i % LPR) && q0 + i < pc_n) {
-                        const int pid = s_pid[pb + q0 + i];
-                        const float yv = (static_cast<float>(dv) * lds_as[q0 + i]) * sdr[q];
-                        const float gate = shared_T > 0 ? 1.0f : gates[pid];
-                        ybuf[static_cast<size_t>(pid) * H + r[q]] = yv * gate;
-                    }
-                }
+            d = reduce_lanes<LPR>(d);
+            if (live && lane == 0) {
+                const int pid = s_pid[pb + i];
+                const float yv = (static_cast<float>(d) * lds_as[i]) * sdr;
+                const float gate = shared_T > 0 ? 1.0f : gates[pid];
+                ybuf[static_cast<size_t>(pid) * H + r] = yv * gate;
             }
         }
     }
@@ -443,12 +421,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 
 template <int LPR>
 hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan, int T, int K,
-                              int E, const int8_t* xq, const float* xs, const int8_t* wg, const float* sg,
+                              const int8_t* xq, const float* xs, const int8_t* wg, const float* sg,
                               const int8_t* wu, const float* su, float* act, int H, int I, int shared_T) {
 #define FOCR_GU(J)                                                                                              \
     case J:                                                                                                     \
-        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, plan, T, K, E, xq, xs, wg, sg, \
-                           wu, su, act, H, I, shared_T);                                                        \
+        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, plan, T, K, xq, xs, wg, sg, wu, \
+                           su, act, H, I, shared_T);                                                            \
         break;
     switch (JC) {
         FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
@@ -460,13 +438,13 @@ hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, cons
 }
 
 template <int LPR>
-hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan, int E,
+hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan,
                            const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf, int H,
                            int I, int shared_T) {
 #define FOCR_DN(J)                                                                                                \
     case J:                                                                                                       \
-        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, plan, E, gates, act, wd, sd, ybuf, H, \
-                           I, shared_T);                                                                          \
+        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, plan, gates, act, wd, sd, ybuf, H, I, \
+                           shared_T);                                                                             \
         break;
     switch (JC) {
         FOCR_DN(1) FOCR_DN(2) FOCR_DN(3) FOCR_DN(4) FOCR_DN(5) FOCR_DN(6) FOCR_DN(7) FOCR_DN(8)
@@ -512,7 +490,7 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan,
     int lpr, jc;
     pick_lpr(d.hidden, &lpr, &jc);
     if (d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
-    const int rows_per_block = 2 * (256 / lpr);
+    const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (inter + rows_per_block - 1) / rows_per_block);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
@@ -520,9 +498,9 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan,
     const int sh = shared ? d.t : 0;
     const MoePlan* pl = static_cast<const MoePlan*>(plan);
     if (lpr == 16)
-        return launch_gate_up_lpr<16>(s, grid, lds, jc, pl, d.t, d.top_k, d.n_experts, xq, xs, wg, sg, wu, su, act,
+        return launch_gate_up_lpr<16>(s, grid, lds, jc, pl, d.t, d.top_k, xq, xs, wg, sg, wu, su, act,
                                       d.hidden, inter, sh);
-    return launch_gate_up_lpr<8>(s, grid, lds, jc, pl, d.t, d.top_k, d.n_experts, xq, xs, wg, sg, wu, su, act,
+    return launch_gate_up_lpr<8>(s, grid, lds, jc, pl, d.t, d.top_k, xq, xs, wg, sg, wu, su, act,
                                  d.hidden, inter, sh);
 }
 
@@ -531,15 +509,15 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* plan, co
     int lpr, jc;
     pick_lpr(inter, &lpr, &jc);
     if (inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
-    const int rows_per_block = 2 * (256 / lpr);
+    const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (d.hidden + rows_per_block - 1) / rows_per_block);
     const size_t lds = static_cast<size_t>(kPairStage) * inter;
     const int sh = shared ? d.t : 0;
     const MoePlan* pl = static_cast<const MoePlan*>(plan);
     if (lpr == 16)
-        return launch_down_lpr<16>(s, grid, lds, jc, pl, d.n_experts, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
-    return launch_down_lpr<8>(s, grid, lds, jc, pl, d.n_experts, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
+        return launch_down_lpr<16>(s, grid, lds, jc, pl, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
+    return launch_down_lpr<8>(s, grid, lds, jc, pl, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
 }
 
 hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out,
