@@ -447,23 +447,23 @@ struct MoeScratch {
     float* ybuf;
     float* shared_act;
     float* shared_y;
-    void* plan;
+    unsigned long long* tok_mask;
 };
 
 int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
     const size_t pairs = t * L->top_k;
-    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, pairs * 8 + 256));
+    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, pairs * 8 + t * 8 + 256));
     s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
     s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
     s->ybuf = static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float)));
     s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
     s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
-    s->plan = ctx->scratch_get_zeroed(kScrPlan, moe_plan_bytes());
-    if (!route || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || !s->plan || (with_shared && !s->shared_y))
+    if (!route || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || (with_shared && !s->shared_y))
         return FOCR_HIP_E_OOM;
     s->idx = reinterpret_cast<uint32_t*>(route);
     s->gates = reinterpret_cast<float*>(route + pairs * 4);
+    s->tok_mask = reinterpret_cast<unsigned long long*>(route + pairs * 8);  // 8-byte aligned
     s->shared_act = with_shared ? s->act + pairs * L->inter : nullptr;
     return FOCR_HIP_OK;
 }
@@ -488,19 +488,14 @@ int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
 }
 
 int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t norm_topk,
-                     float routed_scale, const MoeScratch& s, uint32_t* idx, float* gates, float* probs, void* plan) {
+                     float routed_scale, const MoeScratch& s, uint32_t* idx, float* gates, float* probs,
+                     unsigned long long* tok_mask) {
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     ProfScope ps(ctx, "moe_route");
     FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
-                                  probs, s.flag, plan),
+                                  probs, s.flag, tok_mask),
                  "route launch");
     return FOCR_HIP_OK;
-}
-
-// A step that stopped between route and combine leaves the plan filled;
-// clear it so the next step starts from an empty plan.
-void reset_plan(focr_hip_ctx* ctx, void* plan) {
-    hipMemsetAsync(plan, 0, moe_plan_bytes(), ctx->stream);
 }
 
 }  // namespace
@@ -533,38 +528,34 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
     uint32_t* di = idx ? idx : s.idx;
     float* dg = gates ? gates : s.gates;
     hipStream_t str = ctx->stream;
-    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.plan))) {
-        reset_plan(ctx, s.plan);
-        return st;
-    }
+    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.tok_mask))) return st;
     hipError_t e = hipSuccess;
     {
         ProfScope ps(ctx, "moe_gate_up");
-        e = launch_moe_gate_up(str, d, s.plan, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false);
+        e = launch_moe_gate_up(str, d, di, s.tok_mask, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter,
+                               false);
     }
     if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_down");
-        e = launch_moe_down(str, d, s.plan, dg, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
+        e = launch_moe_down(str, d, di, s.tok_mask, dg, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
     }
     if (e == hipSuccess && with_shared) {
         {
             ProfScope ps(ctx, "moe_shared_gate_up");
-            e = launch_moe_gate_up(str, d, s.plan, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
+            e = launch_moe_gate_up(str, d, di, s.tok_mask, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
                                    (int)L->shared_inter, true);
         }
         if (e == hipSuccess) {
             ProfScope ps(ctx, "moe_shared_down");
-            e = launch_moe_down(str, d, s.plan, dg, s.shared_act, L->swd, L->ssd, s.shared_y, (int)L->shared_inter, true);
+            e = launch_moe_down(str, d, di, s.tok_mask, dg, s.shared_act, L->swd, L->ssd, s.shared_y,
+                                (int)L->shared_inter, true);
         }
     }
     if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_combine");
-        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, out, s.plan);
+        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, out);
     }
-    if (e != hipSuccess) {
-        reset_plan(ctx, s.plan);
-        return hip_fail(e, "moe_decode launch");
-    }
+    if (e != hipSuccess) return hip_fail(e, "moe_decode launch");
     if (check_route) return check_route_flags(ctx, s.flag, t);
     return FOCR_HIP_OK;
 }

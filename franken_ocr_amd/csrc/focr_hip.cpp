@@ -105,13 +105,6 @@ void* focr_hip_ctx::scratch_get(int slot, size_t bytes) {
     return b.p;
 }
 
-void* focr_hip_ctx::scratch_get_zeroed(int slot, size_t bytes) {
-    const bool fresh = scratch[slot].cap < (bytes ? bytes : 16);
-    void* p = scratch_get(slot, bytes);
-    if (p && fresh && hipMemsetAsync(p, 0, scratch[slot].cap, stream) != hipSuccess) return nullptr;
-    return p;
-}
-
 hipEvent_t focr_hip_ctx::take_event() {
     if (!event_pool.empty()) {
         hipEvent_t e = event_pool.back();

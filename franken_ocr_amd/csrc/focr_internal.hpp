@@ -48,7 +48,6 @@ enum ScratchSlot : int {
     kScrI4,     // int4 prefill intermediates
     kScrI4b,
     kScrFlag,   // device status flags
-    kScrPlan,   // MoE step plan (zeroed on allocation)
     kScrCount
 };
 
@@ -77,8 +76,6 @@ struct focr_hip_ctx {
 
     // Grow-only scratch. Returns nullptr (and sets the error) on failure.
     void* scratch_get(int slot, size_t bytes);
-    // As scratch_get, but a fresh allocation is zero-filled (stream-ordered).
-    void* scratch_get_zeroed(int slot, size_t bytes);
     // Make current the device this context lives on.
     hipError_t bind() const { return hipSetDevice(device); }
     hipEvent_t take_event();
@@ -166,24 +163,21 @@ hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, 
 struct MoeDims {
     int t, hidden, inter, n_experts, top_k;
 };
-// The step plan (active-expert mask + per-expert pair lists) lives in zeroed
-// device scratch; route fills it, combine clears it.
-size_t moe_plan_bytes();
-// flag[t] = 1 when token t has fewer than top_k finite router scores. plan
-// may be null (route only).
-hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden,
-                            const float* router, int norm_topk, float routed_scale, int8_t* xq,
-                            float* xs, uint32_t* idx, float* gates, float* probs, int* flag,
-                            void* plan);
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan,
-                              const int8_t* xq, const float* xs, const int8_t* wg,
-                              const float* sg, const int8_t* wu, const float* su, float* act,
+// route writes idx/gates [t][top_k], flag[t] = 1 when token t has fewer than
+// top_k finite router scores, and tok_mask[t] = the token's expert bitmask
+// (tok_mask may be null: route only). gate_up/down find their expert and
+// pairs from tok_mask and idx.
+hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
+                            int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
+                            float* probs, int* flag, unsigned long long* tok_mask);
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const uint32_t* idx,
+                              const unsigned long long* tok_mask, const int8_t* xq, const float* xs,
+                              const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
                               int inter, bool shared);
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* plan,
-                           const float* gates, const float* act, const int8_t* wd,
-                           const float* sd, float* ybuf, int inter, bool shared);
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf,
-                              const float* shared_y, float* out, void* plan);
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
+                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf,
+                           int inter, bool shared);
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out);
 
 // k_int4.hip
 hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,

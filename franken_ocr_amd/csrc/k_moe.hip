@@ -5,31 +5,29 @@
 //            to f32, quantize_row_i8 of the token row, f64 softmax rounded to
 //            f32, greedy top-k (= rank by (prob desc, index asc), NaN
 //            skipped; moe.rs:209-266), optional renorm and scale
-//            (moe.rs:226-236). Writes idx/gates [t][k] and appends each
-//            (token, slot) pair to its expert's list in the step plan (an
-//            active-expert bitmask plus per-expert pair lists, built with
-//            device atomics; the next kernel launch orders the reads).
-//   gate_up  grid (active expert, row block): finds its expert with one
-//            scalar load of the plan's active mask, issues the expert's gate
-//            and up row loads, stages the routed tokens' int8 rows in LDS
-//            meanwhile, and writes act[t*K + j][r] = silu(g) * u
-//            (decoder.rs:1746-1752).
+//            (moe.rs:226-236). Writes idx/gates [t][k] and the token's expert
+//            bitmask; no atomics, nothing carried between calls.
+//   gate_up  grid (active expert, row block): ORs the T token masks (one
+//            load per lane, a wave-level reduction), takes the a-th set bit
+//            as its expert, issues the expert's gate and up row loads, then
+//            stages the token rows in LDS and collects its (token, slot)
+//            pairs by scanning idx in pair order; writes
+//            act[t*K + j][r] = silu(g) * u (decoder.rs:1746-1752).
 //   down     grid (active expert, row block): issues the down row loads,
-//            re-quantizes each pair's act row into LDS (quantize_row_i8)
-//            meanwhile, writes y[t*K + j][r] = dequant * gate
-//            (decoder.rs:2244-2246).
+//            collects the pairs the same way, re-quantizes each pair's act
+//            row into LDS (quantize_row_i8), writes y[t*K + j][r] =
+//            dequant * gate (decoder.rs:2244-2246).
 //   combine  out[t][c] = ((0 + y[t,0]) + y[t,1]) ... (+ shared), slot order
-//            (decoder.rs:2253-2261); deterministic, no atomics. It also
-//            clears the plan for the next step.
+//            (decoder.rs:2253-2261); deterministic, no atomics.
 //
 // Each routed expert's 3.44 MB of weights is read exactly once per step, by
-// exactly as many blocks as it has row blocks. The order of pairs inside an
-// expert's list depends on block timing, but every pair's result is computed
-// independently and stored at its own (token, slot) slot, so outputs are
-// bit-reproducible run to run. GEMV rows use LPR lanes per row (16 for K =
-// 1280 -> 5 chunks of 16 B per lane; 8 for K = 896 -> 7 chunks) and one row
-// per lane group: with few pairs per expert the kernels are latency-bound,
-// and the smaller register footprint buys the occupancy that hides it.
+// exactly as many blocks as it has row blocks. Every pair's result is
+// computed independently and stored at its own (token, slot) slot, so
+// outputs are bit-reproducible run to run. GEMV rows use LPR lanes per row
+// (16 for K = 1280 -> 5 chunks of 16 B per lane; 8 for K = 896 -> 7 chunks)
+// and one row per lane group: with few pairs per expert the kernels are
+// latency-bound, and the smaller register footprint buys the occupancy that
+// hides it.
 #include "focr_internal.hpp"
 #include "k_common.hpp"
 
@@ -39,13 +37,8 @@ namespace {
 constexpr int kMaxT = 64;
 constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
+constexpr int kMaxPairs = kMaxT * kMaxK;
 constexpr int kPairStage = 32;  // pairs staged in LDS per pass
-
-struct MoePlan {
-    unsigned long long mask;   // bit e: expert e has pairs this step
-    int cnt[kMaxE];            // pairs per expert
-    int list[kMaxE][kMaxT];    // pair ids t*K + j, per expert
-};
 
 template <int LPR>
 __device__ __forceinline__ int reduce_lanes(int v) {
@@ -64,165 +57,270 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
 
-template <int NI>  // float4 chunks of a router row per thread, in batches (H <= 64 * 4 * NI)
+// Thread (e, l) = (tid / 16, tid % 16) owns router row e's float4 chunks
+// c = l + 16 i, fetched in batches of NI with the next batch in flight while
+// the current one is consumed; the first batch is issued before the token
+// row, so both round trips overlap.
+template <int NI>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
-    MoePlan* __restrict__ plan) {
+    unsigned long long* __restrict__ tok_mask) {
     __shared__ float4 s_x[512];
     __shared__ float s_logit[kMaxE];
-    __shared__ double s_ex[kMaxE];
-    __shared__ float s_p[kMaxE];
+    __shared__ __align__(16) float s_p[kMaxE];
     __shared__ int s_sel_e[kMaxK];
     __shared__ float s_sel_w[kMaxK];
     __shared__ float s_red[kRouteWaves];
+    __shared__ int s_nvalid;
     const int t = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const float* xr = x + static_cast<size_t>(t) * H;
     const int H4 = H >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(xr);
-    for (int c = threadIdx.x; c < H4; c += kRouteThreads) s_x[c] = x4[c];
-    __syncthreads();
+    const int e = threadIdx.x >> 4;
+    const int l = threadIdx.x & 15;
+    const bool erow = e < E;
+    const float4* gr = reinterpret_cast<const float4*>(G + static_cast<size_t>(erow ? e : 0) * H);
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-    // 1. logits: 16 threads per expert; thread (e, l) covers float4 chunks
-    //    c = l + 16 i of the router row, NI loads in flight per batch.
-    {
-        const int e = threadIdx.x >> 4;
-        const int l = threadIdx.x & 15;
-        double acc = 0.0;
-        if (e < E) {
-            const float4* gr = reinterpret_cast<const float4*>(G + static_cast<size_t>(e) * H);
-#pragma unroll 1
-            for (int c0 = l; c0 < H4; c0 += 16 * NI) {
-                float4 g[NI];
+    // Loads are unconditional (address clamped into the row, a chunk past
+    // the row's end zeroed by a bit mask, threads past E compute unused
+    // values) so they issue as one batch of dwordx4 loads, not as branches.
+    auto router_chunk = [&](int c) {
+        const float4 v = gr[c < H4 ? c : H4 - 1];
+        const unsigned m = c < H4 ? 0xFFFFFFFFu : 0u;
+        return make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
+                           __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
+    };
+    float4 g[NI];
 #pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const int c = c0 + 16 * i;
-                    g[i] = c < H4 ? gr[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                }
-#pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const int c = c0 + 16 * i;
-                    const float4 xv = c < H4 ? s_x[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    acc = fma(static_cast<double>(xv.x), static_cast<double>(g[i].x), acc);
-                    acc = fma(static_cast<double>(xv.y), static_cast<double>(g[i].y), acc);
-                    acc = fma(static_cast<double>(xv.z), static_cast<double>(g[i].z), acc);
-                    acc = fma(static_cast<double>(xv.w), static_cast<double>(g[i].w), acc);
-                }
-            }
-        }
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
-        if (l == 0 && e < E) s_logit[e] = static_cast<float>(acc);
-    }
-
-    // 2. quantize_row_i8 of the token row
+    for (int i = 0; i < NI; ++i) g[i] = router_chunk(l + 16 * i);
+    // 1. stage the token row (H4 <= 512 < 1024 threads: one float4 each) and
+    //    take |x| max on the way for quantize_row_i8
+    float4 xv = z4;
     float amax = 0.0f;
-    for (int i = threadIdx.x; i < H; i += kRouteThreads) amax = fmaxf(amax, fabsf(xr[i]));
+    if (threadIdx.x < H4) {
+        xv = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H)[threadIdx.x];
+        s_x[threadIdx.x] = xv;
+        amax = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
+    }
     amax = wave_max_f(amax);
     if (lane == 0) s_red[wave] = amax;
     __syncthreads();
+
+    // 2. logits
+    double acc = 0.0;
+#pragma unroll 1
+    for (int c0 = l; c0 < H4; c0 += 16 * NI) {
+        float4 gn[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) gn[i] = router_chunk(c0 + 16 * (NI + i));
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c = c0 + 16 * i;
+            const float4 xc = c < H4 ? s_x[c] : z4;
+            acc = fma(static_cast<double>(xc.x), static_cast<double>(g[i].x), acc);
+            acc = fma(static_cast<double>(xc.y), static_cast<double>(g[i].y), acc);
+            acc = fma(static_cast<double>(xc.z), static_cast<double>(g[i].z), acc);
+            acc = fma(static_cast<double>(xc.w), static_cast<double>(g[i].w), acc);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) g[i] = gn[i];
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
+    if (l == 0 && erow) s_logit[e] = static_cast<float>(acc);
+
+    // 3. quantize_row_i8 of the token row from the staged values
     amax = 0.0f;
 #pragma unroll
     for (int w = 0; w < kRouteWaves; ++w) amax = fmaxf(amax, s_red[w]);
     const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / a_scale;
-    for (int i = threadIdx.x; i < H; i += kRouteThreads)
-        xq[static_cast<size_t>(t) * H + i] = quant_i8(xr[i], inv, false);
+    if (threadIdx.x < H4) {
+        char4 q;
+        q.x = quant_i8(xv.x, inv, false);
+        q.y = quant_i8(xv.y, inv, false);
+        q.z = quant_i8(xv.z, inv, false);
+        q.w = quant_i8(xv.w, inv, false);
+        reinterpret_cast<char4*>(xq + static_cast<size_t>(t) * H)[threadIdx.x] = q;
+    }
     if (threadIdx.x == 0) xs[t] = a_scale;
+    __syncthreads();
 
-    // 3. softmax in f64 over the f32 logits: max, exp, then a sequential sum
-    //    in expert order; each probability rounded to f32.
-    const bool valid = wave == 0 && lane < E;
-    double ex = 0.0;
-    if (valid) {
-        double mx = -INFINITY;
-        for (int e = 0; e < E; ++e) {
-            const double v = static_cast<double>(s_logit[e]);
-            mx = v > mx ? v : mx;
+    // 4. softmax in f64 over the f32 logits (wave 0, lane = expert): max,
+    //    exp, butterfly sum, divide, round to f32
+    if (wave == 0) {
+        const bool valid = lane < E;
+        const float lg = valid ? s_logit[lane] : -INFINITY;
+        const double mx = static_cast<double>(wave_max_f(lg));
+        double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
+        double sum = ex;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        const float p = static_cast<float>(ex / sum);
+        if (valid) {
+            s_p[lane] = p;
+            if (probs_out) probs_out[static_cast<size_t>(t) * E + lane] = p;
+        } else {
+            s_p[lane] = __int_as_float(0x7fc00000);  // NaN: never ranked
         }
-        ex = exp(static_cast<double>(s_logit[lane]) - mx);
-        s_ex[lane] = ex;
+        const unsigned long long fin = __ballot(valid && p == p);
+        if (lane == 0) s_nvalid = __popcll(fin);
     }
     __syncthreads();
-    float p = 0.0f;
-    if (valid) {
-        double sum = 0.0;
-        for (int e = 0; e < E; ++e) sum += s_ex[e];
-        p = static_cast<float>(ex / sum);
-        s_p[lane] = p;
-        if (probs_out) probs_out[static_cast<size_t>(t) * E + lane] = p;
-    }
-    __syncthreads();
-    // 4. greedy top-k == rank by (prob desc, index asc) among non-NaN probs
-    int n_valid = 0;
-    if (valid) {
-        int rank = 0;
-        for (int e = 0; e < E; ++e) {
-            const float q = s_p[e];
-            if (q != q) continue;
-            ++n_valid;
-            rank += (q > p || (q == p && e < lane)) ? 1 : 0;
-        }
-        if (p == p && rank < K) {
-            s_sel_e[rank] = lane;
-            s_sel_w[rank] = p;
+
+    // 5. greedy top-k == rank by (prob desc, index asc) among non-NaN probs:
+    //    thread (e, l) counts the experts 4l..4l+3 ahead of e, 16 lanes sum
+    {
+        const float pe = s_p[e];
+        const float4 q = reinterpret_cast<const float4*>(s_p)[l];
+        const int j0 = 4 * l;
+        int ahead = 0;
+        ahead += (q.x > pe || (q.x == pe && j0 + 0 < e)) ? 1 : 0;
+        ahead += (q.y > pe || (q.y == pe && j0 + 1 < e)) ? 1 : 0;
+        ahead += (q.z > pe || (q.z == pe && j0 + 2 < e)) ? 1 : 0;
+        ahead += (q.w > pe || (q.w == pe && j0 + 3 < e)) ? 1 : 0;
+        ahead = reduce16_add(ahead);
+        if (l == 0 && erow && pe == pe && ahead < K) {
+            s_sel_e[ahead] = e;
+            s_sel_w[ahead] = pe;
         }
     }
     __syncthreads();
-    // 5. renormalise (sequential f32 sum in slot order) and scale
-    __shared__ float s_denom;
-    __shared__ int s_bad;
-    if (threadIdx.x == 0) {
-        const bool bad = n_valid < K;
-        s_bad = bad ? 1 : 0;
-        flag[t] = bad ? 1 : 0;
-        float s = 0.0f;
-        for (int j = 0; j < K; ++j) s += bad ? 0.0f : s_sel_w[j];
-        s_denom = s + 1e-20f;
-    }
-    __syncthreads();
-    // 6. publish: one thread per slot (the plan's device atomics run in
-    //    parallel rather than as a serial chain of round trips)
+
+    // 6. renormalise (sequential f32 sum in slot order), scale, publish
     if (threadIdx.x < K) {
         const int j = threadIdx.x;
-        const bool bad = s_bad != 0;
-        const int e = bad ? 0 : s_sel_e[j];
+        const bool bad = s_nvalid < K;
+        float den = 0.0f;
+        for (int jj = 0; jj < K; ++jj) den += bad ? 0.0f : s_sel_w[jj];
+        den += 1e-20f;
+        const int ej = bad ? 0 : s_sel_e[j];
         float w = bad ? 0.0f : s_sel_w[j];
-        if (norm_topk) w = w / s_denom;
-        idx_out[t * K + j] = static_cast<uint32_t>(e);
+        if (norm_topk) w = w / den;
+        idx_out[t * K + j] = static_cast<uint32_t>(ej);
         gates_out[t * K + j] = w * routed_scale;
-        if (plan) {
-            atomicOr(&plan->mask, 1ull << e);
-            const int pos = atomicAdd(&plan->cnt[e], 1);
-            if (pos < kMaxT) plan->list[e][pos] = t * K + j;
+        if (j == 0) {
+            unsigned long long m = 0ull;
+            for (int jj = 0; jj < K; ++jj) m |= 1ull << (bad ? 0 : s_sel_e[jj]);
+            if (tok_mask) tok_mask[t] = m;
+            flag[t] = bad ? 1 : 0;
         }
     }
 }
 
-// Expert of this block: routed mode takes the a-th set bit of the plan's
-// active mask (one scalar load, so the weight loads can issue right after);
-// shared mode is one expert whose pairs are the tokens.
-__device__ __forceinline__ int block_expert(const MoePlan* __restrict__ plan, int shared_T) {
+// Expert of this block: routed mode ORs the T token masks (every wave does
+// it, so no barrier is needed) and takes the a-th set bit; shared mode is one
+// expert whose pairs are the tokens. All loads here and below are issued
+// unconditionally from clamped addresses, with invalid lanes masked
+// arithmetically: a select between a load and a constant tends to become a
+// branch around the load with a full wait inside it, which serialises the
+// memory round trips these kernels depend on overlapping.
+__device__ __forceinline__ int block_expert(const unsigned long long* __restrict__ tok_mask, int T, int shared_T) {
     if (shared_T > 0) return 0;
-    return nth_set_bit(plan->mask, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    unsigned long long m = tok_mask[lane < T ? lane : T - 1];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m |= __shfl_xor(m, o, 64);
+    // lane l holds bit l; the a-th set bit is the set lane with a set bits below
+    const bool set = (m >> lane) & 1ull;
+    const int below = __popcll(m & ((1ull << lane) - 1ull));
+    const unsigned long long hit = __ballot(set && below == static_cast<int>(blockIdx.x));
+    return hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
 }
 
-__device__ __forceinline__ int block_pairs(const MoePlan* __restrict__ plan, int e, int shared_T) {
-    return shared_T > 0 ? shared_T : min(plan->cnt[e], kMaxT);
+// Wave 0 collects the block's pairs in increasing pair id (t*K + j) from
+// idx [T*K <= 512], with their gates when gates is non-null (1.0 for the
+// shared expert); the caller synchronises before reading them.
+__device__ __forceinline__ void block_pairs(const uint32_t* __restrict__ idx, const float* __restrict__ gates, int T,
+                                            int K, int e, int shared_T, int* s_pid, int* s_tok, float* s_gate,
+                                            int* s_np) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    if (shared_T > 0) {
+        for (int p = lane; p < shared_T; p += 64) {
+            s_pid[p] = p;
+            s_tok[p] = p;
+            if (gates) s_gate[p] = 1.0f;
+        }
+        if (lane == 0) *s_np = shared_T;
+        return;
+    }
+    const int TK = T * K;
+    uint32_t v[kMaxPairs / 64];
+    float gv[kMaxPairs / 64];
+#pragma unroll
+    for (int q = 0; q < kMaxPairs / 64; ++q) {
+        const int pid = 64 * q + lane;
+        const int pc = pid < TK ? pid : TK - 1;
+        v[q] = idx[pc] | (pid < TK ? 0u : 0xFFFFFFFFu);
+        gv[q] = gates ? gates[pc] : 0.0f;
+    }
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxPairs / 64; ++q) {
+        const bool hit = v[q] == static_cast<uint32_t>(e);
+        const unsigned long long m = __ballot(hit);
+        if (hit) {
+            const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+            const int pid = 64 * q + lane;
+            s_pid[pos] = pid;
+            s_tok[pos] = pid / K;
+            if (gates) s_gate[pos] = gv[q];
+        }
+        base += __popcll(m);
+    }
+    if (lane == 0) *s_np = base;
 }
 
-// Stage the token rows a block needs into LDS: every token row when T fits
-// (no dependence on the plan, so these loads start immediately), else the
-// rows of the block's pairs [pb, pb + n).
+// Chunk c of a weight row, or zeros when c >= C (address clamped into the
+// row, so the load itself is unconditional).
+__device__ __forceinline__ int4 row_chunk(const int4* row, int c, int C) {
+    const int4 v = ld_stream(row + (c < C ? c : C - 1));
+    const int m = c < C ? -1 : 0;
+    return make_int4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
+
+// Stage int8 token rows into LDS: lds[p * C + c] = row(p)[c] for p < nrows,
+// where row(p) is token rows[p] (or p when rows is null). Four chunks per
+// thread per round, loads issued before the stores. Indices past the end are
+// clamped to the last chunk for the store as well as the load (a conditional
+// store lets the compiler sink the load under the condition): those threads
+// rewrite the last chunk with the value it already holds.
 __device__ __forceinline__ void stage_rows(int4* lds, const int8_t* __restrict__ xq, int H, int C, int nrows,
                                           const int* rows) {
-    for (int i = threadIdx.x; i < nrows * C; i += 256) {
-        const int pp = i / C, c = i - pp * C;
-        const int tok = rows ? rows[pp] : pp;
-        lds[i] = reinterpret_cast<const int4*>(xq + static_cast<size_t>(tok) * H)[c];
+    const int n = nrows * C;
+    for (int base = 0; base < n; base += 4 * 256) {
+        int4 v[4];
+        int at[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = base + 256 * k + static_cast<int>(threadIdx.x);
+            at[k] = i < n ? i : n - 1;
+            const int pp = at[k] / C, c = at[k] - pp * C;
+            const int tok = rows ? rows[pp] : pp;
+            v[k] = reinterpret_cast<const int4*>(xq + static_cast<size_t>(tok) * H)[c];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds[at[k]] = v[k];
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
+
+// Copy n 16-byte chunks src[0..n) to lds[0..n) with gfx950's direct
+// global-to-LDS loads (global_load_lds_dwordx4: lane L of a wave lands at the
+// wave's LDS base + 16 L), no VGPRs involved; the next barrier waits for them.
+// Whole 64-chunk blocks are written, so lds must hold n rounded up to 64.
+__device__ __forceinline__ void stage_lds_dma(int4* lds, const int4* __restrict__ src, int n) {
+    const int lane = threadIdx.x & 63;
+    for (int base = threadIdx.x & ~63; base < n; base += 256) {
+        const int i = base + lane;
+        __builtin_amdgcn_global_load_lds((global_void_t*)(src + (i < n ? i : n - 1)), (lds_void_t*)(lds + base), 16,
+                                         0, 0);
     }
 }
 
@@ -230,26 +328,27 @@ constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
 
 // ---- gate/up ------------------------------------------------------------------
 // Block = 256 threads = (256 / LPR) row groups, one weight row per group held
-// in registers (2 * JC 16-byte loads in flight per lane); the block's routed
-// pairs are then taken one at a time against the staged token rows.
+// in registers (2 * JC 16-byte loads in flight per lane); the block's pairs
+// are then taken one at a time against the staged token rows.
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(
-    const MoePlan* __restrict__ plan, int T, int K, const int8_t* __restrict__ xq,
-    const float* __restrict__ xs, const int8_t* __restrict__ wg, const float* __restrict__ sg,
-    const int8_t* __restrict__ wu, const float* __restrict__ su, float* __restrict__ act, int H, int I,
-    int shared_T) {
+    const uint32_t* __restrict__ idx, const unsigned long long* __restrict__ tok_mask, int T, int K,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, const int8_t* __restrict__ wg,
+    const float* __restrict__ sg, const int8_t* __restrict__ wu, const float* __restrict__ su,
+    float* __restrict__ act, int H, int I, int shared_T) {
     extern __shared__ int4 lds_x[];  // [rows staged][H/16]
-    __shared__ int s_pid[kMaxT];
-    __shared__ int s_tok[kMaxT];
-    __shared__ float s_xs[kMaxT];
+    __shared__ int s_pid[kMaxPairs];
+    __shared__ int s_tok[kMaxPairs];
+    __shared__ float s_xs[64];  // one per lane of the staging wave
+    __shared__ int s_np;
     constexpr int G = 256 / LPR;  // rows per block
-    const int e = block_expert(plan, shared_T);
+    const int e = block_expert(tok_mask, T, shared_T);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int C = H >> 4;
     const int r = blockIdx.y * G + grp;
-    const bool live = r < I;
+    const bool live = r < I;  // rows past I compute unused values from row 0
     const size_t row = static_cast<size_t>(e) * I + (live ? r : 0);
     int4 wgv[JC], wuv[JC];
     {
@@ -258,22 +357,21 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
 #pragma unroll
         for (int j = 0; j < JC; ++j) {
             const int c = lane + LPR * j;
-            wgv[j] = (live && c < C) ? ld_stream(grow + c) : make_int4(0, 0, 0, 0);
-            wuv[j] = (live && c < C) ? ld_stream(urow + c) : make_int4(0, 0, 0, 0);
+            wgv[j] = row_chunk(grow, c, C);
+            wuv[j] = row_chunk(urow, c, C);
         }
     }
-    const float sgr = live ? sg[row] : 0.0f;
-    const float sur = live ? su[row] : 0.0f;
+    const float sgr = sg[row];
+    const float sur = su[row];
     const bool all_tok = T <= kAllTok;
-    if (all_tok) stage_rows(lds_x, xq, H, C, T, nullptr);
-    if (threadIdx.x < T) s_xs[threadIdx.x] = xs[threadIdx.x];
-    const int P = block_pairs(plan, e, shared_T);
-    if (threadIdx.x < P) {
-        const int pid = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
-        s_pid[threadIdx.x] = pid;
-        s_tok[threadIdx.x] = shared_T > 0 ? pid : pid / K;
+    if (all_tok) stage_lds_dma(lds_x, reinterpret_cast<const int4*>(xq), T * C);  // rows are contiguous
+    if (threadIdx.x < 64) {
+        const int tt = threadIdx.x < T ? threadIdx.x : T - 1;
+        __builtin_amdgcn_global_load_lds((global_void_t*)(xs + tt), (lds_void_t*)s_xs, 4, 0, 0);
     }
+    block_pairs(idx, nullptr, T, K, e, shared_T, s_pid, s_tok, nullptr, &s_np);
     __syncthreads();
+    const int P = s_np;
 
     for (int pb = 0; pb < P; pb += kPairStage) {
         const int pc_n = min(kPairStage, P - pb);
@@ -312,14 +410,17 @@ constexpr int NQ = 16;  // act values per lane held in registers when a wave qua
 
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_down_kernel(
-    const MoePlan* __restrict__ plan, const float* __restrict__ gates, const float* __restrict__ act,
-    const int8_t* __restrict__ wd, const float* __restrict__ sd, float* __restrict__ ybuf, int H, int I,
-    int shared_T) {
+    const uint32_t* __restrict__ idx, const unsigned long long* __restrict__ tok_mask, int T, int K,
+    const float* __restrict__ gates, const float* __restrict__ act, const int8_t* __restrict__ wd,
+    const float* __restrict__ sd, float* __restrict__ ybuf, int H, int I, int shared_T) {
     extern __shared__ int4 lds_a[];  // [kPairStage][I/16]
     __shared__ float lds_as[kPairStage];
-    __shared__ int s_pid[kMaxT];
+    __shared__ int s_pid[kMaxPairs];
+    __shared__ int s_tok[kMaxPairs];
+    __shared__ float s_gate[kMaxPairs];
+    __shared__ int s_np;
     constexpr int G = 256 / LPR;
-    const int e = block_expert(plan, shared_T);
+    const int e = block_expert(tok_mask, T, shared_T);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -327,21 +428,18 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     const int wl = threadIdx.x & 63;
     const int C = I >> 4;
     const int r = blockIdx.y * G + grp;
-    const bool live = r < H;
+    const bool live = r < H;  // rows past H compute unused values from row 0
     const size_t row = static_cast<size_t>(e) * H + (live ? r : 0);
     int4 wv[JC];
     {
         const int4* drow = reinterpret_cast<const int4*>(wd + row * I);
 #pragma unroll
-        for (int j = 0; j < JC; ++j) {
-            const int c = lane + LPR * j;
-            wv[j] = (live && c < C) ? ld_stream(drow + c) : make_int4(0, 0, 0, 0);
-        }
+        for (int j = 0; j < JC; ++j) wv[j] = row_chunk(drow, lane + LPR * j, C);
     }
-    const float sdr = live ? sd[row] : 0.0f;
-    const int P = block_pairs(plan, e, shared_T);
-    if (threadIdx.x < P) s_pid[threadIdx.x] = shared_T > 0 ? threadIdx.x : plan->list[e][threadIdx.x];
+    const float sdr = sd[row];
+    block_pairs(idx, gates, T, K, e, shared_T, s_pid, s_tok, s_gate, &s_np);
     __syncthreads();
+    const int P = s_np;
     int8_t* lds_b = reinterpret_cast<int8_t*>(lds_a);
 
     for (int pb = 0; pb < P; pb += kPairStage) {
@@ -363,7 +461,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
             }
             float v[NQ];
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) v[q] = wl + 64 * q < I ? ar[wl + 64 * q] : 0.0f;
+            for (int q = 0; q < NQ; ++q) {
+                const int i = wl + 64 * q;
+                v[q] = ar[i < I ? i : I - 1];  // a duplicate of the last value past I: max unchanged
+            }
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < NQ; ++q) amax = fmaxf(amax, fabsf(v[q]));
@@ -387,8 +488,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
             if (live && lane == 0) {
                 const int pid = s_pid[pb + i];
                 const float yv = (static_cast<float>(d) * lds_as[i]) * sdr;
-                const float gate = shared_T > 0 ? 1.0f : gates[pid];
-                ybuf[static_cast<size_t>(pid) * H + r] = yv * gate;
+                ybuf[static_cast<size_t>(pid) * H + r] = yv * s_gate[pb + i];
             }
         }
     }
@@ -397,15 +497,9 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // ---- combine (slot order) ---------------------------------------------------------
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf,
                                                           const float* __restrict__ shared_y,
-                                                          float* __restrict__ out, int H, int K,
-                                                          MoePlan* __restrict__ plan, int E) {
+                                                          float* __restrict__ out, int H, int K) {
     const int t = blockIdx.y;
     const int c = blockIdx.x * 256 + threadIdx.x;
-    if (plan && blockIdx.x == 0 && blockIdx.y == 0) {
-        // every reader of the plan (gate_up, down) finished before this launch
-        if (threadIdx.x < E) plan->cnt[threadIdx.x] = 0;
-        if (threadIdx.x == 0) plan->mask = 0ull;
-    }
     if (c >= H) return;
     float v[kMaxK];
 #pragma unroll
@@ -419,14 +513,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     out[static_cast<size_t>(t) * H + c] = o;
 }
 
+struct GemvArgs {
+    const uint32_t* idx;
+    const unsigned long long* tok_mask;
+    int T, K, H, I, shared_T;
+};
+
 template <int LPR>
-hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan, int T, int K,
-                              const int8_t* xq, const float* xs, const int8_t* wg, const float* sg,
-                              const int8_t* wu, const float* su, float* act, int H, int I, int shared_T) {
-#define FOCR_GU(J)                                                                                              \
-    case J:                                                                                                     \
-        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, plan, T, K, xq, xs, wg, sg, wu, \
-                           su, act, H, I, shared_T);                                                            \
+hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const int8_t* xq,
+                              const float* xs, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
+                              float* act) {
+#define FOCR_GU(J)                                                                                                 \
+    case J:                                                                                                        \
+        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, xq, \
+                           xs, wg, sg, wu, su, act, a.H, a.I, a.shared_T);                                         \
         break;
     switch (JC) {
         FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
@@ -438,13 +538,12 @@ hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, cons
 }
 
 template <int LPR>
-hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const MoePlan* plan,
-                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf, int H,
-                           int I, int shared_T) {
-#define FOCR_DN(J)                                                                                                \
-    case J:                                                                                                       \
-        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, plan, gates, act, wd, sd, ybuf, H, I, \
-                           shared_T);                                                                             \
+hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const float* gates,
+                           const float* act, const int8_t* wd, const float* sd, float* ybuf) {
+#define FOCR_DN(J)                                                                                              \
+    case J:                                                                                                     \
+        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, gates, \
+                           act, wd, sd, ybuf, a.H, a.I, a.shared_T);                                            \
         break;
     switch (JC) {
         FOCR_DN(1) FOCR_DN(2) FOCR_DN(3) FOCR_DN(4) FOCR_DN(5) FOCR_DN(6) FOCR_DN(7) FOCR_DN(8)
@@ -468,63 +567,56 @@ void pick_lpr(int K, int* lpr, int* jc) {
     }
 }
 
-}  // namespace
+bool dims_ok(const MoeDims& d) {
+    return d.t >= 1 && d.t <= kMaxT && d.n_experts >= 1 && d.n_experts <= kMaxE && d.top_k >= 1 &&
+           d.top_k <= kMaxK && d.top_k <= d.n_experts;
+}
 
-size_t moe_plan_bytes() { return sizeof(MoePlan); }
+}  // namespace
 
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* plan) {
-    if (d.t < 1 || d.t > kMaxT || d.n_experts < 1 || d.n_experts > kMaxE || d.top_k < 1 || d.top_k > kMaxK ||
-        d.top_k > d.n_experts || d.hidden % 4 != 0 || d.hidden > 2048)
-        return hipErrorInvalidValue;
-    MoePlan* pl = static_cast<MoePlan*>(plan);
+                            float* probs, int* flag, unsigned long long* tok_mask) {
+    if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
     hipLaunchKernelGGL((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
-                       d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, pl);
+                       d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, tok_mask);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* plan, const int8_t* xq, const float* xs,
-                              const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, bool shared) {
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
+                              const int8_t* xq, const float* xs, const int8_t* wg, const float* sg, const int8_t* wu,
+                              const float* su, float* act, int inter, bool shared) {
     int lpr, jc;
     pick_lpr(d.hidden, &lpr, &jc);
-    if (d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    if (!dims_ok(d) || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (inter + rows_per_block - 1) / rows_per_block);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
-    const size_t lds = static_cast<size_t>(staged) * d.hidden;
-    const int sh = shared ? d.t : 0;
-    const MoePlan* pl = static_cast<const MoePlan*>(plan);
-    if (lpr == 16)
-        return launch_gate_up_lpr<16>(s, grid, lds, jc, pl, d.t, d.top_k, xq, xs, wg, sg, wu, su, act,
-                                      d.hidden, inter, sh);
-    return launch_gate_up_lpr<8>(s, grid, lds, jc, pl, d.t, d.top_k, xq, xs, wg, sg, wu, su, act,
-                                 d.hidden, inter, sh);
+    const size_t lds = (static_cast<size_t>(staged) * d.hidden + 1023) & ~static_cast<size_t>(1023);
+    const GemvArgs a{idx, tok_mask, d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
+    if (lpr == 16) return launch_gate_up_lpr<16>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
+    return launch_gate_up_lpr<8>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
 }
 
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* plan, const float* gates, const float* act,
-                           const int8_t* wd, const float* sd, float* ybuf, int inter, bool shared) {
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
+                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf,
+                           int inter, bool shared) {
     int lpr, jc;
     pick_lpr(inter, &lpr, &jc);
-    if (inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (d.hidden + rows_per_block - 1) / rows_per_block);
     const size_t lds = static_cast<size_t>(kPairStage) * inter;
-    const int sh = shared ? d.t : 0;
-    const MoePlan* pl = static_cast<const MoePlan*>(plan);
-    if (lpr == 16)
-        return launch_down_lpr<16>(s, grid, lds, jc, pl, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
-    return launch_down_lpr<8>(s, grid, lds, jc, pl, gates, act, wd, sd, ybuf, d.hidden, inter, sh);
+    const GemvArgs a{idx, tok_mask, d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
+    if (lpr == 16) return launch_down_lpr<16>(s, grid, lds, jc, a, gates, act, wd, sd, ybuf);
+    return launch_down_lpr<8>(s, grid, lds, jc, a, gates, act, wd, sd, ybuf);
 }
 
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out,
-                              void* plan) {
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out) {
     const dim3 grid((d.hidden + 255) / 256, d.t);
-    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k,
-                       static_cast<MoePlan*>(plan), d.n_experts);
+    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k);
     return hipGetLastError();
 }
 

@@ -226,14 +226,32 @@ int oracle_lm_head_i8(const float* x, size_t m, const int8_t* w, const float* sc
  * (strict >, lower index on ties, NaN skipped, error if no finite score),
  * optional renormalisation w /= (sum_f32(w) + 1e-20), then w *= scale.
  * Router numerics (documented definition of this build): each logit is an
- * f64 dot product in increasing p, rounded to f32; the softmax is computed in
- * f64 from those f32 logits (max-subtracted, exp, sum in increasing e,
- * divide) and each probability rounded to f32. `probs` (optional) receives
- * the f32 probabilities [t][n_experts]. */
+ * f64 dot product rounded to f32; the softmax is computed in f64 from those
+ * f32 logits (max-subtracted, exp, the sum taken in the order of a 64-lane
+ * xor butterfly, butterfly_sum64 below, divide) and each probability rounded
+ * to f32. Any f64 summation order of a 1280-term dot product or a 64-term sum
+ * rounds to the same f32 except when the f64 value lies within ~2^-29
+ * (relative) of an f32 rounding boundary, so the increasing-q dot order here
+ * and the GPU's strided partial sums agree bit for bit in practice; the
+ * softmax sum order is fixed exactly. `probs` (optional) receives the f32
+ * probabilities [t][n_experts]. */
+/* Sum of v[0..n), n <= 64, in 64-lane xor-butterfly order: lanes i >= n hold
+ * +0; for o = 32, 16, 8, 4, 2, 1 every lane i takes v[i] + v[i ^ o]. All lanes
+ * end equal (each step adds the same two operands in both partner lanes). */
+static double butterfly_sum64(const double* v, size_t n) {
+    double a[64], b[64];
+    for (size_t i = 0; i < 64; ++i) a[i] = i < n ? v[i] : 0.0;
+    for (size_t o = 32; o > 0; o >>= 1) {
+        for (size_t i = 0; i < 64; ++i) b[i] = a[i] + a[i ^ o];
+        memcpy(a, b, sizeof(a));
+    }
+    return a[0];
+}
+
 int oracle_route(const float* hidden, size_t t, size_t h, const float* gate, size_t n_experts,
                  size_t top_k, int norm_topk, float routed_scale, uint32_t* idx, float* w,
                  float* probs) {
-    if (n_experts < top_k || top_k == 0 || n_experts > 4096) return ORACLE_E_SHAPE;
+    if (n_experts < top_k || top_k == 0 || n_experts > 64) return ORACLE_E_SHAPE;
     float* logit = (float*)malloc(n_experts * sizeof(float));
     double* ex = (double*)malloc(n_experts * sizeof(double));
     float* p = (float*)malloc(n_experts * sizeof(float));
@@ -249,11 +267,8 @@ int oracle_route(const float* hidden, size_t t, size_t h, const float* gate, siz
         double mx = -INFINITY;
         for (size_t e = 0; e < n_experts; ++e)
             if ((double)logit[e] > mx) mx = (double)logit[e];
-        double sum = 0.0;
-        for (size_t e = 0; e < n_experts; ++e) {
-            ex[e] = exp((double)logit[e] - mx);
-            sum += ex[e];
-        }
+        for (size_t e = 0; e < n_experts; ++e) ex[e] = exp((double)logit[e] - mx);
+        const double sum = butterfly_sum64(ex, n_experts);
         for (size_t e = 0; e < n_experts; ++e) p[e] = (float)(ex[e] / sum);
         if (probs) memcpy(probs + tok * n_experts, p, n_experts * sizeof(float));
 
