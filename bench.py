@@ -42,15 +42,48 @@ def log(msg: str) -> None:
 
 
 def traffic_for(kernel: str, workload: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
+    """HBM bytes per launch measured with rocprofv3 --pmc: FETCH_SIZE and
+    WRITE_SIZE (one run each) scaled by what the same counters read for a
+    512 MiB device-to-device copy (profiles/traffic.json, written by
+    franken_ocr_amd.rocprof_summary traffic), or None if not recorded."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text()).get(f"{kernel}@{workload}")
-    except Exception:
+        rec = json.loads(f.read_text()).get(f"{kernel}@{workload}")
+    except (OSError, ValueError):
         return None
+    return None if rec is None else rec.get("bytes_per_dispatch")
+
+
+def timed(ctx, step, steps: int):
+    """Time `steps` steps between two device synchronisations, then run the
+    same steps again with per-kernel HIP events. The events ride in each
+    kernel's dispatch packet (hipExtLaunchKernelGGL), so they measure the
+    kernel's own execution — they agree with rocprofv3's kernel trace — but
+    the completion signals they add slow the step as a whole, which is why
+    the throughput comes from the first, unprofiled pass."""
+    ctx.device_synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    for i in range(steps):
+        step(i)
+    prof = ctx.prof_read()
+    ctx.prof_enable(False)
+    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
+    return el, prof, kernels
+
+
+def kernel_us(prof: dict, name: str) -> float:
+    g = prof.get(name)
+    if not g or not g["count"]:
+        return float("nan")
+    return g["ms"] / g["count"] * 1e3
 
 
 # ---------------------------------------------------------------------------
@@ -96,32 +129,17 @@ def bench_moe(args, ctx):
     ctx.device_synchronize()
     # distinct experts actually routed, per copy (for algorithmic bytes)
     U = [len(np.unique(b.numpy())) for b in idx_bufs]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    ctx.device_synchronize()
-    el = time.perf_counter() - t0
+    el, prof, kernels = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     tok_s = T * args.steps / el
-
-    # per-kernel GPU time in a separate profiled pass (events between launches)
-    ctx.prof_enable(True)
-    ctx.prof_reset()
-    nprof = max(args.copies * 4, 32)
-    for i in range(nprof):
-        step(i)
-    prof = ctx.prof_read()
-    ctx.prof_enable(False)
 
     mean_u = float(np.mean([U[i % len(U)] for i in range(args.steps)]))
     pairs = T * K
     gate_up_bytes = mean_u * 2 * (I * H + I * 4) + T * H + T * 4 + pairs * I * 4
     layer_bytes = mean_u * (3 * I * H + 2 * I * 4 + H * 4) + E * H * 4 + 2 * T * H * 4
-    gu = prof.get("moe_gate_up", {"count": 1, "ms": float("nan")})
-    gu_ms = gu["ms"] / max(gu["count"], 1)
+    gu_ms = kernel_us(prof, "moe_gate_up") * 1e-3
     achieved = gate_up_bytes / (gu_ms * 1e-3) / 1e9
     layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
-    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
     log(f"U per copy {U}; per-kernel avg us {kernels}")
     return {
         "metric": "MoE-layer decode tokens/s + achieved HBM GB/s (% of 8 TB/s peak), 1 GPU",
@@ -197,24 +215,12 @@ def bench_lm_head(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    ctx.device_synchronize()
-    el = time.perf_counter() - t0
+    el, prof, kernels = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
-    ctx.prof_enable(True)
-    ctx.prof_reset()
-    for i in range(max(args.copies * 4, 24)):
-        step(i)
-    prof = ctx.prof_read()
-    ctx.prof_enable(False)
-    g = prof.get("lm_head_gemv", {"count": 1, "ms": float("nan")})
-    g_ms = g["ms"] / max(g["count"], 1)
+    g_ms = kernel_us(prof, "lm_head_gemv") * 1e-3
     gemv_bytes = N * Kd + N * 4 + M * Kd + M * 4 + M * N * 4
     total_bytes = gemv_bytes + M * Kd * 4 + M * 4
     achieved = gemv_bytes / (g_ms * 1e-3) / 1e9
-    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
     log(f"per-kernel avg us {kernels}")
     return {
         "metric": "LM-head int8 GEMV + argmax tokens/s (129280x1280), 1 GPU",
@@ -274,19 +280,8 @@ def bench_igemm(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    ctx.device_synchronize()
-    el = time.perf_counter() - t0
-    ctx.prof_enable(True)
-    ctx.prof_reset()
-    for i in range(256):
-        step(i)
-    prof = ctx.prof_read()
-    ctx.prof_enable(False)
-    g = prof["igemm_i8"]
-    g_ms = g["ms"] / g["count"]
+    el, prof, kernels = timed(ctx, step, args.steps)
+    g_ms = kernel_us(prof, "igemm_i8") * 1e-3
     nbytes = N * Kd + M * Kd + 2 * M * N * 4
     achieved = nbytes / (g_ms * 1e-3) / 1e9
     return {
@@ -296,6 +291,7 @@ def bench_igemm(args, ctx):
         "roofline": {"bound": "hbm", "kernel": "igemm_i8", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
+        "kernel_avg_us": kernels,
         "_cpu_inputs": (a, w[: N * Kd]),
     }
 
@@ -349,32 +345,55 @@ def bench_rswa(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    ctx.device_synchronize()
-    el = time.perf_counter() - t0
-    ctx.prof_enable(True)
-    ctx.prof_reset()
-    for i in range(max(copies * 8, 64)):
-        step(i)
-    prof = ctx.prof_read()
-    ctx.prof_enable(False)
-    g = prof["rswa_chunk"]
-    g_ms = g["ms"] / g["count"]
+    el, prof, kernels = timed(ctx, step, args.steps)
+    g_ms = kernel_us(prof, "rswa_chunk") * 1e-3
     keys = sum(G + r for r in ring_lens)
     nbytes = 2 * NH * keys * D * 4 + 2 * B * NH * D * 4
     achieved = nbytes / (g_ms * 1e-3) / 1e9
-    kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
     return {
         "metric": "R-SWA decode attention steps/s (B=8, G=1024, 10x128), 1 GPU",
         "value": round(args.steps / el, 1), "unit": "steps/s", "ms_per_step": round(el / args.steps * 1e3, 5),
         "dtype": "f32", "config": {"workload": "rswa", "streams": B, "ref_rows": G, "ring_lens": ring_lens,
                                    "cache_copies_rotated": copies},
         "roofline": {"bound": "hbm", "kernel": "rswa_chunk", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("rswa_chunk", "rswa"),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
         "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
+# ---------------------------------------------------------------------------
+# calibration: a plain device-to-device copy of known size (the reference
+# point for the FETCH_SIZE / WRITE_SIZE counters)
+# ---------------------------------------------------------------------------
+
+COPY_BYTES = 512 << 20
+
+
+def bench_copy(args, ctx):
+    src = ctx.empty((COPY_BYTES,), np.uint8)
+    dst = ctx.empty((COPY_BYTES,), np.uint8)
+
+    def step(i):
+        dst.copy_from_device(src)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    ctx.device_synchronize()
+    el = time.perf_counter() - t0
+    gbs = 2 * COPY_BYTES * args.steps / el / 1e9
+    return {
+        "metric": "device-to-device copy GB/s (read + write), 1 GPU",
+        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(el / args.steps * 1e3, 5), "dtype": "u8",
+        "config": {"workload": "copy", "bytes": COPY_BYTES},
+        "roofline": {"bound": "hbm", "kernel": "copyBuffer", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "_cpu_inputs": None,
     }
 
@@ -384,6 +403,7 @@ WORKLOADS = {
     "lm_head": (bench_lm_head, cpu_lm_head),
     "igemm": (bench_igemm, cpu_igemm),
     "rswa": (bench_rswa, None),
+    "copy": (bench_copy, None),
 }
 
 
@@ -402,7 +422,7 @@ def main() -> int:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
               file=sys.stderr)
         return 2
-    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4)}
+    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4), "copy": (1, 1)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

@@ -62,20 +62,29 @@ static bool fits_i32(const char* context, size_t v, const char* what, int32_t* s
     return true;
 }
 
+LaunchEvents& launch_events() {
+    static thread_local LaunchEvents le;
+    return le;
+}
+
 ProfScope::ProfScope(focr_hip_ctx* c, const char* n) : ctx(c), name(n) {
     if (ctx && ctx->prof) {
         start = ctx->take_event();
-        if (start) hipEventRecord(start, ctx->stream);
+        stop = ctx->take_event();
+        if (start && stop) launch_events() = LaunchEvents{start, stop, true, false};
     }
 }
 
 ProfScope::~ProfScope() {
-    if (ctx && ctx->prof && start) {
-        hipEvent_t stop = ctx->take_event();
-        if (stop) {
-            hipEventRecord(stop, ctx->stream);
-            ctx->pending.push_back({name, start, stop});
-        }
+    LaunchEvents& le = launch_events();
+    const bool used = le.used && le.stop == stop;
+    if (le.stop == stop) le = LaunchEvents{};
+    if (!start || !stop) return;
+    if (used) {
+        ctx->pending.push_back({name, start, stop});
+    } else {  // nothing launched (an error path): return the events
+        ctx->event_pool.push_back(start);
+        ctx->event_pool.push_back(stop);
     }
 }
 

@@ -3,6 +3,7 @@
 // and the host-side launch functions each kernel file exports.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -127,14 +128,37 @@ struct focr_hip_rswa {
 
 namespace focr {
 
-// RAII profiling bracket around one kernel launch on ctx->stream.
+// Profiling: while a ProfScope is open (and ctx->prof is on), the kernels
+// launched through FOCR_LAUNCH carry the scope's start/stop events in their
+// dispatch (hipExtLaunchKernelGGL), so the recorded interval is the GPU
+// execution of those kernels — first kernel's start to last kernel's end —
+// without the dispatch gap a separately recorded event would include.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool first = false, used = false;
+};
+LaunchEvents& launch_events();  // the calling thread's open scope, if any
+
 struct ProfScope {
     focr_hip_ctx* ctx;
     const char* name;
-    hipEvent_t start = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
     ProfScope(focr_hip_ctx* c, const char* n);
     ~ProfScope();
 };
+
+#define FOCR_LAUNCH(kernel, grid, block, lds, stream, ...)                                                  \
+    do {                                                                                                   \
+        focr::LaunchEvents& le_ = focr::launch_events();                                                   \
+        if (le_.stop) {                                                                                    \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, le_.first ? le_.start : nullptr, le_.stop, \
+                                  0, __VA_ARGS__);                                                          \
+            le_.first = false;                                                                             \
+            le_.used = true;                                                                               \
+        } else {                                                                                           \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                             \
+        }                                                                                                  \
+    } while (0)
 
 constexpr int kNumHeads = 10;
 constexpr int kHeadDim = 128;

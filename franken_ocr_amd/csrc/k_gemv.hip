@@ -179,7 +179,7 @@ int gemv_i8_nparts(int n, int cu_count) {
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
                                 float* a_scales, bool ties_even) {
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_rows_kernel, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales,
+    FOCR_LAUNCH(quantize_rows_kernel, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales,
                        ties_even ? 1 : 0);
     return hipGetLastError();
 }
@@ -198,7 +198,7 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
     while (mc < m) mc <<= 1;
 #define FOCR_GEMV_CASE(MCV)                                                                     \
     case MCV:                                                                                   \
-        hipLaunchKernelGGL((gemv_i8_kernel<MCV, 8>), dim3(grid), dim3(kThreads), lds, s, w, ws, \
+        FOCR_LAUNCH((gemv_i8_kernel<MCV, 8>), dim3(grid), dim3(kThreads), lds, s, w, ws, \
                            n, k, xq, a_scales, m, y, acc, arg_keys, tpb);                       \
         break;
     switch (mc) {
@@ -218,14 +218,14 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
 hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int nparts,
                                 uint32_t* argmax) {
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(m), dim3(kThreads), 0, s, keys, nparts, argmax);
+    FOCR_LAUNCH(argmax_reduce_kernel, dim3(m), dim3(kThreads), 0, s, keys, nparts, argmax);
     return hipGetLastError();
 }
 
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
                               int nparts, uint32_t* argmax) {
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(nparts, m), dim3(kThreads), 0, s, logits, n, keys);
+    FOCR_LAUNCH(argmax_partial_kernel, dim3(nparts, m), dim3(kThreads), 0, s, logits, n, keys);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_argmax_reduce(s, keys, m, nparts, argmax);

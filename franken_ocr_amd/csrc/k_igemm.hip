@@ -116,7 +116,7 @@ hipError_t launch_vec(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* 
     const size_t lds = static_cast<size_t>(mc) * k;
 #define FOCR_IGEMM_CASE(MCV)                                                                   \
     case MCV:                                                                                  \
-        hipLaunchKernelGGL((igemm_vec_kernel<kU8, MCV>), dim3(grid), dim3(kThreads), lds, s, a, \
+        FOCR_LAUNCH((igemm_vec_kernel<kU8, MCV>), dim3(grid), dim3(kThreads), lds, s, a, \
                            b, out, m, k, n);                                                   \
         break;
     switch (mc) {
@@ -148,9 +148,9 @@ hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const 
     const int tiles = (n + kGroups - 1) / kGroups;
     const int grid = tiles < 4096 ? tiles : 4096;
     if (a_unsigned)
-        hipLaunchKernelGGL(igemm_byte_kernel<true>, dim3(grid), dim3(kThreads), 0, s, a8, b, out, m, k, n);
+        FOCR_LAUNCH(igemm_byte_kernel<true>, dim3(grid), dim3(kThreads), 0, s, a8, b, out, m, k, n);
     else
-        hipLaunchKernelGGL(igemm_byte_kernel<false>, dim3(grid), dim3(kThreads), 0, s, a8, b, out, m, k, n);
+        FOCR_LAUNCH(igemm_byte_kernel<false>, dim3(grid), dim3(kThreads), 0, s, a8, b, out, m, k, n);
     return hipGetLastError();
 }
 

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64) void s4s8_packed_kernel(const int8_t* __restric
 hipError_t launch_unpack_i4(hipStream_t s, const uint8_t* b, size_t nbytes, int8_t* out) {
     if (nbytes == 0) return hipSuccess;
     const size_t grid = (nbytes + 255) / 256;
-    hipLaunchKernelGGL(unpack_i4_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, b, nbytes, out);
+    FOCR_LAUNCH(unpack_i4_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, b, nbytes, out);
     return hipGetLastError();
 }
 
@@ -74,7 +74,7 @@ hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,
     if (m == 0 || n == 0) return hipSuccess;
     if (k % 16 != 0 || (group != 16 && group != 32) || k % group != 0) return hipErrorInvalidValue;
     const dim3 grid(n, (m + 63) / 64);
-    hipLaunchKernelGGL(s4s8_packed_kernel, grid, dim3(64), 0, s, a, b, scales, group, m, k, n, out,
+    FOCR_LAUNCH(s4s8_packed_kernel, grid, dim3(64), 0, s, a, b, scales, group, m, k, n, out,
                        partials);
     return hipGetLastError();
 }

@@ -525,7 +525,7 @@ hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, cons
                               float* act) {
 #define FOCR_GU(J)                                                                                                 \
     case J:                                                                                                        \
-        hipLaunchKernelGGL((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, xq, \
+        FOCR_LAUNCH((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, xq, \
                            xs, wg, sg, wu, su, act, a.H, a.I, a.shared_T);                                         \
         break;
     switch (JC) {
@@ -542,7 +542,7 @@ hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const G
                            const float* act, const int8_t* wd, const float* sd, float* ybuf) {
 #define FOCR_DN(J)                                                                                              \
     case J:                                                                                                     \
-        hipLaunchKernelGGL((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, gates, \
+        FOCR_LAUNCH((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, gates, \
                            act, wd, sd, ybuf, a.H, a.I, a.shared_T);                                            \
         break;
     switch (JC) {
@@ -578,7 +578,7 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, unsigned long long* tok_mask) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+    FOCR_LAUNCH((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
                        d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, tok_mask);
     return hipGetLastError();
 }
@@ -616,7 +616,7 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const uint32_t* idx,
 
 hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out) {
     const dim3 grid((d.hidden + 255) / 256, d.t);
-    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k);
+    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k);
     return hipGetLastError();
 }
 

@@ -210,7 +210,7 @@ size_t rswa_partials_bytes(size_t n_streams, size_t max_keys) {
 hipError_t launch_rswa_write(hipStream_t s, const focr_hip_rswa* c, size_t s0,
                              const RswaStepArgs& a, const float* k_steps, const float* v_steps) {
     if (a.n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rswa_write_kernel, dim3(a.n, 2, H), dim3(D), 0, s, geom_of(c), s0, a,
+    FOCR_LAUNCH(rswa_write_kernel, dim3(a.n, 2, H), dim3(D), 0, s, geom_of(c), s0, a,
                        k_steps, v_steps);
     return hipGetLastError();
 }
@@ -223,14 +223,14 @@ hipError_t launch_rswa_attention(hipStream_t s, const focr_hip_rswa* c, size_t s
     const float scale = 1.0f / sqrtf(static_cast<float>(D));  // rswa.rs:52-55
     {
         ProfScope ps(ctx, "rswa_chunk");
-        hipLaunchKernelGGL(rswa_chunk_kernel, dim3(max_chunks, H, a.n), dim3(256), 0, s, geom_of(c),
+        FOCR_LAUNCH(rswa_chunk_kernel, dim3(max_chunks, H, a.n), dim3(256), 0, s, geom_of(c),
                            s0, a, q, scale, partials, max_chunks);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
         ProfScope ps(ctx, "rswa_merge");
-        hipLaunchKernelGGL(rswa_merge_kernel, dim3(H, a.n), dim3(D), 0, s, a, partials, max_chunks, out);
+        FOCR_LAUNCH(rswa_merge_kernel, dim3(H, a.n), dim3(D), 0, s, a, partials, max_chunks, out);
     }
     return hipGetLastError();
 }
