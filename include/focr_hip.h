@@ -254,9 +254,11 @@ int32_t focr_hip_rswa_regions(const focr_hip_rswa* cache, size_t stream, float**
                               float** ref_v, float** ring_k, float** ring_v);
 
 /* ---- profiling (decoder.rs:986-1024 prof counters, GPU-timed) -----------
- * When enabled, the engine ops bracket each kernel with HIP events on the
- * context stream; focr_hip_prof_read synchronises and returns, per kernel
- * name, the launch count and total milliseconds as a JSON object. */
+ * When enabled, every kernel launch carries HIP start/stop events in its
+ * dispatch (hipExtLaunchKernelGGL), timing the kernel's own execution;
+ * focr_hip_prof_read synchronises and returns, per kernel name, the launch
+ * count and total milliseconds as a JSON object. The extra completion
+ * signals slow a sequence of launches, so time throughput with it off. */
 int32_t focr_hip_prof_enable(focr_hip_ctx* ctx, int32_t on);
 int32_t focr_hip_prof_reset(focr_hip_ctx* ctx);
 int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap);
