@@ -447,12 +447,13 @@ struct MoeScratch {
     float* ybuf;
     float* shared_act;
     float* shared_y;
-    unsigned long long* tok_mask;
+    void* sel;
 };
 
 int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
     const size_t pairs = t * L->top_k;
-    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, pairs * 8 + t * 8 + 256));
+    const size_t sel_off = (pairs * 8 + 255) & ~static_cast<size_t>(255);
+    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, sel_off + moe_sel_bytes()));
     s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
     s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
@@ -463,7 +464,7 @@ int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bo
         return FOCR_HIP_E_OOM;
     s->idx = reinterpret_cast<uint32_t*>(route);
     s->gates = reinterpret_cast<float*>(route + pairs * 4);
-    s->tok_mask = reinterpret_cast<unsigned long long*>(route + pairs * 8);  // 8-byte aligned
+    s->sel = route ? route + sel_off : nullptr;
     s->shared_act = with_shared ? s->act + pairs * L->inter : nullptr;
     return FOCR_HIP_OK;
 }
@@ -489,11 +490,11 @@ int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
 
 int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t norm_topk,
                      float routed_scale, const MoeScratch& s, uint32_t* idx, float* gates, float* probs,
-                     unsigned long long* tok_mask) {
+                     void* sel) {
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     ProfScope ps(ctx, "moe_route");
     FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
-                                  probs, s.flag, tok_mask),
+                                  probs, s.flag, sel),
                  "route launch");
     return FOCR_HIP_OK;
 }
@@ -528,32 +529,31 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
     uint32_t* di = idx ? idx : s.idx;
     float* dg = gates ? gates : s.gates;
     hipStream_t str = ctx->stream;
-    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.tok_mask))) return st;
+    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.sel))) return st;
     hipError_t e = hipSuccess;
     {
         ProfScope ps(ctx, "moe_gate_up");
-        e = launch_moe_gate_up(str, d, di, s.tok_mask, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter,
-                               false);
+        e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false);
     }
     if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_down");
-        e = launch_moe_down(str, d, di, s.tok_mask, dg, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
+        e = launch_moe_down(str, d, s.sel, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
     }
     if (e == hipSuccess && with_shared) {
         {
             ProfScope ps(ctx, "moe_shared_gate_up");
-            e = launch_moe_gate_up(str, d, di, s.tok_mask, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
+            e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
                                    (int)L->shared_inter, true);
         }
         if (e == hipSuccess) {
             ProfScope ps(ctx, "moe_shared_down");
-            e = launch_moe_down(str, d, di, s.tok_mask, dg, s.shared_act, L->swd, L->ssd, s.shared_y,
-                                (int)L->shared_inter, true);
+            e = launch_moe_down(str, d, s.sel, s.shared_act, L->swd, L->ssd, s.shared_y, (int)L->shared_inter,
+                                true);
         }
     }
     if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_combine");
-        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, out);
+        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, s.flag, out);
     }
     if (e != hipSuccess) return hip_fail(e, "moe_decode launch");
     if (check_route) return check_route_flags(ctx, s.flag, t);

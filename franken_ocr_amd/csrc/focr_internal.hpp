@@ -188,20 +188,20 @@ struct MoeDims {
     int t, hidden, inter, n_experts, top_k;
 };
 // route writes idx/gates [t][top_k], flag[t] = 1 when token t has fewer than
-// top_k finite router scores, and tok_mask[t] = the token's expert bitmask
-// (tok_mask may be null: route only). gate_up/down find their expert and
-// pairs from tok_mask and idx.
+// top_k finite router scores, and — when sel is non-null — the routing in the
+// layout the expert kernels read (moe_sel_bytes() of device scratch: token
+// masks, per-expert slot and gate columns). Nothing is carried between calls.
+size_t moe_sel_bytes();
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, unsigned long long* tok_mask);
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const uint32_t* idx,
-                              const unsigned long long* tok_mask, const int8_t* xq, const float* xs,
+                            float* probs, int* flag, void* sel);
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
                               const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
                               int inter, bool shared);
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
-                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf,
-                           int inter, bool shared);
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out);
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
+                           const float* sd, float* ybuf, int inter, bool shared);
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y,
+                              const int* flag, float* out);
 
 // k_int4.hip
 hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,

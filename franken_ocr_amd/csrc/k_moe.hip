@@ -5,17 +5,18 @@
 //            to f32, quantize_row_i8 of the token row, f64 softmax rounded to
 //            f32, greedy top-k (= rank by (prob desc, index asc), NaN
 //            skipped; moe.rs:209-266), optional renorm and scale
-//            (moe.rs:226-236). Writes idx/gates [t][k] and the token's expert
-//            bitmask; no atomics, nothing carried between calls.
-//   gate_up  grid (active expert, row block): ORs the T token masks (one
-//            load per lane, a wave-level reduction), takes the a-th set bit
-//            as its expert, issues the expert's gate and up row loads, then
-//            stages the token rows in LDS and collects its (token, slot)
-//            pairs by scanning idx in pair order; writes
-//            act[t*K + j][r] = silu(g) * u (decoder.rs:1746-1752).
-//   down     grid (active expert, row block): issues the down row loads,
-//            collects the pairs the same way, re-quantizes each pair's act
-//            row into LDS (quantize_row_i8), writes y[t*K + j][r] =
+//            (moe.rs:226-236). Writes idx/gates [t][k] and the selection
+//            matrices slot[e][t] / gate[e][t]; no atomics, nothing carried
+//            between calls.
+//   gate_up  grid (active-expert slot a, row block): one ballot over the
+//            experts' slot rows gives the active set and the a-th expert;
+//            issues the expert's gate and up row loads, stages the token rows
+//            in LDS, takes its (token, slot) pairs from column e of the slot
+//            matrix in token order; writes act[t*K + j][r] = silu(g) * u
+//            (decoder.rs:1746-1752).
+//   down     grid (active-expert slot a, row block): issues the down row
+//            loads, collects the pairs the same way, re-quantizes each pair's
+//            act row into LDS (quantize_row_i8), writes y[t*K + j][r] =
 //            dequant * gate (decoder.rs:2244-2246).
 //   combine  out[t][c] = ((0 + y[t,0]) + y[t,1]) ... (+ shared), slot order
 //            (decoder.rs:2253-2261); deterministic, no atomics.
@@ -37,8 +38,17 @@ namespace {
 constexpr int kMaxT = 64;
 constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
-constexpr int kMaxPairs = kMaxT * kMaxK;
 constexpr int kPairStage = 32;  // pairs staged in LDS per pass
+
+// The step's routing in the layout the expert kernels consume, written by
+// route without atomics: slot[e][t] = 1 + the slot j at which token t chose
+// expert e, 0 if it did not (every entry is written each call: the token's
+// block writes column t for e < E, block 0 zeroes the rest); gate[e][t] =
+// that pair's gate (valid where slot != 0).
+struct MoeSel {
+    uint8_t* slot;  // [kMaxE][kMaxT]
+    float* gate;    // [kMaxE][kMaxT]
+};
 
 template <int LPR>
 __device__ __forceinline__ int reduce_lanes(int v) {
@@ -66,7 +76,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
-    unsigned long long* __restrict__ tok_mask) {
+    MoeSel sel) {
     __shared__ float4 s_x[512];
     __shared__ float s_logit[kMaxE];
     __shared__ __align__(16) float s_p[kMaxE];
@@ -183,10 +193,13 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         ahead += (q.z > pe || (q.z == pe && j0 + 2 < e)) ? 1 : 0;
         ahead += (q.w > pe || (q.w == pe && j0 + 3 < e)) ? 1 : 0;
         ahead = reduce16_add(ahead);
-        if (l == 0 && erow && pe == pe && ahead < K) {
+        const bool chosen = erow && pe == pe && ahead < K;
+        if (l == 0 && chosen) {
             s_sel_e[ahead] = e;
             s_sel_w[ahead] = pe;
         }
+        if (sel.slot && l == 0 && erow)
+            sel.slot[e * kMaxT + t] = static_cast<uint8_t>(chosen && s_nvalid >= K ? ahead + 1 : 0);
     }
     __syncthreads();
 
@@ -202,77 +215,67 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         if (norm_topk) w = w / den;
         idx_out[t * K + j] = static_cast<uint32_t>(ej);
         gates_out[t * K + j] = w * routed_scale;
-        if (j == 0) {
-            unsigned long long m = 0ull;
-            for (int jj = 0; jj < K; ++jj) m |= 1ull << (bad ? 0 : s_sel_e[jj]);
-            if (tok_mask) tok_mask[t] = m;
-            flag[t] = bad ? 1 : 0;
+        if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
+        if (j == 0) flag[t] = bad ? 1 : 0;
+    }
+    // block 0 zeroes the slot entries no token block owns (e >= E or t >= T)
+    if (sel.slot && t == 0) {
+        for (int i = threadIdx.x; i < kMaxE * kMaxT; i += kRouteThreads) {
+            const int ei = i / kMaxT, ti = i - ei * kMaxT;
+            if (ei >= E || ti >= static_cast<int>(gridDim.x)) sel.slot[i] = 0;
         }
     }
 }
 
-// Expert of this block: routed mode ORs the T token masks (every wave does
-// it, so no barrier is needed) and takes the a-th set bit; shared mode is one
-// expert whose pairs are the tokens. All loads here and below are issued
-// unconditionally from clamped addresses, with invalid lanes masked
-// arithmetically: a select between a load and a constant tends to become a
-// branch around the load with a full wait inside it, which serialises the
-// memory round trips these kernels depend on overlapping.
-__device__ __forceinline__ int block_expert(const unsigned long long* __restrict__ tok_mask, int T, int shared_T) {
+// Expert of this block: lane e loads expert e's 64-byte slot row (four
+// 16-byte loads in flight) and one ballot gives the set of experts with
+// pairs; the a-th set bit (a = blockIdx.x) is found with one more ballot.
+// Shared mode is one expert whose pairs are the tokens. Slots past the number
+// of active experts get -1.
+__device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T) {
     if (shared_T > 0) return 0;
     const int lane = threadIdx.x & 63;
-    unsigned long long m = tok_mask[lane < T ? lane : T - 1];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m |= __shfl_xor(m, o, 64);
-    // lane l holds bit l; the a-th set bit is the set lane with a set bits below
-    const bool set = (m >> lane) & 1ull;
+    const uint4* row = reinterpret_cast<const uint4*>(sel.slot + lane * kMaxT);
+    const uint4 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3];
+    const unsigned any = (r0.x | r0.y | r0.z | r0.w) | (r1.x | r1.y | r1.z | r1.w) | (r2.x | r2.y | r2.z | r2.w) |
+                         (r3.x | r3.y | r3.z | r3.w);
+    const unsigned long long m = __ballot(any != 0u);
     const int below = __popcll(m & ((1ull << lane) - 1ull));
-    const unsigned long long hit = __ballot(set && below == static_cast<int>(blockIdx.x));
+    const unsigned long long hit = __ballot(any != 0u && below == static_cast<int>(blockIdx.x));
     return hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
 }
 
-// Wave 0 collects the block's pairs in increasing pair id (t*K + j) from
-// idx [T*K <= 512], with their gates when gates is non-null (1.0 for the
-// shared expert); the caller synchronises before reading them.
-__device__ __forceinline__ void block_pairs(const uint32_t* __restrict__ idx, const float* __restrict__ gates, int T,
-                                            int K, int e, int shared_T, int* s_pid, int* s_tok, float* s_gate,
-                                            int* s_np) {
+// Wave 0 collects the block's pairs (t*K + j) in increasing token order from
+// column e of the slot matrix — one load per lane and one ballot — with their
+// gates when s_gate is non-null (1.0 for the shared expert). The caller
+// synchronises before reading them. All loads on these kernels' critical path
+// are issued unconditionally from clamped addresses, with invalid lanes masked
+// arithmetically: a select between a load and a constant tends to become a
+// branch around the load with a full wait inside it, which serialises the
+// memory round trips these kernels depend on overlapping.
+__device__ __forceinline__ void block_pairs(const MoeSel& sel, int T, int K, int e, int shared_T, int* s_pid,
+                                            int* s_tok, float* s_gate, int* s_np) {
     if (threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     if (shared_T > 0) {
-        for (int p = lane; p < shared_T; p += 64) {
-            s_pid[p] = p;
-            s_tok[p] = p;
-            if (gates) s_gate[p] = 1.0f;
+        if (lane < shared_T) {
+            s_pid[lane] = lane;
+            s_tok[lane] = lane;
+            if (s_gate) s_gate[lane] = 1.0f;
         }
         if (lane == 0) *s_np = shared_T;
         return;
     }
-    const int TK = T * K;
-    uint32_t v[kMaxPairs / 64];
-    float gv[kMaxPairs / 64];
-#pragma unroll
-    for (int q = 0; q < kMaxPairs / 64; ++q) {
-        const int pid = 64 * q + lane;
-        const int pc = pid < TK ? pid : TK - 1;
-        v[q] = idx[pc] | (pid < TK ? 0u : 0xFFFFFFFFu);
-        gv[q] = gates ? gates[pc] : 0.0f;
+    const int v = sel.slot[e * kMaxT + lane];  // zero for t >= T
+    const float g = s_gate ? sel.gate[e * kMaxT + lane] : 0.0f;
+    const unsigned long long m = __ballot(v != 0);
+    if (v != 0) {
+        const int pos = __popcll(m & ((1ull << lane) - 1ull));
+        s_pid[pos] = lane * K + v - 1;
+        s_tok[pos] = lane;
+        if (s_gate) s_gate[pos] = g;
     }
-    int base = 0;
-#pragma unroll
-    for (int q = 0; q < kMaxPairs / 64; ++q) {
-        const bool hit = v[q] == static_cast<uint32_t>(e);
-        const unsigned long long m = __ballot(hit);
-        if (hit) {
-            const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-            const int pid = 64 * q + lane;
-            s_pid[pos] = pid;
-            s_tok[pos] = pid / K;
-            if (gates) s_gate[pos] = gv[q];
-        }
-        base += __popcll(m);
-    }
-    if (lane == 0) *s_np = base;
+    if (lane == 0) *s_np = __popcll(m);
 }
 
 // Chunk c of a weight row, or zeros when c >= C (address clamped into the
@@ -332,17 +335,17 @@ constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
 // are then taken one at a time against the staged token rows.
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(
-    const uint32_t* __restrict__ idx, const unsigned long long* __restrict__ tok_mask, int T, int K,
+    const MoeSel sel, int T, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, const int8_t* __restrict__ wg,
     const float* __restrict__ sg, const int8_t* __restrict__ wu, const float* __restrict__ su,
     float* __restrict__ act, int H, int I, int shared_T) {
     extern __shared__ int4 lds_x[];  // [rows staged][H/16]
-    __shared__ int s_pid[kMaxPairs];
-    __shared__ int s_tok[kMaxPairs];
+    __shared__ int s_pid[kMaxT];
+    __shared__ int s_tok[kMaxT];
     __shared__ float s_xs[64];  // one per lane of the staging wave
     __shared__ int s_np;
     constexpr int G = 256 / LPR;  // rows per block
-    const int e = block_expert(tok_mask, T, shared_T);
+    const int e = block_expert(sel, shared_T);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
         const int tt = threadIdx.x < T ? threadIdx.x : T - 1;
         __builtin_amdgcn_global_load_lds((global_void_t*)(xs + tt), (lds_void_t*)s_xs, 4, 0, 0);
     }
-    block_pairs(idx, nullptr, T, K, e, shared_T, s_pid, s_tok, nullptr, &s_np);
+    block_pairs(sel, T, K, e, shared_T, s_pid, s_tok, nullptr, &s_np);
     __syncthreads();
     const int P = s_np;
 
@@ -410,17 +413,16 @@ constexpr int NQ = 16;  // act values per lane held in registers when a wave qua
 
 template <int LPR, int JC>
 __global__ __launch_bounds__(256) void moe_down_kernel(
-    const uint32_t* __restrict__ idx, const unsigned long long* __restrict__ tok_mask, int T, int K,
-    const float* __restrict__ gates, const float* __restrict__ act, const int8_t* __restrict__ wd,
+    const MoeSel sel, int T, int K, const float* __restrict__ act, const int8_t* __restrict__ wd,
     const float* __restrict__ sd, float* __restrict__ ybuf, int H, int I, int shared_T) {
     extern __shared__ int4 lds_a[];  // [kPairStage][I/16]
     __shared__ float lds_as[kPairStage];
-    __shared__ int s_pid[kMaxPairs];
-    __shared__ int s_tok[kMaxPairs];
-    __shared__ float s_gate[kMaxPairs];
+    __shared__ int s_pid[kMaxT];
+    __shared__ int s_tok[kMaxT];
+    __shared__ float s_gate[kMaxT];
     __shared__ int s_np;
     constexpr int G = 256 / LPR;
-    const int e = block_expert(tok_mask, T, shared_T);
+    const int e = block_expert(sel, shared_T);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
         for (int j = 0; j < JC; ++j) wv[j] = row_chunk(drow, lane + LPR * j, C);
     }
     const float sdr = sd[row];
-    block_pairs(idx, gates, T, K, e, shared_T, s_pid, s_tok, s_gate, &s_np);
+    block_pairs(sel, T, K, e, shared_T, s_pid, s_tok, s_gate, &s_np);
     __syncthreads();
     const int P = s_np;
     int8_t* lds_b = reinterpret_cast<int8_t*>(lds_a);
@@ -495,12 +497,20 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 }
 
 // ---- combine (slot order) ---------------------------------------------------------
+// A token whose routing failed (flag[t] != 0: fewer than top_k finite router
+// scores, reported to the caller as a routing error) has no pairs; its row is
+// written as zeros rather than left to stale buffers.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf,
                                                           const float* __restrict__ shared_y,
+                                                          const int* __restrict__ flag,
                                                           float* __restrict__ out, int H, int K) {
     const int t = blockIdx.y;
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= H) return;
+    if (flag[t]) {
+        out[static_cast<size_t>(t) * H + c] = 0.0f;
+        return;
+    }
     float v[kMaxK];
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j) v[j] = j < K ? ybuf[(static_cast<size_t>(t) * K + j) * H + c] : 0.0f;
@@ -514,8 +524,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 }
 
 struct GemvArgs {
-    const uint32_t* idx;
-    const unsigned long long* tok_mask;
+    MoeSel sel;
     int T, K, H, I, shared_T;
 };
 
@@ -523,10 +532,10 @@ template <int LPR>
 hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const int8_t* xq,
                               const float* xs, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
                               float* act) {
-#define FOCR_GU(J)                                                                                                 \
-    case J:                                                                                                        \
-        FOCR_LAUNCH((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, xq, \
-                           xs, wg, sg, wu, su, act, a.H, a.I, a.shared_T);                                         \
+#define FOCR_GU(J)                                                                                               \
+    case J:                                                                                                      \
+        FOCR_LAUNCH((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs, wg, sg, wu, \
+                    su, act, a.H, a.I, a.shared_T);                                                              \
         break;
     switch (JC) {
         FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
@@ -538,12 +547,12 @@ hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, cons
 }
 
 template <int LPR>
-hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const float* gates,
-                           const float* act, const int8_t* wd, const float* sd, float* ybuf) {
-#define FOCR_DN(J)                                                                                              \
-    case J:                                                                                                     \
-        FOCR_LAUNCH((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, a.idx, a.tok_mask, a.T, a.K, gates, \
-                           act, wd, sd, ybuf, a.H, a.I, a.shared_T);                                            \
+hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const float* act,
+                           const int8_t* wd, const float* sd, float* ybuf) {
+#define FOCR_DN(J)                                                                                           \
+    case J:                                                                                                  \
+        FOCR_LAUNCH((moe_down_kernel<LPR, J>), grid, dim3(256), lds, s, a.sel, a.T, a.K, act, wd, sd, ybuf, \
+                    a.H, a.I, a.shared_T);                                                                   \
         break;
     switch (JC) {
         FOCR_DN(1) FOCR_DN(2) FOCR_DN(3) FOCR_DN(4) FOCR_DN(5) FOCR_DN(6) FOCR_DN(7) FOCR_DN(8)
@@ -552,6 +561,12 @@ hipError_t launch_down_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const G
     }
 #undef FOCR_DN
     return hipGetLastError();
+}
+
+MoeSel sel_of(void* buf) {
+    char* b = static_cast<char*>(buf);
+    if (!b) return MoeSel{nullptr, nullptr};
+    return MoeSel{reinterpret_cast<uint8_t*>(b), reinterpret_cast<float*>(b + kMaxE * kMaxT)};
 }
 
 // Lanes per row for a K-byte row: 16 when the 16-byte chunk count is a
@@ -574,49 +589,51 @@ bool dims_ok(const MoeDims& d) {
 
 }  // namespace
 
+size_t moe_sel_bytes() { return kMaxE * kMaxT + kMaxE * kMaxT * 4; }
+
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, unsigned long long* tok_mask) {
+                            float* probs, int* flag, void* sel) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
-    FOCR_LAUNCH((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
-                       d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, tok_mask);
+    FOCR_LAUNCH((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden, d.n_experts,
+                d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel));
     return hipGetLastError();
 }
 
-hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
-                              const int8_t* xq, const float* xs, const int8_t* wg, const float* sg, const int8_t* wu,
-                              const float* su, float* act, int inter, bool shared) {
+hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
+                              const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
+                              int inter, bool shared) {
     int lpr, jc;
     pick_lpr(d.hidden, &lpr, &jc);
-    if (!dims_ok(d) || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    if (!dims_ok(d) || !sel || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (inter + rows_per_block - 1) / rows_per_block);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
     const size_t lds = (static_cast<size_t>(staged) * d.hidden + 1023) & ~static_cast<size_t>(1023);
-    const GemvArgs a{idx, tok_mask, d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
+    const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
     if (lpr == 16) return launch_gate_up_lpr<16>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
     return launch_gate_up_lpr<8>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
 }
 
-hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const uint32_t* idx, const unsigned long long* tok_mask,
-                           const float* gates, const float* act, const int8_t* wd, const float* sd, float* ybuf,
-                           int inter, bool shared) {
+hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
+                           const float* sd, float* ybuf, int inter, bool shared) {
     int lpr, jc;
     pick_lpr(inter, &lpr, &jc);
-    if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    if (!dims_ok(d) || !sel || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
     const dim3 grid(max_active, (d.hidden + rows_per_block - 1) / rows_per_block);
     const size_t lds = static_cast<size_t>(kPairStage) * inter;
-    const GemvArgs a{idx, tok_mask, d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
-    if (lpr == 16) return launch_down_lpr<16>(s, grid, lds, jc, a, gates, act, wd, sd, ybuf);
-    return launch_down_lpr<8>(s, grid, lds, jc, a, gates, act, wd, sd, ybuf);
+    const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
+    if (lpr == 16) return launch_down_lpr<16>(s, grid, lds, jc, a, act, wd, sd, ybuf);
+    return launch_down_lpr<8>(s, grid, lds, jc, a, act, wd, sd, ybuf);
 }
 
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y, float* out) {
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y,
+                              const int* flag, float* out) {
     const dim3 grid((d.hidden + 255) / 256, d.t);
-    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, out, d.hidden, d.top_k);
+    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, flag, out, d.hidden, d.top_k);
     return hipGetLastError();
 }
 
