@@ -10,6 +10,10 @@ and linked into franken_ocr_amd/libfocr_hip.so. Flags that matter for parity:
                       int4 group sums and the MoE combine are bit-reproducible.
 * -Xclang -target-feature -Xclang -packed-fp32-ops
                       keep the compiler from emitting packed-FP32 VALU ops.
+* -mllvm -amdgpu-mfma-vgpr-form
+                      MFMA results land in arch VGPRs: the int4 kernels'
+                      per-group f32 epilogue reads every MFMA output, and from
+                      AGPRs each read would cost an extra v_accvgpr_read.
 No -ffast-math: fp32 division and sqrt stay correctly rounded (the
 quantizer's amax/127 and 1/a_scale must match the CPU bit for bit).
 """
@@ -39,6 +43,8 @@ COMMON = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
     "-Wno-unused-value",

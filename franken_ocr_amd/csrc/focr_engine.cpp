@@ -560,6 +560,121 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
     return FOCR_HIP_OK;
 }
 
+// ---- int4 MoE layer (chunked prefill) ------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+void free_moe_i4(focr_hip_moe_layer_i4* L) {
+    if (!L->owned) return;
+    hipFree(L->wg);
+    hipFree(L->wu);
+    hipFree(L->wd);
+    hipFree(L->sg);
+    hipFree(L->su);
+    hipFree(L->sd);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_moe_layer_i4_create(focr_hip_ctx* ctx, size_t hidden, size_t inter, size_t n_experts, size_t group,
+                                     const uint8_t* wg, const float* sg, const uint8_t* wu, const float* su,
+                                     const uint8_t* wd, const float* sd, int32_t from_device,
+                                     focr_hip_moe_layer_i4** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "moe_layer_i4_create: null out");
+    *out = nullptr;
+    if (!wg || !sg || !wu || !su || !wd || !sd) return fail(FOCR_HIP_E_ARG, "moe_layer_i4_create: null pointer");
+    if (group != 16 && group != 32)
+        return fail(FOCR_HIP_E_SHAPE, fmt("igemm_s4s8_packed: group_size %zu must be 16 or 32", group));
+    if (n_experts < 1 || n_experts > 64)
+        return fail(FOCR_HIP_E_SHAPE, fmt("moe_layer_i4_create: gfx950 tier supports 1..=64 experts (got %zu)", n_experts));
+    if (hidden % 32 || inter % 32 || hidden == 0 || inter == 0 || hidden > 4096 || inter > 4096)
+        return fail(FOCR_HIP_E_SHAPE, fmt("moe_layer_i4_create: hidden/inter must be multiples of 32 in 32..=4096 "
+                                          "(got %zu, %zu)", hidden, inter));
+    if (from_device && (!aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(sg) || !aligned16(su) ||
+                        !aligned16(sd)))
+        return fail(FOCR_HIP_E_ARG, "moe_layer_i4_create: device arrays must be 16-byte aligned");
+    std::unique_ptr<focr_hip_moe_layer_i4> L(new focr_hip_moe_layer_i4());
+    L->ctx = ctx;
+    L->hidden = hidden;
+    L->inter = inter;
+    L->n_experts = n_experts;
+    L->group = group;
+    L->owned = !from_device;
+    const size_t E = n_experts;
+    int32_t st = FOCR_HIP_OK;
+    if ((st = upload(ctx, &L->wg, wg, E * inter * (hidden / 2), from_device, "w_gate")) ||
+        (st = upload(ctx, &L->sg, sg, E * inter * (hidden / group), from_device, "s_gate")) ||
+        (st = upload(ctx, &L->wu, wu, E * inter * (hidden / 2), from_device, "w_up")) ||
+        (st = upload(ctx, &L->su, su, E * inter * (hidden / group), from_device, "s_up")) ||
+        (st = upload(ctx, &L->wd, wd, E * hidden * (inter / 2), from_device, "w_down")) ||
+        (st = upload(ctx, &L->sd, sd, E * hidden * (inter / group), from_device, "s_down"))) {
+        hipStreamSynchronize(ctx->stream);
+        free_moe_i4(L.get());
+        return st;
+    }
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    *out = L.release();
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_layer_i4_free(focr_hip_moe_layer_i4* L) {
+    if (!L) return FOCR_HIP_OK;
+    hipSetDevice(L->ctx->device);
+    hipStreamSynchronize(L->ctx->stream);
+    free_moe_i4(L);
+    delete L;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_prefill_i4(focr_hip_ctx* ctx, const focr_hip_moe_layer_i4* L, const float* x, size_t t,
+                                size_t top_k, const uint32_t* idx, const float* gates, float* out,
+                                int32_t check_idx) {
+    ENGINE_CTX(ctx);
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "moe_prefill_i4: null moe layer");
+    if (!x || !idx || !gates || !out) return fail(FOCR_HIP_E_ARG, "moe_prefill_i4: null pointer");
+    if (top_k < 1 || top_k > 8) return fail(FOCR_HIP_E_SHAPE, fmt("moe_prefill_i4: top_k %zu outside 1..=8", top_k));
+    if (t < 1 || t > 16384) return fail(FOCR_HIP_E_SHAPE, fmt("moe_prefill_i4: t %zu outside 1..=16384", t));
+    const size_t H = L->hidden, I = L->inter, TK = t * top_k;
+    MoeI4Scratch w;
+    char* a = static_cast<char*>(ctx->scratch_get(kScrI4, TK * I * sizeof(float) + TK * H * sizeof(float)));
+    char* b = static_cast<char*>(ctx->scratch_get(
+        kScrI4b, t * H + 256 + t * 4 + 256 + TK * I + 256 + TK * 4 + 256 +
+                     (moe_i4_plan_ints(static_cast<int>(TK), static_cast<int>(L->n_experts)) + 1) * sizeof(int)));
+    if (!a || !b) return FOCR_HIP_E_OOM;
+    auto take = [](char*& p, size_t bytes) {
+        char* r = p;
+        p += (bytes + 255) & ~static_cast<size_t>(255);
+        return r;
+    };
+    w.act = reinterpret_cast<float*>(a);
+    w.ybuf = reinterpret_cast<float*>(a + TK * I * sizeof(float));
+    w.xq = reinterpret_cast<int8_t*>(take(b, t * H));
+    w.xs = reinterpret_cast<float*>(take(b, t * 4));
+    w.aq = reinterpret_cast<int8_t*>(take(b, TK * I));
+    w.as = reinterpret_cast<float*>(take(b, TK * 4));
+    w.plan = reinterpret_cast<int*>(b);
+    w.err = w.plan + moe_i4_plan_ints(static_cast<int>(TK), static_cast<int>(L->n_experts));
+    FOCR_HIP_TRY(launch_moe_prefill_i4(ctx->stream, L, x, static_cast<int>(t), static_cast<int>(top_k), idx, gates, out,
+                                       w, ctx),
+                 "moe_prefill_i4 launch");
+    if (check_idx) {
+        int err = 0;
+        FOCR_HIP_TRY(hipMemcpyAsync(&err, w.err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H err");
+        FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        if (err)
+            return fail(FOCR_HIP_E_SHAPE,
+                        fmt("moe_prefill_i4: expert index out of range (n_experts %zu)", L->n_experts));
+    }
+    return FOCR_HIP_OK;
+}
+
 // ---- R-SWA --------------------------------------------------------------------
 
 int32_t focr_hip_rswa_create(focr_hip_ctx* ctx, size_t n_streams, size_t ref_capacity, focr_hip_rswa** out) {

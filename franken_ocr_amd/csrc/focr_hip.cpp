@@ -353,6 +353,19 @@ int32_t s4_contract(const char* name, const void* a, size_t a_len, const void* b
     return FOCR_HIP_OK;
 }
 
+// The int4 packed GEMM on the matrix cores when the shape allows it (group
+// 16/32, k a multiple of 32 up to 4096), else the per-lane kernel; both give
+// the reference's f32 result bit for bit.
+hipError_t launch_s4s8_any(focr_hip_ctx* ctx, const int8_t* a, const uint8_t* b, const float* scales, int group,
+                           int m, int k, int n, float* out) {
+    if (s4_mfma_supported(group, k)) {
+        ProfScope ps(ctx, "s4s8_mfma");
+        return launch_s4s8_mfma(ctx->stream, a, b, scales, group, m, k, n, out);
+    }
+    ProfScope ps(ctx, "s4s8_packed");
+    return launch_s4s8_packed(ctx->stream, a, b, scales, group, m, k, n, out, nullptr);
+}
+
 int32_t s4s8_host(focr_hip_ctx* ctx, const char* name, const int8_t* a, size_t a_len, const uint8_t* b,
                   size_t b_len, const float* scales, size_t s_len, size_t group, size_t m, size_t k, size_t n,
                   float* out, size_t out_len, int32_t* partials, size_t partials_len) {
@@ -384,11 +397,16 @@ int32_t s4s8_host(focr_hip_ctx* ctx, const char* name, const int8_t* a, size_t a
     float* fout = debug ? reinterpret_cast<float*>(static_cast<char*>(dout) + m * n * groups * sizeof(int32_t))
                         : static_cast<float*>(dout);
     int32_t* dpart = debug ? static_cast<int32_t*>(dout) : nullptr;
-    {
+    if (debug) {
         ProfScope ps(ctx, "s4s8_packed");
         FOCR_HIP_TRY(launch_s4s8_packed(s, static_cast<const int8_t*>(da), static_cast<const uint8_t*>(db),
                                         static_cast<const float*>(ds), static_cast<int>(group), static_cast<int>(m),
                                         static_cast<int>(k), static_cast<int>(n), fout, dpart),
+                     "s4s8 kernel launch");
+    } else {
+        FOCR_HIP_TRY(launch_s4s8_any(ctx, static_cast<const int8_t*>(da), static_cast<const uint8_t*>(db),
+                                     static_cast<const float*>(ds), static_cast<int>(group), static_cast<int>(m),
+                                     static_cast<int>(k), static_cast<int>(n), fout),
                      "s4s8 kernel launch");
     }
     if (debug)
@@ -499,8 +517,8 @@ int32_t focr_hip_igemm_s4s8_packed_dev(focr_hip_ctx* ctx, const int8_t* a, const
     int32_t st = s4_contract("igemm_s4s8_packed", a, m * k, b_packed, n * (k / 2), scales,
                              (group == 16 || group == 32) ? n * (k / group) : 0, group, m, k, n, out, m * n, true);
     if (st) return st;
-    ProfScope ps(ctx, "s4s8_packed");
-    FOCR_HIP_TRY(launch_s4s8_packed(ctx->stream, a, b_packed, scales, (int)group, (int)m, (int)k, (int)n, out, nullptr),
+    if (m * n == 0) return FOCR_HIP_OK;
+    FOCR_HIP_TRY(launch_s4s8_any(ctx, a, b_packed, scales, (int)group, (int)m, (int)k, (int)n, out),
                  "s4s8 kernel launch");
     return FOCR_HIP_OK;
 }

@@ -208,10 +208,29 @@ hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,
                               const float* scales, int group, int m, int k, int n, float* out,
                               int32_t* partials);
 hipError_t launch_unpack_i4(hipStream_t s, const uint8_t* b, size_t nbytes, int8_t* out);
-hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x,
-                                 int t, int top_k, const uint32_t* idx, const float* gates,
-                                 float* out, void* scratch_a, void* scratch_b, size_t* need_a,
-                                 size_t* need_b, focr_hip_ctx* ctx);
+
+// k_s4mfma.hip — int4 x int8 GEMMs on the matrix cores and the int4 prefill
+// MoE. The drop-in path uses the MFMA kernel when s4_mfma_supported().
+bool s4_mfma_supported(int group, int k);
+hipError_t launch_s4s8_mfma(hipStream_t s, const int8_t* a, const uint8_t* b, const float* scales, int group, int m,
+                            int k, int n, float* out);
+// Device scratch of one prefill call (t tokens, top_k slots, TK = t*top_k):
+// xq [t][H] i8, xs [t], act [TK][I] f32, aq [TK][I] i8, as [TK], ybuf
+// [TK][H] f32, plan moe_i4_plan_ints(TK, E) ints, err one int.
+struct MoeI4Scratch {
+    int8_t* xq;
+    float* xs;
+    float* act;
+    int8_t* aq;
+    float* as;
+    float* ybuf;
+    int* plan;
+    int* err;
+};
+size_t moe_i4_plan_ints(int tk, int n_experts);
+hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x, int t, int top_k,
+                                 const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
+                                 focr_hip_ctx* ctx);
 
 // k_rswa.hip
 struct RswaStepArgs {

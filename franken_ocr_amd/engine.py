@@ -172,6 +172,52 @@ class MoeLayer:
             pass
 
 
+class MoeLayerI4:
+    """A MoE layer of int4 experts for chunked prefill, uploaded once.
+
+    Host arrays (simd::int4 packed layout, low nibble = even k): wg/wu
+    [E, inter, hidden/2] u8 with sg/su [E, inter, hidden/group] f32; wd
+    [E, hidden, inter/2] u8 with sd [E, hidden, inter/group]. DeviceArrays are
+    borrowed instead of copied.
+    """
+
+    def __init__(self, hidden: int, inter: int, n_experts: int, group: int, wg, sg, wu, su, wd, sd,
+                 ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.hidden, self.inter, self.n_experts, self.group = int(hidden), int(inter), int(n_experts), int(group)
+        self._h = C.c_void_p()
+        arrs = [wg, sg, wu, su, wd, sd]
+        from_dev = isinstance(wg, DeviceArray)
+        if from_dev:
+            self._keep = arrs
+            ptrs = [a.c_ptr for a in arrs]
+        else:
+            dts = [np.uint8, np.float32, np.uint8, np.float32, np.uint8, np.float32]
+            host = [np.ascontiguousarray(a, dtype=dt) for a, dt in zip(arrs, dts)]
+            ptrs = [_p(a) for a in host]
+        _abi.call("focr_hip_moe_layer_i4_create", self.ctx.handle, self.hidden, self.inter, self.n_experts,
+                  self.group, *ptrs, 1 if from_dev else 0, C.byref(self._h))
+
+    def prefill(self, x: DeviceArray, idx: DeviceArray, gates: DeviceArray, out: DeviceArray,
+                check_idx: bool = True) -> None:
+        """decoder.rs:2142-2181 grouped MoE over int4 experts for x [t, hidden]
+        with routing idx/gates [t, top_k]; out [t, hidden]."""
+        t, top_k = idx.shape
+        _abi.call("focr_hip_moe_prefill_i4", self.ctx.handle, self._h, x.c_ptr, t, top_k, idx.c_ptr, gates.c_ptr,
+                  out.c_ptr, 1 if check_idx else 0)
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_moe_layer_i4_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class RingCache:
     """``n_streams`` R-SWA ring caches of one layer on the device."""
 

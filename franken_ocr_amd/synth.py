@@ -67,3 +67,29 @@ def int_uniform(seed: int, n: int, lo: int, hi: int) -> np.ndarray:
     """Integers uniform in [lo, hi] (inclusive)."""
     span = np.uint64(hi - lo + 1)
     return (u64(seed, n) % span).astype(np.int64) + lo
+
+
+def zipf_routing(seed: int, t: int, n_experts: int = 64, top_k: int = 6, s: float = 1.1):
+    """Synthetic prefill routing: per token, top_k distinct experts drawn
+    without replacement from Zipf(s) over ranks 1..n_experts (p_r ∝ r^-s),
+    through a seeded rank -> expert-id permutation; gates U(0.1, 1)
+    renormalised to sum 1 in f32. Returns idx [t, top_k] u32, gates
+    [t, top_k] f32. Deterministic in (seed, t, n_experts, top_k, s)."""
+    perm = np.argsort(u64(seed, n_experts), kind="stable")  # rank -> expert id
+    w = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    draws = (u64(seed + 1, t * top_k) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+    idx = np.zeros((t, top_k), np.uint32)
+    for tok in range(t):
+        avail = np.ones(n_experts, bool)
+        for j in range(top_k):
+            p = np.where(avail, w, 0.0)
+            c = np.cumsum(p)
+            r = int(np.searchsorted(c, draws[tok * top_k + j] * c[-1], side="right"))
+            r = min(r, n_experts - 1)
+            while not avail[r]:  # guards the c[-1] edge only
+                r -= 1
+            avail[r] = False
+            idx[tok, j] = perm[r]
+    g = f32_uniform(seed + 2, t * top_k, 0.1, 1.0).reshape(t, top_k)
+    gates = (g / g.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    return idx, gates

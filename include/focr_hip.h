@@ -50,6 +50,7 @@ extern "C" {
 typedef struct focr_hip_ctx focr_hip_ctx;
 typedef struct focr_hip_qint8 focr_hip_qint8;
 typedef struct focr_hip_moe_layer focr_hip_moe_layer;
+typedef struct focr_hip_moe_layer_i4 focr_hip_moe_layer_i4;
 typedef struct focr_hip_rswa focr_hip_rswa;
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -217,6 +218,32 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
 int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
                            const float* hidden, size_t t, int32_t norm_topk, float routed_scale,
                            uint32_t* idx, float* gates, float* probs);
+
+/* ---- int4 MoE layer for chunked prefill ----------------------------------
+ * Experts as simd::int4 packed weights (int4.rs:304-343 layout, low nibble =
+ * even k): gate/up [E][inter][hidden/2] with group scales
+ * [E][inter][hidden/group], down [E][hidden][inter/2] with
+ * [E][hidden][inter/group]; group in {16, 32}; hidden, inter multiples of 32
+ * up to 4096. from_device as focr_hip_moe_layer_create. */
+int32_t focr_hip_moe_layer_i4_create(focr_hip_ctx* ctx, size_t hidden, size_t inter,
+                                     size_t n_experts, size_t group, const uint8_t* wg,
+                                     const float* sg, const uint8_t* wu, const float* su,
+                                     const uint8_t* wd, const float* sd, int32_t from_device,
+                                     focr_hip_moe_layer_i4** out);
+int32_t focr_hip_moe_layer_i4_free(focr_hip_moe_layer_i4* layer);
+/* The grouped MoE block of decoder.rs:2142-2181 (moe_block_i8) over int4
+ * experts, for t prefill rows with a given routing: x [t, hidden] f32; idx,
+ * gates [t, top_k] (routing from moe::route or any other source). Per row:
+ * quantize_row_i8_te (decoder.rs:1647-1656); per member (token, slot) of
+ * expert e in (token, slot) order: g, u = int4 GEMMs (int4.rs:304-343 group
+ * rule, exact) times the row scale, act = silu(g) * u, requantized with the
+ * ties-even rule, y = int4 GEMM times the act scale; out[t] = sum of
+ * gate * y over the token's members in ascending expert order. Device
+ * pointers; t <= 16384, top_k <= 8. With check_idx = 1 the call synchronises
+ * and returns E_SHAPE for an expert index >= n_experts. */
+int32_t focr_hip_moe_prefill_i4(focr_hip_ctx* ctx, const focr_hip_moe_layer_i4* layer,
+                                const float* x, size_t t, size_t top_k, const uint32_t* idx,
+                                const float* gates, float* out, int32_t check_idx);
 
 /* ---- R-SWA ring KV cache (rswa.rs:121-152 RingCache, :645-824 batched) ---
  * n_streams independent caches of one layer, f32, head-major per stream:

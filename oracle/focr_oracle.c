@@ -464,7 +464,8 @@ int oracle_s4s8_group_i32(const int8_t* a, const uint8_t* b_packed, size_t group
  * prefill ties-even rule (decoder.rs:1647-1656); each projection is the int4
  * kernel contract (int4.rs:304-343) times the row's activation scale; the
  * grouped structure and ascending-expert scatter `out[t] += w * y` follow
- * moe_block_i8 (decoder.rs:2142-2181). Expert e: wg/wu packed [e][inter][h/2],
+ * moe_block_i8 (decoder.rs:2142-2181): members of expert e in (token, slot)
+ * order, one output row each. Expert e: wg/wu packed [e][inter][h/2],
  * sg/su [e][inter][h/group], wd [e][h][inter/2], sd [e][h][inter/group]. */
 int oracle_moe_prefill_i4(const float* x, size_t t, size_t h, size_t inter, size_t n_experts,
                           size_t top_k, const uint32_t* idx, const float* gates, size_t group,
@@ -488,7 +489,6 @@ int oracle_moe_prefill_i4(const float* x, size_t t, size_t h, size_t inter, size
             for (j = 0; j < top_k; ++j)
                 if (idx[tok * top_k + j] == e) break;
             if (j == top_k) continue;
-            float wj = gates[tok * top_k + j];
             const int8_t* xr = xq + tok * h;
             oracle_igemm_s4s8_packed(xr, wg + e * inter * (h / 2), sg + e * inter * gh, group, 1,
                                      h, inter, g);
@@ -502,11 +502,17 @@ int oracle_moe_prefill_i4(const float* x, size_t t, size_t h, size_t inter, size
             float as2 = oracle_quantize_row_i8_te(act, inter, aq);
             oracle_igemm_s4s8_packed(aq, wd + e * h * (inter / 2), sd + e * h * gi, group, 1,
                                      inter, h, y);
+            /* every slot of this token routed to e is a member (decoder.rs:2156-2160
+             * pushes (t, w) per slot), added in slot order */
             float* o = out + tok * h;
-            for (size_t c = 0; c < h; ++c) {
-                float yv = y[c] * as2;
-                float p = wj * yv;
-                o[c] = o[c] + p;
+            for (; j < top_k; ++j) {
+                if (idx[tok * top_k + j] != e) continue;
+                const float wj = gates[tok * top_k + j];
+                for (size_t c = 0; c < h; ++c) {
+                    float yv = y[c] * as2;
+                    float p = wj * yv;
+                    o[c] = o[c] + p;
+                }
             }
         }
     }
