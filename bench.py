@@ -365,6 +365,97 @@ def bench_rswa(args, ctx):
 
 
 # ---------------------------------------------------------------------------
+# config 4: int4 chunked-prefill MoE expert GEMMs (matrix cores)
+# ---------------------------------------------------------------------------
+
+MFMA_INT8_PEAK_TOPS = 5000.0  # dense int8, MI355X
+
+
+def make_i4_layer(seed: int, group: int = 32):
+    from franken_ocr_amd import synth
+
+    wg = synth.bytes_uniform(synth.seed_of(seed), E * I * H // 2)
+    wu = synth.bytes_uniform(synth.seed_of(seed + 1), E * I * H // 2)
+    wd = synth.bytes_uniform(synth.seed_of(seed + 2), E * H * I // 2)
+    sg = synth.f32_uniform(synth.seed_of(seed + 3), E * I * (H // group), 1e-3, 2e-2)
+    su = synth.f32_uniform(synth.seed_of(seed + 4), E * I * (H // group), 1e-3, 2e-2)
+    sd = synth.f32_uniform(synth.seed_of(seed + 5), E * H * (I // group), 1e-3, 2e-2)
+    return wg, sg, wu, su, wd, sd
+
+
+def bench_prefill_i4(args, ctx):
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import MoeLayerI4
+
+    T, group = args.tokens, 32
+    log(f"moe_prefill_i4: M={T} tokens, top-{K}, Zipf(1.1) routing, group {group}, {args.copies} layer copies")
+    host = make_i4_layer(300, group)
+    layers = [MoeLayerI4(H, I, E, group, *host, ctx=ctx) for _ in range(args.copies)]
+    x = synth.f32_normal(synth.seed_of(350), T * H).reshape(T, H)
+    idx, gates = synth.zipf_routing(synth.seed_of(360), T, E, K)
+    dx, di, dg = ctx.to_device(x), ctx.to_device(idx), ctx.to_device(gates)
+    dout = ctx.empty((T, H), np.float32)
+
+    def step(i):
+        layers[i % len(layers)].prefill(dx, di, dg, dout, check_idx=False)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    pairs = T * K
+    gu_ops = 2.0 * pairs * 2 * I * H
+    dn_ops = 2.0 * pairs * H * I
+    gu_us, dn_us = kernel_us(prof, "i4_gate_up"), kernel_us(prof, "i4_down")
+    gu_tops = gu_ops / (gu_us * 1e-6) / 1e12
+    layer_tops = (gu_ops + dn_ops) / (ms * 1e-3) / 1e12
+    counts = np.bincount(idx.ravel(), minlength=E)
+    wbytes = int((counts > 0).sum()) * (2 * I * H // 2 + H * I // 2 + 4 * (2 * I * (H // group) + H * (I // group)))
+    # warm: one layer, its 137.6 MB resident in the 256 MB Infinity Cache
+    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False),
+                                    max(args.steps // 2, 10))
+    log(f"per-kernel avg us {kernels}; warm {kernels_w}")
+    return {
+        "metric": "int4 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
+        "value": round(T * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int4xint8",
+        "config": {"workload": "moe_prefill_i4", "tokens": T, "hidden": H, "inter": I, "experts": E, "top_k": K,
+                   "group": group, "routing": "zipf(1.1) without replacement", "layer_copies_rotated": args.copies,
+                   "tokens_per_expert_max": int(counts.max()), "experts_hit": int((counts > 0).sum())},
+        "roofline": {"bound": "mfma", "kernel": "i4_gate_up", "achieved": round(gu_tops, 2),
+                     "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(gu_tops / MFMA_INT8_PEAK_TOPS, 4),
+                     "traffic": traffic_for("i4_gate_up", f"moe_prefill_i4_m{T}"),
+                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3)},
+        "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
+                       "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
+                       "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                       "warm_ms_per_step": round(el_w / max(args.steps // 2, 10) * 1e3, 5)},
+        "kernel_avg_us": kernels,
+        "kernel_avg_us_warm": kernels_w,
+        "_cpu_inputs": (x, idx, gates, host),
+    }
+
+
+def cpu_prefill_i4(args, inputs):
+    from oracle import pyoracle
+
+    x, idx, gates, host = inputs
+    n, t0, chunk = 0, time.perf_counter(), 8
+    while True:
+        lo = (n * chunk) % x.shape[0]
+        st, _, _, _ = pyoracle.moe_prefill_i4(x[lo:lo + chunk], idx[lo:lo + chunk], gates[lo:lo + chunk], 32, *host,
+                                              E, I)
+        assert st == 0
+        n += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(n * chunk / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "tier": "scalar (the reference has no x86 int4 kernel, int4.rs:454-460)",
+            "sample": f"{n} chunks of {chunk} tokens of the same layer and routing, {el:.1f} s, single thread"}
+
+
+# ---------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size (the reference
 # point for the FETCH_SIZE / WRITE_SIZE counters)
 # ---------------------------------------------------------------------------
@@ -404,6 +495,7 @@ WORKLOADS = {
     "igemm": (bench_igemm, cpu_igemm),
     "rswa": (bench_rswa, None),
     "copy": (bench_copy, None),
+    "moe_prefill_i4": (bench_prefill_i4, cpu_prefill_i4),
 }
 
 
@@ -422,7 +514,8 @@ def main() -> int:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
               file=sys.stderr)
         return 2
-    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4), "copy": (1, 1)}
+    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4), "copy": (1, 1),
+                "moe_prefill_i4": (512, 3)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

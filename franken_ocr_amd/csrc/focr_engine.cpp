@@ -600,26 +600,51 @@ int32_t focr_hip_moe_layer_i4_create(focr_hip_ctx* ctx, size_t hidden, size_t in
     if (from_device && (!aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(sg) || !aligned16(su) ||
                         !aligned16(sd)))
         return fail(FOCR_HIP_E_ARG, "moe_layer_i4_create: device arrays must be 16-byte aligned");
+    // The layer always owns its weights, in the MFMA-tiled layout: the
+    // reference-layout arrays (uploaded to staging, or the caller's device
+    // arrays) are re-tiled once on the device.
     std::unique_ptr<focr_hip_moe_layer_i4> L(new focr_hip_moe_layer_i4());
     L->ctx = ctx;
     L->hidden = hidden;
     L->inter = inter;
     L->n_experts = n_experts;
     L->group = group;
-    L->owned = !from_device;
+    L->owned = true;
     const size_t E = n_experts;
+    const size_t nb_gu = E * inter * (hidden / 2), ns_gu = E * inter * (hidden / group);
+    const size_t nb_d = E * hidden * (inter / 2), ns_d = E * hidden * (inter / group);
+    struct Src {
+        const uint8_t* b;
+        const float* s;
+        size_t nb, ns;
+        uint8_t** bt;
+        float** st;
+        int n, k;
+    } srcs[3] = {{wg, sg, nb_gu, ns_gu, &L->wg, &L->sg, (int)inter, (int)hidden},
+                 {wu, su, nb_gu, ns_gu, &L->wu, &L->su, (int)inter, (int)hidden},
+                 {wd, sd, nb_d, ns_d, &L->wd, &L->sd, (int)hidden, (int)inter}};
     int32_t st = FOCR_HIP_OK;
-    if ((st = upload(ctx, &L->wg, wg, E * inter * (hidden / 2), from_device, "w_gate")) ||
-        (st = upload(ctx, &L->sg, sg, E * inter * (hidden / group), from_device, "s_gate")) ||
-        (st = upload(ctx, &L->wu, wu, E * inter * (hidden / 2), from_device, "w_up")) ||
-        (st = upload(ctx, &L->su, su, E * inter * (hidden / group), from_device, "s_up")) ||
-        (st = upload(ctx, &L->wd, wd, E * hidden * (inter / 2), from_device, "w_down")) ||
-        (st = upload(ctx, &L->sd, sd, E * hidden * (inter / group), from_device, "s_down"))) {
+    for (auto& m : srcs) {
+        uint8_t* sb = nullptr;  // reference-layout source (staging copy, or the caller's array)
+        float* ss = nullptr;
+        st = upload(ctx, &sb, m.b, m.nb, from_device, "int4 weights");
+        if (!st) st = upload(ctx, &ss, m.s, m.ns, from_device, "int4 scales");
+        hipError_t e = hipSuccess;
+        if (!st) e = hipMalloc(reinterpret_cast<void**>(m.bt), m.nb + s4_tile_pad_bytes());
+        if (!st && e == hipSuccess)
+            e = hipMalloc(reinterpret_cast<void**>(m.st), m.ns * sizeof(float) + s4_tile_pad_bytes());
+        if (!st && e == hipSuccess)
+            e = launch_retile_i4(ctx->stream, sb, ss, (int)E, m.n, m.k, (int)group, *m.bt, *m.st);
         hipStreamSynchronize(ctx->stream);
-        free_moe_i4(L.get());
-        return st;
+        if (!from_device) {
+            hipFree(sb);
+            hipFree(ss);
+        }
+        if (st || e != hipSuccess) {
+            free_moe_i4(L.get());
+            return st ? st : hip_fail(e, "moe_layer_i4_create retile");
+        }
     }
-    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     *out = L.release();
     return FOCR_HIP_OK;
 }

@@ -212,6 +212,7 @@ hipError_t launch_unpack_i4(hipStream_t s, const uint8_t* b, size_t nbytes, int8
 // k_s4mfma.hip — int4 x int8 GEMMs on the matrix cores and the int4 prefill
 // MoE. The drop-in path uses the MFMA kernel when s4_mfma_supported().
 bool s4_mfma_supported(int group, int k);
+size_t s4_tile_pad_bytes();
 hipError_t launch_s4s8_mfma(hipStream_t s, const int8_t* a, const uint8_t* b, const float* scales, int group, int m,
                             int k, int n, float* out);
 // Device scratch of one prefill call (t tokens, top_k slots, TK = t*top_k):
@@ -228,6 +229,11 @@ struct MoeI4Scratch {
     int* err;
 };
 size_t moe_i4_plan_ints(int tk, int n_experts);
+// The int4 layer keeps its experts in the MFMA-tiled layout: b [E][n][k/2]
+// packed and sc [E][n][k/group] are copied into b_tiled / s_tiled (same sizes,
+// each allocation followed by s4_tile_pad_bytes() of readable padding).
+hipError_t launch_retile_i4(hipStream_t s, const uint8_t* b, const float* sc, int n_experts, int n, int k, int group,
+                            uint8_t* b_tiled, float* s_tiled);
 hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
                                  focr_hip_ctx* ctx);
