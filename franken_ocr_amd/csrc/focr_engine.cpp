@@ -444,7 +444,6 @@ struct MoeScratch {
     float* gates;
     int* flag;
     float* act;
-    float* ybuf;
     float* shared_act;
     float* shared_y;
     void* sel;
@@ -457,10 +456,9 @@ int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bo
     s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
     s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
-    s->ybuf = static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float)));
     s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
     s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
-    if (!route || !s->xq || !s->xs || !s->act || !s->ybuf || !s->flag || (with_shared && !s->shared_y))
+    if (!route || !s->xq || !s->xs || !s->act || !s->flag || (with_shared && !s->shared_y))
         return FOCR_HIP_E_OOM;
     s->idx = reinterpret_cast<uint32_t*>(route);
     s->gates = reinterpret_cast<float*>(route + pairs * 4);
@@ -535,10 +533,6 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
         ProfScope ps(ctx, "moe_gate_up");
         e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false);
     }
-    if (e == hipSuccess) {
-        ProfScope ps(ctx, "moe_down");
-        e = launch_moe_down(str, d, s.sel, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
-    }
     if (e == hipSuccess && with_shared) {
         {
             ProfScope ps(ctx, "moe_shared_gate_up");
@@ -552,8 +546,9 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
         }
     }
     if (e == hipSuccess) {
-        ProfScope ps(ctx, "moe_combine");
-        e = launch_moe_combine(str, d, s.ybuf, with_shared ? s.shared_y : nullptr, s.flag, out);
+        ProfScope ps(ctx, "moe_down_combine");
+        e = launch_moe_down_combine(str, d, di, dg, s.flag, s.act, L->wd, L->sd, with_shared ? s.shared_y : nullptr,
+                                    out, (int)L->inter);
     }
     if (e != hipSuccess) return hip_fail(e, "moe_decode launch");
     if (check_route) return check_route_flags(ctx, s.flag, t);

@@ -183,7 +183,7 @@ hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int 
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
                               int nparts, uint32_t* argmax);
 
-// k_moe.hip — decode MoE pipeline (route, gate_up, down, combine).
+// k_moe.hip — decode MoE pipeline (route, gate_up, down + combine; down alone for a shared expert).
 struct MoeDims {
     int t, hidden, inter, n_experts, top_k;
 };
@@ -200,9 +200,11 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, 
                               int inter, bool shared);
 hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
                            const float* sd, float* ybuf, int inter, bool shared);
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y,
-                              const int* flag, float* out);
-
+// down + slot-order combine in one launch, reading the routing from idx /
+// gates / flag ([t][top_k]) and the act rows of every pair (t*top_k + j).
+hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
+                                   const int* flag, const float* act, const int8_t* wd, const float* sd,
+                                   const float* shared_y, float* out, int inter);
 // k_int4.hip
 hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,
                               const float* scales, int group, int m, int k, int n, float* out,

@@ -496,31 +496,113 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     }
 }
 
-// ---- combine (slot order) ---------------------------------------------------------
-// A token whose routing failed (flag[t] != 0: fewer than top_k finite router
-// scores, reported to the caller as a routing error) has no pairs; its row is
-// written as zeros rather than left to stale buffers.
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf,
-                                                          const float* __restrict__ shared_y,
-                                                          const int* __restrict__ flag,
-                                                          float* __restrict__ out, int H, int K) {
-    const int t = blockIdx.y;
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= H) return;
-    if (flag[t]) {
-        out[static_cast<size_t>(t) * H + c] = 0.0f;
-        return;
+// ---- down + combine (one block per token and row block) -----------------------
+// Block (t, rb), DC_THREADS threads = (DC_THREADS / LPR) lane groups; group g
+// < K * R owns slot j = g % K and row r = rb * R + g / K of token t, R =
+// (DC_THREADS / LPR) / K. The expert ids and the token's K act rows are
+// requested first, the down rows as soon as the ids arrive, and the block
+// re-quantizes the act rows (quantize_row_i8, one wave per row, K <= 8) into
+// LDS while the down rows are in flight; each group's dot gives
+// y_j[r] = ((f32)acc * as_j) * sd[e_j][r] * gate_j (decoder.rs:2244-2246),
+// and the block sums y_0..y_{K-1} in slot order (+ shared) into out[t][r]
+// (decoder.rs:2253-2261) — no per-pair buffer, no separate combine launch.
+// A weight row used by several of the step's tokens is read once per token;
+// such blocks run together (t varies fastest), so the repeats mostly hit the
+// caches.
+constexpr int DC_THREADS = 512;
+
+template <int LPR, int JC>
+__global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
+    const uint32_t* __restrict__ idx, const float* __restrict__ gates, const int* __restrict__ flag, int T, int K,
+    const float* __restrict__ act, const int8_t* __restrict__ wd, const float* __restrict__ sd,
+    const float* __restrict__ shared_y, float* __restrict__ out, int H, int I, int E) {
+    extern __shared__ int4 lds_q[];  // [K][I/16] quantized act rows of token t
+    __shared__ float s_as[kMaxK];
+    __shared__ float s_y[DC_THREADS / LPR];
+    constexpr int NG = DC_THREADS / LPR;
+    const int t = blockIdx.x;
+    const int R = NG / K;
+    const int g = threadIdx.x / LPR;
+    const int ln = threadIdx.x % LPR;
+    const int wave = threadIdx.x >> 6;
+    const int wl = threadIdx.x & 63;
+    const int j = g % K;
+    const int r = blockIdx.y * R + g / K;
+    const bool live = g < K * R && r < H;  // dead groups compute unused values from valid addresses
+    const int C = I >> 4;
+    // 1. expert id and gate of slot j, the token's flag, and (wave w < K) act
+    //    row t*K + w — all issued before anything waits
+    const int pid = t * K + (live ? j : 0);
+    const uint32_t eid = idx[pid];
+    const float gate = gates[pid];
+    const int bad = flag[t];
+    const bool qwave = wave < K;  // wave-uniform
+    const float* ar = act + static_cast<size_t>(t * K + (qwave ? wave : 0)) * I;
+    const bool short_row = I <= 64 * NQ;
+    float v[NQ];
+    if (short_row) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int i = wl + 64 * q;
+            v[q] = ar[i < I ? i : I - 1];  // a duplicate of the last value past I: max unchanged
+        }
     }
-    float v[kMaxK];
+    // 2. the down row of (slot j, row r)
+    const uint32_t e = eid < static_cast<uint32_t>(E) ? eid : 0u;
+    const size_t row = static_cast<size_t>(e) * H + (live ? r : 0);
+    int4 wv[JC];
+    {
+        const int4* drow = reinterpret_cast<const int4*>(wd + row * I);
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) v[j] = j < K ? ybuf[(static_cast<size_t>(t) * K + j) * H + c] : 0.0f;
-    const float sh = shared_y ? shared_y[static_cast<size_t>(t) * H + c] : 0.0f;
-    float o = 0.0f;
+        for (int c = 0; c < JC; ++c) wv[c] = row_chunk(drow, ln + LPR * c, C);
+    }
+    const float sdr = sd[row];
+    // 3. quantize_row_i8 of the act rows into LDS
+    if (qwave) {
+        int8_t* qrow = reinterpret_cast<int8_t*>(lds_q) + wave * I;
+        if (short_row) {
+            float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j)
-        if (j < K) o += v[j];
-    if (shared_y) o += sh;
-    out[static_cast<size_t>(t) * H + c] = o;
+            for (int q = 0; q < NQ; ++q) amax = fmaxf(amax, fabsf(v[q]));
+            amax = wave_max_f(amax);
+            const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / a_scale;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+                if (wl + 64 * q < I) qrow[wl + 64 * q] = quant_i8(v[q], inv, false);
+            if (wl == 0) s_as[wave] = a_scale;
+        } else {  // long rows: two passes over L2
+            float amax = 0.0f;
+            for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
+            amax = wave_max_f(amax);
+            const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / a_scale;
+            for (int i = wl; i < I; i += 64) qrow[i] = quant_i8(ar[i], inv, false);
+            if (wl == 0) s_as[wave] = a_scale;
+        }
+    }
+    __syncthreads();
+    int d = 0;
+#pragma unroll
+    for (int c = 0; c < JC; ++c) {
+        const int cc = ln + LPR * c;
+        if (cc < C) d = dot16_i8(wv[c], lds_q[j * C + cc], d);
+    }
+    d = reduce_lanes<LPR>(d);
+    if (ln == 0 && g < NG) s_y[g] = ((static_cast<float>(d) * s_as[j]) * sdr) * gate;
+    __syncthreads();
+    // 4. slot-order sum of the token's K results for each row
+    if (threadIdx.x < R) {
+        const int rr = blockIdx.y * R + threadIdx.x;
+        if (rr < H) {
+            float o = 0.0f;
+            if (!bad) {
+                for (int jj = 0; jj < K; ++jj) o += s_y[threadIdx.x * K + jj];
+                if (shared_y) o += shared_y[static_cast<size_t>(t) * H + rr];
+            }
+            out[static_cast<size_t>(t) * H + rr] = o;
+        }
+    }
 }
 
 struct GemvArgs {
@@ -630,11 +712,26 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, con
     return launch_down_lpr<8>(s, grid, lds, jc, a, act, wd, sd, ybuf);
 }
 
-hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const float* shared_y,
-                              const int* flag, float* out) {
-    const dim3 grid((d.hidden + 255) / 256, d.t);
-    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, shared_y, flag, out, d.hidden, d.top_k);
-    return hipGetLastError();
+hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
+                                   const int* flag, const float* act, const int8_t* wd, const float* sd,
+                                   const float* shared_y, float* out, int inter) {
+    int lpr, jc;
+    pick_lpr(inter, &lpr, &jc);
+    if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
+    const int R = (DC_THREADS / lpr) / d.top_k;
+    const dim3 grid(d.t, (d.hidden + R - 1) / R);
+    const size_t lds = static_cast<size_t>(d.top_k) * inter;
+#define FOCR_DC(L, J)                                                                                             \
+    if (lpr == L && jc == J) {                                                                                   \
+        FOCR_LAUNCH((moe_down_combine_kernel<L, J>), grid, dim3(DC_THREADS), lds, s, idx, gates, flag, d.t,      \
+                    d.top_k, act, wd, sd, shared_y, out, d.hidden, inter, d.n_experts);                          \
+        return hipGetLastError();                                                                                \
+    }
+    FOCR_DC(8, 1) FOCR_DC(8, 2) FOCR_DC(8, 3) FOCR_DC(8, 4) FOCR_DC(8, 5) FOCR_DC(8, 6) FOCR_DC(8, 7) FOCR_DC(8, 8)
+    FOCR_DC(16, 1) FOCR_DC(16, 2) FOCR_DC(16, 3) FOCR_DC(16, 4) FOCR_DC(16, 5) FOCR_DC(16, 6) FOCR_DC(16, 7)
+    FOCR_DC(16, 8)
+#undef FOCR_DC
+    return hipErrorInvalidValue;
 }
 
 }  // namespace focr
