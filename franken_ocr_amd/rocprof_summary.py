@@ -2,6 +2,8 @@
 
     python -m franken_ocr_amd.rocprof_summary kernels DIR [--command "..."]
         per-kernel dispatch statistics from a --kernel-trace run (markdown)
+    python -m franken_ocr_amd.rocprof_summary timeline DIR [--command "..."]
+        idle gaps between consecutive dispatches, by kernel pair (markdown)
     python -m franken_ocr_amd.rocprof_summary counters DIR
         per-kernel mean of every collected counter from a --pmc run
     python -m franken_ocr_amd.rocprof_summary traffic --fetch DIR --write DIR
@@ -68,6 +70,29 @@ def kernels_table(path: str, cmd: str | None = None) -> str:
     return "\n".join(out)
 
 
+def timeline_table(path: str, cmd: str | None = None) -> str:
+    """Idle time between consecutive dispatches on the queue, grouped by the
+    (previous kernel -> next kernel) pair: the launch/dependency gap a step
+    pays per kernel boundary. Gaps over 1 ms (host-side pauses such as the
+    bench's phase changes) are left out."""
+    c = sqlite3.connect(str(_db(path)))
+    rows = list(c.execute("select name, start, duration from kernels order by start"))
+    agg: dict[tuple[str, str], list[float]] = {}
+    for (n0, s0, d0), (n1, s1, _) in zip(rows, rows[1:]):
+        gap = (s1 - (s0 + d0)) / 1000.0
+        if gap > 1000.0:
+            continue
+        agg.setdefault((short_name(n0), short_name(n1)), []).append(gap)
+    out = []
+    if cmd:
+        out.append(f"command: `{cmd}`\n")
+    out.append("| previous kernel | next kernel | count | mean gap us | median gap us | min us |")
+    out.append("|---|---|---:|---:|---:|---:|")
+    for (a, b), v in sorted(agg.items(), key=lambda kv: -len(kv[1])):
+        out.append(f"| `{a}` | `{b}` | {len(v)} | {st.mean(v):.3f} | {st.median(v):.3f} | {min(v):.3f} |")
+    return "\n".join(out)
+
+
 def counter_means(path: str) -> dict[tuple[str, str], float]:
     """{(kernel, counter): mean over dispatches of the per-dispatch value}."""
     c = sqlite3.connect(str(_db(path)))
@@ -120,6 +145,9 @@ def main(argv=None) -> int:
     k = sub.add_parser("kernels")
     k.add_argument("dir")
     k.add_argument("--command", default=None, help="the profiled command, printed above the table")
+    tl = sub.add_parser("timeline")
+    tl.add_argument("dir")
+    tl.add_argument("--command", default=None, help="the profiled command, printed above the table")
     c = sub.add_parser("counters")
     c.add_argument("dir")
     t = sub.add_parser("traffic")
@@ -131,6 +159,8 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.what == "kernels":
         print(kernels_table(a.dir, a.command))
+    if a.what == "timeline":
+        print(timeline_table(a.dir, a.command))
     if a.what == "counters":
         print(counters_table(a.dir))
     if a.what == "traffic":
