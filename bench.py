@@ -126,6 +126,8 @@ def bench_moe(args, ctx):
 
     for i in range(args.warmup):
         step(i)
+    for j in range(len(layers)):  # every copy routes once before its experts are counted
+        step(j)
     ctx.device_synchronize()
     # distinct experts actually routed, per copy (for algorithmic bytes)
     U = [len(np.unique(b.numpy())) for b in idx_bufs]

@@ -520,14 +520,22 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     __shared__ float s_as[kMaxK];
     __shared__ float s_y[DC_THREADS / LPR];
     constexpr int NG = DC_THREADS / LPR;
-    const int t = blockIdx.x;
+    // XCD-aware order: blocks are dispatched to the 8 XCDs round-robin
+    // (block b to XCD b % 8, each with its own L2), and block b takes row
+    // block rb = b % 8 + 8 * (b / (8 T)) of token t = (b / 8) % T, so every
+    // token's block for one row block runs on the same XCD, one after the
+    // other: a down row two tokens share (the same expert) comes from HBM
+    // once and from that L2 the second time.
+    const int b = static_cast<int>(blockIdx.x);
+    const int t = (b >> 3) % T;
+    const int rb = (b & 7) + 8 * ((b >> 3) / T);
     const int R = NG / K;
     const int g = threadIdx.x / LPR;
     const int ln = threadIdx.x % LPR;
     const int wave = threadIdx.x >> 6;
     const int wl = threadIdx.x & 63;
     const int j = g % K;
-    const int r = blockIdx.y * R + g / K;
+    const int r = rb * R + g / K;
     const bool live = g < K * R && r < H;  // dead groups compute unused values from valid addresses
     const int C = I >> 4;
     // 1. expert id and gate of slot j, the token's flag, and (wave w < K) act
@@ -593,7 +601,7 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     __syncthreads();
     // 4. slot-order sum of the token's K results for each row
     if (threadIdx.x < R) {
-        const int rr = blockIdx.y * R + threadIdx.x;
+        const int rr = rb * R + threadIdx.x;
         if (rr < H) {
             float o = 0.0f;
             if (!bad) {
@@ -719,7 +727,8 @@ hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32
     pick_lpr(inter, &lpr, &jc);
     if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int R = (DC_THREADS / lpr) / d.top_k;
-    const dim3 grid(d.t, (d.hidden + R - 1) / R);
+    const int nrb8 = (((d.hidden + R - 1) / R) + 7) & ~7;  // row blocks, a multiple of 8 (the extra ones have no rows)
+    const dim3 grid(static_cast<unsigned>(d.t * nrb8));
     const size_t lds = static_cast<size_t>(d.top_k) * inter;
 #define FOCR_DC(L, J)                                                                                             \
     if (lpr == L && jc == J) {                                                                                   \
