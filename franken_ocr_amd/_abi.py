@@ -22,6 +22,10 @@ E_BAD_HANDLE = -5
 E_ARG = -6
 E_ROUTE = -7
 E_STATE = -8
+E_FORMAT = -9
+E_NOT_FOUND = -10
+
+DT_F32, DT_F16, DT_BF16, DT_QINT8_PER_CHAN, DT_QINT4_PER_GROUP = range(5)
 
 _P = C.c_void_p
 _SZ = C.c_size_t
@@ -80,6 +84,31 @@ _SIGS: dict[str, list] = {
     "focr_hip_rswa_get_state": [_P, _SZ, _P, _P, _P],
     "focr_hip_rswa_set_state": [_P, _SZ, C.c_uint32, C.c_uint32],
     "focr_hip_rswa_regions": [_P, _SZ, _P, _P, _P, _P],
+    "focr_hip_focrq_open": [C.c_char_p, _P],
+    "focr_hip_focrq_from_bytes": [_P, _SZ, _P],
+    "focr_hip_focrq_close": [_P],
+    "focr_hip_focrq_info": [_P, _P, _P, _P, C.c_char_p, _SZ, C.c_char_p, _SZ, C.c_char_p, _SZ],
+    "focr_hip_focrq_name": [_P, _SZ, C.c_char_p, _SZ],
+    "focr_hip_focrq_record": [_P, C.c_char_p, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
+    "focr_hip_focrq_census": [_P, _P, _SZ],
+    "focr_hip_focrq_read_f32": [_P, C.c_char_p, _P, _SZ, _P, _P],
+    "focr_hip_focrq_read_qint8": [_P, C.c_char_p, _P, _SZ, _P, _SZ, _P, _P],
+    "focr_hip_focrq_read_qint4": [_P, C.c_char_p, _P, _SZ, _P, _SZ, _P, _P, _P, _P],
+    "focr_hip_focrq_upload_qint8": [_P, _P, C.c_char_p, C.c_uint64, _P],
+    "focr_hip_focrq_upload_f32": [_P, _P, C.c_char_p, _P, _P, _P],
+    "focr_hip_focrq_moe_layer": [_P, _P, _SZ, _SZ, _SZ, _I32, _P],
+    "focr_hip_focrq_moe_layer_i4": [_P, _P, _SZ, _SZ, _P],
+    "focr_hip_quantize_weight_i8": [_P, _P, _I32, _SZ, _SZ, _P, _P],
+    "focr_hip_pack_weight_i4": [_P, _P, _I32, _SZ, _SZ, _SZ, _P, _P],
+    "focr_hip_focrq_writer_new": [_P],
+    "focr_hip_focrq_writer_free": [_P],
+    "focr_hip_focrq_writer_set_meta": [_P, C.c_uint8, _P, C.c_char_p, C.c_char_p, _I32],
+    "focr_hip_focrq_writer_set_json": [_P, C.c_char_p, C.c_char_p],
+    "focr_hip_focrq_writer_add_tensor": [_P, C.c_char_p, _I32, _P, _SZ, _P, _SZ],
+    "focr_hip_focrq_writer_add_quantized": [_P, C.c_char_p, _I32, _P, _SZ, _P, _SZ, _P, _SZ, C.c_uint64,
+                                            C.c_uint8],
+    "focr_hip_focrq_writer_build": [_P, _P, _SZ, _P],
+    "focr_hip_focrq_writer_write": [_P, C.c_char_p],
     "focr_hip_prof_enable": [_P, _I32],
     "focr_hip_prof_reset": [_P],
     "focr_hip_prof_read": [_P, C.c_char_p, _SZ],
@@ -114,6 +143,14 @@ class StateError(FocrHipError):
 
 class NoDevice(FocrHipError):
     """FOCR_HIP_E_NO_DEVICE: no gfx950 device visible."""
+
+
+class FormatMismatch(FocrHipError, ValueError):
+    """FOCR_HIP_E_FORMAT: FocrError::FormatMismatch of the weight container."""
+
+
+class ModelNotFound(FocrHipError):
+    """FOCR_HIP_E_NOT_FOUND: FocrError::ModelNotFound (weights file unreadable)."""
 
 
 _lock = threading.Lock()
@@ -153,7 +190,8 @@ def last_error() -> str:
     return msg.decode() if msg else ""
 
 
-_ERR = {E_SHAPE: ContractViolation, E_ROUTE: RouteError, E_STATE: StateError, E_NO_DEVICE: NoDevice}
+_ERR = {E_SHAPE: ContractViolation, E_ROUTE: RouteError, E_STATE: StateError, E_NO_DEVICE: NoDevice,
+        E_FORMAT: FormatMismatch, E_NOT_FOUND: ModelNotFound}
 
 
 def check(status: int) -> None:

@@ -240,6 +240,13 @@ hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, 
                                  const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
                                  focr_hip_ctx* ctx);
 
+// k_quant.hip — load/convert-time weight conversions. src is a stored
+// payload of dtype dt (FOCR_HIP_DT_F32/F16/BF16) in device memory.
+hipError_t launch_quant_weight_i8(hipStream_t s, const void* src, int dt, int n, int k, int8_t* q, float* scales);
+hipError_t launch_pack_weight_i4(hipStream_t s, const void* src, int dt, int n, int k, int group, uint8_t* packed,
+                                 float* scales);
+hipError_t launch_widen(hipStream_t s, const void* src, int dt, size_t count, float* dst);
+
 // k_rswa.hip
 struct RswaStepArgs {
     static constexpr int kMax = 64;

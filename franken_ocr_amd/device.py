@@ -112,6 +112,18 @@ class DeviceArray:
         self._p = C.c_void_p()
         _abi.call("focr_hip_dmalloc", ctx.handle, max(self.nbytes, 16), C.byref(self._p))
 
+    @classmethod
+    def adopt(cls, ctx: Context, ptr: C.c_void_p, shape, dtype) -> "DeviceArray":
+        """Take ownership of a device allocation made by the library (freed
+        with focr_hip_dfree like any other DeviceArray)."""
+        a = cls.__new__(cls)
+        a.ctx = ctx
+        a.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        a.dtype = np.dtype(dtype)
+        a.nbytes = int(np.prod(a.shape, dtype=np.int64)) * a.dtype.itemsize
+        a._p = ptr
+        return a
+
     @property
     def ptr(self) -> int:
         return int(self._p.value or 0)

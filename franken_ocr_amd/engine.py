@@ -134,6 +134,15 @@ class MoeLayer:
         if not from_dev:
             del self._host
 
+    @classmethod
+    def adopt(cls, ctx: Context, handle: C.c_void_p, hidden: int, inter: int, n_experts: int,
+              top_k: int) -> "MoeLayer":
+        """Wrap a layer handle created by the library (e.g. from a .focrq)."""
+        m = cls.__new__(cls)
+        m.ctx, m._h = ctx, handle
+        m.hidden, m.inter, m.n_experts, m.top_k = int(hidden), int(inter), int(n_experts), int(top_k)
+        return m
+
     def set_shared(self, shared_inter: int, wg, sg, wu, su, wd, sd) -> None:
         arrs = [wg, sg, wu, su, wd, sd]
         from_dev = isinstance(wg, DeviceArray)
@@ -197,6 +206,15 @@ class MoeLayerI4:
             ptrs = [_p(a) for a in host]
         _abi.call("focr_hip_moe_layer_i4_create", self.ctx.handle, self.hidden, self.inter, self.n_experts,
                   self.group, *ptrs, 1 if from_dev else 0, C.byref(self._h))
+
+    @classmethod
+    def adopt(cls, ctx: Context, handle: C.c_void_p, hidden: int, inter: int, n_experts: int,
+              group: int) -> "MoeLayerI4":
+        """Wrap a layer handle created by the library (e.g. from a .focrq)."""
+        m = cls.__new__(cls)
+        m.ctx, m._h = ctx, handle
+        m.hidden, m.inter, m.n_experts, m.group = int(hidden), int(inter), int(n_experts), int(group)
+        return m
 
     def prefill(self, x: DeviceArray, idx: DeviceArray, gates: DeviceArray, out: DeviceArray,
                 check_idx: bool = True) -> None:

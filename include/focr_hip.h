@@ -46,12 +46,23 @@ extern "C" {
 #define FOCR_HIP_E_ARG (-6)        /* invalid argument (null pointer, bad flag) */
 #define FOCR_HIP_E_ROUTE (-7)      /* moe.rs:261-265 "no finite router score" */
 #define FOCR_HIP_E_STATE (-8)      /* rswa.rs:452-455/869-887 state errors */
+#define FOCR_HIP_E_FORMAT (-9)     /* FocrError::FormatMismatch of the weight container */
+#define FOCR_HIP_E_NOT_FOUND (-10) /* FocrError::ModelNotFound: weights file unreadable */
+
+/* Stored dtypes of the weight container (weights.rs:148-170 DType). */
+#define FOCR_HIP_DT_F32 0
+#define FOCR_HIP_DT_F16 1
+#define FOCR_HIP_DT_BF16 2
+#define FOCR_HIP_DT_QINT8_PER_CHAN 3
+#define FOCR_HIP_DT_QINT4_PER_GROUP 4
 
 typedef struct focr_hip_ctx focr_hip_ctx;
 typedef struct focr_hip_qint8 focr_hip_qint8;
 typedef struct focr_hip_moe_layer focr_hip_moe_layer;
 typedef struct focr_hip_moe_layer_i4 focr_hip_moe_layer_i4;
 typedef struct focr_hip_rswa focr_hip_rswa;
+typedef struct focr_hip_focrq focr_hip_focrq;
+typedef struct focr_hip_focrq_writer focr_hip_focrq_writer;
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* focr_hip_last_error(void);
@@ -279,6 +290,100 @@ int32_t focr_hip_rswa_set_state(focr_hip_rswa* cache, size_t stream, uint32_t ri
 /* Device pointers of one stream's regions (for direct fills/readback). */
 int32_t focr_hip_rswa_regions(const focr_hip_rswa* cache, size_t stream, float** ref_k,
                               float** ref_v, float** ring_k, float** ring_v);
+
+/* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
+ * The reader restates weights.rs:443-620 (format detection by magic, the
+ * 51-byte .focrq prefix, header JSON, model_id / license / sha checks,
+ * validate_directory :949-990) with the reference's FormatMismatch texts
+ * (E_FORMAT). A path is memory-mapped read-only; names are byte-sorted. */
+int32_t focr_hip_focrq_open(const char* path, focr_hip_focrq** out);          /* weights.rs:416-421 load */
+int32_t focr_hip_focrq_from_bytes(const uint8_t* bytes, size_t len,           /* weights.rs:447-453 */
+                                  focr_hip_focrq** out);
+int32_t focr_hip_focrq_close(focr_hip_focrq* f);
+/* is_focrq, arch_target, tensor count, source_sha256 (hex), resolved
+ * model_id, license_notice (weights.rs:687-717 getters). Buffers nullable. */
+int32_t focr_hip_focrq_info(const focr_hip_focrq* f, int32_t* is_focrq, uint8_t* arch_target,
+                            size_t* n_tensors, char* source_sha256, size_t sha_cap, char* model_id,
+                            size_t id_cap, char* license, size_t license_cap);
+/* The index-th name in sorted order (weights.rs:721-723 names). */
+int32_t focr_hip_focrq_name(const focr_hip_focrq* f, size_t index, char* buf, size_t cap);
+/* weights.rs:734-736 record(): dtype code (FOCR_HIP_DT_*), shape, ranges. */
+int32_t focr_hip_focrq_record(const focr_hip_focrq* f, const char* name, int32_t* dtype,
+                              uint64_t* shape, size_t shape_cap, size_t* rank,
+                              uint64_t* byte_offset, uint64_t* byte_len, uint64_t* scales_offset,
+                              uint64_t* scales_len, uint64_t* group_size, uint8_t* tier);
+/* weights.rs:634-670 census: the name set must equal names[0..count). */
+int32_t focr_hip_focrq_census(const focr_hip_focrq* f, const char* const* names, size_t count);
+/* weights.rs:776-819 mat()/vec(): F32/F16/BF16 widened to f32 on the host
+ * (rank 1 reads as [1, len]); out NULL queries rows/cols. */
+int32_t focr_hip_focrq_read_f32(const focr_hip_focrq* f, const char* name, float* out, size_t cap,
+                                uint64_t* rows, uint64_t* cols);
+/* weights.rs:821-862 qint8() / :866-923 qint4(): host copies of the
+ * quantized payloads, with the reference's shape checks and messages. */
+int32_t focr_hip_focrq_read_qint8(const focr_hip_focrq* f, const char* name, int8_t* w,
+                                  size_t w_cap, float* scales, size_t s_cap, uint64_t* n,
+                                  uint64_t* k);
+int32_t focr_hip_focrq_read_qint4(const focr_hip_focrq* f, const char* name, uint8_t* packed,
+                                  size_t p_cap, float* scales, size_t s_cap, uint64_t* n,
+                                  uint64_t* k, uint64_t* group_size, uint8_t* tier);
+
+/* Upload once into HBM (DecoderWeightCacheI8::build, decoder.rs:2018-2116).
+ * decoder.rs:1777-1786 quant_oc_loaded: a QInt8PerChan record is copied
+ * verbatim; an F32/F16/BF16 record is copied raw and quantized per output
+ * channel on the device (quant/int8.rs rule). out_channels 0 = the record's
+ * rows. */
+int32_t focr_hip_focrq_upload_qint8(focr_hip_ctx* ctx, const focr_hip_focrq* f, const char* name,
+                                    uint64_t out_channels, focr_hip_qint8** out);
+/* weights.rs:776-799 mat() widened on the device into a new device array
+ * (*dev, rows*cols f32; release with focr_hip_dfree). */
+int32_t focr_hip_focrq_upload_f32(focr_hip_ctx* ctx, const focr_hip_focrq* f, const char* name,
+                                  float** dev, uint64_t* rows, uint64_t* cols);
+/* decoder.rs:2069-2098: the MoE MLP of model.layers.{layer} — router
+ * mlp.gate.weight [n_experts, hidden] (f32), experts mlp.experts.{e}.
+ * {gate,up,down}_proj.weight and, with with_shared, mlp.shared_experts.* —
+ * as a focr_hip_moe_layer. */
+int32_t focr_hip_focrq_moe_layer(focr_hip_ctx* ctx, const focr_hip_focrq* f, size_t layer,
+                                 size_t n_experts, size_t top_k, int32_t with_shared,
+                                 focr_hip_moe_layer** out);
+/* The same experts as QInt4PerGroup records (one group_size for the
+ * layer), as the int4 prefill layer. */
+int32_t focr_hip_focrq_moe_layer_i4(focr_hip_ctx* ctx, const focr_hip_focrq* f, size_t layer,
+                                    size_t n_experts, focr_hip_moe_layer_i4** out);
+
+/* Converter-side weight quantizers on device arrays (src dtype F32/F16/BF16):
+ * quant/int8.rs:145-163 quantize_int8_f32 -> q [n,k] + scales [n];
+ * quant/int4.rs:142-205 pack_int4_f32 -> packed [n,k/2] + scales
+ * [n,k/group] (group 16 or 32; texts of its asserts). Stream-ordered. */
+int32_t focr_hip_quantize_weight_i8(focr_hip_ctx* ctx, const void* src, int32_t src_dtype, size_t n,
+                                    size_t k, int8_t* q, float* scales);
+int32_t focr_hip_pack_weight_i4(focr_hip_ctx* ctx, const void* src, int32_t src_dtype, size_t n,
+                                size_t k, size_t group, uint8_t* packed, float* scales);
+
+/* quant/focrq.rs:170-714 FocrqBuilder: tensors emitted sorted by name,
+ * canonical header JSON, optional 64-byte payload alignment (align = 1). */
+int32_t focr_hip_focrq_writer_new(focr_hip_focrq_writer** out);
+int32_t focr_hip_focrq_writer_free(focr_hip_focrq_writer* w);
+/* focrq.rs:225-290 with_arch_target / with_source_sha256 (32 bytes,
+ * nullable) / with_license_notice (nullable) / with_model_id (nullable) /
+ * with_alignment. */
+int32_t focr_hip_focrq_writer_set_meta(focr_hip_focrq_writer* w, uint8_t arch_target,
+                                       const uint8_t* source_sha256, const char* license_notice,
+                                       const char* model_id, int32_t align);
+/* focrq.rs:246-270: "provenance" | "model_config" | "packing_manifest". */
+int32_t focr_hip_focrq_writer_set_json(focr_hip_focrq_writer* w, const char* field,
+                                       const char* json);
+int32_t focr_hip_focrq_writer_add_tensor(focr_hip_focrq_writer* w, const char* name, int32_t dtype,
+                                         const uint64_t* shape, size_t rank, const void* data,
+                                         size_t len); /* focrq.rs:299-313 */
+int32_t focr_hip_focrq_writer_add_quantized(focr_hip_focrq_writer* w, const char* name,
+                                            int32_t dtype, const uint64_t* shape, size_t rank,
+                                            const void* data, size_t len, const float* scales,
+                                            size_t n_scales, uint64_t group_size,
+                                            uint8_t tier); /* focrq.rs:327-349 */
+/* The blob (out NULL: *len only). focrq.rs:479-533 build. */
+int32_t focr_hip_focrq_writer_build(const focr_hip_focrq_writer* w, uint8_t* out, size_t cap,
+                                    size_t* len);
+int32_t focr_hip_focrq_writer_write(const focr_hip_focrq_writer* w, const char* path);
 
 /* ---- profiling (decoder.rs:986-1024 prof counters, GPU-timed) -----------
  * When enabled, every kernel launch carries HIP start/stop events in its
