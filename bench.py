@@ -12,8 +12,9 @@ timed steps rotate over --copies distinct layers (each with its own router
 and its own copy of the expert weights; 220 MB each), like consecutive
 decoder layers. Synthetic seeded data (no checkpoint).
 
-Other workloads (--workload): lm_head (config 2), igemm (config 1), rswa
-(config 5). Each prints ONE JSON line with `roofline` (dominant kernel,
+Other workloads (--workload): lm_head (config 2), lm_head_sample (config 2
+with the no-repeat-ngram ban and history append fused in), igemm (config 1),
+rswa (config 5), moe_prefill_i4 (config 4). Each prints ONE JSON line with `roofline` (dominant kernel,
 algorithmic bytes / HIP-event-timed average launch) and, at N = 1,
 `cpu_baseline` (the reference's x86 int8 tier restated in C, oracle/,
 timed on a bounded sample on this host).
@@ -197,12 +198,12 @@ def cpu_moe(args, inputs):
 # config 2: LM head GEMV + argmax
 # ---------------------------------------------------------------------------
 
-def bench_lm_head(args, ctx):
+def bench_lm_head(args, ctx, sampler=False):
     from franken_ocr_amd import synth
-    from franken_ocr_amd.engine import QInt8, lm_head_i8
+    from franken_ocr_amd.engine import QInt8, lm_head_i8, lm_head_sample_i8
 
     M, N, Kd = args.tokens, 129280, 1280
-    log(f"lm_head: M={M}, {args.copies} weight copies")
+    log(f"lm_head: M={M}, {args.copies} weight copies, fused sampler={sampler}")
     w = synth.int8_uniform(synth.seed_of(20), N * Kd)
     s = synth.f32_uniform(synth.seed_of(21), N, 1e-3, 2e-2)
     heads = [QInt8(w, s, N, Kd, ctx) for _ in range(args.copies)]
@@ -210,9 +211,19 @@ def bench_lm_head(args, ctx):
     dx = ctx.to_device(x)
     dl = ctx.empty((M, N), np.float32)
     da = ctx.empty((M,), np.uint32)
+    if sampler:
+        # each stream starts with 128 generated tokens; every step bans over the
+        # 35-gram / 128-token window and appends its token on the device
+        cap = 128 + args.warmup + args.steps
+        hist = np.zeros((M, cap), np.uint32)
+        hist[:, :128] = synth.int_uniform(synth.seed_of(23), M * 128, 0, N - 1).reshape(M, 128)
+        dh, dlen = ctx.to_device(hist), ctx.to_device(np.full(M, 128, np.uint32))
 
     def step(i):
-        lm_head_i8(heads[i % len(heads)], dx, da, dl)
+        if sampler:
+            lm_head_sample_i8(heads[i % len(heads)], dx, da, dh, dlen, 35, 128, append=True, logits=dl)
+        else:
+            lm_head_i8(heads[i % len(heads)], dx, da, dl)
 
     for i in range(args.warmup):
         step(i)
@@ -224,10 +235,16 @@ def bench_lm_head(args, ctx):
     total_bytes = gemv_bytes + M * Kd * 4 + M * 4
     achieved = gemv_bytes / (g_ms * 1e-3) / 1e9
     log(f"per-kernel avg us {kernels}")
+    metric = ("LM-head int8 GEMV + no-repeat-ngram ban + argmax + history append tokens/s (129280x1280, 35-gram, "
+              "window 128), 1 GPU" if sampler else "LM-head int8 GEMV + argmax tokens/s (129280x1280), 1 GPU")
+    cfg = {"workload": "lm_head_sample" if sampler else "lm_head", "rows": M, "vocab": N, "hidden": Kd,
+           "weight_copies_rotated": args.copies}
+    if sampler:
+        cfg.update({"no_repeat_ngram_size": 35, "ngram_window": 128, "history_start_len": 128})
     return {
-        "metric": "LM-head int8 GEMV + argmax tokens/s (129280x1280), 1 GPU",
+        "metric": metric,
         "value": round(M * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
-        "config": {"workload": "lm_head", "rows": M, "vocab": N, "hidden": Kd, "weight_copies_rotated": args.copies},
+        "config": cfg,
         "roofline": {"bound": "hbm", "kernel": "lm_head_gemv", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("lm_head_gemv", f"lm_head_m{M}"),
@@ -494,6 +511,7 @@ def bench_copy(args, ctx):
 WORKLOADS = {
     "moe_decode": (bench_moe, cpu_moe),
     "lm_head": (bench_lm_head, cpu_lm_head),
+    "lm_head_sample": (lambda args, ctx: bench_lm_head(args, ctx, sampler=True), None),
     "igemm": (bench_igemm, cpu_igemm),
     "rswa": (bench_rswa, None),
     "copy": (bench_copy, None),
@@ -516,7 +534,8 @@ def main() -> int:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
               file=sys.stderr)
         return 2
-    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "igemm": (1, 64), "rswa": (8, 4), "copy": (1, 1),
+    defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
+                "copy": (1, 1),
                 "moe_prefill_i4": (512, 3)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt

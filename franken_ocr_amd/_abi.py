@@ -24,6 +24,7 @@ E_ROUTE = -7
 E_STATE = -8
 E_FORMAT = -9
 E_NOT_FOUND = -10
+E_NOT_IMPLEMENTED = -11
 
 DT_F32, DT_F16, DT_BF16, DT_QINT8_PER_CHAN, DT_QINT4_PER_GROUP = range(5)
 
@@ -67,6 +68,10 @@ _SIGS: dict[str, list] = {
     "focr_hip_gemv_i8_prequant": [_P, _P, _P, _P, _SZ, _P, _P],
     "focr_hip_lm_head_i8": [_P, _P, _P, _SZ, _P, _P],
     "focr_hip_argmax_rows": [_P, _P, _SZ, _SZ, _P],
+    "focr_hip_lm_head_sample_i8": [_P, _P, _P, _SZ, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _F32, C.c_uint32, _I32, _P,
+                                   _P, _P, _I32],
+    "focr_hip_sample_rows": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _F32, C.c_uint32, _I32, _P, _P,
+                             _I32],
     "focr_hip_moe_layer_create": [_P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _I32, _P],
     "focr_hip_moe_layer_set_shared": [_P, _SZ, _P, _P, _P, _P, _P, _P, _I32],
     "focr_hip_moe_layer_free": [_P],
@@ -153,6 +158,10 @@ class ModelNotFound(FocrHipError):
     """FOCR_HIP_E_NOT_FOUND: FocrError::ModelNotFound (weights file unreadable)."""
 
 
+class NotImplementedPath(FocrHipError, NotImplementedError):
+    """FOCR_HIP_E_NOT_IMPLEMENTED: FocrError::NotImplemented (temperature > 0 sampling)."""
+
+
 _lock = threading.Lock()
 _lib: C.CDLL | None = None
 
@@ -191,7 +200,7 @@ def last_error() -> str:
 
 
 _ERR = {E_SHAPE: ContractViolation, E_ROUTE: RouteError, E_STATE: StateError, E_NO_DEVICE: NoDevice,
-        E_FORMAT: FormatMismatch, E_NOT_FOUND: ModelNotFound}
+        E_FORMAT: FormatMismatch, E_NOT_FOUND: ModelNotFound, E_NOT_IMPLEMENTED: NotImplementedPath}
 
 
 def check(status: int) -> None:

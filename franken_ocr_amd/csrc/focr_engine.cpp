@@ -290,6 +290,128 @@ int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const fl
     return FOCR_HIP_OK;
 }
 
+}  // extern "C"
+
+// ---- greedy sampler --------------------------------------------------------
+
+namespace {
+
+int32_t sampler_args(focr_hip_ctx* ctx, const char* name, size_t m, size_t vocab, uint32_t* history,
+                     size_t history_cap, uint32_t* history_len, size_t ngram_size, size_t window,
+                     const uint32_t* whitelist, size_t n_whitelist, float temperature, int32_t append,
+                     SamplerArgs& a) {
+    // sampler.rs:362-367: temperature > 0 is outside the greedy spine (a NaN
+    // temperature is greedy, sampler.rs:96-100).
+    if (temperature > 0.0f)
+        return fail(FOCR_HIP_E_NOT_IMPLEMENTED,
+                    fmt("native_engine::sampler::%s — temperature>0 sampling is outside the greedy fp32 spine", name));
+    if (vocab == 0) return fail(FOCR_HIP_E_SHAPE, "sampler::argmax_row: empty logits row");
+    const size_t imax = static_cast<size_t>(std::numeric_limits<int32_t>::max());
+    if (history_cap > imax || ngram_size > imax || window > imax || n_whitelist > 4096 || vocab > imax)
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: history_cap / ngram_size / window / whitelist exceed the gfx950 tier "
+                                          "limits", name));
+    if ((ngram_size > 0 || append) && (!history || !history_len || history_cap == 0))
+        return fail(FOCR_HIP_E_ARG, fmt("%s: the no-repeat-ngram ban and append need history, history_len and a "
+                                        "positive history_cap", name));
+    if (n_whitelist && !whitelist) return fail(FOCR_HIP_E_ARG, fmt("%s: null whitelist", name));
+    const size_t words = (vocab + 31) / 32;
+    a.history = history;
+    a.history_mut = append ? history : nullptr;
+    a.history_len = history_len;
+    a.cap = static_cast<int>(history_cap);
+    a.ngram = static_cast<int>(ngram_size);
+    a.window = static_cast<int>(window);
+    a.whitelist = whitelist;
+    a.n_white = static_cast<int>(n_whitelist);
+    a.vocab = static_cast<int>(vocab);
+    a.ban_words = static_cast<int>(words);
+    a.ban_bits = static_cast<uint32_t*>(ctx->scratch_get(kScrBan, m * words * sizeof(uint32_t)));
+    a.err = static_cast<int*>(ctx->scratch_get(kScrFlag, m * sizeof(int)));
+    if (!a.ban_bits || !a.err) return FOCR_HIP_E_OOM;
+    return FOCR_HIP_OK;
+}
+
+int32_t sampler_check(focr_hip_ctx* ctx, const SamplerArgs& a, size_t m) {
+    std::vector<int> flags(m);
+    FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), a.err, m * sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+                 "D2H sampler flags");
+    FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    for (size_t r = 0; r < m; ++r) {
+        if (flags[r] & 1)
+            return fail(FOCR_HIP_E_SHAPE, fmt("sampler: history_len of row %zu exceeds history_cap %d", r, a.cap));
+        if (flags[r] & 2)
+            return fail(FOCR_HIP_E_SHAPE, fmt("sampler: row %zu history is full (history_cap %d); the token was not "
+                                              "appended", r, a.cap));
+    }
+    return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_lm_head_sample_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+                                   uint32_t* history, size_t history_cap, uint32_t* history_len, size_t ngram_size,
+                                   size_t window, const uint32_t* whitelist, size_t n_whitelist, float temperature,
+                                   uint32_t eos_token_id, int32_t append, float* logits, uint32_t* tokens,
+                                   uint8_t* is_eos, int32_t check) {
+    ENGINE_CTX(ctx);
+    int32_t st = gemv_checks("lm_head_sample_i8", w, m);
+    if (st) return st;
+    if (!x || !tokens) return fail(FOCR_HIP_E_ARG, "lm_head_sample_i8: null device pointer");
+    SamplerArgs a;
+    if ((st = sampler_args(ctx, "decode_step_premasked", m, w->n, history, history_cap, history_len, ngram_size,
+                           window, whitelist, n_whitelist, temperature, append, a)))
+        return st;
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
+    const int nparts = gemv_i8_nparts((int)w->n, ctx->cu_count);
+    uint64_t* keys = static_cast<uint64_t*>(ctx->scratch_get(kScrArg, m * nparts * sizeof(uint64_t)));
+    float* y = logits ? logits : static_cast<float*>(ctx->scratch_get(kScrLogits, m * w->n * sizeof(float)));
+    if (!xq || !xs || !keys || !y) return FOCR_HIP_E_OOM;
+    {
+        ProfScope ps(ctx, "sampler_prep");
+        FOCR_HIP_TRY(launch_sampler_prep(ctx->stream, (int)m, x, (int)w->k, xq, xs, a), "sampler_prep launch");
+    }
+    int np = 0;
+    {
+        ProfScope ps(ctx, "lm_head_gemv");
+        FOCR_HIP_TRY(launch_gemv_i8_banned(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y,
+                                           nullptr, keys, &np, ctx->cu_count, a.ban_bits, a.ban_words),
+                     "lm_head gemv launch");
+    }
+    {
+        ProfScope ps(ctx, "sample_finish");
+        FOCR_HIP_TRY(launch_sample_finish(ctx->stream, (int)m, keys, np, eos_token_id, tokens, is_eos, a),
+                     "sample_finish launch");
+    }
+    return check ? sampler_check(ctx, a, m) : FOCR_HIP_OK;
+}
+
+int32_t focr_hip_sample_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n, uint32_t* history,
+                             size_t history_cap, uint32_t* history_len, size_t ngram_size, size_t window,
+                             const uint32_t* whitelist, size_t n_whitelist, float temperature, uint32_t eos_token_id,
+                             int32_t append, uint32_t* tokens, uint8_t* is_eos, int32_t check) {
+    ENGINE_CTX(ctx);
+    if (m == 0) return FOCR_HIP_OK;
+    if (!logits || !tokens) return fail(FOCR_HIP_E_ARG, "sample_rows: null device pointer");
+    if (m > 65535) return fail(FOCR_HIP_E_SHAPE, "sample_rows: m exceeds the gfx950 tier limit of 65535 rows");
+    SamplerArgs a;
+    int32_t st = sampler_args(ctx, "sample", m, n, history, history_cap, history_len, ngram_size, window, whitelist,
+                              n_whitelist, temperature, append, a);
+    if (st) return st;
+    const int nparts = static_cast<int>(std::min<size_t>(256, (n + 4095) / 4096));
+    uint64_t* keys = static_cast<uint64_t*>(ctx->scratch_get(kScrArg, m * nparts * sizeof(uint64_t)));
+    if (!keys) return FOCR_HIP_E_OOM;
+    ProfScope ps(ctx, "sample_rows");
+    FOCR_HIP_TRY(launch_sampler_prep(ctx->stream, (int)m, nullptr, 0, nullptr, nullptr, a), "sampler_prep launch");
+    FOCR_HIP_TRY(launch_argmax_partial(ctx->stream, logits, (int)m, (int)n, keys, nparts, a.ban_bits, a.ban_words),
+                 "argmax launch");
+    FOCR_HIP_TRY(launch_sample_finish(ctx->stream, (int)m, keys, nparts, eos_token_id, tokens, is_eos, a),
+                 "sample_finish launch");
+    return check ? sampler_check(ctx, a, m) : FOCR_HIP_OK;
+}
+
 int32_t focr_hip_argmax_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n, uint32_t* argmax) {
     ENGINE_CTX(ctx);
     if (m == 0) return FOCR_HIP_OK;

@@ -49,6 +49,7 @@ enum ScratchSlot : int {
     kScrI4,     // int4 prefill intermediates
     kScrI4b,
     kScrFlag,   // device status flags
+    kScrBan,    // sampler ban bitmaps
     kScrCount
 };
 
@@ -178,8 +179,17 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
                           const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                           uint64_t* arg_keys, int* nparts_out, int cu_count);
 int gemv_i8_nparts(int n, int cu_count);
+// The same GEMV with a per-row ban bitmap (ban_words u32 per row): a set bit
+// n writes y[i][n] = -inf and keys see -inf.
+hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
+                                 const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
+                                 uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,
+                                 int ban_words);
 hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int nparts,
                                 uint32_t* argmax);
+// Per-block argmax keys [m][nparts] of a logits matrix (ban_bits nullable).
+hipError_t launch_argmax_partial(hipStream_t s, const float* logits, int m, int n, uint64_t* keys, int nparts,
+                                 const uint32_t* ban_bits, int ban_words);
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
                               int nparts, uint32_t* argmax);
 
@@ -239,6 +249,31 @@ hipError_t launch_retile_i4(hipStream_t s, const uint8_t* b, const float* sc, in
 hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
                                  focr_hip_ctx* ctx);
+
+// k_sampler.hip — greedy decode sampler (sampler.rs): per-row ban bitmaps
+// of the sliding-window no-repeat-ngram processor, then token / EOS / history
+// append from the argmax keys.
+struct SamplerArgs {
+    const uint32_t* history;  // [m][cap] token ids
+    uint32_t* history_mut;    // same array when appending, else null
+    uint32_t* history_len;    // [m] (device)
+    int cap;
+    int ngram, window;
+    const uint32_t* whitelist;
+    int n_white;
+    int vocab;
+    uint32_t* ban_bits;  // [m][ban_words]
+    int ban_words;
+    int* err;  // [m]: 1 = history_len > cap, 2 = append past cap
+};
+// One block per row: optionally quantize x row r (decoder.rs:1588-1597) into
+// xq/xs, then write row r's ban bitmap.
+hipError_t launch_sampler_prep(hipStream_t s, int m, const float* x, int k, int8_t* xq, float* xs,
+                               const SamplerArgs& a);
+// keys [m][nparts] -> tokens [m], is_eos [m] (nullable), and with
+// a.history_mut the token appended to each row's history.
+hipError_t launch_sample_finish(hipStream_t s, int m, const uint64_t* keys, int nparts, uint32_t eos,
+                                uint32_t* tokens, uint8_t* is_eos, const SamplerArgs& a);
 
 // k_quant.hip — load/convert-time weight conversions. src is a stored
 // payload of dtype dt (FOCR_HIP_DT_F32/F16/BF16) in device memory.

@@ -101,6 +101,26 @@ __device__ __forceinline__ int8_t quant_i8(float v, float inv, bool ties_even) {
     return static_cast<int8_t>(static_cast<int>(r));
 }
 
+// decoder.rs:1588-1597 / :1647-1656 for one row, by a whole block of
+// THREADS lanes: amax = max|x|, a_scale = amax / 127 (1.0 for an all-zero
+// row), q = quant_i8(x * (1 / a_scale)). red holds THREADS / 64 floats of LDS.
+template <int THREADS>
+__device__ __forceinline__ void block_quantize_row(const float* __restrict__ xr, int K, int8_t* __restrict__ q,
+                                                   float* __restrict__ a_scale_out, bool ties_even, float* red) {
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < K; i += THREADS) amax = fmaxf(amax, fabsf(xr[i]));
+    amax = wave_max_f(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < THREADS / 64; ++w) amax = fmaxf(amax, red[w]);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+    for (int i = threadIdx.x; i < K; i += THREADS) q[i] = quant_i8(xr[i], inv, ties_even);
+    if (threadIdx.x == 0) *a_scale_out = a_scale;
+}
+
 // decoder.rs:1079-1083 silu(x) = x / (1 + e^-x), accurate expf (no fast math).
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 

@@ -25,27 +25,19 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float* __
                                                                  int ties_even) {
     __shared__ float red[kThreads / 64];
     const int row = blockIdx.x;
-    const float* xr = x + static_cast<size_t>(row) * K;
-    float amax = 0.0f;
-    for (int i = threadIdx.x; i < K; i += kThreads) amax = fmaxf(amax, fabsf(xr[i]));
-    amax = wave_max_f(amax);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    const float inv = 1.0f / a_scale;
-    int8_t* q = xq + static_cast<size_t>(row) * K;
-    for (int i = threadIdx.x; i < K; i += kThreads) q[i] = quant_i8(xr[i], inv, ties_even != 0);
-    if (threadIdx.x == 0) a_scales[row] = a_scale;
+    block_quantize_row<kThreads>(x + static_cast<size_t>(row) * K, K, xq + static_cast<size_t>(row) * K,
+                                 a_scales + row, ties_even != 0, red);
 }
 
-// JB = row chunks (16 B) a lane holds in flight per batch.
-template <int MC, int JB>
+// JB = row chunks (16 B) a lane holds in flight per batch. BAN: output
+// channel n of row i is written -inf when bit n of ban_bits[i] is set (the
+// no-repeat-ngram ban folded into the dequant epilogue, decoder.rs:2319-2357).
+template <int MC, int JB, bool BAN>
 __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
     float* __restrict__ y, int32_t* __restrict__ acc_out, uint64_t* __restrict__ keys,
-    int tiles_per_block) {
+    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words) {
     extern __shared__ int4 lds_x[];  // [MC][K/16]
     __shared__ uint64_t lds_keys[kGroups][MC];
     __shared__ float lds_as[MC];
@@ -94,7 +86,9 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
             const int v = reduce16_add(acc[i]);
             if (n < N && i < M && lane == (i & 15)) {
                 const float t0 = static_cast<float>(v) * lds_as[i];
-                const float yv = t0 * wscale;
+                float yv = t0 * wscale;
+                if (BAN && ((ban_bits[static_cast<size_t>(i) * ban_words + (n >> 5)] >> (n & 31)) & 1u))
+                    yv = -__builtin_inff();
                 y[static_cast<size_t>(i) * N + n] = yv;
                 if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = v;
                 if (keys) {
@@ -139,15 +133,22 @@ __global__ __launch_bounds__(kThreads) void argmax_reduce_kernel(const uint64_t*
     }
 }
 
-// Partial argmax keys over a logits matrix: grid (nparts, m).
+// Partial argmax keys over a logits matrix: grid (nparts, m). With ban_bits,
+// a banned entry counts as -inf (sampler.rs:245-257 masked copy, then
+// argmax_row) without writing the logits.
 __global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float* __restrict__ logits,
-                                                                  int n, uint64_t* __restrict__ keys) {
+                                                                  int n, uint64_t* __restrict__ keys,
+                                                                  const uint32_t* __restrict__ ban_bits,
+                                                                  int ban_words) {
     __shared__ uint64_t red[kThreads / 64];
     const int row = blockIdx.y;
     const float* lr = logits + static_cast<size_t>(row) * n;
+    const uint32_t* bb = ban_bits ? ban_bits + static_cast<size_t>(row) * ban_words : nullptr;
     uint64_t b = 0ull;
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-        const uint64_t k = argmax_key(lr[i], static_cast<uint32_t>(i));
+        float v = lr[i];
+        if (bb && ((bb[i >> 5] >> (i & 31)) & 1u)) v = -__builtin_inff();
+        const uint64_t k = argmax_key(v, static_cast<uint32_t>(i));
         b = k > b ? k : b;
     }
     b = wave_max_u64(b);
@@ -187,7 +188,16 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int
 hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
                           const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                           uint64_t* arg_keys, int* nparts_out, int cu_count) {
+    return launch_gemv_i8_banned(s, w, ws, n, k, xq, a_scales, m, y, acc, arg_keys, nparts_out, cu_count, nullptr,
+                                 0);
+}
+
+hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
+                                 const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
+                                 uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,
+                                 int ban_words) {
     if (m < 1 || m > 32 || k % 16 != 0 || k <= 0) return hipErrorInvalidValue;
+    if (ban_bits && ban_words * 32 < n) return hipErrorInvalidValue;
     const int tiles = (n + kGroups - 1) / kGroups;
     const int tpb = tiles_per_block_for(n, cu_count);
     const int grid = (tiles + tpb - 1) / tpb;
@@ -196,10 +206,14 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
     if (lds > 57344) return hipErrorInvalidValue;
     int mc = 1;
     while (mc < m) mc <<= 1;
-#define FOCR_GEMV_CASE(MCV)                                                                     \
-    case MCV:                                                                                   \
-        FOCR_LAUNCH((gemv_i8_kernel<MCV, 8>), dim3(grid), dim3(kThreads), lds, s, w, ws, \
-                           n, k, xq, a_scales, m, y, acc, arg_keys, tpb);                       \
+#define FOCR_GEMV_CASE(MCV)                                                                              \
+    case MCV:                                                                                            \
+        if (ban_bits)                                                                                    \
+            FOCR_LAUNCH((gemv_i8_kernel<MCV, 8, true>), dim3(grid), dim3(kThreads), lds, s, w, ws, n, k, \
+                        xq, a_scales, m, y, acc, arg_keys, tpb, ban_bits, ban_words);                    \
+        else                                                                                             \
+            FOCR_LAUNCH((gemv_i8_kernel<MCV, 8, false>), dim3(grid), dim3(kThreads), lds, s, w, ws, n,   \
+                        k, xq, a_scales, m, y, acc, arg_keys, tpb, nullptr, 0);                          \
         break;
     switch (mc) {
         FOCR_GEMV_CASE(1)
@@ -225,10 +239,16 @@ hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int 
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int m, int n, uint64_t* keys,
                               int nparts, uint32_t* argmax) {
     if (m == 0) return hipSuccess;
-    FOCR_LAUNCH(argmax_partial_kernel, dim3(nparts, m), dim3(kThreads), 0, s, logits, n, keys);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_argmax_partial(s, logits, m, n, keys, nparts, nullptr, 0);
     if (e != hipSuccess) return e;
     return launch_argmax_reduce(s, keys, m, nparts, argmax);
+}
+
+hipError_t launch_argmax_partial(hipStream_t s, const float* logits, int m, int n, uint64_t* keys, int nparts,
+                                 const uint32_t* ban_bits, int ban_words) {
+    if (m == 0) return hipSuccess;
+    FOCR_LAUNCH(argmax_partial_kernel, dim3(nparts, m), dim3(kThreads), 0, s, logits, n, keys, ban_bits, ban_words);
+    return hipGetLastError();
 }
 
 }  // namespace focr

@@ -106,6 +106,48 @@ def argmax_rows(logits: DeviceArray, argmax: DeviceArray) -> None:
     _abi.call("focr_hip_argmax_rows", logits.ctx.handle, logits.c_ptr, m, n, argmax.c_ptr)
 
 
+# sampler.rs:33-36 defaults: no_repeat_ngram_size 35, ngram_window 128
+# (single image; 1024 multi-image), EOS id 1.
+DEFAULT_NO_REPEAT_NGRAM_SIZE = 35
+NGRAM_WINDOW_SINGLE = 128
+NGRAM_WINDOW_MULTI = 1024
+DEFAULT_EOS_TOKEN_ID = 1
+
+
+def _sampler_args(history, history_len, ngram_size, window, whitelist, temperature, eos, append):
+    cap = history.shape[1] if history is not None else 0
+    nw = whitelist.shape[0] if whitelist is not None else 0
+    return [_p(history), cap, _p(history_len), int(ngram_size), int(window), _p(whitelist), nw, float(temperature),
+            int(eos), 1 if append else 0]
+
+
+def lm_head_sample_i8(w: QInt8, x: DeviceArray, tokens: DeviceArray, history: DeviceArray | None = None,
+                      history_len: DeviceArray | None = None, ngram_size: int = DEFAULT_NO_REPEAT_NGRAM_SIZE,
+                      window: int = NGRAM_WINDOW_SINGLE, whitelist: DeviceArray | None = None,
+                      temperature: float = 0.0, eos: int = DEFAULT_EOS_TOKEN_ID, append: bool = False,
+                      logits: DeviceArray | None = None, is_eos: DeviceArray | None = None,
+                      check: bool = False) -> None:
+    """Greedy decode step with the no-repeat-ngram ban in the LM-head epilogue
+    (decoder.rs:2319-2400, sampler.rs:191-235, :426-460) for m streams:
+    history [m, cap] u32 and history_len [m] u32 live on the device."""
+    m = x.shape[0]
+    _abi.call("focr_hip_lm_head_sample_i8", w.ctx.handle, w.handle, x.c_ptr, m,
+              *_sampler_args(history, history_len, ngram_size, window, whitelist, temperature, eos, append),
+              _p(logits), tokens.c_ptr, _p(is_eos), 1 if check else 0)
+
+
+def sample_rows(logits: DeviceArray, tokens: DeviceArray, history: DeviceArray | None = None,
+                history_len: DeviceArray | None = None, ngram_size: int = DEFAULT_NO_REPEAT_NGRAM_SIZE,
+                window: int = NGRAM_WINDOW_SINGLE, whitelist: DeviceArray | None = None, temperature: float = 0.0,
+                eos: int = DEFAULT_EOS_TOKEN_ID, append: bool = False, is_eos: DeviceArray | None = None,
+                check: bool = False) -> None:
+    """sampler.rs:491-545 batched_sample / batched_decode_step over device logits [m, n]."""
+    m, n = logits.shape
+    _abi.call("focr_hip_sample_rows", logits.ctx.handle, logits.c_ptr, m, n,
+              *_sampler_args(history, history_len, ngram_size, window, whitelist, temperature, eos, append),
+              tokens.c_ptr, _p(is_eos), 1 if check else 0)
+
+
 class MoeLayer:
     """A MoE layer's router (f32) and int8 experts, uploaded once.
 

@@ -48,6 +48,7 @@ extern "C" {
 #define FOCR_HIP_E_STATE (-8)      /* rswa.rs:452-455/869-887 state errors */
 #define FOCR_HIP_E_FORMAT (-9)     /* FocrError::FormatMismatch of the weight container */
 #define FOCR_HIP_E_NOT_FOUND (-10) /* FocrError::ModelNotFound: weights file unreadable */
+#define FOCR_HIP_E_NOT_IMPLEMENTED (-11) /* FocrError::NotImplemented (temperature > 0) */
 
 /* Stored dtypes of the weight container (weights.rs:148-170 DType). */
 #define FOCR_HIP_DT_F32 0
@@ -190,6 +191,35 @@ int32_t focr_hip_gemv_i8_prequant(focr_hip_ctx* ctx, const focr_hip_qint8* w, co
  * u32: first index of the maximum, NaN skipped, all-NaN row -> 0. */
 int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x,
                             size_t m, float* logits, uint32_t* argmax);
+/* Greedy decode with the sliding-window no-repeat-ngram ban folded into the
+ * LM-head epilogue: decoder.rs:2319-2357 gemv_i8_ngram_masked /
+ * :2381-2400 lm_head_cached_i8_ngram_masked (input = the already final-normed
+ * rows) with the ban set of sampler.rs:191-235 / :269-278, then
+ * sampler.rs:426-460 decode_step_premasked, for m streams at once (the
+ * batched spine's per-stream ban, sampler.rs:491-545). Per row r:
+ * history[r][0..history_len[r]) is stream r's generated sequence (device,
+ * [m][history_cap] u32; history_len device [m]); bans use ngram_size /
+ * window (0 = the whole history) / whitelist (device, nullable); logits
+ * (nullable) receive the masked row; tokens [m] the argmax; is_eos
+ * (nullable, u8 [m]) token == eos_token_id. With append = 1 the token is
+ * written at history[r][history_len[r]] and history_len[r] is incremented
+ * on the device. temperature > 0 -> E_NOT_IMPLEMENTED (sampler.rs:362-367).
+ * check = 1 synchronises and reports a history_len over history_cap (or a
+ * full history on append) as E_SHAPE. m <= 32. */
+int32_t focr_hip_lm_head_sample_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x,
+                                   size_t m, uint32_t* history, size_t history_cap,
+                                   uint32_t* history_len, size_t ngram_size, size_t window,
+                                   const uint32_t* whitelist, size_t n_whitelist, float temperature,
+                                   uint32_t eos_token_id, int32_t append, float* logits,
+                                   uint32_t* tokens, uint8_t* is_eos, int32_t check);
+/* sampler.rs:491-545 batched_sample / batched_decode_step (and :346-395
+ * sample per row) over given device logits [m, n] (read only): the same ban,
+ * argmax, EOS flag and optional append as focr_hip_lm_head_sample_i8. */
+int32_t focr_hip_sample_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n,
+                             uint32_t* history, size_t history_cap, uint32_t* history_len,
+                             size_t ngram_size, size_t window, const uint32_t* whitelist,
+                             size_t n_whitelist, float temperature, uint32_t eos_token_id,
+                             int32_t append, uint32_t* tokens, uint8_t* is_eos, int32_t check);
 /* sampler.rs:168-186 argmax_row over m rows of n f32 logits. */
 int32_t focr_hip_argmax_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n,
                              uint32_t* argmax);

@@ -221,6 +221,56 @@ int oracle_lm_head_i8(const float* x, size_t m, const int8_t* w, const float* sc
     return ORACLE_OK;
 }
 
+/* ---- src/native_engine/sampler.rs no-repeat-ngram ban + greedy sample ------
+ * sampler.rs:191-235 for_each_sliding_window_ngram_ban: nothing when ngram is
+ * 0 or len < ngram; scan idx in [start, len - ngram + 1) with start =
+ * len - window (saturating) or 0 for window 0; an n-gram whose first ngram-1
+ * tokens equal the last ngram-1 tokens of seq bans its last token, unless
+ * whitelisted or >= vocab. Writes the bans in scan order (repeats kept),
+ * returns how many. */
+size_t oracle_ngram_bans(const uint32_t* seq, size_t len, size_t ngram, size_t window, const uint32_t* white,
+                         size_t n_white, size_t vocab, uint32_t* bans) {
+    size_t nb = 0;
+    if (ngram == 0 || len < ngram) return 0;
+    size_t start = window == 0 ? 0 : (len > window ? len - window : 0);
+    size_t end = len - ngram + 1;
+    if (end <= start) return 0;
+    const uint32_t* prefix = seq + (len - (ngram - 1));
+    for (size_t idx = start; idx < end; ++idx) {
+        int match = 1;
+        for (size_t j = 0; j + 1 < ngram; ++j)
+            if (seq[idx + j] != prefix[j]) {
+                match = 0;
+                break;
+            }
+        if (!match) continue;
+        uint32_t banned = seq[idx + ngram - 1];
+        int wl = 0;
+        for (size_t j = 0; j < n_white; ++j) wl |= white[j] == banned;
+        if (wl || banned >= vocab) continue;
+        bans[nb++] = banned;
+    }
+    return nb;
+}
+
+/* sampler.rs:346-395 sample (greedy): the row with every banned id set to
+ * -inf (the :245-257 masked copy; written to masked when non-NULL), then
+ * argmax_row. */
+int oracle_sample(const float* row, size_t n, const uint32_t* seq, size_t len, size_t ngram, size_t window,
+                  const uint32_t* white, size_t n_white, float* masked, uint32_t* token) {
+    if (n == 0) return ORACLE_E_SHAPE;
+    float* m = (float*)malloc(n * sizeof(float));
+    uint32_t* bans = (uint32_t*)malloc((len + 1) * sizeof(uint32_t));
+    memcpy(m, row, n * sizeof(float));
+    size_t nb = oracle_ngram_bans(seq, len, ngram, window, white, n_white, n, bans);
+    for (size_t i = 0; i < nb; ++i) m[bans[i]] = -INFINITY;
+    int st = oracle_argmax_row(m, n, token);
+    if (masked) memcpy(masked, m, n * sizeof(float));
+    free(m);
+    free(bans);
+    return st;
+}
+
 /* ---- src/native_engine/moe.rs:181-266 route --------------------------------
  * logits = x . G^T, softmax over experts, greedy top-k by descending prob
  * (strict >, lower index on ties, NaN skipped, error if no finite score),

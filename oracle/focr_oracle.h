@@ -20,6 +20,10 @@
  *   quantize_row_i8*  — quantizer known answers (quant/int8.rs:300-366,
  *                       nn.rs:600-628) + half-away vs ties-even split cases.
  *   argmax_row        — sampler.rs:618-640 (ties, NaN, -inf, all-NaN -> 0).
+ *   ngram_bans/sample — sampler.rs:717-925 known answers (n-gram sizes 1/2/35,
+ *                       window 0/2/16/128/1024 boundaries, whitelist,
+ *                       out-of-range ids, all-banned row) + a brute-force
+ *                       re-derivation from the n-gram definition.
  *   route             — moe.rs:777-1028 known answers; the f64 logit/softmax
  *                       rule is this build's documented definition
  *                       (router numerics in the reference live in the
@@ -75,6 +79,12 @@ void oracle_dequant_i8(const int32_t* acc, size_t m, size_t n, const float* a_sc
 /* ---- src/native_engine/sampler.rs --------------------------------------- */
 int oracle_argmax_row(const float* logits, size_t n, uint32_t* idx);
 
+/* sampler.rs:191-235 ban set (scan order, repeats kept) and :346-395 greedy
+ * sample of one row under it (masked nullable). */
+size_t oracle_ngram_bans(const uint32_t* seq, size_t len, size_t ngram, size_t window, const uint32_t* white,
+                         size_t n_white, size_t vocab, uint32_t* bans);
+int oracle_sample(const float* row, size_t n, const uint32_t* seq, size_t len, size_t ngram, size_t window,
+                  const uint32_t* white, size_t n_white, float* masked, uint32_t* token);
 /* LM head: per-row quantize + GEMV + dequant + argmax (decoder.rs:2275-2296,
  * 2943-2965 with sampler.rs:168-186). */
 int oracle_lm_head_i8(const float* x, size_t m, const int8_t* w, const float* scales, size_t n,

@@ -32,6 +32,8 @@ _SIGS = {
     "oracle_dequant_i8": ([_P, _SZ, _SZ, _P, _P, _P], None),
     "oracle_argmax_row": ([_P, _SZ, _P], C.c_int),
     "oracle_lm_head_i8": ([_P, _SZ, _P, _P, _SZ, _SZ, _P, _P], C.c_int),
+    "oracle_ngram_bans": ([_P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _P], _SZ),
+    "oracle_sample": ([_P, _SZ, _P, _SZ, _SZ, _SZ, _P, _SZ, _P, _P], C.c_int),
     "oracle_route": ([_P, _SZ, _SZ, _P, _SZ, _SZ, C.c_int, C.c_float, _P, _P, _P], C.c_int),
     "oracle_silu": ([C.c_float], C.c_float),
     "oracle_expert_i8": ([_P, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P], None),
@@ -153,6 +155,28 @@ def lm_head_i8(x, w, scales, n, k):
     am = np.zeros(m, np.uint32)
     assert lib().oracle_lm_head_i8(p(x), m, p(_c(w, np.int8)), p(_c(scales, np.float32)), n, k, p(logits), p(am)) == 0
     return logits.reshape(m, n), am
+
+
+def ngram_bans(seq, ngram, window, vocab, whitelist=()):
+    """sampler.rs:191-235: the banned ids in scan order (repeats kept)."""
+    seq = _c(seq, np.uint32)
+    white = _c(list(whitelist), np.uint32)
+    out = np.zeros(max(seq.size, 1), np.uint32)
+    nb = lib().oracle_ngram_bans(p(seq) if seq.size else None, seq.size, ngram, window,
+                                 p(white) if white.size else None, white.size, vocab, p(out))
+    return out[:nb]
+
+
+def sample(row, seq, ngram, window, whitelist=()):
+    """sampler.rs:346-395 greedy sample: (status, token, masked row)."""
+    row = _c(row, np.float32).reshape(-1)
+    seq = _c(seq, np.uint32)
+    white = _c(list(whitelist), np.uint32)
+    masked = np.zeros(max(row.size, 1), np.float32)
+    tok = C.c_uint32()
+    st = lib().oracle_sample(p(row) if row.size else None, row.size, p(seq) if seq.size else None, seq.size, ngram,
+                             window, p(white) if white.size else None, white.size, p(masked), C.byref(tok))
+    return st, tok.value, masked[:row.size]
 
 
 def route(hidden, gate, n_experts, top_k, norm_topk=False, routed_scale=1.0):
