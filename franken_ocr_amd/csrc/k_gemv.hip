@@ -29,10 +29,14 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float* __
                                  a_scales + row, ties_even != 0, red);
 }
 
-// JB = row chunks (16 B) a lane holds in flight per batch. BAN: output
+// JB = row chunks (16 B) a lane holds in flight per batch; R = weight rows a
+// 16-lane group computes per activation chunk it reads from LDS (LDS bytes
+// per weight byte = M / R: at M = 8 the one-row form is LDS-bound). A tile
+// is 16 * R rows: row base + r * 16 + group, so every load instruction of a
+// wave covers four adjacent rows, 256 contiguous bytes each. BAN: output
 // channel n of row i is written -inf when bit n of ban_bits[i] is set (the
 // no-repeat-ngram ban folded into the dequant epilogue, decoder.rs:2319-2357).
-template <int MC, int JB, bool BAN>
+template <int MC, int JB, int R, bool BAN>
 __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
@@ -41,6 +45,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     extern __shared__ int4 lds_x[];  // [MC][K/16]
     __shared__ uint64_t lds_keys[kGroups][MC];
     __shared__ float lds_as[MC];
+    constexpr int MB = MC > 16 ? MC / 16 : 1;  // rows i a lane writes: lane == (i & 15)
     const int group = threadIdx.x >> 4;
     const int lane = threadIdx.x & 15;
     const int C = K >> 4;
@@ -49,65 +54,233 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     if (threadIdx.x < MC) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     __syncthreads();
 
-    uint64_t best[MC];
+    // the argmax key of row i is kept by lane i & 15 only: best[i >> 4]
+    uint64_t best[MB];
 #pragma unroll
-    for (int i = 0; i < MC; ++i) best[i] = 0ull;
+    for (int q = 0; q < MB; ++q) best[q] = 0ull;
 
     const int tile0 = blockIdx.x * tiles_per_block;
     for (int t = 0; t < tiles_per_block; ++t) {
-        const int n = (tile0 + t) * kGroups + group;
-        if ((tile0 + t) * kGroups >= N) break;
-        int acc[MC];
+        const int base = (tile0 + t) * kGroups * R;
+        if (base >= N) break;
+        // ban words of this lane's outputs, fetched ahead of the weights
+        uint32_t banw[R][MB];
+        if (BAN) {
 #pragma unroll
-        for (int i = 0; i < MC; ++i) acc[i] = 0;
-        if (n < N) {
-            const int4* wrow = reinterpret_cast<const int4*>(W + static_cast<size_t>(n) * K);
-            for (int cb = 0; cb < C; cb += 16 * JB) {
-                int4 w[JB];
+            for (int r = 0; r < R; ++r) {
+                const int n = base + r * kGroups + group;
 #pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    const int c = cb + lane + 16 * j;
-                    w[j] = c < C ? ld_stream(wrow + c) : make_int4(0, 0, 0, 0);
-                }
-#pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    const int c = cb + lane + 16 * j;
-                    if (c < C) {
-#pragma unroll
-                        for (int i = 0; i < MC; ++i)
-                            if (i < M) acc[i] = dot16_i8(w[j], lds_x[i * C + c], acc[i]);
-                    }
+                for (int q = 0; q < MB; ++q) {
+                    const int i = lane + 16 * q;
+                    banw[r][q] = (n < N && i < M) ? ban_bits[static_cast<size_t>(i) * ban_words + (n >> 5)] : 0u;
                 }
             }
         }
-        const float wscale = n < N ? ws[n] : 0.0f;
+        int acc[R][MC];
 #pragma unroll
-        for (int i = 0; i < MC; ++i) {
-            const int v = reduce16_add(acc[i]);
-            if (n < N && i < M && lane == (i & 15)) {
-                const float t0 = static_cast<float>(v) * lds_as[i];
-                float yv = t0 * wscale;
-                if (BAN && ((ban_bits[static_cast<size_t>(i) * ban_words + (n >> 5)] >> (n & 31)) & 1u))
-                    yv = -__builtin_inff();
-                y[static_cast<size_t>(i) * N + n] = yv;
-                if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = v;
-                if (keys) {
-                    const uint64_t k = argmax_key(yv, static_cast<uint32_t>(n));
-                    best[i] = k > best[i] ? k : best[i];
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < MC; ++i) acc[r][i] = 0;
+        for (int cb = 0; cb < C; cb += 16 * JB) {
+            int4 w[R][JB];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int n = base + r * kGroups + group;
+                const int4* wrow = reinterpret_cast<const int4*>(W + static_cast<size_t>(n < N ? n : 0) * K);
+#pragma unroll
+                for (int j = 0; j < JB; ++j) {
+                    const int c = cb + lane + 16 * j;
+                    w[r][j] = (n < N && c < C) ? ld_stream(wrow + c) : make_int4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+                const int c = cb + lane + 16 * j;
+                if (c < C) {
+#pragma unroll
+                    for (int i = 0; i < MC; ++i)
+                        if (i < M) {
+                            const int4 xv = lds_x[i * C + c];
+#pragma unroll
+                            for (int r = 0; r < R; ++r) acc[r][i] = dot16_i8(w[r][j], xv, acc[r][i]);
+                        }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = base + r * kGroups + group;
+            const float wscale = n < N ? ws[n] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < MC; ++i) {
+                const int v = reduce16_add(acc[r][i]);
+                if (n < N && i < M && lane == (i & 15)) {
+                    const float t0 = static_cast<float>(v) * lds_as[i];
+                    float yv = t0 * wscale;
+                    if (BAN && ((banw[r][i >> 4] >> (n & 31)) & 1u)) yv = -__builtin_inff();
+                    y[static_cast<size_t>(i) * N + n] = yv;
+                    if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = v;
+                    if (keys) {
+                        const uint64_t k = argmax_key(yv, static_cast<uint32_t>(n));
+                        best[i >> 4] = k > best[i >> 4] ? k : best[i >> 4];
+                    }
                 }
             }
         }
     }
     if (keys) {
-        // best[i] lives in lane (i & 15) of each group; fold the 16 groups.
+        // best[i >> 4] of row i lives in lane (i & 15) of each group; fold the 16 groups.
 #pragma unroll
         for (int i = 0; i < MC; ++i)
-            if (lane == (i & 15)) lds_keys[group][i] = best[i];
+            if (lane == (i & 15)) lds_keys[group][i] = best[i >> 4];
         __syncthreads();
         if (threadIdx.x < M) {
             uint64_t b = 0ull;
             for (int g = 0; g < kGroups; ++g) b = lds_keys[g][threadIdx.x] > b ? lds_keys[g][threadIdx.x] : b;
             keys[static_cast<size_t>(threadIdx.x) * gridDim.x + blockIdx.x] = b;
+        }
+    }
+}
+
+// The GEMV on the matrix cores (K % 256 == 0, M <= 32). A wave owns tiles
+// of 16 weight rows and walks each in 256-byte column chunks:
+//   * global -> VGPRs: 4 coalesced 16-byte loads per lane per chunk (each
+//     load instruction covers 4 rows x 256 contiguous bytes), issued two
+//     chunks ahead of the math;
+//   * VGPRs -> LDS (a wave-private buffer [16][256]) with the
+//     16-byte piece p of row r stored at slot p ^ r, so both the writes and
+//     the 16-row B-fragment reads are bank-conflict free;
+//   * v_mfma_i32_16x16x64_i8 with the activations as A (16 rows staged
+//     once per block, rows >= M zero; M > 16 runs a second pass) and the
+//     weights as B.
+// The VALU does no dot products (the sdot4 form is VALU-bound from M = 4
+// up); output element v of lane l is row 4*(l/16) + v of channel
+// n0 + l%16, dequantized as ((f32)acc * a_s) * w_s like the sdot4 kernel.
+typedef int v4i_m __attribute__((ext_vector_type(4)));
+constexpr int kMfmaMinRows = 2;  // below this the sdot4 kernel is already HBM-bound
+constexpr int kMfmaTileBytes = 16 * 256;  // one chunk of one tile
+
+template <bool BAN>
+__global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
+    const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
+    float* __restrict__ y, int32_t* __restrict__ acc_out, uint64_t* __restrict__ keys,
+    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words) {
+    extern __shared__ int4 lds_dyn[];  // x [16][K/16 + 1] then per-wave [16][16] chunks
+    __shared__ uint64_t lds_keys[kThreads / 64][16];
+    __shared__ float lds_as[16];
+    const int C = K >> 4;
+    const int xs = C + 1;  // x row stride in 16-byte chunks (one chunk of padding)
+    const int wave = threadIdx.x >> 6;
+    const int l = threadIdx.x & 63;
+    const int g = l >> 4, col = l & 15;
+    int4* lds_xv = lds_dyn;
+    int4* wbuf = lds_dyn + 16 * xs + wave * (kMfmaTileBytes / 16);
+
+    const int nch = K >> 8;  // 256-byte chunks per row
+    const int tile0 = blockIdx.x * tiles_per_block;
+    int my_tiles = 0;  // tiles tile0 + wave + 4j of this block that hold rows
+    for (int tt = wave; tt < tiles_per_block && (tile0 + tt) * 16 < N; tt += kThreads / 64) ++my_tiles;
+    const int nq = my_tiles * nch;
+    // chunk q of this wave: tile tile0 + wave + 4 * (q / nch), column chunk q % nch
+    auto load = [&](int q, int4 (&rg)[4]) {
+        const int n0 = (tile0 + wave + (kThreads / 64) * (q / nch)) * 16;
+        const int kc = q % nch;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * j + g;  // this lane's row for load j
+            rg[j] = n < N ? ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n) * K + kc * 256) + col)
+                          : make_int4(0, 0, 0, 0);
+        }
+    };
+    // One chunk buffer per wave: the chunk q + 1 store follows the chunk q
+    // reads in the same wave, and a wave's LDS operations execute in order.
+    auto store = [&](const int4 (&rg)[4]) {
+        int4* b = wbuf;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = 4 * j + g;
+            b[r * 16 + (col ^ r)] = rg[j];
+        }
+    };
+    // the first two chunks are in flight while the activations are staged
+    int4 rg0[4], rg1[4];
+    if (nq > 0) load(0, rg0);
+    if (nq > 1) load(1, rg1);
+    const int4* x4 = reinterpret_cast<const int4*>(xq);
+    for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
+        const int r = i / C, c = i - r * C;
+        lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+    }
+    if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+    __syncthreads();
+    if (nq > 0) store(rg0);
+
+    uint64_t best[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) best[v] = 0ull;
+    v4i_m acc = {0, 0, 0, 0};
+    // Chunk q is read from LDS while q + 1 (in rg_next) and q + 2 (issued
+    // into rg_free, whose chunk q is already in LDS) are in flight.
+    auto iter = [&](int q, int4 (&rg_next)[4], int4 (&rg_free)[4]) {
+        const int kc = q % nch;
+        if (kc == 0) acc = v4i_m{0, 0, 0, 0};
+        if (q + 2 < nq) load(q + 2, rg_free);
+        const int4* b = wbuf;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int piece = 4 * st + g;
+            const int4 bw = b[col * 16 + (piece ^ col)];
+            const int4 a = lds_xv[col * xs + kc * 16 + piece];
+            const v4i_m bv = {bw.x, bw.y, bw.z, bw.w};
+            const v4i_m av = {a.x, a.y, a.z, a.w};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc, 0, 0, 0);
+        }
+        if (kc == nch - 1) {
+            const int n = (tile0 + wave + (kThreads / 64) * (q / nch)) * 16 + col;
+            const bool valid = n < N;
+            const float wscale = valid ? ws[n] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = 4 * g + v;
+                if (valid && i < M) {
+                    const int av = acc[v];
+                    const float t0 = static_cast<float>(av) * lds_as[i];
+                    float yv = t0 * wscale;
+                    if (BAN && ((ban_bits[static_cast<size_t>(i) * ban_words + (n >> 5)] >> (n & 31)) & 1u))
+                        yv = -__builtin_inff();
+                    y[static_cast<size_t>(i) * N + n] = yv;
+                    if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = av;
+                    if (keys) {
+                        const uint64_t k = argmax_key(yv, static_cast<uint32_t>(n));
+                        best[v] = k > best[v] ? k : best[v];
+                    }
+                }
+            }
+        }
+        if (q + 1 < nq) store(rg_next);
+    };
+    for (int q = 0; q < nq; q += 2) {
+        iter(q, rg1, rg0);
+        if (q + 1 < nq) iter(q + 1, rg0, rg1);
+    }
+    if (keys) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            uint64_t bk = best[v];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) {
+                const uint64_t w2 = __shfl_xor(bk, o, 16);
+                bk = w2 > bk ? w2 : bk;
+            }
+            if (col == 0) lds_keys[wave][4 * g + v] = bk;
+        }
+        __syncthreads();
+        if (threadIdx.x < M) {
+            uint64_t bk = 0ull;
+            for (int w2 = 0; w2 < kThreads / 64; ++w2)
+                bk = lds_keys[w2][threadIdx.x] > bk ? lds_keys[w2][threadIdx.x] : bk;
+            keys[static_cast<size_t>(threadIdx.x) * gridDim.x + blockIdx.x] = bk;
         }
     }
 }
@@ -198,30 +371,65 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
                                  int ban_words) {
     if (m < 1 || m > 32 || k % 16 != 0 || k <= 0) return hipErrorInvalidValue;
     if (ban_bits && ban_words * 32 < n) return hipErrorInvalidValue;
-    const int tiles = (n + kGroups - 1) / kGroups;
-    const int tpb = tiles_per_block_for(n, cu_count);
-    const int grid = (tiles + tpb - 1) / tpb;
-    if (nparts_out) *nparts_out = grid;
     const size_t lds = static_cast<size_t>(m) * k;
     if (lds > 57344) return hipErrorInvalidValue;
     int mc = 1;
     while (mc < m) mc <<= 1;
-#define FOCR_GEMV_CASE(MCV)                                                                              \
-    case MCV:                                                                                            \
-        if (ban_bits)                                                                                    \
-            FOCR_LAUNCH((gemv_i8_kernel<MCV, 8, true>), dim3(grid), dim3(kThreads), lds, s, w, ws, n, k, \
-                        xq, a_scales, m, y, acc, arg_keys, tpb, ban_bits, ban_words);                    \
-        else                                                                                             \
-            FOCR_LAUNCH((gemv_i8_kernel<MCV, 8, false>), dim3(grid), dim3(kThreads), lds, s, w, ws, n,   \
-                        k, xq, a_scales, m, y, acc, arg_keys, tpb, nullptr, 0);                          \
+    const size_t lds_mfma = (static_cast<size_t>(16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) *
+                            sizeof(int4);
+    if (m >= kMfmaMinRows && k % 256 == 0 && lds_mfma <= 65536) {
+        const int tiles = (n + 15) / 16;
+        // four blocks per CU (16 waves, 37 KB of LDS each at K = 1280): the
+        // measured optimum between 2 and 8 at M = 8 and M = 16
+        const int target_blocks = (cu_count > 0 ? cu_count : 256) * 4;
+        int tpb = (tiles + target_blocks - 1) / target_blocks;
+        tpb = (tpb + 3) & ~3;  // whole rounds of the block's four waves
+        const int grid = (tiles + tpb - 1) / tpb;
+        if (nparts_out) *nparts_out = grid;
+        // up to 16 activation rows per pass; rows 16..31 take a second pass
+        // over the weights with every row-indexed pointer advanced
+        for (int r0 = 0; r0 < m; r0 += 16) {
+            const int mr = m - r0 < 16 ? m - r0 : 16;
+            const int8_t* xq_r = xq + static_cast<size_t>(r0) * k;
+            float* y_r = y + static_cast<size_t>(r0) * n;
+            int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
+            uint64_t* keys_r = arg_keys ? arg_keys + static_cast<size_t>(r0) * grid : nullptr;
+            if (ban_bits)
+                FOCR_LAUNCH((gemv_i8_mfma_kernel<true>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k, xq_r,
+                            a_scales + r0, mr, y_r, acc_r, keys_r, tpb, ban_bits + static_cast<size_t>(r0) * ban_words,
+                            ban_words);
+            else
+                FOCR_LAUNCH((gemv_i8_mfma_kernel<false>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k,
+                            xq_r, a_scales + r0, mr, y_r, acc_r, keys_r, tpb, nullptr, 0);
+        }
+        return hipGetLastError();
+    }
+    // rows per group: one for M <= 2 (HBM-bound already), four up to M = 8,
+    // two beyond (accumulator registers grow as R * M)
+    const int R = mc <= 2 ? 1 : (mc <= 8 ? 4 : 2);
+    const int rows_per_tile = kGroups * R;
+    const int tiles = (n + rows_per_tile - 1) / rows_per_tile;
+    const int target_blocks = (cu_count > 0 ? cu_count : 256) * 8;
+    int tpb = (tiles + target_blocks - 1) / target_blocks;
+    tpb = tpb < 1 ? 1 : tpb;
+    const int grid = (tiles + tpb - 1) / tpb;
+    if (nparts_out) *nparts_out = grid;
+#define FOCR_GEMV_CASE(MCV, JBV, RV)                                                                      \
+    case MCV:                                                                                             \
+        if (ban_bits)                                                                                     \
+            FOCR_LAUNCH((gemv_i8_kernel<MCV, JBV, RV, true>), dim3(grid), dim3(kThreads), lds, s, w, ws, n, \
+                        k, xq, a_scales, m, y, acc, arg_keys, tpb, ban_bits, ban_words);                  \
+        else                                                                                              \
+            FOCR_LAUNCH((gemv_i8_kernel<MCV, JBV, RV, false>), dim3(grid), dim3(kThreads), lds, s, w, ws, n,\
+                        k, xq, a_scales, m, y, acc, arg_keys, tpb, nullptr, 0);                           \
         break;
     switch (mc) {
-        FOCR_GEMV_CASE(1)
-        FOCR_GEMV_CASE(2)
-        FOCR_GEMV_CASE(4)
-        FOCR_GEMV_CASE(8)
-        FOCR_GEMV_CASE(16)
-        FOCR_GEMV_CASE(32)
+        FOCR_GEMV_CASE(1, 8, 1)
+        FOCR_GEMV_CASE(2, 8, 1)
+        FOCR_GEMV_CASE(4, 5, 4)
+        FOCR_GEMV_CASE(8, 5, 4)
+        FOCR_GEMV_CASE(16, 4, 2)
+        FOCR_GEMV_CASE(32, 4, 2)
         default:
             return hipErrorInvalidValue;
     }
