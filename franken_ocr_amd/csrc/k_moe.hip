@@ -66,89 +66,98 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
 // ---- route: one block (16 waves) per token ---------------------------------
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteEPW = 4;  // router rows per wave (16 waves x 4 = kMaxE)
+constexpr int kRouteNC = 5;   // float4 chunks per lane per batch: 64 x 5 x 4 = 1280 floats
 
-// Thread (e, l) = (tid / 16, tid % 16) owns router row e's float4 chunks
-// c = l + 16 i, fetched in batches of NI with the next batch in flight while
-// the current one is consumed; the first batch is issued before the token
-// row, so both round trips overlap.
-template <int NI>
-__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+// Wave w owns router rows e = 4w..4w+3 and lane l the float4 chunks
+// c = l + 64 i of a row. All of a batch's loads — the token row's chunks
+// first, then the four router rows' — are issued before any is used, so the
+// block has its whole 327 KB router request in flight at once (H = 1280 is
+// one batch). Every wave holds the whole token row, so each computes max|x|
+// for quantize_row_i8 itself; there is no barrier before the logits.
+__global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void moe_route_kernel(
     const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
     MoeSel sel) {
-    __shared__ float4 s_x[512];
     __shared__ float s_logit[kMaxE];
     __shared__ __align__(16) float s_p[kMaxE];
     __shared__ int s_sel_e[kMaxK];
     __shared__ float s_sel_w[kMaxK];
-    __shared__ float s_red[kRouteWaves];
     __shared__ int s_nvalid;
     const int t = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int H4 = H >> 2;
-    const int e = threadIdx.x >> 4;
-    const int l = threadIdx.x & 15;
-    const bool erow = e < E;
-    const float4* gr = reinterpret_cast<const float4*>(G + static_cast<size_t>(erow ? e : 0) * H);
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-
-    // Loads are unconditional (address clamped into the row, a chunk past
-    // the row's end zeroed by a bit mask, threads past E compute unused
-    // values) so they issue as one batch of dwordx4 loads, not as branches.
-    auto router_chunk = [&](int c) {
-        const float4 v = gr[c < H4 ? c : H4 - 1];
-        const unsigned m = c < H4 ? 0xFFFFFFFFu : 0u;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H);
+    const float4* gr[kRouteEPW];
+#pragma unroll
+    for (int k = 0; k < kRouteEPW; ++k) {
+        const int e = wave * kRouteEPW + k;
+        gr[k] = reinterpret_cast<const float4*>(G + static_cast<size_t>(e < E ? e : E - 1) * H);
+    }
+    // Loads are unconditional (address clamped into the row, a chunk past the
+    // row's end zeroed by a bit mask) so they issue as one batch of dwordx4
+    // loads, not as branches around each load.
+    auto masked = [](float4 v, unsigned m) {
         return make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
                            __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
     };
-    float4 g[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) g[i] = router_chunk(l + 16 * i);
-    // 1. stage the token row (H4 <= 512 < 1024 threads: one float4 each) and
-    //    take |x| max on the way for quantize_row_i8
-    float4 xv = z4;
-    float amax = 0.0f;
-    if (threadIdx.x < H4) {
-        xv = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H)[threadIdx.x];
-        s_x[threadIdx.x] = xv;
-        amax = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-    }
-    amax = wave_max_f(amax);
-    if (lane == 0) s_red[wave] = amax;
-    __syncthreads();
 
-    // 2. logits
-    double acc = 0.0;
+    // 1. logits as f64 dot products (rounded to f32 below) and max|x|
+    double acc[kRouteEPW];
+#pragma unroll
+    for (int k = 0; k < kRouteEPW; ++k) acc[k] = 0.0;
+    float amax = 0.0f;
 #pragma unroll 1
-    for (int c0 = l; c0 < H4; c0 += 16 * NI) {
-        float4 gn[NI];
+    for (int c0 = lane; c0 < H4 + lane; c0 += 64 * kRouteNC) {
+        float4 xv[kRouteNC];
+        float4 gv[kRouteEPW][kRouteNC];
+        unsigned m[kRouteNC];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) gn[i] = router_chunk(c0 + 16 * (NI + i));
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int c = c0 + 16 * i;
-            const float4 xc = c < H4 ? s_x[c] : z4;
-            acc = fma(static_cast<double>(xc.x), static_cast<double>(g[i].x), acc);
-            acc = fma(static_cast<double>(xc.y), static_cast<double>(g[i].y), acc);
-            acc = fma(static_cast<double>(xc.z), static_cast<double>(g[i].z), acc);
-            acc = fma(static_cast<double>(xc.w), static_cast<double>(g[i].w), acc);
+        for (int i = 0; i < kRouteNC; ++i) {
+            const int c = c0 + 64 * i;
+            m[i] = c < H4 ? 0xFFFFFFFFu : 0u;
+            xv[i] = xr[c < H4 ? c : H4 - 1];
         }
 #pragma unroll
-        for (int i = 0; i < NI; ++i) g[i] = gn[i];
+        for (int k = 0; k < kRouteEPW; ++k)
+#pragma unroll
+            for (int i = 0; i < kRouteNC; ++i) {
+                const int c = c0 + 64 * i;
+                gv[k][i] = gr[k][c < H4 ? c : H4 - 1];
+            }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first use
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const float4 xc = masked(xv[i], m[i]);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xc.x), fabsf(xc.y)), fmaxf(fabsf(xc.z), fabsf(xc.w))));
+            const double x0 = xc.x, x1 = xc.y, x2 = xc.z, x3 = xc.w;
+#pragma unroll
+            for (int k = 0; k < kRouteEPW; ++k) {
+                const float4 g = gv[k][i];
+                acc[k] = fma(x0, static_cast<double>(g.x), acc[k]);
+                acc[k] = fma(x1, static_cast<double>(g.y), acc[k]);
+                acc[k] = fma(x2, static_cast<double>(g.z), acc[k]);
+                acc[k] = fma(x3, static_cast<double>(g.w), acc[k]);
+            }
+        }
     }
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
-    if (l == 0 && erow) s_logit[e] = static_cast<float>(acc);
+    for (int k = 0; k < kRouteEPW; ++k) acc[k] = wave_sum_d(acc[k]);
+    if (lane < kRouteEPW) {
+        const int e = wave * kRouteEPW + lane;
+        const double a = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
+        if (e < E) s_logit[e] = static_cast<float>(a);
+    }
 
-    // 3. quantize_row_i8 of the token row from the staged values
-    amax = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kRouteWaves; ++w) amax = fmaxf(amax, s_red[w]);
+    // 2. quantize_row_i8 of the token row (thread c owns chunk c; its wave
+    //    holds max|x| of the whole row)
+    amax = wave_max_f(amax);
     const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    const float inv = 1.0f / a_scale;
     if (threadIdx.x < H4) {
+        const float inv = 1.0f / a_scale;
+        const float4 xv = xr[threadIdx.x];
         char4 q;
         q.x = quant_i8(xv.x, inv, false);
         q.y = quant_i8(xv.y, inv, false);
@@ -184,6 +193,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     // 5. greedy top-k == rank by (prob desc, index asc) among non-NaN probs:
     //    thread (e, l) counts the experts 4l..4l+3 ahead of e, 16 lanes sum
     {
+        const int e = threadIdx.x >> 4;
+        const int l = threadIdx.x & 15;
+        const bool erow = e < E;
         const float pe = s_p[e];
         const float4 q = reinterpret_cast<const float4*>(s_p)[l];
         const int j0 = 4 * l;
@@ -218,11 +230,18 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
         if (j == 0) flag[t] = bad ? 1 : 0;
     }
-    // block 0 zeroes the slot entries no token block owns (e >= E or t >= T)
+    // block 0 zeroes the slot entries no token block owns (e >= E or t >= T):
+    // thread i owns bytes 4i..4i+3 (one expert row, tokens t0..t0+3) and
+    // writes them as one word unless a token block owns some of them
+    static_assert(kMaxE * kMaxT == 4 * kRouteThreads, "one slot word per thread");
     if (sel.slot && t == 0) {
-        for (int i = threadIdx.x; i < kMaxE * kMaxT; i += kRouteThreads) {
-            const int ei = i / kMaxT, ti = i - ei * kMaxT;
-            if (ei >= E || ti >= static_cast<int>(gridDim.x)) sel.slot[i] = 0;
+        const int T = static_cast<int>(gridDim.x);
+        const int ei = threadIdx.x / (kMaxT / 4), t0 = 4 * (threadIdx.x % (kMaxT / 4));
+        uint8_t* w = sel.slot + 4 * threadIdx.x;
+        if (ei >= E || t0 >= T) {
+            *reinterpret_cast<uint32_t*>(w) = 0u;
+        } else {
+            for (int ti = T; ti < t0 + 4; ++ti) w[ti - t0] = 0;
         }
     }
 }
@@ -685,7 +704,7 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, void* sel) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
-    FOCR_LAUNCH((moe_route_kernel<5>), dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden, d.n_experts,
+    FOCR_LAUNCH(moe_route_kernel, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden, d.n_experts,
                 d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel));
     return hipGetLastError();
 }
