@@ -568,6 +568,7 @@ struct MoeScratch {
     float* act;
     float* shared_act;
     float* shared_y;
+    float* ybuf;  // [pairs][hidden] weighted expert outputs (grouped down path only)
     void* sel;
 };
 
@@ -580,7 +581,9 @@ int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bo
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
     s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
     s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
-    if (!route || !s->xq || !s->xs || !s->act || !s->flag || (with_shared && !s->shared_y))
+    const bool grouped = static_cast<int>(t) >= kMoeGroupedDownT;
+    s->ybuf = grouped ? static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float))) : nullptr;
+    if (!route || !s->xq || !s->xs || !s->act || !s->flag || (with_shared && !s->shared_y) || (grouped && !s->ybuf))
         return FOCR_HIP_E_OOM;
     s->idx = reinterpret_cast<uint32_t*>(route);
     s->gates = reinterpret_cast<float*>(route + pairs * 4);
@@ -667,7 +670,16 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
                                 true);
         }
     }
-    if (e == hipSuccess) {
+    if (e == hipSuccess && s.ybuf) {
+        {
+            ProfScope ps(ctx, "moe_down");
+            e = launch_moe_down(str, d, s.sel, s.act, L->wd, L->sd, s.ybuf, (int)L->inter, false);
+        }
+        if (e == hipSuccess) {
+            ProfScope ps(ctx, "moe_combine");
+            e = launch_moe_combine(str, d, s.ybuf, s.flag, with_shared ? s.shared_y : nullptr, out);
+        }
+    } else if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_down_combine");
         e = launch_moe_down_combine(str, d, di, dg, s.flag, s.act, L->wd, L->sd, with_shared ? s.shared_y : nullptr,
                                     out, (int)L->inter);

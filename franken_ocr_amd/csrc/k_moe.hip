@@ -351,8 +351,11 @@ constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
 // ---- gate/up ------------------------------------------------------------------
 // Block = 256 threads = (256 / LPR) row groups, one weight row per group held
 // in registers (2 * JC 16-byte loads in flight per lane); the block's pairs
-// are then taken one at a time against the staged token rows.
-template <int LPR, int JC>
+// are then taken one at a time against the staged token rows. ALLTOK (T <=
+// kAllTok) stages every token row once; its own instantiation, without the
+// per-pass staging path, fits 64 VGPRs, i.e. 8 waves per SIMD, so about
+// every block of a T = 8 step is resident at once.
+template <int LPR, int JC, bool ALLTOK>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     const MoeSel sel, int T, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, const int8_t* __restrict__ wg,
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     }
     const float sgr = sg[row];
     const float sur = su[row];
-    const bool all_tok = T <= kAllTok;
+    constexpr bool all_tok = ALLTOK;
     if (all_tok) stage_lds_dma(lds_x, reinterpret_cast<const int4*>(xq), T * C);  // rows are contiguous
     if (threadIdx.x < 64) {
         const int tt = threadIdx.x < T ? threadIdx.x : T - 1;
@@ -632,6 +635,37 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     }
 }
 
+// ---- combine (after the grouped down kernel) ----------------------------------
+// out[t][c] = ((0 + y[t*K + 0][c]) + y[t*K + 1][c]) ... (+ shared[t][c]) in
+// slot order (decoder.rs:2253-2261), the same sums in the same order as the
+// down + combine kernel; a token whose routing failed (flag) combines to zero.
+// Thread = 4 consecutive columns of one token.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf, const int* __restrict__ flag,
+                                                          const float* __restrict__ shared_y, float* __restrict__ out,
+                                                          int K, int H) {
+    const int t = blockIdx.y;
+    const int c4 = blockIdx.x * 256 + static_cast<int>(threadIdx.x);
+    if (c4 >= (H >> 2)) return;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (!flag[t]) {
+        for (int j = 0; j < K; ++j) {
+            const float4 y = reinterpret_cast<const float4*>(ybuf + static_cast<size_t>(t * K + j) * H)[c4];
+            o.x += y.x;
+            o.y += y.y;
+            o.z += y.z;
+            o.w += y.w;
+        }
+        if (shared_y) {
+            const float4 y = reinterpret_cast<const float4*>(shared_y + static_cast<size_t>(t) * H)[c4];
+            o.x += y.x;
+            o.y += y.y;
+            o.z += y.z;
+            o.w += y.w;
+        }
+    }
+    reinterpret_cast<float4*>(out + static_cast<size_t>(t) * H)[c4] = o;
+}
+
 struct GemvArgs {
     MoeSel sel;
     int T, K, H, I, shared_T;
@@ -641,10 +675,14 @@ template <int LPR>
 hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const int8_t* xq,
                               const float* xs, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
                               float* act) {
-#define FOCR_GU(J)                                                                                               \
-    case J:                                                                                                      \
-        FOCR_LAUNCH((moe_gate_up_kernel<LPR, J>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs, wg, sg, wu, \
-                    su, act, a.H, a.I, a.shared_T);                                                              \
+#define FOCR_GU(J)                                                                                              \
+    case J:                                                                                                     \
+        if (a.T <= kAllTok)                                                                                     \
+            FOCR_LAUNCH((moe_gate_up_kernel<LPR, J, true>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs, wg, \
+                        sg, wu, su, act, a.H, a.I, a.shared_T);                                                 \
+        else                                                                                                    \
+            FOCR_LAUNCH((moe_gate_up_kernel<LPR, J, false>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs,    \
+                        wg, sg, wu, su, act, a.H, a.I, a.shared_T);                                             \
         break;
     switch (JC) {
         FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
@@ -737,6 +775,14 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, con
     const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
     if (lpr == 16) return launch_down_lpr<16>(s, grid, lds, jc, a, act, wd, sd, ybuf);
     return launch_down_lpr<8>(s, grid, lds, jc, a, act, wd, sd, ybuf);
+}
+
+hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const int* flag,
+                              const float* shared_y, float* out) {
+    if (!dims_ok(d) || d.hidden % 4 != 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>((d.hidden / 4 + 255) / 256), static_cast<unsigned>(d.t));
+    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, flag, shared_y, out, d.top_k, d.hidden);
+    return hipGetLastError();
 }
 
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,

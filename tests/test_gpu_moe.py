@@ -150,6 +150,51 @@ def test_moe_shared_expert(ctx, layer_w):
     assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
 
 
+@pytest.mark.parametrize("t", [40, 48, 64])
+def test_moe_grouped_down_matches_per_token_down(ctx, gpu_layer, t):
+    """From T = 40 the layer runs the expert-grouped down kernel + slot-order
+    combine; below it, down + combine per token. Both compute every pair's
+    y = ((f32)acc * as) * sd * gate and sum a token's slots in the same
+    order, so a T-token step equals its 8-token chunks bit for bit — the
+    reference's batched == per-stream invariant (tests/batched_moe_parity.rs).
+    Row 5 has no finite router score: both paths write zeros for it."""
+    _say(f"moe grouped vs per-token t={t}")
+    x = synth.f32_normal(synth.seed_of(700 + t), t * H).reshape(t, H)
+    x[5] = np.nan
+    full = ctx.empty((t, H), np.float32)
+    gpu_layer.decode(ctx.to_device(x), full, norm_topk=True, check_route=False)
+    parts = []
+    for lo in range(0, t, 8):
+        n = min(8, t - lo)
+        d = ctx.empty((n, H), np.float32)
+        gpu_layer.decode(ctx.to_device(np.ascontiguousarray(x[lo:lo + n])), d, norm_topk=True, check_route=False)
+        parts.append(d.numpy())
+    got = full.numpy()
+    assert np.array_equal(got, np.concatenate(parts))
+    assert not got[5].any() and np.isfinite(got).all()
+
+
+def test_moe_shared_expert_grouped_path(ctx, layer_w):
+    from franken_ocr_amd.engine import MoeLayer
+
+    si = 1792
+    swg = synth.int8_uniform(synth.seed_of(610), si * H)
+    swu = synth.int8_uniform(synth.seed_of(611), si * H)
+    swd = synth.int8_uniform(synth.seed_of(612), H * si)
+    ssg = synth.f32_uniform(synth.seed_of(613), si, 1e-3, 2e-2)
+    ssu = synth.f32_uniform(synth.seed_of(614), si, 1e-3, 2e-2)
+    ssd = synth.f32_uniform(synth.seed_of(615), H, 1e-3, 2e-2)
+    L = MoeLayer(H, I, E, K, *layer_w, ctx=ctx)
+    L.set_shared(si, swg, ssg, swu, ssu, swd, ssd)
+    t = 44
+    x = synth.f32_normal(synth.seed_of(616), t * H).reshape(t, H)
+    dout = ctx.empty((t, H), np.float32)
+    L.decode(ctx.to_device(x), dout, with_shared=True)
+    st, out, _, _ = O.moe_decode(x, *layer_w, E, K, I, shared=(si, swg, ssg, swu, ssu, swd, ssd))
+    assert st == 0
+    assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
+
+
 def test_route_nan_reports_error(ctx, gpu_layer):
     from franken_ocr_amd._abi import RouteError
 
