@@ -212,14 +212,15 @@ int32_t focr_hip_qint8_free(focr_hip_qint8* w) {
 // ---- GEMV / LM head ------------------------------------------------------
 
 int32_t focr_hip_quantize_rows_i8(focr_hip_ctx* ctx, const float* x, size_t m, size_t k, int8_t* xq,
-                                  float* a_scales, int32_t ties_even) {
+                                  float* a_scales, int32_t rule) {
     ENGINE_CTX(ctx);
+    if (rule < 0 || rule > kQuantRuleDynamic) return fail(FOCR_HIP_E_ARG, fmt("quantize_rows_i8: unknown rule %d", rule));
     if (m == 0) return FOCR_HIP_OK;
     if (!x || !xq || !a_scales) return fail(FOCR_HIP_E_ARG, "quantize_rows_i8: null device pointer");
     if (m > 65535 || k > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
         return fail(FOCR_HIP_E_SHAPE, "quantize_rows_i8: too many rows");
     ProfScope ps(ctx, "quantize_rows");
-    FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)k, xq, a_scales, ties_even != 0), "quantize launch");
+    FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)k, xq, a_scales, rule), "quantize launch");
     return FOCR_HIP_OK;
 }
 
@@ -825,6 +826,89 @@ int32_t focr_hip_moe_prefill_i4(focr_hip_ctx* ctx, const focr_hip_moe_layer_i4* 
         if (err)
             return fail(FOCR_HIP_E_SHAPE,
                         fmt("moe_prefill_i4: expert index out of range (n_experts %zu)", L->n_experts));
+    }
+    return FOCR_HIP_OK;
+}
+
+// ---- prefill: int8 linear and int8 MoE on the matrix cores ------------------------
+
+int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+                                   const float* bias, float* y) {
+    ENGINE_CTX(ctx);
+    if (!w) return fail(FOCR_HIP_E_BAD_HANDLE, "linear_int8_dynamic: null weight handle");
+    if (!x || !y) return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: null device pointer");
+    if (m < 1 || m > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, fmt("linear_int8_dynamic: m %zu outside 1..=1048576", m));
+    if (!i8_mfma_supported(static_cast<int>(w->k)))
+        return fail(FOCR_HIP_E_SHAPE,
+                    fmt("linear_int8_dynamic: k %zu is not a multiple of 64 (the matrix-core K stage)", w->k));
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
+    if (!xq || !xs) return FOCR_HIP_E_OOM;
+    {
+        ProfScope ps(ctx, "quantize_rows_dyn");
+        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
+                     "quantize launch");
+    }
+    ProfScope ps(ctx, "linear_i8");
+    FOCR_HIP_TRY(launch_linear_i8(ctx->stream, xq, xs, (int)m, (int)w->k, w->w, w->scales, (int)w->n, bias, y),
+                 "linear_i8 launch");
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
+                                const uint32_t* idx, const float* gates, int32_t with_shared, float* out,
+                                int32_t check_idx) {
+    ENGINE_CTX(ctx);
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "moe_prefill_i8: null moe layer");
+    if (!x || !idx || !gates || !out) return fail(FOCR_HIP_E_ARG, "moe_prefill_i8: null pointer");
+    if (t < 1 || t > 16384) return fail(FOCR_HIP_E_SHAPE, fmt("moe_prefill_i8: t %zu outside 1..=16384", t));
+    if (with_shared && !L->swg)
+        return fail(FOCR_HIP_E_ARG, "moe_prefill_i8: with_shared set but no shared expert uploaded");
+    const size_t H = L->hidden, I = L->inter, K = L->top_k, TK = t * K;
+    if (!i8_mfma_supported((int)H) || !i8_mfma_supported((int)I) ||
+        (with_shared && !i8_mfma_supported((int)L->shared_inter)))
+        return fail(FOCR_HIP_E_SHAPE,
+                    fmt("moe_prefill_i8: hidden %zu / inter %zu must be multiples of 64 (the matrix-core K stage)", H,
+                        I));
+    auto take = [](char*& p, size_t bytes) {
+        char* r = p;
+        p += (bytes + 255) & ~static_cast<size_t>(255);
+        return r;
+    };
+    MoeI8Scratch w{};
+    char* a = static_cast<char*>(ctx->scratch_get(kScrI4, TK * I * sizeof(float) + 256 + TK * H * sizeof(float)));
+    char* b = static_cast<char*>(ctx->scratch_get(
+        kScrI4b, t * H + 256 + t * 4 + 256 + TK * I + 256 + TK * 4 + 256 +
+                     (moe_i4_plan_ints(static_cast<int>(TK), static_cast<int>(L->n_experts)) + 1) * sizeof(int)));
+    const size_t SI = with_shared ? L->shared_inter : 0;
+    char* c = with_shared ? static_cast<char*>(ctx->scratch_get(
+                                kScrShared, t * SI * 4 + 256 + t * SI + 256 + t * 4 + 256 + t * H * 4))
+                          : nullptr;
+    if (!a || !b || (with_shared && !c)) return FOCR_HIP_E_OOM;
+    w.act = reinterpret_cast<float*>(take(a, TK * I * sizeof(float)));
+    w.ybuf = reinterpret_cast<float*>(a);
+    w.xq = reinterpret_cast<int8_t*>(take(b, t * H));
+    w.xs = reinterpret_cast<float*>(take(b, t * 4));
+    w.aq = reinterpret_cast<int8_t*>(take(b, TK * I));
+    w.as = reinterpret_cast<float*>(take(b, TK * 4));
+    w.plan = reinterpret_cast<int*>(b);
+    w.err = w.plan + moe_i4_plan_ints(static_cast<int>(TK), static_cast<int>(L->n_experts));
+    if (c) {
+        w.shared_act = reinterpret_cast<float*>(take(c, t * SI * 4));
+        w.shared_aq = reinterpret_cast<int8_t*>(take(c, t * SI));
+        w.shared_as = reinterpret_cast<float*>(take(c, t * 4));
+        w.shared_y = reinterpret_cast<float*>(c);
+    }
+    FOCR_HIP_TRY(launch_moe_prefill_i8(ctx->stream, L, x, static_cast<int>(t), static_cast<int>(K), idx, gates,
+                                       with_shared, out, w, ctx),
+                 "moe_prefill_i8 launch");
+    if (check_idx) {
+        int err = 0;
+        FOCR_HIP_TRY(hipMemcpyAsync(&err, w.err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H err");
+        FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        if (err)
+            return fail(FOCR_HIP_E_SHAPE,
+                        fmt("moe_prefill_i8: expert index out of range (n_experts %zu)", L->n_experts));
     }
     return FOCR_HIP_OK;
 }

@@ -171,8 +171,11 @@ hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const 
                            int32_t* out, int m, int k, int n);
 
 // k_gemv.hip
+// rule: 0 quantize_row_i8 (half away), 1 quantize_row_i8_te (ties even), 2
+// the dynamic activation rule of linear_int8_dynamic (true division, ties even).
+constexpr int kQuantRuleDynamic = 2;
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
-                                float* a_scales, bool ties_even);
+                                float* a_scales, int rule);
 // y[m,n] = ((f32)acc * a_scales[m]) * ws[n]; acc (nullable) gets raw i32;
 // arg_keys (nullable) gets per-block argmax keys [m][nparts].
 hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
@@ -251,6 +254,30 @@ struct MoeI4Scratch {
     int* err;
 };
 size_t moe_i4_plan_ints(int tk, int n_experts);
+// The prefill MoE plan (int4 and int8 layers): a stable counting sort of the
+// (token, slot) pairs by expert into 64-row tiles, carved from moe_i4_plan_ints
+// ints: perm [tk] (sorted row -> pair id), the tile list (expert, first row,
+// rows), each expert's tile count and first tile, the tile count.
+constexpr int kMoePlanTileRows = 64;
+struct MoePlan {
+    int* perm;
+    int* tile_e;
+    int* tile_r0;
+    int* tile_nr;
+    int* exp_nt;
+    int* exp_t0;
+    int* n_tiles;
+    int max_tiles;
+};
+MoePlan moe_plan_view(int* plan, int tk, int n_experts);
+// Quantize the t token rows of x by `rule` into xq/xs and build the plan from
+// idx [t][top_k]; an expert id >= E sets *err. One launch.
+hipError_t launch_moe_prefill_plan(hipStream_t s, const float* x, int t, int H, int rule, int8_t* xq, float* xs,
+                                   const uint32_t* idx, int top_k, int E, const MoePlan& p, int* err);
+// out[t] = the token's pair rows of ybuf [t*top_k][H] summed in ascending
+// expert order (slot order among equal experts), + shared_y[t] if non-null.
+hipError_t launch_moe_prefill_combine(hipStream_t s, const float* ybuf, const uint32_t* idx, int t, int H,
+                                      int top_k, const float* shared_y, float* out);
 // The int4 layer keeps its experts in the MFMA-tiled layout: b [E][n][k/2]
 // packed and sc [E][n][k/group] are copied into b_tiled / s_tiled (same sizes,
 // each allocation followed by s4_tile_pad_bytes() of readable padding).
@@ -259,6 +286,35 @@ hipError_t launch_retile_i4(hipStream_t s, const uint8_t* b, const float* sc, in
 hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
                                  focr_hip_ctx* ctx);
+
+// k_i8mfma.hip — int8 x int8 GEMMs on the matrix cores (prefill). K must be
+// a multiple of 64.
+bool i8_mfma_supported(int k);
+// y[m][n] = ((f32)(xq[m] . w[n]) * xs[m]) * ws[n] (+ bias[n]) — nn::linear_int8_dynamic
+// on rows already quantized by the dynamic rule.
+hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* w,
+                            const float* ws, int n, const float* bias, float* y);
+// act[m][n] = silu(((f32)acc_g * xs[m]) * sg[n]) * (((f32)acc_u * xs[m]) * su[n]).
+hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
+                            const float* sg, const int8_t* wu, const float* su, int n, float* act);
+struct MoeI8Scratch {
+    int8_t* xq;       // [t][hidden]
+    float* xs;        // [t]
+    float* act;       // [t*top_k][inter], sorted-row order
+    int8_t* aq;       // [t*top_k][inter]
+    float* as;        // [t*top_k]
+    float* ybuf;      // [t*top_k][hidden], pair order
+    int* plan;        // moe_i4_plan_ints(t*top_k, E)
+    int* err;
+    float* shared_act;  // with the shared expert: [t][shared_inter]
+    int8_t* shared_aq;
+    float* shared_as;
+    float* shared_y;    // [t][hidden]
+};
+// moe_block_i8 over the routing idx/gates [t][top_k] (+ the shared expert).
+hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
+                                 const uint32_t* idx, const float* gates, int with_shared, float* out,
+                                 MoeI8Scratch& w, focr_hip_ctx* ctx);
 
 // k_sampler.hip — greedy decode sampler (sampler.rs): per-row ban bitmaps
 // of the sliding-window no-repeat-ngram processor, then token / EOS / history

@@ -101,12 +101,29 @@ __device__ __forceinline__ int8_t quant_i8(float v, float inv, bool ties_even) {
     return static_cast<int8_t>(static_cast<int>(r));
 }
 
-// decoder.rs:1588-1597 / :1647-1656 for one row, by a whole block of
-// THREADS lanes: amax = max|x|, a_scale = amax / 127 (1.0 for an all-zero
-// row), q = quant_i8(x * (1 / a_scale)). red holds THREADS / 64 floats of LDS.
+// The three row quantization rules, all with a_scale = max|x| / 127 (1.0 for
+// an all-zero row) and a clamp into [-127, 127]:
+//   kQuantHalfAway  quantize_row_i8 (decoder.rs:1588-1597): x * (1 / a_scale), half away from zero;
+//   kQuantTiesEven  quantize_row_i8_te (decoder.rs:1647-1656): x * (1 / a_scale), ties to even;
+//   kQuantDynamic   the dynamic activation rule of linear_int8_dynamic
+//                   (docs/focrq-format.md:296-320): x / a_scale (true division), ties to even.
+enum QuantRule : int { kQuantHalfAway = 0, kQuantTiesEven = 1, kQuantDynamic = 2 };
+
+__device__ __forceinline__ int8_t quant_rule(float v, float a_scale, float inv, int rule) {
+    if (rule == kQuantDynamic) {
+        float r = v / a_scale;
+        if (r != r) return 0;
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        return static_cast<int8_t>(static_cast<int>(rintf(r)));
+    }
+    return quant_i8(v, inv, rule == kQuantTiesEven);
+}
+
+// One row by a whole block of THREADS lanes: amax = max|x|, a_scale, q by
+// `rule` (a QuantRule). red holds THREADS / 64 floats of LDS.
 template <int THREADS>
 __device__ __forceinline__ void block_quantize_row(const float* __restrict__ xr, int K, int8_t* __restrict__ q,
-                                                   float* __restrict__ a_scale_out, bool ties_even, float* red) {
+                                                   float* __restrict__ a_scale_out, int rule, float* red) {
     float amax = 0.0f;
     for (int i = threadIdx.x; i < K; i += THREADS) amax = fmaxf(amax, fabsf(xr[i]));
     amax = wave_max_f(amax);
@@ -117,7 +134,7 @@ __device__ __forceinline__ void block_quantize_row(const float* __restrict__ xr,
     for (int w = 1; w < THREADS / 64; ++w) amax = fmaxf(amax, red[w]);
     const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / a_scale;
-    for (int i = threadIdx.x; i < K; i += THREADS) q[i] = quant_i8(xr[i], inv, ties_even);
+    for (int i = threadIdx.x; i < K; i += THREADS) q[i] = quant_rule(xr[i], a_scale, inv, rule);
     if (threadIdx.x == 0) *a_scale_out = a_scale;
 }
 

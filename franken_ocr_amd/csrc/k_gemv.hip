@@ -22,11 +22,11 @@ constexpr int kGroups = kThreads / 16;
 __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float* __restrict__ x, int K,
                                                                  int8_t* __restrict__ xq,
                                                                  float* __restrict__ a_scales,
-                                                                 int ties_even) {
+                                                                 int rule) {
     __shared__ float red[kThreads / 64];
     const int row = blockIdx.x;
     block_quantize_row<kThreads>(x + static_cast<size_t>(row) * K, K, xq + static_cast<size_t>(row) * K,
-                                 a_scales + row, ties_even != 0, red);
+                                 a_scales + row, rule, red);
 }
 
 // JB = row chunks (16 B) a lane holds in flight per batch; R = weight rows a
@@ -351,10 +351,9 @@ int gemv_i8_nparts(int n, int cu_count) {
 }
 
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
-                                float* a_scales, bool ties_even) {
+                                float* a_scales, int rule) {
     if (m == 0) return hipSuccess;
-    FOCR_LAUNCH(quantize_rows_kernel, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales,
-                       ties_even ? 1 : 0);
+    FOCR_LAUNCH(quantize_rows_kernel, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales, rule);
     return hipGetLastError();
 }
 

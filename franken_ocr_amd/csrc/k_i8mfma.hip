@@ -1,0 +1,350 @@
+// k_i8mfma.hip — int8 x int8 GEMMs on gfx950 matrix cores for prefill.
+//
+//   * nn::linear_int8_dynamic (nn.rs:151-173): rows quantized by the dynamic
+//     activation rule (docs/focrq-format.md:296-320: x / scale, ties to even),
+//     C = A · Bᵀ in i32 on v_mfma_i32_32x32x32_i8, y = ((f32)acc * a_s) * w_s
+//     (+ bias), the decoder's dequant order (decoder.rs:1636).
+//   * moe_block_i8 (decoder.rs:2142-2181) over an uploaded int8 MoE layer:
+//     the prefill plan shared with the int4 layer (stable counting sort of the
+//     (token, slot) pairs by expert into 64-row tiles), a grouped gate/up GEMM
+//     with the SwiGLU epilogue (expert_mlp_i8, decoder.rs:2120-2135),
+//     re-quantization of the act rows by the dynamic rule, a grouped down GEMM
+//     whose epilogue multiplies by the pair's gate, the combine in ascending
+//     expert order, and the shared expert (all rows, dense) added last.
+//
+// Integer sums are exact, so every i32 accumulator equals the CPU's; the f32
+// outputs follow the reference's formulas (SiLU through expf).
+//
+// Block = 4 waves over a 64-row tile. Wave w computes 64 rows x 64 columns
+// (2 x 2 MFMA tiles of 32 x 32); for SwiGLU 64 rows x 32 columns of the gate
+// and the same 32 of the up matrix, so each (row, column)'s gate and up sums
+// sit in the same lane and register: the epilogue needs no exchange.
+// Operand layout of v_mfma_i32_32x32x32_i8: lane l holds A row l % 32 and B
+// column l % 32, bytes 16 (l / 32) + [0, 16) of the 32-wide K step; C element
+// v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.
+//
+// Activations: 512-byte K chunks of the tile's 64 rows (32 KB) are staged in
+// LDS with gfx950's direct global -> LDS loads (no VGPRs; two buffers, the
+// next chunk in flight while the current one is consumed). A wave's load
+// writes 1 KB of contiguous LDS (two 512-byte rows), so the 16-byte piece p
+// of row r holds the row's chunk p ^ (r & 15): the 16 rows a quarter-wave's
+// fragment read touches then start on 16 different banks.
+// Weights ([E][N][K], output-channel-major, as uploaded for decode) go global
+// -> VGPR, each lane loading exactly the 16-byte fragments its MFMAs take,
+// four 64-byte K stages ahead; lanes l and l + 32 read adjacent 16 bytes, so
+// a wave reads 64 contiguous bytes of each of its rows per stage.
+#include <type_traits>
+
+#include "focr_internal.hpp"
+#include "k_common.hpp"
+
+namespace focr {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int BM = kMoePlanTileRows;  // 64 rows per block tile
+constexpr int KB = 64;                // K bytes per stage (two MFMA K steps)
+constexpr int KC = 512;               // K bytes per staged activation chunk
+constexpr int SPC = KC / KB;          // stages per chunk
+constexpr int kXcds = 8;
+
+enum I8Epi { kI8Linear = 0, kI8Swiglu = 1, kI8Down = 2 };
+
+template <int EPI>
+constexpr int bcols() {
+    return EPI == kI8Swiglu ? 128 : 256;
+}
+
+struct I8Args {
+    const int8_t* A;        // activation rows [rows][K]
+    const float* a_scale;   // scale per A row
+    const int* perm;        // MoE: sorted row -> pair id (t * top_k + j); null: direct rows
+    int top_k;
+    const int8_t* B0;       // weights [E][N][K]
+    const float* s0;        // [E][N]
+    const int8_t* B1;       // SwiGLU: up weights
+    const float* s1;
+    const float* bias;      // linear: [N] or null
+    const float* gates;     // down: [pairs]
+    float* out;             // linear [rows][N]; SwiGLU act [rows][N]; down ybuf [pairs][N]
+    int K, N;
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
+
+// One block tile: rows [r0, r0 + nr) (nr <= 64) of expert e against column
+// block cb. Every thread of the block calls it (it synchronises).
+template <int EPI>
+__device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, int cb) {
+    // two chunk buffers as distinct objects, so the compiler can tell reads of
+    // one from the direct loads in flight into the other
+    __shared__ __align__(16) int8_t lds_a0[BM * KC];
+    __shared__ __align__(16) int8_t lds_a1[BM * KC];
+    __shared__ int s_arow[BM];
+    __shared__ int s_dst[BM];
+    __shared__ float s_rs[BM];
+    __shared__ float s_gate[BM];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int l = tid & 63;
+    const int h = l >> 5;
+    const int c32 = l & 31;
+    const int K = a.K, N = a.N;
+    const int S = K / KB;
+
+    if (tid < BM) {
+        const int row = r0 + (tid < nr ? tid : nr - 1);  // rows past nr repeat the last one, never stored
+        int arow = row, dst = row;
+        float g = 1.0f;
+        if (a.perm) {
+            const int pid = a.perm[row];
+            dst = pid;
+            if (EPI == kI8Swiglu) arow = pid / a.top_k;  // the pair's token row
+            if (EPI == kI8Down) g = a.gates[pid];
+        }
+        s_arow[tid] = arow;
+        s_dst[tid] = dst;
+        s_rs[tid] = a.a_scale[arow];
+        s_gate[tid] = g;
+    }
+
+    // this lane's two weight columns (tile j = 0, 1) and their row pointers
+    int col[2];
+    const int8_t* bp[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        col[j] = EPI == kI8Swiglu ? cb * 128 + wave * 32 + c32 : cb * 256 + wave * 64 + 32 * j + c32;
+        const int nc = col[j] < N ? col[j] : N - 1;
+        const int8_t* B = (EPI == kI8Swiglu && j == 1) ? a.B1 : a.B0;
+        bp[j] = B + (static_cast<size_t>(e) * N + nc) * K + 16 * h;
+    }
+    // fragments f[2 j + s]: column tile j, K step s of stage st (clamped past the end)
+    auto load_b = [&](int st, v4i (&f)[4]) {
+        const int ss = st < S ? st : S - 1;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) f[2 * j + s] = *reinterpret_cast<const v4i*>(bp[j] + ss * KB + 32 * s);
+    };
+    // a ring of four stages of fragments, stage st in f[st % 4], loaded four
+    // stages ahead (SPC = 8 stages per chunk keeps the ring index a constant)
+    v4i f[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) load_b(q, f[q]);
+    __syncthreads();  // the row tables
+
+    // Chunk c of the activations into LDS buffer c & 1: wave w's load i covers
+    // rows r0p = 2 (4 i + w) and r0p + 1 (lane l: row r0p + l / 32, piece
+    // l % 32; a direct load lands at the wave-uniform LDS address + 16 l); the
+    // lane at piece p fetches the row's chunk p ^ (row & 15), clamped into the
+    // row past K (never read).
+    const int nchunks = (K + KC - 1) / KC;
+    auto stage_chunk_dma = [&](int c, int8_t* base) {
+#pragma unroll
+        for (int i = 0; i < BM / 8; ++i) {
+            const int r0p = 2 * (4 * i + wave);  // first row of this load's pair
+            const int r = r0p + h;
+            const int p = c32 ^ (r & 15);
+            int kb = c * KC + 16 * p;
+            kb = kb < K ? kb : 0;
+            __builtin_amdgcn_global_load_lds((global_void_t*)(a.A + static_cast<size_t>(s_arow[r]) * K + kb),
+                                             (lds_void_t*)(base + r0p * KC), 16, 0, 0);
+        }
+    };
+
+    v16i acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+    // live = false (a stage past K): the weight fragments are zeroed by a
+    // select, so the MFMAs add nothing and the code stays branch-free (a
+    // branch around them costs the compiler its exact load-count waits).
+    auto compute = [&](const int8_t* buf, int ls, const v4i (&f)[4], bool live) {
+        const v4i z = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int c16 = 4 * ls + 2 * s + h;  // 16-byte chunk of the 512-byte row
+            const v4i a0 = *reinterpret_cast<const v4i*>(buf + c32 * KC + 16 * (c16 ^ (c32 & 15)));
+            const v4i a1 = *reinterpret_cast<const v4i*>(buf + (32 + c32) * KC + 16 * (c16 ^ ((32 + c32) & 15)));
+            const v4i b0 = live ? f[s] : z;
+            const v4i b1 = live ? f[2 + s] : z;
+            acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);
+            acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);
+            acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);
+            acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);
+        }
+    };
+
+    static_assert(SPC % 4 == 0, "the fragment ring must divide a chunk's stages");
+    // Chunk c: wait for it, start chunk c + 1 into the other buffer, run its
+    // SPC stages. Stages past K (the last chunk's tail) multiply zeros; their
+    // fragment loads still run (clamped to the last stage), so every stage
+    // issues the same loads and the waits stay exact.
+    auto chunk = [&](int c, const int8_t* buf, int8_t* next) {
+        __syncthreads();  // chunk c has landed; the other buffer is free
+        if (c + 1 < nchunks) stage_chunk_dma(c + 1, next);
+#pragma unroll
+        for (int ls = 0; ls < SPC; ++ls) {
+            const int st = c * SPC + ls;
+            compute(buf, ls, f[ls % 4], st < S);
+            load_b(st + 4, f[ls % 4]);
+        }
+    };
+    stage_chunk_dma(0, lds_a0);
+    for (int c = 0; c < nchunks; c += 2) {
+        chunk(c, lds_a0, lds_a1);
+        if (c + 1 < nchunks) chunk(c + 1, lds_a1, lds_a0);
+    }
+
+    // epilogue
+    const bool ok0 = col[0] < N, ok1 = col[1] < N;
+    const float ws0 = a.s0[static_cast<size_t>(e) * N + (ok0 ? col[0] : 0)];
+    const float ws1 = EPI == kI8Swiglu ? a.s1[static_cast<size_t>(e) * N + (ok0 ? col[0] : 0)]
+                                       : a.s0[static_cast<size_t>(e) * N + (ok1 ? col[1] : 0)];
+    const float b0 = (EPI == kI8Linear && a.bias) ? a.bias[ok0 ? col[0] : 0] : 0.0f;
+    const float b1 = (EPI == kI8Linear && a.bias) ? a.bias[ok1 ? col[1] : 0] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m >= nr) continue;
+            const float rs = s_rs[m];
+            const int i0 = t ? acc10[v] : acc00[v];
+            const int i1 = t ? acc11[v] : acc01[v];
+            if (EPI == kI8Swiglu) {
+                if (!ok0) continue;
+                const float g = (static_cast<float>(i0) * rs) * ws0;
+                const float u = (static_cast<float>(i1) * rs) * ws1;
+                a.out[static_cast<size_t>(r0 + m) * N + col[0]] = silu_f(g) * u;
+            } else {
+                const size_t orow = static_cast<size_t>(EPI == kI8Down ? s_dst[m] : r0 + m) * N;
+                if (ok0) {
+                    float y = (static_cast<float>(i0) * rs) * ws0;
+                    if (EPI == kI8Linear && a.bias) y = y + b0;
+                    if (EPI == kI8Down) y = s_gate[m] * y;
+                    a.out[orow + col[0]] = y;
+                }
+                if (ok1) {
+                    float y = (static_cast<float>(i1) * rs) * ws1;
+                    if (EPI == kI8Linear && a.bias) y = y + b1;
+                    if (EPI == kI8Down) y = s_gate[m] * y;
+                    a.out[orow + col[1]] = y;
+                }
+            }
+        }
+    }
+}
+
+// Dense: grid (row tile, column block) over the M rows of one matrix.
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i8_gemm_kernel(I8Args a, int M) {
+    const int r0 = blockIdx.x * BM;
+    i8_tile<EPI>(a, 0, r0, min(BM, M - r0), blockIdx.y);
+}
+
+// Grouped over the plan's tiles, XCD-aware like the int4 layer's: the units
+// (tile, column block) are ordered expert by expert, column block by column
+// block, tile by tile, and cut into 8 contiguous parts, part x for XCD x
+// (block b runs unit (b % 8) * per + b / 8), so an expert's row tiles that
+// share a weight slab run together on one XCD and its L2 serves the repeats.
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i8_grouped_kernel(
+    I8Args a, const int* __restrict__ n_tiles, const int* __restrict__ tile_e, const int* __restrict__ tile_r0,
+    const int* __restrict__ tile_nr, const int* __restrict__ exp_nt, const int* __restrict__ exp_t0) {
+    constexpr int BNB = bcols<EPI>();
+    const int ncb = (a.N + BNB - 1) / BNB;
+    const int units = *n_tiles * ncb;
+    const int per = (units + kXcds - 1) / kXcds;
+    const int k = static_cast<int>(blockIdx.x) / kXcds;
+    const int g = (static_cast<int>(blockIdx.x) % kXcds) * per + k;
+    if (k >= per || g >= units) return;
+    const int e = tile_e[g / ncb];
+    const int t0 = exp_t0[e], nt = exp_nt[e];
+    const int loc = g - ncb * t0;
+    const int cb = loc / nt;
+    const int tile = t0 + (loc - cb * nt);
+    i8_tile<EPI>(a, e, tile_r0[tile], tile_nr[tile], cb);
+}
+
+}  // namespace
+
+bool i8_mfma_supported(int k) { return k > 0 && k % KB == 0 && k <= 65536; }
+
+hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* w,
+                            const float* ws, int n, const float* bias, float* y) {
+    if (!i8_mfma_supported(k) || m <= 0 || n <= 0) return hipErrorInvalidValue;
+    I8Args a{xq, xs, nullptr, 1, w, ws, nullptr, nullptr, bias, nullptr, y, k, n};
+    const dim3 grid((m + BM - 1) / BM, (n + bcols<kI8Linear>() - 1) / bcols<kI8Linear>());
+    FOCR_LAUNCH(i8_gemm_kernel<kI8Linear>, grid, dim3(256), 0, s, a, m);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
+                            const float* sg, const int8_t* wu, const float* su, int n, float* act) {
+    if (!i8_mfma_supported(k) || m <= 0 || n <= 0) return hipErrorInvalidValue;
+    I8Args a{xq, xs, nullptr, 1, wg, sg, wu, su, nullptr, nullptr, act, k, n};
+    const dim3 grid((m + BM - 1) / BM, (n + bcols<kI8Swiglu>() - 1) / bcols<kI8Swiglu>());
+    FOCR_LAUNCH(i8_gemm_kernel<kI8Swiglu>, grid, dim3(256), 0, s, a, m);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
+                                 const uint32_t* idx, const float* gates, int with_shared, float* out,
+                                 MoeI8Scratch& w, focr_hip_ctx* ctx) {
+    const int H = static_cast<int>(L->hidden), I = static_cast<int>(L->inter), E = static_cast<int>(L->n_experts);
+    const int TK = t * top_k;
+    const MoePlan p = moe_plan_view(w.plan, TK, E);
+    hipError_t e;
+    {
+        ProfScope ps(ctx, "i8_prep");
+        if ((e = launch_moe_prefill_plan(s, x, t, H, kQuantDynamic, w.xq, w.xs, idx, top_k, E, p, w.err)) !=
+            hipSuccess)
+            return e;
+    }
+    auto grouped = [&](auto epi, const I8Args& a) {
+        constexpr int EPI = decltype(epi)::value;
+        const int ncb = (a.N + bcols<EPI>() - 1) / bcols<EPI>();
+        const int max_units = p.max_tiles * ncb;
+        const dim3 grid(static_cast<unsigned>(kXcds * ((max_units + kXcds - 1) / kXcds)));
+        FOCR_LAUNCH(i8_grouped_kernel<EPI>, grid, dim3(256), 0, s, a, p.n_tiles, p.tile_e, p.tile_r0, p.tile_nr,
+                    p.exp_nt, p.exp_t0);
+        return hipGetLastError();
+    };
+    {
+        ProfScope ps(ctx, "i8_gate_up");
+        const I8Args a{w.xq, w.xs, p.perm, top_k, L->wg, L->sg, L->wu, L->su, nullptr, nullptr, w.act, H, I};
+        if ((e = grouped(std::integral_constant<int, kI8Swiglu>(), a)) != hipSuccess) return e;
+    }
+    {
+        ProfScope ps(ctx, "i8_quantize_act");
+        if ((e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, kQuantDynamic)) != hipSuccess) return e;
+    }
+    {
+        ProfScope ps(ctx, "i8_down");
+        const I8Args a{w.aq, w.as, p.perm, top_k, L->wd, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
+        if ((e = grouped(std::integral_constant<int, kI8Down>(), a)) != hipSuccess) return e;
+    }
+    if (with_shared) {
+        const int SI = static_cast<int>(L->shared_inter);
+        ProfScope ps(ctx, "i8_shared");
+        if ((e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg, L->ssg, L->swu, L->ssu, SI, w.shared_act)) !=
+            hipSuccess)
+            return e;
+        if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
+            hipSuccess)
+            return e;
+        if ((e = launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd, L->ssd, H, nullptr, w.shared_y)) !=
+            hipSuccess)
+            return e;
+    }
+    {
+        ProfScope ps(ctx, "i8_combine");
+        if ((e = launch_moe_prefill_combine(s, w.ybuf, idx, t, H, top_k, with_shared ? w.shared_y : nullptr, out)) !=
+            hipSuccess)
+            return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace focr

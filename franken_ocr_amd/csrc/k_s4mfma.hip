@@ -443,7 +443,9 @@ __global__ __launch_bounds__(256) void retile_s_kernel(const float* __restrict__
 }
 
 // ---- quantize x + plan (one launch) -------------------------------------------
-// Blocks [0, qblocks): quantize_row_i8_te (decoder.rs:1647-1656) of token rows,
+// Blocks [0, qblocks): quantize the token rows by `rule` (quantize_row_i8_te,
+// decoder.rs:1647-1656, for the int4 layer; the dynamic rule of
+// linear_int8_dynamic for the int8 one),
 // four rows per block (one per 256 threads). The last block: the plan, a
 // stable counting sort of the (token, slot) pairs by expert. Pairs whose
 // expert is out of range set *err (the oracle's shape error). Output:
@@ -477,7 +479,7 @@ __device__ __forceinline__ unsigned long long match7(uint32_t e) {
     return same;
 }
 
-__global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __restrict__ x, int T, int H,
+__global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __restrict__ x, int T, int H, int rule,
                                                                int8_t* __restrict__ xq, float* __restrict__ xs,
                                                                const uint32_t* __restrict__ idx, int TK, int E,
                                                                int* __restrict__ perm, int* __restrict__ n_tiles,
@@ -509,7 +511,7 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         const float inv = 1.0f / a_scale;
         if (ok) {
             int8_t* q = xq + static_cast<size_t>(row) * H;
-            for (int i = st; i < H; i += 256) q[i] = quant_i8(xr[i], inv, true);
+            for (int i = st; i < H; i += 256) q[i] = quant_rule(xr[i], a_scale, inv, rule);
             if (st == 0) xs[row] = a_scale;
         }
         return;
@@ -578,9 +580,11 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
 
 // ---- combine: out[t] = sum of the token's pair rows in ascending expert order --
 // The token's slots sorted by (expert, slot): slot j's rank counts the slots
-// ahead of it, the first K threads publish order[rank] = j.
+// ahead of it, the first K threads publish order[rank] = j. shared_y (the
+// shared expert's output, nullable) is added last (decoder.rs:2176-2179).
 __global__ __launch_bounds__(256) void i4_combine_kernel(const float* __restrict__ ybuf,
                                                          const uint32_t* __restrict__ idx, int H, int K,
+                                                         const float* __restrict__ shared_y,
                                                          float* __restrict__ out) {
     __shared__ int s_order[kMaxK];
     const int t = blockIdx.y;
@@ -605,6 +609,7 @@ __global__ __launch_bounds__(256) void i4_combine_kernel(const float* __restrict
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j)
         if (j < K) o = o + v[j];
+    if (shared_y) o = o + shared_y[static_cast<size_t>(t) * H + c];
     out[static_cast<size_t>(t) * H + c] = o;
 }
 
@@ -674,30 +679,51 @@ size_t moe_i4_plan_ints(int tk, int n_experts) {
     return static_cast<size_t>(tk) + 3 * static_cast<size_t>(max_tiles) + 2 * kMaxE + 2;
 }
 
+MoePlan moe_plan_view(int* plan, int tk, int n_experts) {
+    MoePlan p;
+    p.max_tiles = (tk + BM - 1) / BM + n_experts;
+    p.perm = plan;
+    p.tile_e = p.perm + tk;
+    p.tile_r0 = p.tile_e + p.max_tiles;
+    p.tile_nr = p.tile_r0 + p.max_tiles;
+    p.exp_nt = p.tile_nr + p.max_tiles;
+    p.exp_t0 = p.exp_nt + kMaxE;
+    p.n_tiles = p.exp_t0 + kMaxE;
+    return p;
+}
+
+hipError_t launch_moe_prefill_plan(hipStream_t s, const float* x, int t, int H, int rule, int8_t* xq, float* xs,
+                                   const uint32_t* idx, int top_k, int E, const MoePlan& p, int* err) {
+    const int qblocks = (t + kQRows - 1) / kQRows;
+    FOCR_LAUNCH(i4_prep_kernel, dim3(qblocks + 1), dim3(kPlanThreads), 0, s, x, t, H, rule, xq, xs, idx, t * top_k,
+                E, p.perm, p.n_tiles, p.tile_e, p.tile_r0, p.tile_nr, p.exp_nt, p.exp_t0, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_prefill_combine(hipStream_t s, const float* ybuf, const uint32_t* idx, int t, int H,
+                                      int top_k, const float* shared_y, float* out) {
+    FOCR_LAUNCH(i4_combine_kernel, dim3((H + 255) / 256, t), dim3(256), 0, s, ybuf, idx, H, top_k, shared_y, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, float* out, MoeI4Scratch& w,
                                  focr_hip_ctx* ctx) {
     const int H = static_cast<int>(L->hidden), I = static_cast<int>(L->inter), E = static_cast<int>(L->n_experts);
     const int group = static_cast<int>(L->group);
     const int TK = t * top_k;
-    const int max_tiles = (TK + BM - 1) / BM + E;
-    int* perm = w.plan;
-    int* tile_e = perm + TK;
-    int* tile_r0 = tile_e + max_tiles;
-    int* tile_nr = tile_r0 + max_tiles;
-    int* exp_nt = tile_nr + max_tiles;
-    int* exp_t0 = exp_nt + kMaxE;
-    int* n_tiles = exp_t0 + kMaxE;
+    const MoePlan p = moe_plan_view(w.plan, TK, E);
+    const int max_tiles = p.max_tiles;
+    const int* perm = p.perm;
     hipError_t e;
     {
         ProfScope ps(ctx, "i4_prep");
-        const int qblocks = (t + kQRows - 1) / kQRows;
-        FOCR_LAUNCH(i4_prep_kernel, dim3(qblocks + 1), dim3(kPlanThreads), 0, s, x, t, H, w.xq, w.xs, idx, TK, E,
-                    perm, n_tiles, tile_e, tile_r0, tile_nr, exp_nt, exp_t0, w.err);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = launch_moe_prefill_plan(s, x, t, H, kQuantTiesEven, w.xq, w.xs, idx, top_k, E, p, w.err)) !=
+            hipSuccess)
+            return e;
     }
-    const TileList tl{n_tiles, tile_e, tile_r0, tile_nr};
-    const ExpertTiles et{exp_nt, exp_t0};
+    const TileList tl{p.n_tiles, p.tile_e, p.tile_r0, p.tile_nr};
+    const ExpertTiles et{p.exp_nt, p.exp_t0};
     {
         ProfScope ps(ctx, "i4_gate_up");
         const EpiArgs ep{w.act, perm, w.xs, nullptr, top_k};
@@ -707,7 +733,7 @@ hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, 
     }
     {
         ProfScope ps(ctx, "i4_quantize_act");
-        if ((e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, true)) != hipSuccess) return e;
+        if ((e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, kQuantTiesEven)) != hipSuccess) return e;
     }
     {
         ProfScope ps(ctx, "i4_down");
@@ -718,8 +744,7 @@ hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, 
     }
     {
         ProfScope ps(ctx, "i4_combine");
-        FOCR_LAUNCH(i4_combine_kernel, dim3((H + 255) / 256, t), dim3(256), 0, s, w.ybuf, idx, H, top_k, out);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = launch_moe_prefill_combine(s, w.ybuf, idx, t, H, top_k, nullptr, out)) != hipSuccess) return e;
     }
     return hipSuccess;
 }

@@ -78,9 +78,24 @@ class QInt8:
             pass
 
 
-def quantize_rows_i8(x: DeviceArray, xq: DeviceArray, a_scales: DeviceArray, ties_even: bool = False) -> None:
+QUANT_HALF_AWAY, QUANT_TIES_EVEN, QUANT_DYNAMIC = 0, 1, 2
+
+
+def quantize_rows_i8(x: DeviceArray, xq: DeviceArray, a_scales: DeviceArray, ties_even: bool = False,
+                     rule: int | None = None) -> None:
+    """Per-row int8 quantization: quantize_row_i8 (decoder.rs:1588-1597),
+    quantize_row_i8_te (ties_even, :1647-1656), or rule=QUANT_DYNAMIC, the
+    dynamic activation rule of linear_int8_dynamic (true division)."""
     m, k = x.shape
-    _abi.call("focr_hip_quantize_rows_i8", x.ctx.handle, x.c_ptr, m, k, xq.c_ptr, a_scales.c_ptr, 1 if ties_even else 0)
+    r = (QUANT_TIES_EVEN if ties_even else QUANT_HALF_AWAY) if rule is None else int(rule)
+    _abi.call("focr_hip_quantize_rows_i8", x.ctx.handle, x.c_ptr, m, k, xq.c_ptr, a_scales.c_ptr, r)
+
+
+def linear_i8_dynamic(w: QInt8, x: DeviceArray, y: DeviceArray, bias: DeviceArray | None = None) -> None:
+    """nn::linear_int8_dynamic (nn.rs:151-173) on the matrix cores: x [m, k]
+    f32 -> y [m, n] f32 (k a multiple of 64)."""
+    m = x.shape[0] if len(x.shape) > 1 else 1
+    _abi.call("focr_hip_linear_i8_dynamic", w.ctx.handle, w.handle, x.c_ptr, m, _p(bias), y.c_ptr)
 
 
 def gemv_i8(w: QInt8, x: DeviceArray, y: DeviceArray) -> None:
@@ -210,6 +225,14 @@ class MoeLayer:
         _abi.call("focr_hip_moe_decode", self.ctx.handle, self._h, hidden.c_ptr, t, 1 if norm_topk else 0,
                   float(routed_scale), 1 if with_shared else 0, out.c_ptr, _p(idx), _p(gates),
                   1 if check_route else 0)
+
+    def prefill(self, x: DeviceArray, idx: DeviceArray, gates: DeviceArray, out: DeviceArray,
+                with_shared: bool = False, check_idx: bool = True) -> None:
+        """moe_block_i8 (decoder.rs:2142-2181) on the matrix cores for prefill
+        rows x [t, hidden] with routing idx/gates [t, top_k]; out [t, hidden]."""
+        t = idx.shape[0]
+        _abi.call("focr_hip_moe_prefill_i8", self.ctx.handle, self._h, x.c_ptr, t, idx.c_ptr, gates.c_ptr,
+                  1 if with_shared else 0, out.c_ptr, 1 if check_idx else 0)
 
     def free(self) -> None:
         if self._h:

@@ -169,11 +169,13 @@ int32_t focr_hip_qint8_from_device(focr_hip_ctx* ctx, const int8_t* w, const flo
                                    size_t n, size_t k, focr_hip_qint8** out);
 int32_t focr_hip_qint8_free(focr_hip_qint8* w);
 
-/* decoder.rs:1588-1597 quantize_row_i8 (ties_even = 0: round half away,
- * reciprocal multiply) and :1647-1656 quantize_row_i8_te (ties_even = 1),
- * one scale per row: x [m,k] f32 -> xq [m,k] i8, a_scales [m]. */
+/* One scale per row, x [m,k] f32 -> xq [m,k] i8, a_scales [m], by rule:
+ * 0 = decoder.rs:1588-1597 quantize_row_i8 (round half away, reciprocal
+ * multiply), 1 = :1647-1656 quantize_row_i8_te (ties to even, reciprocal
+ * multiply), 2 = the dynamic activation rule of nn::linear_int8_dynamic
+ * (docs/focrq-format.md:296-320: ties to even, true division). */
 int32_t focr_hip_quantize_rows_i8(focr_hip_ctx* ctx, const float* x, size_t m, size_t k,
-                                  int8_t* xq, float* a_scales, int32_t ties_even);
+                                  int8_t* xq, float* a_scales, int32_t rule);
 
 /* decoder.rs:1607 gemv_i8 (m = 1) and :2703-2747 gemv_i8_batched (m rows):
  * each row quantized with quantize_row_i8, y[m,n] = ((f32)acc * a_scale[m])
@@ -285,6 +287,27 @@ int32_t focr_hip_moe_layer_i4_free(focr_hip_moe_layer_i4* layer);
 int32_t focr_hip_moe_prefill_i4(focr_hip_ctx* ctx, const focr_hip_moe_layer_i4* layer,
                                 const float* x, size_t t, size_t top_k, const uint32_t* idx,
                                 const float* gates, float* out, int32_t check_idx);
+
+/* ---- prefill on int8 weights (int8 matrix cores, i32 accumulation) --------- */
+/* nn.rs:151-173 linear_int8_dynamic on an uploaded QInt8 [n, k]: each row of
+ * x [m, k] f32 quantized by the dynamic rule (rule 2 above), y [m, n] =
+ * ((f32)acc * a_scale[row]) * w_scale[col] (+ bias[col]; bias nullable).
+ * Device pointers. k must be a multiple of 64 (E_SHAPE otherwise). */
+int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x,
+                                   size_t m, const float* bias, float* y);
+/* decoder.rs:2142-2181 moe_block_i8 on an uploaded int8 MoE layer (the
+ * decode layer's handle, focr_hip_moe_layer_create), for t prefill rows with
+ * a given routing idx, gates [t, top_k] (e.g. moe::route_default): per member
+ * (token, slot) of expert e, expert_mlp_i8 (decoder.rs:2120-2135) — three
+ * linear_int8_dynamic products, act = silu(g) * u — and out[t] = the sum of
+ * gate * y over the token's members in ascending expert order, plus (with
+ * with_shared) the shared expert's expert_mlp_i8 of every row at weight 1.0.
+ * Device pointers; t <= 16384; hidden and inter multiples of 64. With
+ * check_idx = 1 the call synchronises and returns E_SHAPE for an expert
+ * index >= n_experts. */
+int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer, const float* x,
+                                size_t t, const uint32_t* idx, const float* gates,
+                                int32_t with_shared, float* out, int32_t check_idx);
 
 /* ---- R-SWA ring KV cache (rswa.rs:121-152 RingCache, :645-824 batched) ---
  * n_streams independent caches of one layer, f32, head-major per stream:

@@ -574,6 +574,122 @@ int oracle_moe_prefill_i4(const float* x, size_t t, size_t h, size_t inter, size
     return ORACLE_OK;
 }
 
+/* ---- nn::linear_int8_dynamic (nn.rs:151-173) --------------------------------
+ * ft-kernel-cpu's linear_int8_dynamic_f32 is not in the reference tree; its
+ * activation rule is the documented one (docs/focrq-format.md:296-320, pinned
+ * by nn.rs:601-628 ties-even); the dequant is the decoder's order
+ * ((f32)acc * scale_a) * w_scale (decoder.rs:1636), then + bias. */
+float oracle_quantize_row_dynamic(const float* x, size_t k, int8_t* q) {
+    float amax = 0.0f;
+    for (size_t i = 0; i < k; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    for (size_t i = 0; i < k; ++i) {
+        float v = x[i] / a_scale;
+        if (v != v) {
+            q[i] = 0;
+            continue;
+        }
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        q[i] = (int8_t)(int)rintf(v);
+    }
+    return a_scale;
+}
+
+int oracle_linear_i8_dynamic(const float* x, size_t m, size_t k, const int8_t* w, const float* w_scales,
+                             size_t n, const float* bias, float* y, int8_t* xq, float* x_scales) {
+    size_t t;
+    if (!mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t)) return ORACLE_E_SHAPE;
+    int32_t* acc = (int32_t*)calloc((m * n) > 0 ? (m * n) : 1, sizeof(int32_t));
+    if (!acc) return ORACLE_E_SHAPE;
+    for (size_t r = 0; r < m; ++r) x_scales[r] = oracle_quantize_row_dynamic(x + r * k, k, xq + r * k);
+    oracle_igemm_s8s8(xq, w, m, k, n, acc);
+    for (size_t r = 0; r < m; ++r)
+        for (size_t o = 0; o < n; ++o) {
+            float v = (float)acc[r * n + o] * x_scales[r];
+            v = v * w_scales[o];
+            if (bias) v = v + bias[o];
+            y[r * n + o] = v;
+        }
+    free(acc);
+    return ORACLE_OK;
+}
+
+/* expert_mlp_i8 (decoder.rs:2120-2135) over rows x[0..rows) of width h:
+ * y [rows][h]. */
+static int expert_mlp_i8_rows(const float* x, size_t rows, size_t h, size_t inter, const int8_t* wg,
+                              const float* sg, const int8_t* wu, const float* su, const int8_t* wd,
+                              const float* sd, float* y) {
+    float* g = (float*)malloc(rows * inter * sizeof(float));
+    float* u = (float*)malloc(rows * inter * sizeof(float));
+    int8_t* xq = (int8_t*)malloc(rows * (h > inter ? h : inter));
+    float* xs = (float*)malloc(rows * sizeof(float));
+    int st = ORACLE_E_SHAPE;
+    if (g && u && xq && xs) {
+        st = oracle_linear_i8_dynamic(x, rows, h, wg, sg, inter, NULL, g, xq, xs);
+        if (st == ORACLE_OK) st = oracle_linear_i8_dynamic(x, rows, h, wu, su, inter, NULL, u, xq, xs);
+        if (st == ORACLE_OK) {
+            for (size_t i = 0; i < rows * inter; ++i) g[i] = oracle_silu(g[i]) * u[i];
+            st = oracle_linear_i8_dynamic(g, rows, inter, wd, sd, h, NULL, y, xq, xs);
+        }
+    }
+    free(g);
+    free(u);
+    free(xq);
+    free(xs);
+    return st;
+}
+
+int oracle_moe_prefill_i8(const float* x, size_t t, size_t h, size_t inter, size_t n_experts,
+                          size_t top_k, const uint32_t* idx, const float* gates, const int8_t* wg,
+                          const float* sg, const int8_t* wu, const float* su, const int8_t* wd,
+                          const float* sd, const int8_t* shared_wg, const float* shared_sg,
+                          const int8_t* shared_wu, const float* shared_su, const int8_t* shared_wd,
+                          const float* shared_sd, size_t shared_inter, float* out) {
+    for (size_t r = 0; r < t * top_k; ++r)
+        if (idx[r] >= n_experts) return ORACLE_E_SHAPE;
+    memset(out, 0, t * h * sizeof(float));
+    /* members of expert e in (token, slot) order (decoder.rs:2152-2157) */
+    size_t* mem_t = (size_t*)malloc((t * top_k + 1) * sizeof(size_t));
+    float* mem_w = (float*)malloc((t * top_k + 1) * sizeof(float));
+    float* sub = (float*)malloc((t * top_k + 1) * h * sizeof(float));
+    float* y = (float*)malloc((t * top_k + 1) * h * sizeof(float));
+    int st = (mem_t && mem_w && sub && y) ? ORACLE_OK : ORACLE_E_SHAPE;
+    for (size_t e = 0; e < n_experts && st == ORACLE_OK; ++e) {
+        size_t m = 0;
+        for (size_t tok = 0; tok < t; ++tok)
+            for (size_t j = 0; j < top_k; ++j)
+                if (idx[tok * top_k + j] == e) {
+                    mem_t[m] = tok;
+                    mem_w[m] = gates[tok * top_k + j];
+                    memcpy(sub + m * h, x + tok * h, h * sizeof(float));
+                    ++m;
+                }
+        if (m == 0) continue;
+        st = expert_mlp_i8_rows(sub, m, h, inter, wg + e * inter * h, sg + e * inter, wu + e * inter * h,
+                                su + e * inter, wd + e * h * inter, sd + e * h, y);
+        for (size_t r = 0; r < m && st == ORACLE_OK; ++r) {
+            float* o = out + mem_t[r] * h;
+            for (size_t c = 0; c < h; ++c) {
+                float p = mem_w[r] * y[r * h + c];
+                o[c] = o[c] + p;
+            }
+        }
+    }
+    if (st == ORACLE_OK && shared_wg) {
+        float* sy = (float*)malloc(t * h * sizeof(float));
+        st = sy ? expert_mlp_i8_rows(x, t, h, shared_inter, shared_wg, shared_sg, shared_wu, shared_su,
+                                     shared_wd, shared_sd, sy)
+                : ORACLE_E_SHAPE;
+        for (size_t i = 0; i < t * h && st == ORACLE_OK; ++i) out[i] = out[i] + sy[i];
+        free(sy);
+    }
+    free(mem_t);
+    free(mem_w);
+    free(sub);
+    free(y);
+    return st;
+}
+
 /* ---- src/quant/int8.rs:110-163 quantize_int8_f32 --------------------------
  * scale = max|row|/127 (all-zero row: scale 1, q 0); q =
  * clamp(round_ties_even(w / scale), -127, 127) with true division. */

@@ -106,6 +106,28 @@ int oracle_moe_decode(const float* hidden, size_t t, size_t h, size_t inter, siz
                       const int8_t* shared_wd, const float* shared_sd, size_t shared_inter,
                       float* out, uint32_t* idx, float* gates);
 
+/* ---- prefill int8 linear: nn::linear_int8_dynamic (nn.rs:151-173) ---------
+ * The dynamic activation rule of docs/focrq-format.md:296-320: scale_a =
+ * max|x|/127 (1.0 for an all-zero row), q = round_ties_even(clamp(x / scale_a,
+ * -127, 127)) with TRUE division (not a reciprocal multiply). */
+float oracle_quantize_row_dynamic(const float* x, size_t k, int8_t* q);
+/* y[r][o] = ((f32)acc * scale_a[r]) * w_scale[o] (+ bias[o]); bias may be NULL.
+ * xq [m][k] / x_scales [m] receive the quantized rows. */
+int oracle_linear_i8_dynamic(const float* x, size_t m, size_t k, const int8_t* w, const float* w_scales,
+                             size_t n, const float* bias, float* y, int8_t* xq, float* x_scales);
+/* moe_block_i8 (decoder.rs:2142-2181) over given routing: each routed
+ * expert's expert_mlp_i8 (decoder.rs:2120-2135: linear_int8_dynamic gate, silu,
+ * linear_int8_dynamic up, product, linear_int8_dynamic down) on its member
+ * tokens, scattered out[t] += w * y in ascending expert order (slot order
+ * inside an expert); with shared_wg != NULL the shared expert's
+ * expert_mlp_i8 over every token is added last at weight 1.0. */
+int oracle_moe_prefill_i8(const float* x, size_t t, size_t h, size_t inter, size_t n_experts,
+                          size_t top_k, const uint32_t* idx, const float* gates, const int8_t* wg,
+                          const float* sg, const int8_t* wu, const float* su, const int8_t* wd,
+                          const float* sd, const int8_t* shared_wg, const float* shared_sg,
+                          const int8_t* shared_wu, const float* shared_su, const int8_t* shared_wd,
+                          const float* shared_sd, size_t shared_inter, float* out);
+
 /* ---- src/simd/int4.rs ---------------------------------------------------- */
 int8_t oracle_sign_extend_nibble(uint8_t nib);
 void oracle_unpack_byte(uint8_t b, int8_t* lo, int8_t* hi);

@@ -46,6 +46,10 @@ _SIGS = {
     "oracle_s4s8_group_i32": ([_P, _P, _SZ, _SZ, _SZ, _SZ, _P], C.c_int),
     "oracle_moe_prefill_i4": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P],
                               C.c_int),
+    "oracle_quantize_row_dynamic": ([_P, _SZ, _P], C.c_float),
+    "oracle_linear_i8_dynamic": ([_P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P], C.c_int),
+    "oracle_moe_prefill_i8": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                               _SZ, _P], C.c_int),
     "oracle_quantize_int8_f32": ([_P, _SZ, _SZ, _P, _P], C.c_int),
     "oracle_pack_int4_f32": ([_P, _SZ, _SZ, _SZ, _P, _P], C.c_int),
     "oracle_ring_write": ([_P, _P, _P, _P, _P, _P, _P], C.c_int),
@@ -271,6 +275,46 @@ def moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, n_experts, inte
                                      p(_c(wu, np.uint8)), p(_c(su, np.float32)), p(_c(wd, np.uint8)),
                                      p(_c(sd, np.float32)), p(out), p(xq), p(xs))
     return st, out.reshape(t, h), xq.reshape(t, h), xs
+
+
+def quantize_row_dynamic(x):
+    """docs/focrq-format.md:296-320 dynamic activation rule (ties-even, true division)."""
+    x = _c(x, np.float32)
+    q = np.zeros(x.size, np.int8)
+    s = lib().oracle_quantize_row_dynamic(p(x), x.size, p(q))
+    return q, np.float32(s)
+
+
+def linear_i8_dynamic(x, w, w_scales, n, bias=None):
+    """nn::linear_int8_dynamic (nn.rs:151-173): y [m, n], xq [m, k], x scales [m]."""
+    x = _c(x, np.float32)
+    m, k = x.shape
+    y = np.zeros(m * n, np.float32)
+    xq = np.zeros(m * k, np.int8)
+    xs = np.zeros(m, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    st = lib().oracle_linear_i8_dynamic(p(x), m, k, p(_c(w, np.int8)), p(_c(w_scales, np.float32)), n,
+                                        None if b is None else p(b), p(y), p(xq), p(xs))
+    return st, y.reshape(m, n), xq.reshape(m, k), xs
+
+
+def moe_prefill_i8(x, idx, gates, wg, sg, wu, su, wd, sd, n_experts, inter, shared=None):
+    """moe_block_i8 (decoder.rs:2142-2181) over given routing, int8 experts."""
+    x = _c(x, np.float32)
+    t, h = x.shape
+    top_k = idx.shape[1]
+    out = np.zeros(t * h, np.float32)
+    if shared is None:
+        sh = [None] * 6
+        si = 0
+    else:
+        si = shared[0]
+        sh = [p(_c(a, np.int8 if i % 2 == 0 else np.float32)) for i, a in enumerate(shared[1:])]
+    st = lib().oracle_moe_prefill_i8(p(x), t, h, inter, n_experts, top_k, p(_c(idx, np.uint32)),
+                                     p(_c(gates, np.float32)), p(_c(wg, np.int8)), p(_c(sg, np.float32)),
+                                     p(_c(wu, np.int8)), p(_c(su, np.float32)), p(_c(wd, np.int8)),
+                                     p(_c(sd, np.float32)), *sh, si, p(out))
+    return st, out.reshape(t, h)
 
 
 class Ring:

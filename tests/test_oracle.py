@@ -503,3 +503,115 @@ def test_attention_empty_key_set_is_error():
     r.record_prefill(np.zeros((H, 0, D), np.float32), np.zeros((H, 0, D), np.float32), 0)
     st, _ = r.attend(np.zeros(H * D, np.float32))
     assert st != 0
+
+
+# ---- prefill int8 linear (nn::linear_int8_dynamic) and moe_block_i8 --------------------
+
+def test_linear_i8_dynamic_known_answers():
+    # nn.rs:549-556: x=[[1,2,3]], W=[[1,0,1],[0,1,0]] quantized per channel -> y ~ [4, 2]
+    st, wq, ws = 0, np.zeros(6, np.int8), np.zeros(2, np.float32)
+    assert O.lib().oracle_quantize_int8_f32(O.p(np.array([1, 0, 1, 0, 1, 0], np.float32)), 2, 3, O.p(wq),
+                                            O.p(ws)) == 0
+    st, y, _, _ = O.linear_i8_dynamic(np.array([[1, 2, 3]], np.float32), wq, ws, 2)
+    assert st == 0 and abs(y[0, 0] - 4.0) < 0.1 and abs(y[0, 1] - 2.0) < 0.1
+    # nn.rs:601-628: ties round to even (a half-away quantizer gives [1, 3])
+    x = np.array([[-127, -2.5, -1.5, -0.5, 0.5, 1.5, 2.5, 127], [0] * 8], np.float32)
+    w = np.array([[0, 0, 0, 0, 1, 0, 0, 0], [0, 0, 0, 0, 0, 0, 1, 0]], np.int8)
+    st, y, xq, xs = O.linear_i8_dynamic(x, w, np.ones(2, np.float32), 2)
+    assert st == 0 and y.ravel().tolist() == [0.0, 2.0, 0.0, 0.0]
+    assert xq[0].tolist() == [-127, -2, -2, 0, 0, 2, 2, 127] and xs.tolist() == [1.0, 1.0]  # all-zero row: 1.0
+    st, y2, _, _ = O.linear_i8_dynamic(x, w, np.ones(2, np.float32), 2)
+    assert np.array_equal(y, y2)
+
+
+def test_quantize_row_dynamic_is_true_division(rng):
+    # docs/focrq-format.md:296-320: q = round_ties_even(clamp(x / scale)), true
+    # division. Find rows where x * (1/scale) rounds differently from x / scale
+    # and check the oracle takes the division.
+    hits = 0
+    for _ in range(400):
+        x = rng.standard_normal(256).astype(np.float32)
+        s = np.float32(np.abs(x).max()) / np.float32(127.0)
+        # plant exact ties x = (k + 0.5) * s (rounded to f32) so the two rules can split
+        k = rng.integers(-120, 120, 32)
+        x[:32] = ((k + 0.5).astype(np.float32) * s).astype(np.float32)
+        x[32] = np.float32(127.0) * s  # keep amax (and so s) fixed
+        s = np.float32(np.abs(x).max()) / np.float32(127.0)
+        div = np.rint(np.clip(x / s, -127, 127)).astype(np.int8)
+        rec = np.rint(np.clip(x * (np.float32(1.0) / s), -127, 127)).astype(np.int8)
+        q, qs = O.quantize_row_dynamic(x)
+        assert qs == s and np.array_equal(q, div)
+        hits += int((div != rec).any())
+    assert hits > 0, "no row separated true division from a reciprocal multiply"
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 16, 8), (7, 64, 33), (64, 1280, 96)])
+def test_linear_i8_dynamic_vs_int64_and_float64(m, k, n, rng):
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    x[0, :5] = 0.0
+    w = rng.integers(-127, 128, n * k).astype(np.int8)
+    ws = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    st, y, xq, xs = O.linear_i8_dynamic(x, w, ws, n, bias=b)
+    assert st == 0
+    for r in range(m):
+        q, s = O.quantize_row_dynamic(x[r])
+        assert np.array_equal(xq[r], q) and xs[r] == s
+    acc = xq.astype(np.int64) @ w.reshape(n, k).astype(np.int64).T  # |acc| < 2^31 here
+    want = acc * xs.astype(np.float64)[:, None] * ws.astype(np.float64)[None, :] + b.astype(np.float64)[None, :]
+    np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5)
+
+
+def _np_expert_mlp_i8(x, wg, sg, wu, su, wd, sd, inter):
+    """expert_mlp_i8 (decoder.rs:2120-2135) composed from three oracle
+    linear_int8_dynamic calls (each pinned above) and the f32 SiLU."""
+    h = x.shape[1]
+    _, g, _, _ = O.linear_i8_dynamic(x, wg, sg, inter)
+    _, u, _, _ = O.linear_i8_dynamic(x, wu, su, inter)
+    silu = np.vectorize(lambda v: O.lib().oracle_silu(float(v)), otypes=[np.float32])
+    act = (silu(g) * u).astype(np.float32)  # f32 silu(g) * u, as decoder.rs:2125-2131
+    _, y, _, _ = O.linear_i8_dynamic(act, wd, sd, h)
+    return y
+
+
+def test_moe_prefill_i8_ascending_expert_scatter_and_shared(rng):
+    h, inter, E, K, t = 48, 32, 8, 3, 10
+    wg = rng.integers(-127, 128, E * inter * h).astype(np.int8)
+    wu = rng.integers(-127, 128, E * inter * h).astype(np.int8)
+    wd = rng.integers(-127, 128, E * h * inter).astype(np.int8)
+    sg = rng.uniform(1e-3, 2e-2, E * inter).astype(np.float32)
+    su = rng.uniform(1e-3, 2e-2, E * inter).astype(np.float32)
+    sd = rng.uniform(1e-3, 2e-2, E * h).astype(np.float32)
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(t)]).astype(np.uint32)
+    idx[3] = [5, 5, 1]  # a token routed twice to one expert: both slots are members
+    gates = rng.uniform(0.05, 1.0, (t, K)).astype(np.float32)
+    st, out = O.moe_prefill_i8(x, idx, gates, wg, sg, wu, su, wd, sd, E, inter)
+    assert st == 0
+    want32 = np.zeros((t, h), np.float32)
+    want64 = np.zeros((t, h), np.float64)
+    for e in range(E):  # ascending expert order, (token, slot) order inside
+        sl = slice(e * inter * h, (e + 1) * inter * h)
+        for r in range(t):
+            for j in range(K):
+                if idx[r, j] != e:
+                    continue
+                y = _np_expert_mlp_i8(x[r:r + 1], wg[sl], sg[e * inter:(e + 1) * inter], wu[sl],
+                                      su[e * inter:(e + 1) * inter], wd[e * h * inter:(e + 1) * h * inter],
+                                      sd[e * h:(e + 1) * h], inter)[0]
+                want32[r] = (want32[r] + (np.float32(gates[r, j]) * y).astype(np.float32)).astype(np.float32)
+                want64[r] += float(gates[r, j]) * y.astype(np.float64)
+    assert np.array_equal(out, want32)
+    np.testing.assert_allclose(out, want64, rtol=1e-5, atol=1e-6)
+    # the shared expert is added last at weight 1.0
+    si = 40
+    sw = [rng.integers(-127, 128, si * h).astype(np.int8), rng.uniform(1e-3, 2e-2, si).astype(np.float32),
+          rng.integers(-127, 128, si * h).astype(np.int8), rng.uniform(1e-3, 2e-2, si).astype(np.float32),
+          rng.integers(-127, 128, h * si).astype(np.int8), rng.uniform(1e-3, 2e-2, h).astype(np.float32)]
+    st, out_s = O.moe_prefill_i8(x, idx, gates, wg, sg, wu, su, wd, sd, E, inter, shared=(si, *sw))
+    assert st == 0
+    ys = _np_expert_mlp_i8(x, sw[0], sw[1], sw[2], sw[3], sw[4], sw[5], si)
+    assert np.array_equal(out_s, (out + ys).astype(np.float32))
+    bad = idx.copy()
+    bad[0, 0] = E
+    assert O.moe_prefill_i8(x, bad, gates, wg, sg, wu, su, wd, sd, E, inter)[0] != 0
