@@ -475,6 +475,103 @@ def cpu_prefill_i4(args, inputs):
 
 
 # ---------------------------------------------------------------------------
+# prefill on int8 weights (int8 matrix cores): the dense linear and the MoE block
+# ---------------------------------------------------------------------------
+
+def bench_linear_i8(args, ctx):
+    """nn::linear_int8_dynamic at the dense layer-0 MLP gate shape (N = 6848,
+    K = 1280) over M prefill rows: dynamic-rule quantize + int8 MFMA GEMM."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import QInt8, linear_i8_dynamic
+
+    M, N, Kd = args.tokens, 6848, H
+    log(f"linear_i8: M={M} N={N} K={Kd}, {args.copies} weight copies")
+    w = synth.int8_uniform(synth.seed_of(700), N * Kd)
+    ws = synth.f32_uniform(synth.seed_of(701), N, 1e-3, 2e-2)
+    qs = [QInt8(w, ws, N, Kd, ctx) for _ in range(args.copies)]
+    x = synth.f32_normal(synth.seed_of(702), M * Kd).reshape(M, Kd)
+    dx, dy = ctx.to_device(x), ctx.empty((M, N), np.float32)
+
+    def step(i):
+        linear_i8_dynamic(qs[i % len(qs)], dx, dy)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    ops = 2.0 * M * N * Kd
+    g_us = kernel_us(prof, "linear_i8")
+    tops = ops / (g_us * 1e-6) / 1e12
+    log(f"per-kernel avg us {kernels}")
+    return {
+        "metric": "prefill int8 linear (linear_int8_dynamic) rows/s + int8 MFMA utilisation, 1 GPU",
+        "value": round(M * args.steps / el, 1), "unit": "rows/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "linear_i8", "rows": M, "n": N, "k": Kd, "weight_copies_rotated": args.copies},
+        "roofline": {"bound": "mfma", "kernel": "linear_i8", "achieved": round(tops, 2),
+                     "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4),
+                     "traffic": traffic_for("linear_i8", f"linear_i8_m{M}"),
+                     "algorithmic_ops_per_launch": ops, "avg_launch_us": round(g_us, 3)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
+def bench_prefill_i8(args, ctx):
+    """moe_block_i8 over M prefill rows with Zipf(1.1) top-6 routing (config
+    4's routing) on the int8 MoE layer the decode path uses."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import MoeLayer
+
+    T = args.tokens
+    log(f"moe_prefill_i8: M={T} tokens, top-{K}, Zipf(1.1) routing, {args.copies} layer copies")
+    base = make_moe_host(100)
+    layers = [MoeLayer(H, I, E, K, *base, ctx=ctx) for _ in range(args.copies)]
+    x = synth.f32_normal(synth.seed_of(350), T * H).reshape(T, H)
+    idx, gates = synth.zipf_routing(synth.seed_of(360), T, E, K)
+    dx, di, dg = ctx.to_device(x), ctx.to_device(idx), ctx.to_device(gates)
+    dout = ctx.empty((T, H), np.float32)
+
+    def step(i):
+        layers[i % len(layers)].prefill(dx, di, dg, dout, check_idx=False)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    pairs = T * K
+    gu_ops = 2.0 * pairs * 2 * I * H
+    dn_ops = 2.0 * pairs * H * I
+    gu_us = kernel_us(prof, "i8_gate_up")
+    gu_tops = gu_ops / (gu_us * 1e-6) / 1e12
+    layer_tops = (gu_ops + dn_ops) / (ms * 1e-3) / 1e12
+    counts = np.bincount(idx.ravel(), minlength=E)
+    wbytes = int((counts > 0).sum()) * (3 * I * H + 4 * (2 * I + H))
+    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False),
+                                    max(args.steps // 2, 10))
+    log(f"per-kernel avg us {kernels}; warm {kernels_w}")
+    return {
+        "metric": "int8 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
+        "value": round(T * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "moe_prefill_i8", "tokens": T, "hidden": H, "inter": I, "experts": E, "top_k": K,
+                   "routing": "zipf(1.1) without replacement", "layer_copies_rotated": args.copies,
+                   "tokens_per_expert_max": int(counts.max()), "experts_hit": int((counts > 0).sum())},
+        "roofline": {"bound": "mfma", "kernel": "i8_gate_up", "achieved": round(gu_tops, 2),
+                     "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(gu_tops / MFMA_INT8_PEAK_TOPS, 4),
+                     "traffic": traffic_for("i8_gate_up", f"moe_prefill_i8_m{T}"),
+                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3)},
+        "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
+                       "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
+                       "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                       "warm_ms_per_step": round(el_w / max(args.steps // 2, 10) * 1e3, 5)},
+        "kernel_avg_us": kernels,
+        "kernel_avg_us_warm": kernels_w,
+        "_cpu_inputs": None,
+    }
+
+
+# ---------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size (the reference
 # point for the FETCH_SIZE / WRITE_SIZE counters)
 # ---------------------------------------------------------------------------
@@ -516,6 +613,8 @@ WORKLOADS = {
     "rswa": (bench_rswa, None),
     "copy": (bench_copy, None),
     "moe_prefill_i4": (bench_prefill_i4, cpu_prefill_i4),
+    "moe_prefill_i8": (bench_prefill_i8, None),
+    "linear_i8": (bench_linear_i8, None),
 }
 
 
@@ -536,7 +635,7 @@ def main() -> int:
         return 2
     defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
                 "copy": (1, 1),
-                "moe_prefill_i4": (512, 3)}
+                "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

@@ -199,12 +199,15 @@ int32_t focr_hip_qint8_from_device(focr_hip_ctx* ctx, const int8_t* w, const flo
 
 int32_t focr_hip_qint8_free(focr_hip_qint8* w) {
     if (!w) return FOCR_HIP_OK;
-    if (w->owned) {
+    if (w->owned || w->w_mfma) {
         hipSetDevice(w->ctx->device);
         hipStreamSynchronize(w->ctx->stream);
+    }
+    if (w->owned) {
         hipFree(w->w);
         hipFree(w->scales);
     }
+    hipFree(w->w_mfma);
     delete w;
     return FOCR_HIP_OK;
 }
@@ -463,6 +466,7 @@ void free_moe(focr_hip_moe_layer* L) {
         hipFree(L->ssu);
         hipFree(L->ssd);
     }
+    for (int8_t* p : {L->wg_mfma, L->wu_mfma, L->wd_mfma, L->swg_mfma, L->swu_mfma, L->swd_mfma}) hipFree(p);
 }
 
 }  // namespace
@@ -535,6 +539,10 @@ int32_t focr_hip_moe_layer_set_shared(focr_hip_moe_layer* L, size_t shared_inter
         hipFree(L->ssg);
         hipFree(L->ssu);
         hipFree(L->ssd);
+    }
+    for (int8_t** p : {&L->swg_mfma, &L->swu_mfma, &L->swd_mfma}) {  // rebuilt by the next prefill
+        hipFree(*p);
+        *p = nullptr;
     }
     L->shared_inter = shared_inter;
     L->swg = tmp.swg;
@@ -832,6 +840,32 @@ int32_t focr_hip_moe_prefill_i4(focr_hip_ctx* ctx, const focr_hip_moe_layer_i4* 
 
 // ---- prefill: int8 linear and int8 MoE on the matrix cores ------------------------
 
+}  // extern "C"
+
+namespace {
+
+// The fragment-ordered copy of n_mats [n][k] int8 matrices (launch_retile_i8),
+// allocated and written on the context's stream the first time.
+int32_t ensure_tiled(focr_hip_ctx* ctx, int8_t** dst, const int8_t* src, size_t n_mats, size_t n, size_t k,
+                     const char* what) {
+    if (*dst) return FOCR_HIP_OK;
+    const size_t bytes = i8_tiled_bytes((int)n_mats, (int)n, (int)k);
+    int8_t* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess)
+        return fail(FOCR_HIP_E_OOM, fmt("%s: fragment-order copy of %zu bytes", what, bytes));
+    hipError_t e = launch_retile_i8(ctx->stream, src, (int)n_mats, (int)n, (int)k, p);
+    if (e != hipSuccess) {
+        hipFree(p);
+        return hip_fail(e, "retile launch");
+    }
+    *dst = p;
+    return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
                                    const float* bias, float* y) {
     ENGINE_CTX(ctx);
@@ -841,6 +875,8 @@ int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
     if (!i8_mfma_supported(static_cast<int>(w->k)))
         return fail(FOCR_HIP_E_SHAPE,
                     fmt("linear_int8_dynamic: k %zu is not a multiple of 64 (the matrix-core K stage)", w->k));
+    int32_t st = ensure_tiled(ctx, &w->w_mfma, w->w, 1, w->n, w->k, "linear_int8_dynamic");
+    if (st) return st;
     int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
     float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
     if (!xq || !xs) return FOCR_HIP_E_OOM;
@@ -850,7 +886,7 @@ int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
                      "quantize launch");
     }
     ProfScope ps(ctx, "linear_i8");
-    FOCR_HIP_TRY(launch_linear_i8(ctx->stream, xq, xs, (int)m, (int)w->k, w->w, w->scales, (int)w->n, bias, y),
+    FOCR_HIP_TRY(launch_linear_i8(ctx->stream, xq, xs, (int)m, (int)w->k, w->w_mfma, w->scales, (int)w->n, bias, y),
                  "linear_i8 launch");
     return FOCR_HIP_OK;
 }
@@ -870,6 +906,19 @@ int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, 
         return fail(FOCR_HIP_E_SHAPE,
                     fmt("moe_prefill_i8: hidden %zu / inter %zu must be multiples of 64 (the matrix-core K stage)", H,
                         I));
+    int32_t st;
+    const size_t E = L->n_experts;
+    if ((st = ensure_tiled(ctx, &L->wg_mfma, L->wg, E, I, H, "moe_prefill_i8")) ||
+        (st = ensure_tiled(ctx, &L->wu_mfma, L->wu, E, I, H, "moe_prefill_i8")) ||
+        (st = ensure_tiled(ctx, &L->wd_mfma, L->wd, E, H, I, "moe_prefill_i8")))
+        return st;
+    if (with_shared) {
+        const size_t S = L->shared_inter;
+        if ((st = ensure_tiled(ctx, &L->swg_mfma, L->swg, 1, S, H, "moe_prefill_i8")) ||
+            (st = ensure_tiled(ctx, &L->swu_mfma, L->swu, 1, S, H, "moe_prefill_i8")) ||
+            (st = ensure_tiled(ctx, &L->swd_mfma, L->swd, 1, H, S, "moe_prefill_i8")))
+            return st;
+    }
     auto take = [](char*& p, size_t bytes) {
         char* r = p;
         p += (bytes + 255) & ~static_cast<size_t>(255);

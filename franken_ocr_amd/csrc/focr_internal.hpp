@@ -89,6 +89,9 @@ struct focr_hip_qint8 {
     float* scales = nullptr;
     size_t n = 0, k = 0;
     bool owned = false;
+    // the weights in the matrix-core fragment order (launch_retile_i8), built
+    // the first time the handle is used for prefill; always owned
+    mutable int8_t* w_mfma = nullptr;
 };
 
 struct focr_hip_moe_layer {
@@ -103,6 +106,10 @@ struct focr_hip_moe_layer {
     int8_t *swg = nullptr, *swu = nullptr, *swd = nullptr;
     float *ssg = nullptr, *ssu = nullptr, *ssd = nullptr;
     bool shared_owned = false;
+    // fragment-ordered copies for prefill (launch_retile_i8), built on the
+    // first prefill call; always owned
+    mutable int8_t *wg_mfma = nullptr, *wu_mfma = nullptr, *wd_mfma = nullptr;
+    mutable int8_t *swg_mfma = nullptr, *swu_mfma = nullptr, *swd_mfma = nullptr;
 };
 
 struct focr_hip_moe_layer_i4 {
@@ -288,13 +295,21 @@ hipError_t launch_moe_prefill_i4(hipStream_t s, const focr_hip_moe_layer_i4* L, 
                                  focr_hip_ctx* ctx);
 
 // k_i8mfma.hip — int8 x int8 GEMMs on the matrix cores (prefill). K must be
-// a multiple of 64.
+// a multiple of 64. The weights are read in the fragment order that
+// launch_retile_i8 writes: for matrix e of [n_mats][N][K], column tile nt =
+// n / 32 (N padded to a multiple of 32 with zero columns), 32-byte K step ks,
+// half h, column c = n % 32, the 16 bytes k = 32 ks + 16 h + [0, 16) of
+// column n sit at 16-byte unit ((e * NT + nt) * KS + ks) * 64 + 32 h + c, so
+// a wave's fragment load is 1 KB contiguous.
 bool i8_mfma_supported(int k);
+size_t i8_tiled_bytes(int n_mats, int n, int k);
+hipError_t launch_retile_i8(hipStream_t s, const int8_t* src, int n_mats, int n, int k, int8_t* dst);
 // y[m][n] = ((f32)(xq[m] . w[n]) * xs[m]) * ws[n] (+ bias[n]) — nn::linear_int8_dynamic
-// on rows already quantized by the dynamic rule.
+// on rows already quantized by the dynamic rule; w in fragment order.
 hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* w,
                             const float* ws, int n, const float* bias, float* y);
-// act[m][n] = silu(((f32)acc_g * xs[m]) * sg[n]) * (((f32)acc_u * xs[m]) * su[n]).
+// act[m][n] = silu(((f32)acc_g * xs[m]) * sg[n]) * (((f32)acc_u * xs[m]) * su[n]);
+// wg, wu in fragment order.
 hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
                             const float* sg, const int8_t* wu, const float* su, int n, float* act);
 struct MoeI8Scratch {
@@ -311,7 +326,8 @@ struct MoeI8Scratch {
     float* shared_as;
     float* shared_y;    // [t][hidden]
 };
-// moe_block_i8 over the routing idx/gates [t][top_k] (+ the shared expert).
+// moe_block_i8 over the routing idx/gates [t][top_k] (+ the shared expert),
+// on the layer's fragment-ordered copies (moe_prefill_i8_prepare).
 hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, int with_shared, float* out,
                                  MoeI8Scratch& w, focr_hip_ctx* ctx);

@@ -24,15 +24,19 @@
 // v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.
 //
 // Activations: 512-byte K chunks of the tile's 64 rows (32 KB) are staged in
-// LDS with gfx950's direct global -> LDS loads (no VGPRs; two buffers, the
-// next chunk in flight while the current one is consumed). A wave's load
-// writes 1 KB of contiguous LDS (two 512-byte rows), so the 16-byte piece p
-// of row r holds the row's chunk p ^ (r & 15): the 16 rows a quarter-wave's
-// fragment read touches then start on 16 different banks.
-// Weights ([E][N][K], output-channel-major, as uploaded for decode) go global
-// -> VGPR, each lane loading exactly the 16-byte fragments its MFMAs take,
-// four 64-byte K stages ahead; lanes l and l + 32 read adjacent 16 bytes, so
-// a wave reads 64 contiguous bytes of each of its rows per stage.
+// LDS through registers (two buffers; the next chunk's loads are in flight
+// while the current one's 8 stages run, and land in the other buffer at the
+// end), the 16-byte piece p of row r at slot p ^ (r & 15): the 16 rows a
+// quarter-wave's fragment read touches then start on 16 different banks.
+// (Direct global -> LDS loads would save the registers, but the compiler
+// cannot tell the buffer they fill from the one being read and drains every
+// load before each LDS read.)
+// Weights go global -> VGPR, each lane loading exactly the 16-byte fragments
+// its MFMAs take, four 64-byte K stages ahead, from a fragment-ordered copy
+// (launch_retile_i8) made once per handle: a wave's fragment load is then
+// 1 KB contiguous. Read in the upload layout ([E][N][K], output-channel-major,
+// what decode uses), each load touched 32 rows — 32 cache lines — and the
+// L1 address path, not the MFMA, bound the kernel (TA busy 74%, MFMA 12%).
 #include <type_traits>
 
 #include "focr_internal.hpp"
@@ -62,9 +66,9 @@ struct I8Args {
     const float* a_scale;   // scale per A row
     const int* perm;        // MoE: sorted row -> pair id (t * top_k + j); null: direct rows
     int top_k;
-    const int8_t* B0;       // weights [E][N][K]
+    const int8_t* B0;       // weights [E][N][K] in the fragment order of launch_retile_i8
     const float* s0;        // [E][N]
-    const int8_t* B1;       // SwiGLU: up weights
+    const int8_t* B1;       // SwiGLU: up weights (fragment order)
     const float* s1;
     const float* bias;      // linear: [N] or null
     const float* gates;     // down: [pairs]
@@ -72,15 +76,11 @@ struct I8Args {
     int K, N;
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void global_void_t;
-
 // One block tile: rows [r0, r0 + nr) (nr <= 64) of expert e against column
 // block cb. Every thread of the block calls it (it synchronises).
 template <int EPI>
 __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, int cb) {
-    // two chunk buffers as distinct objects, so the compiler can tell reads of
-    // one from the direct loads in flight into the other
+    // two chunk buffers
     __shared__ __align__(16) int8_t lds_a0[BM * KC];
     __shared__ __align__(16) int8_t lds_a1[BM * KC];
     __shared__ int s_arow[BM];
@@ -111,15 +111,17 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
         s_gate[tid] = g;
     }
 
-    // this lane's two weight columns (tile j = 0, 1) and their row pointers
+    // this lane's two weight columns (tile j = 0, 1) and their fragment
+    // streams: 1 KB per (column tile, 32-byte K step), lane l at 16 l
+    const int NT = (N + 31) >> 5, KS = K >> 5;
     int col[2];
     const int8_t* bp[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        col[j] = EPI == kI8Swiglu ? cb * 128 + wave * 32 + c32 : cb * 256 + wave * 64 + 32 * j + c32;
-        const int nc = col[j] < N ? col[j] : N - 1;
+        const int tile = EPI == kI8Swiglu ? cb * 4 + wave : cb * 8 + 2 * wave + j;
+        col[j] = 32 * tile + c32;
         const int8_t* B = (EPI == kI8Swiglu && j == 1) ? a.B1 : a.B0;
-        bp[j] = B + (static_cast<size_t>(e) * N + nc) * K + 16 * h;
+        bp[j] = B + (static_cast<size_t>(e * NT + (tile < NT ? tile : NT - 1)) * KS * 64 + l) * 16;
     }
     // fragments f[2 j + s]: column tile j, K step s of stage st (clamped past the end)
     auto load_b = [&](int st, v4i (&f)[4]) {
@@ -127,7 +129,8 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int s = 0; s < 2; ++s) f[2 * j + s] = *reinterpret_cast<const v4i*>(bp[j] + ss * KB + 32 * s);
+            for (int s = 0; s < 2; ++s)
+                f[2 * j + s] = *reinterpret_cast<const v4i*>(bp[j] + static_cast<size_t>(2 * ss + s) * 1024);
     };
     // a ring of four stages of fragments, stage st in f[st % 4], loaded four
     // stages ahead (SPC = 8 stages per chunk keeps the ring index a constant)
@@ -136,22 +139,29 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
     for (int q = 0; q < 4; ++q) load_b(q, f[q]);
     __syncthreads();  // the row tables
 
-    // Chunk c of the activations into LDS buffer c & 1: wave w's load i covers
-    // rows r0p = 2 (4 i + w) and r0p + 1 (lane l: row r0p + l / 32, piece
-    // l % 32; a direct load lands at the wave-uniform LDS address + 16 l); the
-    // lane at piece p fetches the row's chunk p ^ (row & 15), clamped into the
-    // row past K (never read).
+    // Chunk c of the activations: 64 rows x 32 pieces of 16 bytes; thread tid
+    // loads pieces tid + 256 i (row q / 32, piece q % 32: 32 threads read a
+    // row's 512 contiguous bytes) into registers, and stores piece p of row r
+    // at LDS slot p ^ (r & 15). Pieces past K are clamped into the row (never
+    // read).
     const int nchunks = (K + KC - 1) / KC;
-    auto stage_chunk_dma = [&](int c, int8_t* base) {
+    constexpr int APT = BM * KC / 16 / 256;  // pieces per thread per chunk
+    auto load_chunk = [&](int c, v4i (&v)[APT]) {
 #pragma unroll
-        for (int i = 0; i < BM / 8; ++i) {
-            const int r0p = 2 * (4 * i + wave);  // first row of this load's pair
-            const int r = r0p + h;
-            const int p = c32 ^ (r & 15);
+        for (int i = 0; i < APT; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 5, p = q & 31;
             int kb = c * KC + 16 * p;
             kb = kb < K ? kb : 0;
-            __builtin_amdgcn_global_load_lds((global_void_t*)(a.A + static_cast<size_t>(s_arow[r]) * K + kb),
-                                             (lds_void_t*)(base + r0p * KC), 16, 0, 0);
+            v[i] = *reinterpret_cast<const v4i*>(a.A + static_cast<size_t>(s_arow[r]) * K + kb);
+        }
+    };
+    auto store_chunk = [&](int8_t* base, const v4i (&v)[APT]) {
+#pragma unroll
+        for (int i = 0; i < APT; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 5, p = q & 31;
+            *reinterpret_cast<v4i*>(base + r * KC + 16 * (p ^ (r & 15))) = v[i];
         }
     };
 
@@ -176,24 +186,30 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
     };
 
     static_assert(SPC % 4 == 0, "the fragment ring must divide a chunk's stages");
-    // Chunk c: wait for it, start chunk c + 1 into the other buffer, run its
-    // SPC stages. Stages past K (the last chunk's tail) multiply zeros; their
-    // fragment loads still run (clamped to the last stage), so every stage
-    // issues the same loads and the waits stay exact.
-    auto chunk = [&](int c, const int8_t* buf, int8_t* next) {
-        __syncthreads();  // chunk c has landed; the other buffer is free
-        if (c + 1 < nchunks) stage_chunk_dma(c + 1, next);
+    // Chunk c: its SPC stages from LDS, the next chunk's loads in flight
+    // meanwhile, stored to the other buffer at the end (the last chunk
+    // reloads itself: every iteration is the same straight-line code, which
+    // keeps the compiler's load-count waits exact). Stages past K (the last
+    // chunk's tail) multiply zeros; their fragment loads still run (clamped
+    // to the last stage).
+    v4i av[APT];
+    load_chunk(0, av);
+    store_chunk(lds_a0, av);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int8_t* buf = (c & 1) ? lds_a1 : lds_a0;
+        int8_t* next = (c & 1) ? lds_a0 : lds_a1;
+        load_chunk(c + 1 < nchunks ? c + 1 : c, av);
 #pragma unroll
         for (int ls = 0; ls < SPC; ++ls) {
             const int st = c * SPC + ls;
             compute(buf, ls, f[ls % 4], st < S);
+            __builtin_amdgcn_sched_barrier(0);  // keep each stage's refill after its MFMAs
             load_b(st + 4, f[ls % 4]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-    };
-    stage_chunk_dma(0, lds_a0);
-    for (int c = 0; c < nchunks; c += 2) {
-        chunk(c, lds_a0, lds_a1);
-        if (c + 1 < nchunks) chunk(c + 1, lds_a1, lds_a0);
+        store_chunk(next, av);
+        __syncthreads();  // chunk c + 1 is in LDS; chunk c's buffer is free
     }
 
     // epilogue
@@ -267,9 +283,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     i8_tile<EPI>(a, e, tile_r0[tile], tile_nr[tile], cb);
 }
 
+// One thread per 16-byte destination unit d = ((e * NT + nt) * KS + ks) * 64
+// + 32 h + c: column n = 32 nt + c of matrix e, bytes 32 ks + 16 h; zero for
+// the padding columns n >= N.
+__global__ __launch_bounds__(256) void retile_i8_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst,
+                                                        size_t units, int N, int K) {
+    const size_t d = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (d >= units) return;
+    const int NT = (N + 31) >> 5, KS = K >> 5;
+    const int c = static_cast<int>(d & 31);
+    const int h = static_cast<int>((d >> 5) & 1);
+    size_t r = d >> 6;
+    const int ks = static_cast<int>(r % KS);
+    r /= KS;
+    const int nt = static_cast<int>(r % NT);
+    const size_t e = r / NT;
+    const int n = 32 * nt + c;
+    v4i v = {0, 0, 0, 0};
+    if (n < N) v = *reinterpret_cast<const v4i*>(src + (e * N + n) * K + 32 * ks + 16 * h);
+    reinterpret_cast<v4i*>(dst)[d] = v;
+}
+
 }  // namespace
 
 bool i8_mfma_supported(int k) { return k > 0 && k % KB == 0 && k <= 65536; }
+
+size_t i8_tiled_bytes(int n_mats, int n, int k) {
+    return static_cast<size_t>(n_mats) * static_cast<size_t>((n + 31) & ~31) * static_cast<size_t>(k);
+}
+
+hipError_t launch_retile_i8(hipStream_t s, const int8_t* src, int n_mats, int n, int k, int8_t* dst) {
+    if (k % 32 || n <= 0 || n_mats <= 0) return hipErrorInvalidValue;
+    const size_t units = i8_tiled_bytes(n_mats, n, k) / 16;
+    FOCR_LAUNCH(retile_i8_kernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0, s, src, dst, units,
+                n, k);
+    return hipGetLastError();
+}
 
 hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* w,
                             const float* ws, int n, const float* bias, float* y) {
@@ -313,7 +362,7 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     };
     {
         ProfScope ps(ctx, "i8_gate_up");
-        const I8Args a{w.xq, w.xs, p.perm, top_k, L->wg, L->sg, L->wu, L->su, nullptr, nullptr, w.act, H, I};
+        const I8Args a{w.xq, w.xs, p.perm, top_k, L->wg_mfma, L->sg, L->wu_mfma, L->su, nullptr, nullptr, w.act, H, I};
         if ((e = grouped(std::integral_constant<int, kI8Swiglu>(), a)) != hipSuccess) return e;
     }
     {
@@ -322,19 +371,19 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     }
     {
         ProfScope ps(ctx, "i8_down");
-        const I8Args a{w.aq, w.as, p.perm, top_k, L->wd, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
+        const I8Args a{w.aq, w.as, p.perm, top_k, L->wd_mfma, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
         if ((e = grouped(std::integral_constant<int, kI8Down>(), a)) != hipSuccess) return e;
     }
     if (with_shared) {
         const int SI = static_cast<int>(L->shared_inter);
         ProfScope ps(ctx, "i8_shared");
-        if ((e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg, L->ssg, L->swu, L->ssu, SI, w.shared_act)) !=
+        if ((e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg_mfma, L->ssg, L->swu_mfma, L->ssu, SI, w.shared_act)) !=
             hipSuccess)
             return e;
         if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
             hipSuccess)
             return e;
-        if ((e = launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd, L->ssd, H, nullptr, w.shared_y)) !=
+        if ((e = launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd_mfma, L->ssd, H, nullptr, w.shared_y)) !=
             hipSuccess)
             return e;
     }
