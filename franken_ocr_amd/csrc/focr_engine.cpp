@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -648,10 +649,15 @@ int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const
     return check_route_flags(ctx, s.flag, t);
 }
 
-int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
-                            int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
-                            float* gates, int32_t check_route) {
-    ENGINE_CTX(ctx);
+}  // extern "C"
+
+namespace {
+
+// decode_mlp_i8 over t rows; with resid non-null, out = resid + the layer's
+// output (the decode layer's residual, decoder.rs:2625).
+int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                        int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
+                        float* gates, int32_t check_route, const float* resid) {
     int32_t st = moe_checks("moe_decode", L, hidden, t, with_shared);
     if (st) return st;
     if (!out) return fail(FOCR_HIP_E_ARG, "moe_decode: null out");
@@ -686,16 +692,28 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
         }
         if (e == hipSuccess) {
             ProfScope ps(ctx, "moe_combine");
-            e = launch_moe_combine(str, d, s.ybuf, s.flag, with_shared ? s.shared_y : nullptr, out);
+            e = launch_moe_combine(str, d, s.ybuf, s.flag, with_shared ? s.shared_y : nullptr, resid, out);
         }
     } else if (e == hipSuccess) {
         ProfScope ps(ctx, "moe_down_combine");
         e = launch_moe_down_combine(str, d, di, dg, s.flag, s.act, L->wd, L->sd, with_shared ? s.shared_y : nullptr,
-                                    out, (int)L->inter);
+                                    resid, out, (int)L->inter);
     }
     if (e != hipSuccess) return hip_fail(e, "moe_decode launch");
     if (check_route) return check_route_flags(ctx, s.flag, t);
     return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                            int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
+                            float* gates, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    return moe_decode_impl(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
+                           nullptr);
 }
 
 // ---- int4 MoE layer (chunked prefill) ------------------------------------------
@@ -1104,6 +1122,176 @@ int32_t focr_hip_rswa_step(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* q, 
     int32_t st = rswa_write_all(ctx, c, k_steps, v_steps, nullptr);
     if (st) return st;
     return rswa_attend_all(ctx, c, q, out);
+}
+
+// ---- one decoder layer's decode step (decoder.rs:2542-2627, :2812-2933) --------
+
+int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n_heads, size_t head_dim,
+                                      const float* input_ln, const float* post_attn_ln, const focr_hip_qint8* qkv,
+                                      const focr_hip_qint8* o_proj, const focr_hip_moe_layer* moe,
+                                      const focr_hip_qint8* dense_gate, const focr_hip_qint8* dense_up,
+                                      const focr_hip_qint8* dense_down, float rms_eps, float rope_theta,
+                                      focr_hip_decoder_layer** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "decoder_layer_create: null out");
+    *out = nullptr;
+    if (!input_ln || !post_attn_ln || !qkv || !o_proj)
+        return fail(FOCR_HIP_E_ARG, "decoder_layer_create: null norm weight or projection");
+    const bool dense = dense_gate || dense_up || dense_down;
+    if ((moe != nullptr) == dense || (dense && !(dense_gate && dense_up && dense_down)))
+        return fail(FOCR_HIP_E_ARG, "decoder_layer_create: exactly one of moe or (dense_gate, dense_up, dense_down)");
+    const size_t D = n_heads * head_dim;
+    if (hidden == 0 || hidden > 4096 || hidden % 64 || head_dim % 2 || D == 0 || D % 16 ||
+        qkv->n != 3 * D || qkv->k != hidden || o_proj->n != hidden || o_proj->k != D)
+        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_layer_create: qkv [%zu, %zu] / o_proj [%zu, %zu] do not match "
+                                          "hidden %zu, heads %zu x %zu",
+                                          qkv->n, qkv->k, o_proj->n, o_proj->k, hidden, n_heads, head_dim));
+    if (moe && moe->hidden != hidden)
+        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_layer_create: moe hidden %zu != %zu", moe->hidden, hidden));
+    if (dense && (dense_gate->k != hidden || dense_up->k != hidden || dense_up->n != dense_gate->n ||
+                  dense_down->n != hidden || dense_down->k != dense_gate->n))
+        return fail(FOCR_HIP_E_SHAPE, "decoder_layer_create: dense gate/up [i, hidden], down [hidden, i] expected");
+    auto* L = new focr_hip_decoder_layer();
+    L->ctx = ctx;
+    L->hidden = hidden;
+    L->n_heads = n_heads;
+    L->head_dim = head_dim;
+    L->eps = rms_eps;
+    L->qkv = qkv;
+    L->o_proj = o_proj;
+    L->moe = moe;
+    L->gate = dense_gate;
+    L->up = dense_up;
+    L->down = dense_down;
+    // RopeTable::build's table (decoder.rs:197-205): f64 pow, narrowed to f32
+    std::vector<float> inv(head_dim / 2);
+    for (size_t i = 0; i < inv.size(); ++i)
+        inv[i] = static_cast<float>(1.0 / std::pow(static_cast<double>(rope_theta),
+                                                   static_cast<double>(2 * i) / static_cast<double>(head_dim)));
+    hipError_t e = hipMalloc(&L->input_ln, hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&L->post_ln, hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&L->inv_freq, inv.size() * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(L->input_ln, input_ln, hidden * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L->post_ln, post_attn_ln, hidden * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L->inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(L->input_ln);
+        hipFree(L->post_ln);
+        hipFree(L->inv_freq);
+        delete L;
+        return hip_fail(e, "decoder_layer_create upload");
+    }
+    *out = L;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* L) {
+    if (!L) return FOCR_HIP_OK;
+    hipSetDevice(L->ctx->device);
+    hipStreamSynchronize(L->ctx->stream);
+    hipFree(L->input_ln);
+    hipFree(L->post_ln);
+    hipFree(L->inv_freq);
+    delete L;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+                                    const uint32_t* positions, float* x, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null layer");
+    if (!cache) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null rswa cache");
+    if (!positions || !x) return fail(FOCR_HIP_E_ARG, "decoder_layer_step: null positions or x");
+    const size_t B = cache->n_streams, H = L->hidden, D = L->n_heads * L->head_dim;
+    if (L->n_heads != 10 || L->head_dim != 128)
+        return fail(FOCR_HIP_E_SHAPE, "decoder_layer_step: the R-SWA cache holds 10 heads x 128");
+    const size_t max_b = L->gate ? std::min<size_t>(32, 57344 / L->gate->n) : 32;
+    if (B < 1 || B > max_b)
+        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_layer_step: %zu streams outside 1..=%zu", B, max_b));
+    const size_t I = L->gate ? L->gate->n : 0;
+    // one scratch slot carved into the step's intermediates
+    const size_t fl = B * (3 * D + 3 * D + D + H + H + H) + (L->gate ? 3 * B * I : 0);
+    char* base = static_cast<char*>(ctx->scratch_get(kScrLayer, fl * 4 + B * H + B * I + 16 * 256));
+    if (!base) return FOCR_HIP_E_OOM;
+    auto take = [&](size_t bytes) {
+        char* r = base;
+        base += (bytes + 255) & ~static_cast<size_t>(255);
+        return r;
+    };
+    float* qkv = reinterpret_cast<float*>(take(B * 3 * D * 4));
+    float* q = reinterpret_cast<float*>(take(B * D * 4));
+    float* k = reinterpret_cast<float*>(take(B * D * 4));
+    float* v = reinterpret_cast<float*>(take(B * D * 4));
+    float* cx = reinterpret_cast<float*>(take(B * D * 4));
+    float* attn = reinterpret_cast<float*>(take(B * H * 4));
+    float* h = reinterpret_cast<float*>(take(B * H * 4));
+    float* nrm = reinterpret_cast<float*>(take(B * H * 4));
+    int8_t* xq = reinterpret_cast<int8_t*>(take(B * (H > D ? H : D)));
+    float* xs = reinterpret_cast<float*>(take(B * 4));
+    uint32_t* dpos = reinterpret_cast<uint32_t*>(take(B * 4));
+    hipStream_t s = ctx->stream;
+    // 1. input RMSNorm + quantize_row_i8; 2. the fused qkv GEMV
+    {
+        ProfScope ps(ctx, "layer_norm_quant");
+        FOCR_HIP_TRY(launch_rms_norm_quant(s, x, L->input_ln, (int)B, (int)H, L->eps, xq, xs), "rms_norm launch");
+    }
+    {
+        ProfScope ps(ctx, "layer_qkv");
+        FOCR_HIP_TRY(launch_gemv_i8(s, L->qkv->w, L->qkv->scales, (int)(3 * D), (int)H, xq, xs, (int)B, qkv, nullptr,
+                                    nullptr, nullptr, ctx->cu_count),
+                     "qkv gemv launch");
+    }
+    // 3. RoPE at each stream's position, ring write, attention
+    FOCR_HIP_TRY(hipMemcpyAsync(dpos, positions, B * 4, hipMemcpyHostToDevice, s), "positions H2D");
+    {
+        ProfScope ps(ctx, "layer_rope");
+        FOCR_HIP_TRY(launch_rope_split(s, qkv, dpos, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, k, v),
+                     "rope launch");
+    }
+    int32_t st = rswa_write_all(ctx, cache, k, v, nullptr);
+    if (st) return st;
+    if ((st = rswa_attend_all(ctx, cache, q, cx))) return st;
+    // 4. o_proj; 5. residual + post-attention RMSNorm
+    {
+        ProfScope ps(ctx, "layer_o_quant");
+        FOCR_HIP_TRY(launch_quantize_rows(s, cx, (int)B, (int)D, xq, xs, 0), "quantize launch");
+    }
+    {
+        ProfScope ps(ctx, "layer_o_proj");
+        FOCR_HIP_TRY(launch_gemv_i8(s, L->o_proj->w, L->o_proj->scales, (int)H, (int)D, xq, xs, (int)B, attn, nullptr,
+                                    nullptr, nullptr, ctx->cu_count),
+                     "o_proj gemv launch");
+    }
+    {
+        ProfScope ps(ctx, "layer_residual_norm");
+        FOCR_HIP_TRY(launch_residual_rms_norm(s, x, attn, L->post_ln, (int)B, (int)H, L->eps, h, nrm),
+                     "residual rms_norm launch");
+    }
+    // 6. decode_mlp_i8 (decoder.rs:2199-2268) and the residual
+    if (L->moe) {
+        // route_default (moe.rs:53-76: norm_topk_prob false, scaling 1.0) + the shared expert
+        return moe_decode_impl(ctx, L->moe, nrm, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, nullptr, nullptr, check_route, h);
+    }
+    // dense (layer 0): expert_gemv_i8 (decoder.rs:1711-1720)
+    float* g = reinterpret_cast<float*>(take(B * I * 4));
+    float* u = reinterpret_cast<float*>(take(B * I * 4));
+    float* act = reinterpret_cast<float*>(take(B * I * 4));
+    int8_t* aq = reinterpret_cast<int8_t*>(take(B * I));
+    ProfScope ps(ctx, "layer_dense_mlp");
+    FOCR_HIP_TRY(launch_quantize_rows(s, nrm, (int)B, (int)H, xq, xs, 0), "quantize launch");
+    FOCR_HIP_TRY(launch_gemv_i8(s, L->gate->w, L->gate->scales, (int)I, (int)H, xq, xs, (int)B, g, nullptr, nullptr,
+                                nullptr, ctx->cu_count),
+                 "dense gate launch");
+    FOCR_HIP_TRY(launch_gemv_i8(s, L->up->w, L->up->scales, (int)I, (int)H, xq, xs, (int)B, u, nullptr, nullptr,
+                                nullptr, ctx->cu_count),
+                 "dense up launch");
+    FOCR_HIP_TRY(launch_silu_mul(s, g, u, act, B * I), "silu launch");
+    FOCR_HIP_TRY(launch_quantize_rows(s, act, (int)B, (int)I, aq, xs, 0), "quantize launch");
+    FOCR_HIP_TRY(launch_gemv_i8(s, L->down->w, L->down->scales, (int)H, (int)I, aq, xs, (int)B, attn, nullptr, nullptr,
+                                nullptr, ctx->cu_count),
+                 "dense down launch");
+    FOCR_HIP_TRY(launch_add_rows(s, h, attn, x, B * H), "residual launch");
+    return FOCR_HIP_OK;
 }
 
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,

@@ -50,6 +50,7 @@ enum ScratchSlot : int {
     kScrI4b,
     kScrFlag,   // device status flags
     kScrBan,    // sampler ban bitmaps
+    kScrLayer,  // decoder layer step intermediates
     kScrCount
 };
 
@@ -110,6 +111,22 @@ struct focr_hip_moe_layer {
     // first prefill call; always owned
     mutable int8_t *wg_mfma = nullptr, *wu_mfma = nullptr, *wd_mfma = nullptr;
     mutable int8_t *swg_mfma = nullptr, *swu_mfma = nullptr, *swd_mfma = nullptr;
+};
+
+// One decoder layer for decode steps (decoder.rs:1971-1982 CachedLayerI8):
+// borrowed weight handles, device copies of the two RMSNorm weights and the
+// RoPE inverse frequencies.
+struct focr_hip_decoder_layer {
+    focr_hip_ctx* ctx = nullptr;
+    size_t hidden = 0, n_heads = 0, head_dim = 0;
+    float eps = 1e-6f;
+    float* input_ln = nullptr;   // [hidden]
+    float* post_ln = nullptr;    // [hidden]
+    float* inv_freq = nullptr;   // [head_dim / 2]
+    const focr_hip_qint8* qkv = nullptr;   // [3 * n_heads * head_dim, hidden]
+    const focr_hip_qint8* o_proj = nullptr;  // [hidden, n_heads * head_dim]
+    const focr_hip_moe_layer* moe = nullptr;  // MoE MLP, or the dense one below
+    const focr_hip_qint8 *gate = nullptr, *up = nullptr, *down = nullptr;
 };
 
 struct focr_hip_moe_layer_i4 {
@@ -221,9 +238,10 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, 
 hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
                            const float* sd, float* ybuf, int inter, bool shared);
 // out[t] = slot-order sum of ybuf[t*top_k + j] (+ shared_y[t]); zero for a
-// token whose flag is set. Follows launch_moe_down over the routed experts.
+// token whose flag is set; then resid[t] + that when resid is non-null (the
+// decode layer's residual). Follows launch_moe_down over the routed experts.
 hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const int* flag,
-                              const float* shared_y, float* out);
+                              const float* shared_y, const float* resid, float* out);
 // Tokens per step from which the decode layer runs the expert-grouped down
 // kernel (each down row read once per step) + combine instead of down +
 // combine per token (each down row read once per token that routes to it).
@@ -234,7 +252,19 @@ constexpr int kMoeGroupedDownT = 40;
 // gates / flag ([t][top_k]) and the act rows of every pair (t*top_k + j).
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
                                    const int* flag, const float* act, const int8_t* wd, const float* sd,
-                                   const float* shared_y, float* out, int inter);
+                                   const float* shared_y, const float* resid, float* out, int inter);
+// k_layer.hip — the decode layer's ops around the GEMVs / attention / MoE.
+// xq, xs = quantize_row_i8(rms_norm(x) * w) per row (n <= 4096).
+hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, int rows, int n, float eps,
+                                 int8_t* xq, float* xs);
+// h = x + a; y = rms_norm(h) * w per row.
+hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
+                                    float eps, float* h, float* y);
+// Split fused qkv rows [streams][3 D] into q, k (RoPE at pos[stream]) and v.
+hipError_t launch_rope_split(hipStream_t s, const float* qkv, const uint32_t* pos, const float* inv_freq, int streams,
+                             int n_heads, int head_dim, float* q, float* k, float* v);
+hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n);
+hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n);
 // k_int4.hip
 hipError_t launch_s4s8_packed(hipStream_t s, const int8_t* a, const uint8_t* b,
                               const float* scales, int group, int m, int k, int n, float* out,

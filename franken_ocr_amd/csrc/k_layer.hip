@@ -1,0 +1,167 @@
+// k_layer.hip — the decode layer's small ops around the GEMVs, attention and
+// MoE kernels (decode_step_with_cache_i8, decoder.rs:2542-2627; batched form
+// batched_decode_step_i8_streams, :2812-2933):
+//
+//   * RMSNorm of each row (nn::rms_norm, nn.rs:240-253), either fused with
+//     quantize_row_i8 of the normed row for the qkv GEMV (the reference's
+//     FOCR_FUSE_NORM_QUANT form, byte-identical to norm-then-quantize,
+//     decoder.rs:1680-1706), or fused with the residual add before it
+//     (add_residual, decoder.rs:529-546, then the post-attention norm);
+//   * RoPE of q and k at each stream's own position (RopeTable::build +
+//     apply_rope, decoder.rs:150-268), splitting the fused qkv row into the
+//     contiguous q / k / v rows the ring write and attention take;
+//   * a row-wise add (the dense MLP's residual).
+//
+// RMSNorm arithmetic (ft-kernel-cpu's rms_norm_forward_f32 is not in the
+// reference tree, so this build fixes it): the sum of squares in f64,
+// rstd = (float)(1 / sqrt(ss / n + eps)) in f64, y = (x * rstd) * w in f32.
+#include "focr_internal.hpp"
+#include "k_common.hpp"
+
+namespace focr {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Sum of (double)v^2 over a row by the whole block; every thread gets it.
+__device__ __forceinline__ double block_sum_sq(const float* __restrict__ r, int n, double* red) {
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const double v = static_cast<double>(r[i]);
+        ss = fma(v, v, ss);
+    }
+    ss = wave_sum_d(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+    return t;
+}
+
+// MODE 0: y = rms_norm(x) * w, then quantize_row_i8 (half away) -> xq, xs.
+// MODE 1: h = x + a (written), y = rms_norm(h) * w (written, f32).
+// One block per row; n <= 4096 (the row is staged in LDS).
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ a,
+                                                                 const float* __restrict__ w, int n, float eps,
+                                                                 float* __restrict__ h, float* __restrict__ y,
+                                                                 int8_t* __restrict__ xq, float* __restrict__ xs) {
+    __shared__ float s_row[4096];
+    __shared__ double s_red[kThreads / 64];
+    __shared__ float s_max[kThreads / 64];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        float v = x[base + i];
+        if (MODE == 1) {
+            v = v + a[base + i];
+            h[base + i] = v;
+        }
+        s_row[i] = v;
+    }
+    __syncthreads();
+    const double ss = block_sum_sq(s_row, n, s_red);
+    const float rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
+    if (MODE == 1) {
+        for (int i = threadIdx.x; i < n; i += kThreads) y[base + i] = (s_row[i] * rstd) * w[i];
+        return;
+    }
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = (s_row[i] * rstd) * w[i];
+        s_row[i] = v;  // each thread rewrites only its own elements
+        amax = fmaxf(amax, fabsf(v));
+    }
+    amax = wave_max_f(amax);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = s_max[0];
+#pragma unroll
+    for (int wv = 1; wv < kThreads / 64; ++wv) amax = fmaxf(amax, s_max[wv]);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+    for (int i = threadIdx.x; i < n; i += kThreads) xq[base + i] = quant_i8(s_row[i], inv, false);
+    if (threadIdx.x == 0) xs[blockIdx.x] = a_scale;
+}
+
+// One block per stream: the fused row qkv [3D] -> q, k rotated at pos[s]
+// (inv_freq [half], the reference's f64-then-f32 table) and v copied, each
+// [D] contiguous. Thread = (head, i < half) pairs.
+__global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __restrict__ qkv,
+                                                              const uint32_t* __restrict__ pos,
+                                                              const float* __restrict__ inv_freq, int n_heads,
+                                                              int head_dim, float* __restrict__ q,
+                                                              float* __restrict__ k, float* __restrict__ v) {
+    const int s = blockIdx.x;
+    const int D = n_heads * head_dim;
+    const int half = head_dim >> 1;
+    const float* row = qkv + static_cast<size_t>(s) * 3 * D;
+    const float p = static_cast<float>(pos[s]);
+    for (int t = threadIdx.x; t < n_heads * half; t += kThreads) {
+        const int hd = t / half, i = t - hd * half;
+        const float angle = p * inv_freq[i];
+        const float sn = sinf(angle), cs = cosf(angle);
+        const int j0 = hd * head_dim + i, j1 = j0 + half;
+        const float qa = row[j0], qb = row[j1];
+        const float ka = row[D + j0], kb = row[D + j1];
+        q[static_cast<size_t>(s) * D + j0] = qa * cs - qb * sn;
+        q[static_cast<size_t>(s) * D + j1] = qb * cs + qa * sn;
+        k[static_cast<size_t>(s) * D + j0] = ka * cs - kb * sn;
+        k[static_cast<size_t>(s) * D + j1] = kb * cs + ka * sn;
+    }
+    for (int j = threadIdx.x; j < D; j += kThreads) v[static_cast<size_t>(s) * D + j] = row[2 * D + j];
+}
+
+// act = silu(g) * u (decoder.rs:1746-1752), the dense MLP's SwiGLU.
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                            float* __restrict__ act, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) act[i] = silu_f(g[i]) * u[i];
+}
+
+__global__ __launch_bounds__(kThreads) void add_rows_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                            float* __restrict__ out, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, int rows, int n, float eps,
+                                 int8_t* xq, float* xs) {
+    if (n > 4096 || rows < 1) return hipErrorInvalidValue;
+    FOCR_LAUNCH(rms_norm_rows_kernel<0>, dim3(rows), dim3(kThreads), 0, s, x, nullptr, w, n, eps, nullptr, nullptr,
+                xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
+                                    float eps, float* h, float* y) {
+    if (n > 4096 || rows < 1) return hipErrorInvalidValue;
+    FOCR_LAUNCH(rms_norm_rows_kernel<1>, dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, nullptr,
+                nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_split(hipStream_t s, const float* qkv, const uint32_t* pos, const float* inv_freq, int streams,
+                             int n_heads, int head_dim, float* q, float* k, float* v) {
+    if (head_dim % 2 || streams < 1) return hipErrorInvalidValue;
+    FOCR_LAUNCH(rope_split_kernel, dim3(streams), dim3(kThreads), 0, s, qkv, pos, inv_freq, n_heads, head_dim, q, k,
+                v);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n) {
+    FOCR_LAUNCH(silu_mul_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g,
+                u, act, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n) {
+    FOCR_LAUNCH(add_rows_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, a,
+                b, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace focr

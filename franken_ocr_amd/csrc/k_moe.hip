@@ -537,7 +537,8 @@ template <int LPR, int JC>
 __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     const uint32_t* __restrict__ idx, const float* __restrict__ gates, const int* __restrict__ flag, int T, int K,
     const float* __restrict__ act, const int8_t* __restrict__ wd, const float* __restrict__ sd,
-    const float* __restrict__ shared_y, float* __restrict__ out, int H, int I, int E) {
+    const float* __restrict__ shared_y, const float* __restrict__ resid, float* __restrict__ out, int H, int I,
+    int E) {
     extern __shared__ int4 lds_q[];  // [K][I/16] quantized act rows of token t
     __shared__ float s_as[kMaxK];
     __shared__ float s_y[DC_THREADS / LPR];
@@ -630,6 +631,7 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
                 for (int jj = 0; jj < K; ++jj) o += s_y[threadIdx.x * K + jj];
                 if (shared_y) o += shared_y[static_cast<size_t>(t) * H + rr];
             }
+            if (resid) o = resid[static_cast<size_t>(t) * H + rr] + o;  // h + mlp_out (decoder.rs:2625)
             out[static_cast<size_t>(t) * H + rr] = o;
         }
     }
@@ -641,7 +643,8 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
 // down + combine kernel; a token whose routing failed (flag) combines to zero.
 // Thread = 4 consecutive columns of one token.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ybuf, const int* __restrict__ flag,
-                                                          const float* __restrict__ shared_y, float* __restrict__ out,
+                                                          const float* __restrict__ shared_y,
+                                                          const float* __restrict__ resid, float* __restrict__ out,
                                                           int K, int H) {
     const int t = blockIdx.y;
     const int c4 = blockIdx.x * 256 + static_cast<int>(threadIdx.x);
@@ -662,6 +665,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
             o.z += y.z;
             o.w += y.w;
         }
+    }
+    if (resid) {  // the layer's residual: h + mlp_out (decoder.rs:2625)
+        const float4 r = reinterpret_cast<const float4*>(resid + static_cast<size_t>(t) * H)[c4];
+        o = make_float4(r.x + o.x, r.y + o.y, r.z + o.z, r.w + o.w);
     }
     reinterpret_cast<float4*>(out + static_cast<size_t>(t) * H)[c4] = o;
 }
@@ -778,16 +785,16 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, con
 }
 
 hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf, const int* flag,
-                              const float* shared_y, float* out) {
+                              const float* shared_y, const float* resid, float* out) {
     if (!dims_ok(d) || d.hidden % 4 != 0) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>((d.hidden / 4 + 255) / 256), static_cast<unsigned>(d.t));
-    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, flag, shared_y, out, d.top_k, d.hidden);
+    FOCR_LAUNCH(moe_combine_kernel, grid, dim3(256), 0, s, ybuf, flag, shared_y, resid, out, d.top_k, d.hidden);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
                                    const int* flag, const float* act, const int8_t* wd, const float* sd,
-                                   const float* shared_y, float* out, int inter) {
+                                   const float* shared_y, const float* resid, float* out, int inter) {
     int lpr, jc;
     pick_lpr(inter, &lpr, &jc);
     if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
@@ -798,7 +805,7 @@ hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32
 #define FOCR_DC(L, J)                                                                                             \
     if (lpr == L && jc == J) {                                                                                   \
         FOCR_LAUNCH((moe_down_combine_kernel<L, J>), grid, dim3(DC_THREADS), lds, s, idx, gates, flag, d.t,      \
-                    d.top_k, act, wd, sd, shared_y, out, d.hidden, inter, d.n_experts);                          \
+                    d.top_k, act, wd, sd, shared_y, resid, out, d.hidden, inter, d.n_experts);                   \
         return hipGetLastError();                                                                                \
     }
     FOCR_DC(8, 1) FOCR_DC(8, 2) FOCR_DC(8, 3) FOCR_DC(8, 4) FOCR_DC(8, 5) FOCR_DC(8, 6) FOCR_DC(8, 7) FOCR_DC(8, 8)

@@ -347,3 +347,46 @@ class RingCache:
             self.free()
         except Exception:
             pass
+
+
+class DecoderLayer:
+    """One decoder layer for decode steps (decoder.rs:2542-2627 per stream,
+    :2812-2933 batched): input RMSNorm, fused qkv GEMV, RoPE, ring write +
+    R-SWA attention, o_proj, residual, post-attention RMSNorm, the MoE layer
+    (route_default + its shared expert) or the dense SwiGLU MLP, residual.
+
+    Borrows the weight handles (kept alive by this object); input_ln and
+    post_ln are host f32 [hidden]."""
+
+    def __init__(self, hidden: int, input_ln, post_ln, qkv: QInt8, o_proj: QInt8, moe: MoeLayer | None = None,
+                 dense: tuple[QInt8, QInt8, QInt8] | None = None, n_heads: int = 10, head_dim: int = 128,
+                 eps: float = 1e-6, rope_theta: float = 10000.0, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.hidden = int(hidden)
+        self._keep = (qkv, o_proj, moe, dense)
+        self._h = C.c_void_p()
+        ln1 = np.ascontiguousarray(input_ln, dtype=np.float32)
+        ln2 = np.ascontiguousarray(post_ln, dtype=np.float32)
+        g, u, d = dense if dense is not None else (None, None, None)
+        _abi.call("focr_hip_decoder_layer_create", self.ctx.handle, self.hidden, int(n_heads), int(head_dim),
+                  ln1.ctypes.data_as(C.c_void_p), ln2.ctypes.data_as(C.c_void_p), qkv.handle, o_proj.handle,
+                  moe._h if moe is not None else None, g.handle if g else None, u.handle if u else None,
+                  d.handle if d else None, float(eps), float(rope_theta), C.byref(self._h))
+
+    def step(self, cache: "RingCache", positions, x: DeviceArray, check_route: bool = True) -> None:
+        """x [n_streams, hidden] (device) updated in place; positions: each
+        stream's absolute position."""
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        _abi.call("focr_hip_decoder_layer_step", self.ctx.handle, self._h, cache._h, pos.ctypes.data_as(C.c_void_p),
+                  x.c_ptr, 1 if check_route else 0)
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_decoder_layer_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass

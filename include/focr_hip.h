@@ -61,6 +61,7 @@ typedef struct focr_hip_ctx focr_hip_ctx;
 typedef struct focr_hip_qint8 focr_hip_qint8;
 typedef struct focr_hip_moe_layer focr_hip_moe_layer;
 typedef struct focr_hip_moe_layer_i4 focr_hip_moe_layer_i4;
+typedef struct focr_hip_decoder_layer focr_hip_decoder_layer;
 typedef struct focr_hip_rswa focr_hip_rswa;
 typedef struct focr_hip_focrq focr_hip_focrq;
 typedef struct focr_hip_focrq_writer focr_hip_focrq_writer;
@@ -343,6 +344,34 @@ int32_t focr_hip_rswa_set_state(focr_hip_rswa* cache, size_t stream, uint32_t ri
 /* Device pointers of one stream's regions (for direct fills/readback). */
 int32_t focr_hip_rswa_regions(const focr_hip_rswa* cache, size_t stream, float** ref_k,
                               float** ref_v, float** ring_k, float** ring_v);
+
+/* ---- one decoder layer's decode step -------------------------------------
+ * decoder.rs:2812-2933 batched_decode_step_i8_streams for one layer over every
+ * stream of an R-SWA cache (decode_step_with_cache_i8, :2542-2627, per
+ * stream): input RMSNorm + quantize_row_i8, the fused qkv GEMV [3 D, hidden],
+ * RoPE at each stream's position (RopeTable::build + apply_rope, :150-268),
+ * the ring write and decode attention, o_proj [hidden, D], h = x + attn,
+ * post-attention RMSNorm, decode_mlp_i8 (:2199-2268: the MoE layer with
+ * route_default — norm_topk_prob false, scaling 1.0 — plus its shared expert
+ * when one is set, or the dense SwiGLU MLP of layer 0), x = h + mlp.
+ * RMSNorm: y = (x * rstd) * w, rstd from the f64 mean of squares + eps.
+ * The layer borrows the weight handles (they must outlive it) and copies the
+ * two norm weights (host pointers, [hidden]). Exactly one of moe or the three
+ * dense handles. D = n_heads * head_dim must be 10 x 128 for the cache. */
+int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n_heads, size_t head_dim,
+                                      const float* input_ln, const float* post_attn_ln,
+                                      const focr_hip_qint8* qkv, const focr_hip_qint8* o_proj,
+                                      const focr_hip_moe_layer* moe, const focr_hip_qint8* dense_gate,
+                                      const focr_hip_qint8* dense_up, const focr_hip_qint8* dense_down,
+                                      float rms_eps, float rope_theta, focr_hip_decoder_layer** out);
+int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* layer);
+/* x [n_streams, hidden] f32 device, updated in place; positions [n_streams]
+ * host (each stream's absolute position, SPEC-095). With check_route = 1 a
+ * MoE layer synchronises and returns E_ROUTE for a row with no finite router
+ * score. n_streams <= 32 (<= 8 for the 6848-wide dense MLP). */
+int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
+                                    focr_hip_rswa* cache, const uint32_t* positions, float* x,
+                                    int32_t check_route);
 
 /* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
  * The reader restates weights.rs:443-620 (format detection by magic, the

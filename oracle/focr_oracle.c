@@ -574,6 +574,36 @@ int oracle_moe_prefill_i4(const float* x, size_t t, size_t h, size_t inter, size
     return ORACLE_OK;
 }
 
+/* ---- decode-layer ops: nn::rms_norm and RoPE ------------------------------- */
+void oracle_rms_norm(const float* x, size_t n, const float* w, float eps, float* y) {
+    double ss = 0.0;
+    for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    const float rstd = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+    for (size_t i = 0; i < n; ++i) {
+        float v = x[i] * rstd;
+        y[i] = w ? v * w[i] : v;
+    }
+}
+
+/* decoder.rs:170-227 RopeTable::build (one position), :229-268 apply_rope. */
+int oracle_rope(float* x, size_t n_heads, size_t head_dim, size_t pos, float theta) {
+    if (head_dim == 0 || head_dim % 2) return ORACLE_E_SHAPE;
+    const size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const double exponent = (double)(2 * i) / (double)head_dim;
+        const float inv_freq = (float)(1.0 / pow((double)theta, exponent));
+        const float angle = (float)pos * inv_freq;
+        const float s = sinf(angle), c = cosf(angle);
+        for (size_t h = 0; h < n_heads; ++h) {
+            float* r = x + h * head_dim;
+            const float a = r[i], b = r[half + i];
+            r[i] = a * c - b * s;
+            r[half + i] = b * c + a * s;
+        }
+    }
+    return ORACLE_OK;
+}
+
 /* ---- nn::linear_int8_dynamic (nn.rs:151-173) --------------------------------
  * ft-kernel-cpu's linear_int8_dynamic_f32 is not in the reference tree; its
  * activation rule is the documented one (docs/focrq-format.md:296-320, pinned

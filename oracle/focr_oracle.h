@@ -128,6 +128,19 @@ int oracle_moe_prefill_i8(const float* x, size_t t, size_t h, size_t inter, size
                           const int8_t* shared_wu, const float* shared_su, const int8_t* shared_wd,
                           const float* shared_sd, size_t shared_inter, float* out);
 
+/* ---- the decode layer's other ops (decoder.rs:2542-2627) ------------------
+ * nn::rms_norm (nn.rs:240-253) calls ft-kernel-cpu's rms_norm_forward_f32,
+ * which is not in the reference tree; this build fixes y = (x * rstd) * w
+ * with the sum of squares in f64 (increasing index) and rstd = (float)(1 /
+ * sqrt(ss / n + eps)) in f64 (w NULL: no weight). Pinned by the reference's
+ * hand values at 1e-6 (nn.rs:438-458); the exact f32 bits are unpinned. */
+void oracle_rms_norm(const float* x, size_t n, const float* w, float eps, float* y);
+/* RopeTable::build + apply_rope (decoder.rs:150-268) on one row of n_heads
+ * blocks of head_dim at absolute position pos: inv_freq[i] = (f32)(1 /
+ * theta^(2i/head_dim)) in f64, angle = (f32)pos * inv_freq[i], NEOX
+ * rotate_half over the two halves of each head. */
+int oracle_rope(float* x, size_t n_heads, size_t head_dim, size_t pos, float theta);
+
 /* ---- src/simd/int4.rs ---------------------------------------------------- */
 int8_t oracle_sign_extend_nibble(uint8_t nib);
 void oracle_unpack_byte(uint8_t b, int8_t* lo, int8_t* hi);

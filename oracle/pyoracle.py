@@ -47,6 +47,8 @@ _SIGS = {
     "oracle_moe_prefill_i4": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P],
                               C.c_int),
     "oracle_quantize_row_dynamic": ([_P, _SZ, _P], C.c_float),
+    "oracle_rms_norm": ([_P, _SZ, _P, C.c_float, _P], None),
+    "oracle_rope": ([_P, _SZ, _SZ, _SZ, C.c_float], C.c_int),
     "oracle_linear_i8_dynamic": ([_P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P], C.c_int),
     "oracle_moe_prefill_i8": ([_P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _SZ, _P], C.c_int),
@@ -315,6 +317,62 @@ def moe_prefill_i8(x, idx, gates, wg, sg, wu, su, wd, sd, n_experts, inter, shar
                                      p(_c(wu, np.int8)), p(_c(su, np.float32)), p(_c(wd, np.int8)),
                                      p(_c(sd, np.float32)), *sh, si, p(out))
     return st, out.reshape(t, h)
+
+
+def rms_norm(x, w=None, eps=1e-6):
+    """nn::rms_norm as this build fixes it (f64 sum of squares); rows of x."""
+    x = _c(x, np.float32)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.zeros_like(rows)
+    wc = None if w is None else _c(w, np.float32)
+    for r in range(rows.shape[0]):
+        lib().oracle_rms_norm(p(rows[r]), rows.shape[1], None if wc is None else p(wc), float(eps), p(out[r]))
+    return out.reshape(x.shape)
+
+
+def rope(x, pos, n_heads=10, head_dim=128, theta=10000.0):
+    """RopeTable::build + apply_rope (decoder.rs:150-268) on one row."""
+    y = np.array(_c(x, np.float32), copy=True)
+    assert lib().oracle_rope(p(y), n_heads, head_dim, int(pos), float(theta)) == 0
+    return y
+
+
+def decoder_layer_step(x, positions, rings, lw, eps=1e-6, theta=10000.0):
+    """One layer of batched_decode_step_i8_streams (decoder.rs:2812-2933) for
+    rows x [B, H] (stream s at positions[s], its RingCache rings[s]):
+    RMSNorm -> fused qkv GEMV -> RoPE -> ring write -> R-SWA -> o_proj ->
+    residual -> RMSNorm -> decode_mlp_i8 (MoE: route_default + the shared
+    expert; dense: one SwiGLU expert) -> residual. lw: dict with input_ln,
+    post_ln, qkv (w, s), o (w, s) and either moe (router, wg, sg, wu, su, wd,
+    sd, n_experts, top_k, inter, shared) or dense (wg, sg, wu, su, wd, sd, inter)."""
+    x = _c(x, np.float32)
+    B, H = x.shape
+    D = 10 * 128
+    out = np.zeros_like(x)
+    normed = rms_norm(x, lw["input_ln"], eps)
+    qkv = gemv_i8_batched(normed, lw["qkv"][0], lw["qkv"][1], 3 * D, H)[0]
+    ctx = np.zeros((B, D), np.float32)
+    for s in range(B):
+        q = rope(qkv[s, :D], positions[s], theta=theta)
+        k = rope(qkv[s, D:2 * D], positions[s], theta=theta)
+        rings[s].write(k, qkv[s, 2 * D:])
+        st, ctx[s] = rings[s].attend(q)
+        assert st == 0
+    attn = gemv_i8_batched(ctx, lw["o"][0], lw["o"][1], H, D)[0]
+    h = (x + attn).astype(np.float32)
+    normed2 = rms_norm(h, lw["post_ln"], eps)
+    if "moe" in lw:
+        m = lw["moe"]
+        st, mlp, _, _ = moe_decode(normed2, m["router"], m["wg"], m["sg"], m["wu"], m["su"], m["wd"], m["sd"],
+                                   m["n_experts"], m["top_k"], m["inter"], norm_topk=False, routed_scale=1.0,
+                                   shared=m.get("shared"))
+        assert st == 0
+    else:
+        d = lw["dense"]
+        mlp = np.stack([expert_i8(normed2[s], H, d["inter"], d["wg"], d["sg"], d["wu"], d["su"], d["wd"], d["sd"])[0]
+                        for s in range(B)])
+    out[:] = (h + mlp).astype(np.float32)
+    return out
 
 
 class Ring:

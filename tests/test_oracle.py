@@ -615,3 +615,112 @@ def test_moe_prefill_i8_ascending_expert_scatter_and_shared(rng):
     bad = idx.copy()
     bad[0, 0] = E
     assert O.moe_prefill_i8(x, bad, gates, wg, sg, wu, su, wd, sd, E, inter)[0] != 0
+
+
+# ---- decode-layer ops: RMSNorm, RoPE, the layer step ------------------------------------
+
+def test_rms_norm_hand_values():
+    # nn.rs:438-458: [3, 4], eps 0 -> rstd = 1/sqrt(12.5); weight [2, 0.5]
+    rstd = 1.0 / math.sqrt(12.5)
+    y = O.rms_norm(np.array([[3.0, 4.0]], np.float32), eps=0.0)
+    np.testing.assert_allclose(y[0], [3 * rstd, 4 * rstd], atol=1e-6)
+    y = O.rms_norm(np.array([[3.0, 4.0]], np.float32), np.array([2.0, 0.5], np.float32), eps=0.0)
+    np.testing.assert_allclose(y[0], [3 * rstd * 2, 4 * rstd * 0.5], atol=1e-6)
+
+
+def test_rms_norm_vs_float64(rng):
+    x = (rng.standard_normal((5, 1280)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 1280).astype(np.float32)
+    y = O.rms_norm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(y, want, rtol=2e-7, atol=1e-7)
+
+
+def test_rope_known_answers():
+    # decoder.rs:3711-3720 position 0 is the identity
+    np.testing.assert_array_equal(O.rope(np.array([1, 2, 3, 4], np.float32), 0, 1, 4), [1, 2, 3, 4])
+    # :3723-3739 head_dim 2, pos 1: [a c - b s, b c + a s]
+    s, c = math.sin(1.0), math.cos(1.0)
+    np.testing.assert_allclose(O.rope(np.array([3, 5], np.float32), 1, 1, 2), [3 * c - 5 * s, 5 * c + 3 * s],
+                               atol=1e-5)
+    # :3766-3780 two heads share the phase
+    s, c = math.sin(2.0), math.cos(2.0)
+    np.testing.assert_allclose(O.rope(np.array([1, 0, 0, 1], np.float32), 2, 2, 2), [c, s, -s, c], atol=1e-5)
+
+
+def test_rope_rotation_vs_float64(rng):
+    # the NEOX rotate_half over each head's halves, angle pos * theta^(-2i/d)
+    x = rng.standard_normal(10 * 128).astype(np.float32)
+    for pos in (0, 7, 1023, 4000):
+        y = O.rope(x, pos)
+        inv = (1.0 / 10000.0 ** (np.arange(64) * 2 / 128)).astype(np.float32).astype(np.float64)
+        ang = pos * inv
+        xh = x.astype(np.float64).reshape(10, 2, 64)
+        want = np.stack([xh[:, 0] * np.cos(ang) - xh[:, 1] * np.sin(ang),
+                         xh[:, 1] * np.cos(ang) + xh[:, 0] * np.sin(ang)], axis=1).reshape(-1)
+        np.testing.assert_allclose(y, want, rtol=0, atol=2e-5 * max(1.0, pos / 100))
+        # per-head norms preserved (decoder.rs:3742-3763)
+        np.testing.assert_allclose((y.reshape(10, 128) ** 2).sum(1), (x.reshape(10, 128) ** 2).sum(1), rtol=1e-5)
+
+
+def _small_layer(rng, moe=True):
+    H, D = 1280, 1280
+    lw = {"input_ln": rng.uniform(0.5, 1.5, H).astype(np.float32),
+          "post_ln": rng.uniform(0.5, 1.5, H).astype(np.float32),
+          "qkv": (rng.integers(-127, 128, 3 * D * H).astype(np.int8), rng.uniform(1e-3, 2e-2, 3 * D).astype(np.float32)),
+          "o": (rng.integers(-127, 128, H * D).astype(np.int8), rng.uniform(1e-3, 2e-2, H).astype(np.float32))}
+    E, I = 8, 64
+    if moe:
+        lw["moe"] = {"router": (rng.standard_normal((E, H)) * 0.02).astype(np.float32),
+                     "wg": rng.integers(-127, 128, E * I * H).astype(np.int8), "sg": rng.uniform(1e-3, 2e-2, E * I).astype(np.float32),
+                     "wu": rng.integers(-127, 128, E * I * H).astype(np.int8), "su": rng.uniform(1e-3, 2e-2, E * I).astype(np.float32),
+                     "wd": rng.integers(-127, 128, E * H * I).astype(np.int8), "sd": rng.uniform(1e-3, 2e-2, E * H).astype(np.float32),
+                     "n_experts": E, "top_k": 2, "inter": I}
+    else:
+        lw["dense"] = {"wg": rng.integers(-127, 128, I * H).astype(np.int8), "sg": rng.uniform(1e-3, 2e-2, I).astype(np.float32),
+                       "wu": rng.integers(-127, 128, I * H).astype(np.int8), "su": rng.uniform(1e-3, 2e-2, I).astype(np.float32),
+                       "wd": rng.integers(-127, 128, H * I).astype(np.int8), "sd": rng.uniform(1e-3, 2e-2, H).astype(np.float32),
+                       "inter": I}
+    return lw
+
+
+@pytest.mark.parametrize("moe", [True, False])
+def test_decoder_layer_step_batched_equals_per_stream(rng, moe):
+    # batched_decode_step_i8_streams == decode_step_with_cache_i8 per stream
+    # (the reference's tests/batched_attention_parity.rs / batched_moe_parity.rs invariant)
+    lw = _small_layer(rng, moe)
+    B, G = 3, 16
+    x = rng.standard_normal((B, 1280)).astype(np.float32)
+    pos = [G, G + 5, G + 9]
+
+    def rings():
+        rs = []
+        for s in range(B):
+            r = O.Ring(64)
+            kv = np.random.default_rng(s).standard_normal((2, 10 * G * 128)).astype(np.float32)
+            r.record_prefill(kv[0], kv[1], G)
+            rs.append(r)
+        return rs
+
+    rb = rings()
+    got = O.decoder_layer_step(x, pos, rb, lw)
+    got2 = O.decoder_layer_step(got, [p + 1 for p in pos], rb, lw)  # a second step reads the first's ring slot
+    rs = rings()
+    for s in range(B):
+        one = O.decoder_layer_step(x[s:s + 1], [pos[s]], [rs[s]], lw)
+        assert np.array_equal(one[0], got[s])
+        two = O.decoder_layer_step(one, [pos[s] + 1], [rs[s]], lw)
+        assert np.array_equal(two[0], got2[s])
+    assert all(r.ring_len.value == 2 for r in rb)
+
+
+def test_decoder_layer_step_zero_projections_is_identity(rng):
+    # o_proj and the MLP's down weights zero: both residual branches add 0
+    lw = _small_layer(rng, True)
+    lw["o"] = (np.zeros_like(lw["o"][0]), lw["o"][1])
+    lw["moe"]["wd"] = np.zeros_like(lw["moe"]["wd"])
+    r = O.Ring(16)
+    r.record_prefill(np.ones(10 * 4 * 128, np.float32), np.ones(10 * 4 * 128, np.float32), 4)
+    x = rng.standard_normal((1, 1280)).astype(np.float32)
+    assert np.array_equal(O.decoder_layer_step(x, [4], [r], lw), x)
