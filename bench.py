@@ -572,6 +572,81 @@ def bench_prefill_i8(args, ctx):
 
 
 # ---------------------------------------------------------------------------
+# one decoder layer's decode step (MoE layer + shared expert, R-SWA attention)
+# ---------------------------------------------------------------------------
+
+def bench_decode_layer(args, ctx):
+    """decode_step_with_cache_i8 for one MoE layer over B streams (each with a
+    1024-token reference block and a ring filled by the warm-up steps):
+    RMSNorm, qkv GEMV, RoPE, ring write + R-SWA, o_proj, residual + RMSNorm,
+    MoE (route_default + the 1792-wide shared expert), residual. Layer copies
+    (each with its own weights and caches) rotate so weights come from HBM."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import DecoderLayer, MoeLayer, QInt8, RingCache
+
+    B, G, D, SI = args.tokens, 1024, 1280, 1792
+    log(f"decode_layer: {B} streams, ref {G} tokens, {args.copies} layer copies")
+    base = make_moe_host(100)
+    sh = [synth.int8_uniform(synth.seed_of(800), SI * H), synth.f32_uniform(synth.seed_of(801), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(802), SI * H), synth.f32_uniform(synth.seed_of(803), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(804), H * SI), synth.f32_uniform(synth.seed_of(805), H, 1e-3, 2e-2)]
+    wqkv = synth.int8_uniform(synth.seed_of(806), 3 * D * H)
+    sqkv = synth.f32_uniform(synth.seed_of(807), 3 * D, 1e-3, 2e-2)
+    wo = synth.int8_uniform(synth.seed_of(808), H * D)
+    so = synth.f32_uniform(synth.seed_of(809), H, 1e-3, 2e-2)
+    ln1 = synth.f32_uniform(synth.seed_of(810), H, 0.5, 1.5)
+    ln2 = synth.f32_uniform(synth.seed_of(811), H, 0.5, 1.5)
+    kv = [ctx.to_device(synth.f32_normal(synth.seed_of(820 + i), 10 * G * 128)) for i in range(2)]
+    layers, caches = [], []
+    for c in range(args.copies):
+        router = synth.f32_normal(synth.seed_of(1000 + c), E * H, 0.0, 0.02).reshape(E, H)
+        moe = MoeLayer(H, I, E, K, router, *base[1:], ctx=ctx)
+        moe.set_shared(SI, *sh)
+        layers.append(DecoderLayer(H, ln1, ln2, QInt8(wqkv, sqkv, 3 * D, H, ctx), QInt8(wo, so, H, D, ctx), moe=moe,
+                                   ctx=ctx))
+        cache = RingCache(B, G, ctx=ctx)
+        for s in range(B):
+            cache.record_prefill(s, kv[0], kv[1], G)
+        caches.append(cache)
+    x = ctx.to_device(synth.f32_normal(synth.seed_of(830), B * H).reshape(B, H))
+    idx = [ctx.empty((B, K), np.uint32) for _ in layers]
+    pos = np.full(B, G, np.uint32)
+    n = len(layers)
+
+    def step(i):
+        j = i % n
+        layers[j].step(caches[j], pos + i // n, x, idx[j], check_route=False)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    U = [len(np.unique(b.numpy())) for b in idx]
+    el, prof, kernels = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    ring = min(128, (args.warmup + 2 * args.steps) // n)  # about where the rings are during the timed passes
+    keys = G + ring
+    mean_u = float(np.mean(U))
+    attn_bytes = B * 2 * 10 * keys * 128 * 4
+    w_bytes = (3 * D * H + 3 * D * 4) + (H * D + H * 4) + mean_u * (3 * I * H + 2 * I * 4 + H * 4) + \
+        (3 * SI * H + 2 * SI * 4 + H * 4) + E * H * 4
+    layer_bytes = w_bytes + attn_bytes + 2 * B * H * 4
+    gbs = layer_bytes / (ms * 1e-3) / 1e9
+    log(f"U per copy {U}; per-kernel avg us {kernels}")
+    return {
+        "metric": "decoder-layer decode step tokens/s + achieved HBM GB/s (% of 8 TB/s peak), 1 GPU",
+        "value": round(B * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "decode_layer", "streams": B, "ref_tokens": G, "ring_tokens_approx": ring,
+                   "hidden": H, "heads": 10, "head_dim": 128, "experts": E, "top_k": K, "inter": I,
+                   "shared_inter": SI, "layer_copies_rotated": n, "distinct_experts_mean": mean_u},
+        "roofline": {"bound": "hbm", "kernel": "layer (all kernels)", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": int(layer_bytes), "avg_step_us": round(ms * 1e3, 3)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
+# ---------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size (the reference
 # point for the FETCH_SIZE / WRITE_SIZE counters)
 # ---------------------------------------------------------------------------
@@ -615,6 +690,7 @@ WORKLOADS = {
     "moe_prefill_i4": (bench_prefill_i4, cpu_prefill_i4),
     "moe_prefill_i8": (bench_prefill_i8, None),
     "linear_i8": (bench_linear_i8, None),
+    "decode_layer": (bench_decode_layer, None),
 }
 
 
@@ -635,7 +711,8 @@ def main() -> int:
         return 2
     defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
                 "copy": (1, 1),
-                "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3)}
+                "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
+                "decode_layer": (8, 6)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

@@ -578,6 +578,8 @@ struct MoeScratch {
     float* act;
     float* shared_act;
     float* shared_y;
+    int8_t* shared_aq;  // [t][shared_inter] quantized shared act rows
+    float* shared_as;   // [t]
     float* ybuf;  // [pairs][hidden] weighted expert outputs (grouped down path only)
     void* sel;
 };
@@ -589,7 +591,13 @@ int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bo
     s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
     s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
     s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
-    s->shared_y = with_shared ? static_cast<float*>(ctx->scratch_get(kScrShared, t * L->hidden * sizeof(float))) : nullptr;
+    char* shb = with_shared ? static_cast<char*>(ctx->scratch_get(
+                                  kScrShared, t * L->hidden * sizeof(float) + 256 + t * L->shared_inter + 256 + t * 4))
+                            : nullptr;
+    s->shared_y = reinterpret_cast<float*>(shb);
+    s->shared_aq = shb ? reinterpret_cast<int8_t*>(shb + ((t * L->hidden * sizeof(float) + 255) & ~size_t(255))) : nullptr;
+    s->shared_as = shb ? reinterpret_cast<float*>(reinterpret_cast<char*>(s->shared_aq) + ((t * L->shared_inter + 255) & ~size_t(255)))
+                       : nullptr;
     s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
     const bool grouped = static_cast<int>(t) >= kMoeGroupedDownT;
     s->ybuf = grouped ? static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float))) : nullptr;
@@ -680,9 +688,19 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
                                    (int)L->shared_inter, true);
         }
         if (e == hipSuccess) {
+            // quantize_row_i8 of the act rows, then the int8 GEMV: the same
+            // products, scales and rounding as the expert's down projection
+            // (decoder.rs:1753-1754), with the GEMV's full-grid weight stream
             ProfScope ps(ctx, "moe_shared_down");
-            e = launch_moe_down(str, d, s.sel, s.shared_act, L->swd, L->ssd, s.shared_y, (int)L->shared_inter,
-                                true);
+            const int SI = (int)L->shared_inter;
+            e = launch_quantize_rows(str, s.shared_act, (int)t, SI, s.shared_aq, s.shared_as, 0);
+            const int rows = 57344 / SI < 32 ? 57344 / SI : 32;  // the GEMV's activation stage: m * k <= 56 KiB
+            for (int r0 = 0; e == hipSuccess && r0 < (int)t; r0 += rows) {
+                const int mr = (int)t - r0 < rows ? (int)t - r0 : rows;
+                e = launch_gemv_i8(str, L->swd, L->ssd, (int)L->hidden, SI, s.shared_aq + (size_t)r0 * SI,
+                                   s.shared_as + r0, mr, s.shared_y + (size_t)r0 * L->hidden, nullptr, nullptr,
+                                   nullptr, ctx->cu_count);
+            }
         }
     }
     if (e == hipSuccess && s.ybuf) {
@@ -1197,7 +1215,7 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* L) {
 }
 
 int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
-                                    const uint32_t* positions, float* x, int32_t check_route) {
+                                    const uint32_t* positions, float* x, uint32_t* route_idx, int32_t check_route) {
     ENGINE_CTX(ctx);
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null layer");
     if (!cache) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null rswa cache");
@@ -1228,7 +1246,6 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     float* nrm = reinterpret_cast<float*>(take(B * H * 4));
     int8_t* xq = reinterpret_cast<int8_t*>(take(B * (H > D ? H : D)));
     float* xs = reinterpret_cast<float*>(take(B * 4));
-    uint32_t* dpos = reinterpret_cast<uint32_t*>(take(B * 4));
     hipStream_t s = ctx->stream;
     // 1. input RMSNorm + quantize_row_i8; 2. the fused qkv GEMV
     {
@@ -1242,10 +1259,11 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
                      "qkv gemv launch");
     }
     // 3. RoPE at each stream's position, ring write, attention
-    FOCR_HIP_TRY(hipMemcpyAsync(dpos, positions, B * 4, hipMemcpyHostToDevice, s), "positions H2D");
     {
+        RopePositions rp{};
+        for (size_t i = 0; i < B; ++i) rp.p[i] = positions[i];
         ProfScope ps(ctx, "layer_rope");
-        FOCR_HIP_TRY(launch_rope_split(s, qkv, dpos, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, k, v),
+        FOCR_HIP_TRY(launch_rope_split(s, qkv, rp, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, k, v),
                      "rope launch");
     }
     int32_t st = rswa_write_all(ctx, cache, k, v, nullptr);
@@ -1270,7 +1288,8 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     // 6. decode_mlp_i8 (decoder.rs:2199-2268) and the residual
     if (L->moe) {
         // route_default (moe.rs:53-76: norm_topk_prob false, scaling 1.0) + the shared expert
-        return moe_decode_impl(ctx, L->moe, nrm, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, nullptr, nullptr, check_route, h);
+        return moe_decode_impl(ctx, L->moe, nrm, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, route_idx, nullptr, check_route,
+                               h);
     }
     // dense (layer 0): expert_gemv_i8 (decoder.rs:1711-1720)
     float* g = reinterpret_cast<float*>(take(B * I * 4));

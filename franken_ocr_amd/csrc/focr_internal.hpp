@@ -260,9 +260,13 @@ hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, 
 // h = x + a; y = rms_norm(h) * w per row.
 hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
                                     float eps, float* h, float* y);
-// Split fused qkv rows [streams][3 D] into q, k (RoPE at pos[stream]) and v.
-hipError_t launch_rope_split(hipStream_t s, const float* qkv, const uint32_t* pos, const float* inv_freq, int streams,
-                             int n_heads, int head_dim, float* q, float* k, float* v);
+// Split fused qkv rows [streams][3 D] into q, k (RoPE at pos.p[stream]) and v.
+struct RopePositions {
+    static constexpr int kMax = 32;
+    uint32_t p[kMax];
+};
+hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
+                             int streams, int n_heads, int head_dim, float* q, float* k, float* v);
 hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n);
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n);
 // k_int4.hip

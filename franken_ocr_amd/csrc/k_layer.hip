@@ -85,11 +85,11 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __
     if (threadIdx.x == 0) xs[blockIdx.x] = a_scale;
 }
 
-// One block per stream: the fused row qkv [3D] -> q, k rotated at pos[s]
-// (inv_freq [half], the reference's f64-then-f32 table) and v copied, each
-// [D] contiguous. Thread = (head, i < half) pairs.
-__global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __restrict__ qkv,
-                                                              const uint32_t* __restrict__ pos,
+// One block per stream: the fused row qkv [3D] -> q, k rotated at
+// pos.p[s] (inv_freq [half], the reference's f64-then-f32 table) and v
+// copied, each [D] contiguous. Thread = (head, i < half) pairs. The
+// positions ride in the kernel arguments (no copy per step).
+__global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __restrict__ qkv, RopePositions pos,
                                                               const float* __restrict__ inv_freq, int n_heads,
                                                               int head_dim, float* __restrict__ q,
                                                               float* __restrict__ k, float* __restrict__ v) {
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __res
     const int D = n_heads * head_dim;
     const int half = head_dim >> 1;
     const float* row = qkv + static_cast<size_t>(s) * 3 * D;
-    const float p = static_cast<float>(pos[s]);
+    const float p = static_cast<float>(pos.p[s]);
     for (int t = threadIdx.x; t < n_heads * half; t += kThreads) {
         const int hd = t / half, i = t - hd * half;
         const float angle = p * inv_freq[i];
@@ -144,9 +144,9 @@ hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* 
     return hipGetLastError();
 }
 
-hipError_t launch_rope_split(hipStream_t s, const float* qkv, const uint32_t* pos, const float* inv_freq, int streams,
-                             int n_heads, int head_dim, float* q, float* k, float* v) {
-    if (head_dim % 2 || streams < 1) return hipErrorInvalidValue;
+hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
+                             int streams, int n_heads, int head_dim, float* q, float* k, float* v) {
+    if (head_dim % 2 || streams < 1 || streams > RopePositions::kMax) return hipErrorInvalidValue;
     FOCR_LAUNCH(rope_split_kernel, dim3(streams), dim3(kThreads), 0, s, qkv, pos, inv_freq, n_heads, head_dim, q, k,
                 v);
     return hipGetLastError();

@@ -373,12 +373,14 @@ class DecoderLayer:
                   moe._h if moe is not None else None, g.handle if g else None, u.handle if u else None,
                   d.handle if d else None, float(eps), float(rope_theta), C.byref(self._h))
 
-    def step(self, cache: "RingCache", positions, x: DeviceArray, check_route: bool = True) -> None:
+    def step(self, cache: "RingCache", positions, x: DeviceArray, route_idx: DeviceArray | None = None,
+             check_route: bool = True) -> None:
         """x [n_streams, hidden] (device) updated in place; positions: each
-        stream's absolute position."""
+        stream's absolute position; route_idx [n_streams, top_k] (optional)
+        receives a MoE layer's expert ids."""
         pos = np.ascontiguousarray(positions, dtype=np.uint32)
         _abi.call("focr_hip_decoder_layer_step", self.ctx.handle, self._h, cache._h, pos.ctypes.data_as(C.c_void_p),
-                  x.c_ptr, 1 if check_route else 0)
+                  x.c_ptr, _p(route_idx), 1 if check_route else 0)
 
     def free(self) -> None:
         if self._h:

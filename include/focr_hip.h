@@ -366,12 +366,13 @@ int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n
                                       float rms_eps, float rope_theta, focr_hip_decoder_layer** out);
 int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* layer);
 /* x [n_streams, hidden] f32 device, updated in place; positions [n_streams]
- * host (each stream's absolute position, SPEC-095). With check_route = 1 a
- * MoE layer synchronises and returns E_ROUTE for a row with no finite router
- * score. n_streams <= 32 (<= 8 for the 6848-wide dense MLP). */
+ * host (each stream's absolute position, SPEC-095); route_idx (device,
+ * nullable) receives a MoE layer's expert ids [n_streams, top_k]. With
+ * check_route = 1 a MoE layer synchronises and returns E_ROUTE for a row with
+ * no finite router score. n_streams <= 32 (<= 8 for the 6848-wide dense MLP). */
 int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
                                     focr_hip_rswa* cache, const uint32_t* positions, float* x,
-                                    int32_t check_route);
+                                    uint32_t* route_idx, int32_t check_route);
 
 /* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
  * The reader restates weights.rs:443-620 (format detection by magic, the
