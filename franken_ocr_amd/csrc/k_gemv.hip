@@ -285,7 +285,92 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
     }
 }
 
-// One block per row: fold nparts keys -> the argmax index.
+// The same GEMV for small N (a few thousand rows: a layer's qkv, o_proj,
+// a shared expert's down projection), split along K: one block per 16-row
+// tile, wave w takes the 256-byte column chunks w, w + 4, ... (all of them
+// loaded before the first is used), and the four waves' i32 accumulators are
+// added through LDS before wave 0's epilogue. With one tile per wave instead,
+// N = 1280 gives only 20 blocks for the 256 CUs. Integer sums, so the
+// result is bit-identical to the kernel above.
+constexpr int kSplitKMaxChunks = 4;  // per wave: K <= 16 * 256
+__global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
+    const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out) {
+    extern __shared__ int4 lds_dyn[];  // x [16][K/16 + 1], then per-wave [16][16] chunks
+    __shared__ v4i_m red[kThreads / 64][64];
+    __shared__ float lds_as[16];
+    const int C = K >> 4;
+    const int xs = C + 1;
+    const int wave = threadIdx.x >> 6;
+    const int l = threadIdx.x & 63;
+    const int g = l >> 4, col = l & 15;
+    int4* lds_xv = lds_dyn;
+    int4* wbuf = lds_dyn + 16 * xs + wave * (kMfmaTileBytes / 16);
+    const int nch = K >> 8;
+    const int n0 = blockIdx.x * 16;
+    int4 rg[kSplitKMaxChunks][4];
+#pragma unroll
+    for (int c = 0; c < kSplitKMaxChunks; ++c) {
+        const int kc = wave + 4 * c;
+        const int kcl = kc < nch ? kc : nch - 1;  // loads past this wave's chunks re-read its last one (unused)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * j + g;
+            rg[c][j] = n < N ? ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n) * K + kcl * 256) + col)
+                             : make_int4(0, 0, 0, 0);
+        }
+    }
+    const int4* x4 = reinterpret_cast<const int4*>(xq);
+    for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
+        const int r = i / C, c = i - r * C;
+        lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+    }
+    if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+    __syncthreads();
+    v4i_m acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < kSplitKMaxChunks; ++c) {
+        const int kc = wave + 4 * c;
+        if (kc >= nch) break;  // wave-uniform
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = 4 * j + g;
+            wbuf[r * 16 + (col ^ r)] = rg[c][j];
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int piece = 4 * st + g;
+            const int4 bw = wbuf[col * 16 + (piece ^ col)];
+            const int4 a = lds_xv[col * xs + kc * 16 + piece];
+            const v4i_m bv = {bw.x, bw.y, bw.z, bw.w};
+            const v4i_m av = {a.x, a.y, a.z, a.w};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc, 0, 0, 0);
+        }
+    }
+    red[wave][l] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w2 = 1; w2 < kThreads / 64; ++w2) {
+        const v4i_m o = red[w2][l];
+        acc = v4i_m{acc[0] + o[0], acc[1] + o[1], acc[2] + o[2], acc[3] + o[3]};
+    }
+    const int n = n0 + col;
+    if (n >= N) return;
+    const float wscale = ws[n];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int i = 4 * g + v;
+        if (i < M) {
+            const int av = acc[v];
+            const float t0 = static_cast<float>(av) * lds_as[i];
+            y[static_cast<size_t>(i) * N + n] = t0 * wscale;
+            if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = av;
+        }
+    }
+}
+
+// One block per row: fold nparts keys -> the argmax index.// One block per row: fold nparts keys -> the argmax index.
 __global__ __launch_bounds__(kThreads) void argmax_reduce_kernel(const uint64_t* __restrict__ keys,
                                                                  int nparts,
                                                                  uint32_t* __restrict__ argmax) {
@@ -376,6 +461,19 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
     while (mc < m) mc <<= 1;
     const size_t lds_mfma = (static_cast<size_t>(16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) *
                             sizeof(int4);
+    if (m >= kMfmaMinRows && k % 256 == 0 && lds_mfma <= 65536 && !arg_keys && !ban_bits &&
+        k <= 256 * 4 * kSplitKMaxChunks && (n + 15) / 16 < 4 * (cu_count > 0 ? cu_count : 256)) {
+        // small N: one 16-row tile per block, K split over the four waves
+        const int grid = (n + 15) / 16;
+        if (nparts_out) *nparts_out = grid;
+        for (int r0 = 0; r0 < m; r0 += 16) {
+            const int mr = m - r0 < 16 ? m - r0 : 16;
+            FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel, dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k,
+                        xq + static_cast<size_t>(r0) * k, a_scales + r0, mr, y + static_cast<size_t>(r0) * n,
+                        acc ? acc + static_cast<size_t>(r0) * n : nullptr);
+        }
+        return hipGetLastError();
+    }
     if (m >= kMfmaMinRows && k % 256 == 0 && lds_mfma <= 65536) {
         const int tiles = (n + 15) / 16;
         // four blocks per CU (16 waves, 37 KB of LDS each at K = 1280): the
