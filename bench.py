@@ -646,6 +646,92 @@ def bench_decode_layer(args, ctx):
     }
 
 
+def bench_decode_step(args, ctx):
+    """One decode token for B streams through the whole decoder: 12 layers
+    (decoder.rs:2542-2627 per layer; layer 0 the 6848-wide dense MLP, layers
+    1-11 MoE with the 1792-wide shared expert), the final RMSNorm and the
+    129280-row LM head + argmax (decoder.rs:2275-2296; sampler.rs:168-186).
+    Each stream has a 1024-token reference block; every layer has its own
+    weights and cache. The step's input row stands in for the token-embedding
+    lookup (the embedding table is outside this path)."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import DecoderLayer, MoeLayer, QInt8, RingCache, lm_head_i8, rms_norm
+
+    B, G, D, SI, ID, V, NL = args.tokens, 1024, 1280, 1792, 6848, 129280, 12
+    log(f"decode_step: {B} streams, {NL} layers, ref {G} tokens")
+    base = make_moe_host(100)
+    sh = [synth.int8_uniform(synth.seed_of(800), SI * H), synth.f32_uniform(synth.seed_of(801), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(802), SI * H), synth.f32_uniform(synth.seed_of(803), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(804), H * SI), synth.f32_uniform(synth.seed_of(805), H, 1e-3, 2e-2)]
+    wqkv = synth.int8_uniform(synth.seed_of(806), 3 * D * H)
+    sqkv = synth.f32_uniform(synth.seed_of(807), 3 * D, 1e-3, 2e-2)
+    wo = synth.int8_uniform(synth.seed_of(808), H * D)
+    so = synth.f32_uniform(synth.seed_of(809), H, 1e-3, 2e-2)
+    ln = [synth.f32_uniform(synth.seed_of(810 + i), H, 0.5, 1.5) for i in range(3)]
+    kv = [ctx.to_device(synth.f32_normal(synth.seed_of(820 + i), 10 * G * 128)) for i in range(2)]
+    dense = [synth.int8_uniform(synth.seed_of(840), ID * H), synth.f32_uniform(synth.seed_of(841), ID, 1e-3, 2e-2),
+             synth.int8_uniform(synth.seed_of(842), ID * H), synth.f32_uniform(synth.seed_of(843), ID, 1e-3, 2e-2),
+             synth.int8_uniform(synth.seed_of(844), H * ID), synth.f32_uniform(synth.seed_of(845), H, 1e-3, 2e-2)]
+    layers, caches = [], []
+    for l in range(NL):
+        qkv, o = QInt8(wqkv, sqkv, 3 * D, H, ctx), QInt8(wo, so, H, D, ctx)
+        if l == 0:
+            mlp = dict(dense=(QInt8(dense[0], dense[1], ID, H, ctx), QInt8(dense[2], dense[3], ID, H, ctx),
+                              QInt8(dense[4], dense[5], H, ID, ctx)))
+        else:
+            router = synth.f32_normal(synth.seed_of(1000 + l), E * H, 0.0, 0.02).reshape(E, H)
+            moe = MoeLayer(H, I, E, K, router, *base[1:], ctx=ctx)
+            moe.set_shared(SI, *sh)
+            mlp = dict(moe=moe)
+        layers.append(DecoderLayer(H, ln[0], ln[1], qkv, o, ctx=ctx, **mlp))
+        cache = RingCache(B, G, ctx=ctx)
+        for st in range(B):
+            cache.record_prefill(st, kv[0], kv[1], G)
+        caches.append(cache)
+    lm = QInt8(synth.int8_uniform(synth.seed_of(850), V * H), synth.f32_uniform(synth.seed_of(851), V, 1e-3, 2e-2), V,
+               H, ctx)
+    final_ln = ctx.to_device(ln[2])
+    x0 = ctx.to_device(synth.f32_normal(synth.seed_of(830), B * H).reshape(B, H))
+    x, xn = ctx.empty((B, H), np.float32), ctx.empty((B, H), np.float32)
+    tok = ctx.empty((B,), np.uint32)
+    pos = np.full(B, G, np.uint32)
+    idx = [ctx.empty((B, K), np.uint32) for _ in range(NL)]
+
+    def step(i):
+        x.copy_from_device(x0)  # stands in for the embedding lookup of the previous token
+        for l in range(NL):
+            layers[l].step(caches[l], pos + i, x, idx[l], check_route=False)
+        rms_norm(x, xn, final_ln)
+        lm_head_i8(lm, xn, tok)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    U = [len(np.unique(idx[l].numpy())) for l in range(1, NL)]
+    el, prof, kernels = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    keys = G + min(128, args.warmup + args.steps)  # the rings' fill during the timed pass
+    attn = B * 2 * 10 * keys * 128 * 4
+    proj = (3 * D * H + 3 * D * 4) + (H * D + H * 4)
+    moe_b = sum(u * (3 * I * H + 2 * I * 4 + H * 4) for u in U) + \
+        (NL - 1) * ((3 * SI * H + 2 * SI * 4 + H * 4) + E * H * 4)
+    dense_b = 3 * ID * H + 2 * ID * 4 + H * 4
+    step_bytes = NL * (proj + attn) + moe_b + dense_b + (V * H + V * 4)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"distinct experts per MoE layer {U}; per-kernel avg us {kernels}")
+    return {
+        "metric": "full decode step (12 layers + LM head) tokens/s, 1 GPU",
+        "value": round(B * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "decode_step", "streams": B, "layers": NL, "ref_tokens": G, "hidden": H,
+                   "experts": E, "top_k": K, "vocab": V, "dense_inter": ID, "shared_inter": SI},
+        "roofline": {"bound": "hbm", "kernel": "the whole step", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": int(step_bytes), "avg_step_us": round(ms * 1e3, 3)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
 # ---------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size (the reference
 # point for the FETCH_SIZE / WRITE_SIZE counters)
@@ -691,6 +777,7 @@ WORKLOADS = {
     "moe_prefill_i8": (bench_prefill_i8, None),
     "linear_i8": (bench_linear_i8, None),
     "decode_layer": (bench_decode_layer, None),
+    "decode_step": (bench_decode_step, None),
 }
 
 
@@ -712,7 +799,7 @@ def main() -> int:
     defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
                 "copy": (1, 1),
                 "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
-                "decode_layer": (8, 6)}
+                "decode_layer": (8, 6), "decode_step": (8, 1)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

@@ -82,6 +82,7 @@ _SIGS: dict[str, list] = {
     "focr_hip_moe_prefill_i4": [_P, _P, _P, _SZ, _SZ, _P, _P, _P, _I32],
     "focr_hip_linear_i8_dynamic": [_P, _P, _P, _SZ, _P, _P],
     "focr_hip_moe_prefill_i8": [_P, _P, _P, _SZ, _P, _P, _I32, _P, _I32],
+    "focr_hip_rms_norm": [_P, _P, _SZ, _SZ, _P, _F32, _P],
     "focr_hip_decoder_layer_create": [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _F32, _P],
     "focr_hip_decoder_layer_free": [_P],
     "focr_hip_decoder_layer_step": [_P, _P, _P, _P, _P, _P, _I32],

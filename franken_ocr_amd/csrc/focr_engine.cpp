@@ -1144,6 +1144,17 @@ int32_t focr_hip_rswa_step(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* q, 
 
 // ---- one decoder layer's decode step (decoder.rs:2542-2627, :2812-2933) --------
 
+int32_t focr_hip_rms_norm(focr_hip_ctx* ctx, const float* x, size_t rows, size_t n, const float* w, float eps,
+                          float* y) {
+    ENGINE_CTX(ctx);
+    if (rows == 0) return FOCR_HIP_OK;
+    if (!x || !y) return fail(FOCR_HIP_E_ARG, "rms_norm: null device pointer");
+    if (n == 0 || n > 4096 || rows > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, fmt("rms_norm: cols %zu outside 1..=4096", n));
+    ProfScope ps(ctx, "rms_norm");
+    FOCR_HIP_TRY(launch_rms_norm(ctx->stream, x, w, (int)rows, (int)n, eps, y), "rms_norm launch");
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n_heads, size_t head_dim,
                                       const float* input_ln, const float* post_attn_ln, const focr_hip_qint8* qkv,
                                       const focr_hip_qint8* o_proj, const focr_hip_moe_layer* moe,

@@ -257,6 +257,8 @@ hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32
 // xq, xs = quantize_row_i8(rms_norm(x) * w) per row (n <= 4096).
 hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, int rows, int n, float eps,
                                  int8_t* xq, float* xs);
+// y = rms_norm(x) * w per row (w nullable).
+hipError_t launch_rms_norm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y);
 // h = x + a; y = rms_norm(h) * w per row.
 hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
                                     float eps, float* h, float* y);

@@ -10,6 +10,8 @@
 // dot products, activations (M <= 32 rows) staged once per block in LDS and
 // read as broadcast 16-byte LDS reads. Each block walks a contiguous range of
 // 16-row tiles so the per-block prologue (staging xq) is amortised.
+#include <atomic>
+
 #include "focr_internal.hpp"
 #include "k_common.hpp"
 
@@ -291,12 +293,16 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
 // loaded before the first is used), and the four waves' i32 accumulators are
 // added through LDS before wave 0's epilogue. With one tile per wave instead,
 // N = 1280 gives only 20 blocks for the 256 CUs. Integer sums, so the
-// result is bit-identical to the kernel above.
-constexpr int kSplitKMaxChunks = 4;  // per wave: K <= 16 * 256
+// result is bit-identical to the kernel above. K need only be a multiple of
+// 64: the pieces of a last, partial chunk past K are zeroed on both sides
+// (the weight pieces by a mask on the loaded data, the activation pieces
+// likewise), so they add nothing.
+constexpr int kSplitKMaxChunks = 8;  // per wave: K <= 32 * 256
+template <int CPW>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out) {
-    extern __shared__ int4 lds_dyn[];  // x [16][K/16 + 1], then per-wave [16][16] chunks
+    extern __shared__ int4 lds_dyn[];  // x [M][K/16 + 1], then per-wave [16][16] chunks
     __shared__ v4i_m red[kThreads / 64][64];
     __shared__ float lds_as[16];
     const int C = K >> 4;
@@ -305,31 +311,34 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int l = threadIdx.x & 63;
     const int g = l >> 4, col = l & 15;
     int4* lds_xv = lds_dyn;
-    int4* wbuf = lds_dyn + 16 * xs + wave * (kMfmaTileBytes / 16);
-    const int nch = K >> 8;
+    int4* wbuf = lds_dyn + M * xs + wave * (kMfmaTileBytes / 16);
+    const int nch = (K + 255) >> 8;
     const int n0 = blockIdx.x * 16;
-    int4 rg[kSplitKMaxChunks][4];
+    int4 rg[CPW][4];
 #pragma unroll
-    for (int c = 0; c < kSplitKMaxChunks; ++c) {
+    for (int c = 0; c < CPW; ++c) {
         const int kc = wave + 4 * c;
         const int kcl = kc < nch ? kc : nch - 1;  // loads past this wave's chunks re-read its last one (unused)
+        const int pc = kcl * 16 + col;            // this lane's 16-byte piece of the row
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + 4 * j + g;
-            rg[c][j] = n < N ? ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n) * K + kcl * 256) + col)
-                             : make_int4(0, 0, 0, 0);
+            const int4 v = ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n < N ? n : N - 1) * K) +
+                                     (pc < C ? pc : C - 1));
+            const int mm = (n < N && pc < C) ? -1 : 0;  // past N or past K: zero
+            rg[c][j] = make_int4(v.x & mm, v.y & mm, v.z & mm, v.w & mm);
         }
     }
     const int4* x4 = reinterpret_cast<const int4*>(xq);
-    for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
+    for (int i = threadIdx.x; i < M * C; i += kThreads) {  // only the M live rows; the rest read as zero
         const int r = i / C, c = i - r * C;
-        lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+        lds_xv[r * xs + c] = x4[r * C + c];
     }
     if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     __syncthreads();
     v4i_m acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < kSplitKMaxChunks; ++c) {
+    for (int c = 0; c < CPW; ++c) {
         const int kc = wave + 4 * c;
         if (kc >= nch) break;  // wave-uniform
 #pragma unroll
@@ -341,9 +350,11 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         for (int st = 0; st < 4; ++st) {
             const int piece = 4 * st + g;
             const int4 bw = wbuf[col * 16 + (piece ^ col)];
-            const int4 a = lds_xv[col * xs + kc * 16 + piece];
+            const int pa = kc * 16 + piece;
+            const int4 a = lds_xv[(col < M ? col : 0) * xs + (pa < C ? pa : C - 1)];
+            const int ma = (pa < C && col < M) ? -1 : 0;
             const v4i_m bv = {bw.x, bw.y, bw.z, bw.w};
-            const v4i_m av = {a.x, a.y, a.z, a.w};
+            const v4i_m av = {a.x & ma, a.y & ma, a.z & ma, a.w & ma};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc, 0, 0, 0);
         }
     }
@@ -370,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     }
 }
 
-// One block per row: fold nparts keys -> the argmax index.// One block per row: fold nparts keys -> the argmax index.
+// One block per row: fold nparts keys -> the argmax index.
 __global__ __launch_bounds__(kThreads) void argmax_reduce_kernel(const uint64_t* __restrict__ keys,
                                                                  int nparts,
                                                                  uint32_t* __restrict__ argmax) {
@@ -435,6 +446,21 @@ int gemv_i8_nparts(int n, int cu_count) {
     return (tiles + tpb - 1) / tpb;
 }
 
+// The current device's LDS limit per block (160 KB on gfx950, where a
+// kernel may take more than 64 KB of dynamic LDS), queried once per device.
+size_t max_lds_per_block() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 65536;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return static_cast<size_t>(v);
+}
+
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
                                 float* a_scales, int rule) {
     if (m == 0) return hipSuccess;
@@ -461,16 +487,32 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
     while (mc < m) mc <<= 1;
     const size_t lds_mfma = (static_cast<size_t>(16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) *
                             sizeof(int4);
-    if (m >= kMfmaMinRows && k % 256 == 0 && lds_mfma <= 65536 && !arg_keys && !ban_bits &&
+    // x rows of one pass (<= 16) + the waves' transpose tiles; + the static
+    // reduction buffer and scales
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    if (m >= kMfmaMinRows && k % 64 == 0 && lds_splitk + lds_splitk_static <= max_lds_per_block() && !arg_keys &&
+        !ban_bits &&
         k <= 256 * 4 * kSplitKMaxChunks && (n + 15) / 16 < 4 * (cu_count > 0 ? cu_count : 256)) {
         // small N: one 16-row tile per block, K split over the four waves
         const int grid = (n + 15) / 16;
         if (nparts_out) *nparts_out = grid;
+        const int cpw = ((k + 255) / 256 + 3) / 4;
         for (int r0 = 0; r0 < m; r0 += 16) {
             const int mr = m - r0 < 16 ? m - r0 : 16;
-            FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel, dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k,
-                        xq + static_cast<size_t>(r0) * k, a_scales + r0, mr, y + static_cast<size_t>(r0) * n,
-                        acc ? acc + static_cast<size_t>(r0) * n : nullptr);
+            const int8_t* xq_r = xq + static_cast<size_t>(r0) * k;
+            float* y_r = y + static_cast<size_t>(r0) * n;
+            int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
+            if (cpw <= 2)
+                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<2>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
+                            xq_r, a_scales + r0, mr, y_r, acc_r);
+            else if (cpw <= 4)
+                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<4>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
+                            xq_r, a_scales + r0, mr, y_r, acc_r);
+            else
+                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<8>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
+                            xq_r, a_scales + r0, mr, y_r, acc_r);
         }
         return hipGetLastError();
     }

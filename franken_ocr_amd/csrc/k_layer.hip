@@ -41,6 +41,7 @@ __device__ __forceinline__ double block_sum_sq(const float* __restrict__ r, int 
 
 // MODE 0: y = rms_norm(x) * w, then quantize_row_i8 (half away) -> xq, xs.
 // MODE 1: h = x + a (written), y = rms_norm(h) * w (written, f32).
+// MODE 2: y = rms_norm(x) * w (f32; w null: no weight).
 // One block per row; n <= 4096 (the row is staged in LDS).
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __restrict__ x,
@@ -65,6 +66,13 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __
     const float rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
     if (MODE == 1) {
         for (int i = threadIdx.x; i < n; i += kThreads) y[base + i] = (s_row[i] * rstd) * w[i];
+        return;
+    }
+    if (MODE == 2) {
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            const float v = s_row[i] * rstd;
+            y[base + i] = w ? v * w[i] : v;
+        }
         return;
     }
     float amax = 0.0f;
@@ -140,6 +148,13 @@ hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* 
                                     float eps, float* h, float* y) {
     if (n > 4096 || rows < 1) return hipErrorInvalidValue;
     FOCR_LAUNCH(rms_norm_rows_kernel<1>, dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, nullptr,
+                nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
+    if (n > 4096 || rows < 1) return hipErrorInvalidValue;
+    FOCR_LAUNCH(rms_norm_rows_kernel<2>, dim3(rows), dim3(kThreads), 0, s, x, nullptr, w, n, eps, nullptr, y, nullptr,
                 nullptr);
     return hipGetLastError();
 }

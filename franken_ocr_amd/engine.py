@@ -349,6 +349,12 @@ class RingCache:
             pass
 
 
+def rms_norm(x: DeviceArray, y: DeviceArray, w: DeviceArray | None = None, eps: float = 1e-6) -> None:
+    """nn::rms_norm (nn.rs:240-253) of the rows of x [rows, n] into y."""
+    rows, n = x.shape
+    _abi.call("focr_hip_rms_norm", x.ctx.handle, x.c_ptr, rows, n, _p(w), float(eps), y.c_ptr)
+
+
 class DecoderLayer:
     """One decoder layer for decode steps (decoder.rs:2542-2627 per stream,
     :2812-2933 batched): input RMSNorm, fused qkv GEMV, RoPE, ring write +

@@ -345,6 +345,13 @@ int32_t focr_hip_rswa_set_state(focr_hip_rswa* cache, size_t stream, uint32_t ri
 int32_t focr_hip_rswa_regions(const focr_hip_rswa* cache, size_t stream, float** ref_k,
                               float** ref_v, float** ring_k, float** ring_v);
 
+/* nn.rs:240-253 rms_norm over rows x [rows, n] f32 -> y (device pointers; w
+ * [n] device, nullable): y = (x * rstd) * w, rstd = 1 / sqrt(mean(x^2) + eps)
+ * with the sum of squares in f64. n <= 4096. The final norm before the LM
+ * head (lm_head_cached_i8, decoder.rs:2275-2296). */
+int32_t focr_hip_rms_norm(focr_hip_ctx* ctx, const float* x, size_t rows, size_t n, const float* w,
+                          float eps, float* y);
+
 /* ---- one decoder layer's decode step -------------------------------------
  * decoder.rs:2812-2933 batched_decode_step_i8_streams for one layer over every
  * stream of an R-SWA cache (decode_step_with_cache_i8, :2542-2627, per

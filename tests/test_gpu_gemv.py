@@ -25,7 +25,8 @@ def _weights(n, k, seed):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 896, 1280), (16, 896, 1280), (2, 1280, 896), (5, 3840, 1280),
-                                   (32, 100, 1280), (8, 17, 16)])
+                                   (32, 100, 1280), (8, 17, 16), (8, 1280, 6848), (20, 1280, 1792),
+                                   (3, 131, 3200), (1, 64, 8192)])
 def test_gemv_i8_bit_exact(ctx, m, n, k):
     from franken_ocr_amd.engine import QInt8, gemv_i8, gemv_i8_prequant, quantize_rows_i8
 
