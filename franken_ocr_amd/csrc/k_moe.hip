@@ -248,7 +248,12 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
 
 // Expert of this block: lane e loads expert e's 64-byte slot row (four
 // 16-byte loads in flight) and one ballot gives the set of experts with
-// pairs; the a-th set bit (a = blockIdx.x) is found with one more ballot.
+// pairs; the a-th set bit (a = blockIdx.y) is found with one more ballot.
+// The row block is blockIdx.x: with linear block id x + X y and blocks dealt
+// to the eight XCDs round-robin, an expert's row blocks spread over all of
+// them (X = 56 is a multiple of 8), where blockIdx.x = expert would put all of
+// an expert's weights through one XCD and leave the XCDs a whole expert
+// apart in load.
 // Shared mode is one expert whose pairs are the tokens. Slots past the number
 // of active experts get -1.
 __device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T) {
@@ -260,7 +265,7 @@ __device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T) {
                          (r3.x | r3.y | r3.z | r3.w);
     const unsigned long long m = __ballot(any != 0u);
     const int below = __popcll(m & ((1ull << lane) - 1ull));
-    const unsigned long long hit = __ballot(any != 0u && below == static_cast<int>(blockIdx.x));
+    const unsigned long long hit = __ballot(any != 0u && below == static_cast<int>(blockIdx.y));
     return hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
 }
 
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int C = H >> 4;
-    const int r = blockIdx.y * G + grp;
+    const int r = blockIdx.x * G + grp;
     const bool live = r < I;  // rows past I compute unused values from row 0
     const size_t row = static_cast<size_t>(e) * I + (live ? r : 0);
     int4 wgv[JC], wuv[JC];
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     const int wave = threadIdx.x >> 6;
     const int wl = threadIdx.x & 63;
     const int C = I >> 4;
-    const int r = blockIdx.y * G + grp;
+    const int r = blockIdx.x * G + grp;
     const bool live = r < H;  // rows past H compute unused values from row 0
     const size_t row = static_cast<size_t>(e) * H + (live ? r : 0);
     int4 wv[JC];
@@ -762,7 +767,7 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, 
     if (!dims_ok(d) || !sel || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
-    const dim3 grid(max_active, (inter + rows_per_block - 1) / rows_per_block);
+    const dim3 grid((inter + rows_per_block - 1) / rows_per_block, max_active);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
     const size_t lds = (static_cast<size_t>(staged) * d.hidden + 1023) & ~static_cast<size_t>(1023);
     const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
@@ -777,7 +782,7 @@ hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, con
     if (!dims_ok(d) || !sel || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
-    const dim3 grid(max_active, (d.hidden + rows_per_block - 1) / rows_per_block);
+    const dim3 grid((d.hidden + rows_per_block - 1) / rows_per_block, max_active);
     const size_t lds = static_cast<size_t>(kPairStage) * inter;
     const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
     if (lpr == 16) return launch_down_lpr<16>(s, grid, lds, jc, a, act, wd, sd, ybuf);
