@@ -256,13 +256,11 @@ int32_t focr_hip_gemv_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float
     int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
     float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
     if (!xq || !xs) return FOCR_HIP_E_OOM;
-    {
-        ProfScope ps(ctx, "quantize_rows");
-        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, false), "quantize launch");
-    }
+    // quantize_row_i8 + the GEMV (one launch where the rows fit the blocks'
+    // own quantization)
     ProfScope ps(ctx, "gemv_i8");
-    FOCR_HIP_TRY(launch_gemv_i8(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y, nullptr,
-                                nullptr, nullptr, ctx->cu_count),
+    FOCR_HIP_TRY(launch_gemv_i8_f32(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, x, nullptr, 0.0f, (int)m, y,
+                                    xq, xs, ctx->cu_count),
                  "gemv launch");
     return FOCR_HIP_OK;
 }
@@ -693,13 +691,12 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
             // (decoder.rs:1753-1754), with the GEMV's full-grid weight stream
             ProfScope ps(ctx, "moe_shared_down");
             const int SI = (int)L->shared_inter;
-            e = launch_quantize_rows(str, s.shared_act, (int)t, SI, s.shared_aq, s.shared_as, 0);
             const int rows = 57344 / SI < 32 ? 57344 / SI : 32;  // the GEMV's activation stage: m * k <= 56 KiB
             for (int r0 = 0; e == hipSuccess && r0 < (int)t; r0 += rows) {
                 const int mr = (int)t - r0 < rows ? (int)t - r0 : rows;
-                e = launch_gemv_i8(str, L->swd, L->ssd, (int)L->hidden, SI, s.shared_aq + (size_t)r0 * SI,
-                                   s.shared_as + r0, mr, s.shared_y + (size_t)r0 * L->hidden, nullptr, nullptr,
-                                   nullptr, ctx->cu_count);
+                e = launch_gemv_i8_f32(str, L->swd, L->ssd, (int)L->hidden, SI, s.shared_act + (size_t)r0 * SI,
+                                       nullptr, 0.0f, mr, s.shared_y + (size_t)r0 * L->hidden,
+                                       s.shared_aq + (size_t)r0 * SI, s.shared_as + r0, ctx->cu_count);
             }
         }
     }
@@ -1258,15 +1255,12 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     int8_t* xq = reinterpret_cast<int8_t*>(take(B * (H > D ? H : D)));
     float* xs = reinterpret_cast<float*>(take(B * 4));
     hipStream_t s = ctx->stream;
-    // 1. input RMSNorm + quantize_row_i8; 2. the fused qkv GEMV
-    {
-        ProfScope ps(ctx, "layer_norm_quant");
-        FOCR_HIP_TRY(launch_rms_norm_quant(s, x, L->input_ln, (int)B, (int)H, L->eps, xq, xs), "rms_norm launch");
-    }
+    // 1. input RMSNorm + quantize_row_i8 and 2. the fused qkv GEMV, in one
+    //    launch whose blocks norm and quantize the rows themselves
     {
         ProfScope ps(ctx, "layer_qkv");
-        FOCR_HIP_TRY(launch_gemv_i8(s, L->qkv->w, L->qkv->scales, (int)(3 * D), (int)H, xq, xs, (int)B, qkv, nullptr,
-                                    nullptr, nullptr, ctx->cu_count),
+        FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->qkv->w, L->qkv->scales, (int)(3 * D), (int)H, x, L->input_ln, L->eps,
+                                        (int)B, qkv, xq, xs, ctx->cu_count),
                      "qkv gemv launch");
     }
     // 3. RoPE at each stream's position, ring write, attention
@@ -1280,15 +1274,12 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     int32_t st = rswa_write_all(ctx, cache, k, v, nullptr);
     if (st) return st;
     if ((st = rswa_attend_all(ctx, cache, q, cx))) return st;
-    // 4. o_proj; 5. residual + post-attention RMSNorm
-    {
-        ProfScope ps(ctx, "layer_o_quant");
-        FOCR_HIP_TRY(launch_quantize_rows(s, cx, (int)B, (int)D, xq, xs, 0), "quantize launch");
-    }
+    // 4. quantize_row_i8 of the contexts + o_proj (one launch); 5. residual +
+    //    post-attention RMSNorm
     {
         ProfScope ps(ctx, "layer_o_proj");
-        FOCR_HIP_TRY(launch_gemv_i8(s, L->o_proj->w, L->o_proj->scales, (int)H, (int)D, xq, xs, (int)B, attn, nullptr,
-                                    nullptr, nullptr, ctx->cu_count),
+        FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->o_proj->w, L->o_proj->scales, (int)H, (int)D, cx, nullptr, 0.0f, (int)B,
+                                        attn, xq, xs, ctx->cu_count),
                      "o_proj gemv launch");
     }
     {
@@ -1308,17 +1299,15 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     float* act = reinterpret_cast<float*>(take(B * I * 4));
     int8_t* aq = reinterpret_cast<int8_t*>(take(B * I));
     ProfScope ps(ctx, "layer_dense_mlp");
-    FOCR_HIP_TRY(launch_quantize_rows(s, nrm, (int)B, (int)H, xq, xs, 0), "quantize launch");
-    FOCR_HIP_TRY(launch_gemv_i8(s, L->gate->w, L->gate->scales, (int)I, (int)H, xq, xs, (int)B, g, nullptr, nullptr,
-                                nullptr, ctx->cu_count),
+    FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->gate->w, L->gate->scales, (int)I, (int)H, nrm, nullptr, 0.0f, (int)B, g,
+                                    xq, xs, ctx->cu_count),
                  "dense gate launch");
-    FOCR_HIP_TRY(launch_gemv_i8(s, L->up->w, L->up->scales, (int)I, (int)H, xq, xs, (int)B, u, nullptr, nullptr,
-                                nullptr, ctx->cu_count),
+    FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->up->w, L->up->scales, (int)I, (int)H, nrm, nullptr, 0.0f, (int)B, u, xq,
+                                    xs, ctx->cu_count),
                  "dense up launch");
     FOCR_HIP_TRY(launch_silu_mul(s, g, u, act, B * I), "silu launch");
-    FOCR_HIP_TRY(launch_quantize_rows(s, act, (int)B, (int)I, aq, xs, 0), "quantize launch");
-    FOCR_HIP_TRY(launch_gemv_i8(s, L->down->w, L->down->scales, (int)H, (int)I, aq, xs, (int)B, attn, nullptr, nullptr,
-                                nullptr, ctx->cu_count),
+    FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->down->w, L->down->scales, (int)H, (int)I, act, nullptr, 0.0f, (int)B, attn,
+                                    aq, xs, ctx->cu_count),
                  "dense down launch");
     FOCR_HIP_TRY(launch_add_rows(s, h, attn, x, B * H), "residual launch");
     return FOCR_HIP_OK;

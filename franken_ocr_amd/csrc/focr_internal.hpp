@@ -208,6 +208,14 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
 int gemv_i8_nparts(int n, int cu_count);
 // The same GEMV with a per-row ban bitmap (ban_words u32 per row): a set bit
 // n writes y[i][n] = -inf and keys see -inf.
+// y = dequant(W . quantize_row_i8(x)) for m f32 rows x [m][k] (after
+// rms_norm with weight norm_w and eps when norm_w is non-null): for small N
+// and k <= 2048 one launch whose blocks quantize the rows themselves;
+// otherwise the norm / quantize kernel into xq_tmp [m][k] / xs_tmp [m], then
+// the GEMV. Any m >= 1 (rows in groups).
+hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
+                              const float* norm_w, float eps, int m, float* y, int8_t* xq_tmp, float* xs_tmp,
+                              int cu_count);
 hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
                                  const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                                  uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,

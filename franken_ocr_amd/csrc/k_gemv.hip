@@ -298,10 +298,67 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
 // (the weight pieces by a mask on the loaded data, the activation pieces
 // likewise), so they add nothing.
 constexpr int kSplitKMaxChunks = 8;  // per wave: K <= 32 * 256
-template <int CPW>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
+constexpr int kFqMaxK = 2048;  // f32-input form: a row's float4s held by one wave's lanes (8 per lane)
+
+// quantize_row_i8 (half away, reciprocal) of one f32 row held as float4
+// chunks c = lane + 64 j (zero past K4), after an RMSNorm when nw is set
+// (y = (x * rstd) * w, the sum of squares in f64), written as int8 into the
+// LDS stage row `dst`; returns the row's activation scale.
+template <int NF>
+__device__ __forceinline__ float fq_row_to_lds(const float4 (&v)[NF], const float4 (&wv)[NF], bool norm, float eps,
+                                               int K, int K4, int lane, int8_t* dst) {
+    float rstd = 1.0f;
+    if (norm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const double a = v[j].x, b = v[j].y, c = v[j].z, d = v[j].w;
+            ss = fma(a, a, ss);
+            ss = fma(b, b, ss);
+            ss = fma(c, c, ss);
+            ss = fma(d, d, ss);
+        }
+        ss = wave_sum_d(ss);
+        rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(K) + static_cast<double>(eps)));
+    }
+    float4 u[NF];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        u[j] = norm ? make_float4((v[j].x * rstd) * wv[j].x, (v[j].y * rstd) * wv[j].y, (v[j].z * rstd) * wv[j].z,
+                                  (v[j].w * rstd) * wv[j].w)
+                    : v[j];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(u[j].x), fabsf(u[j].y)), fmaxf(fabsf(u[j].z), fabsf(u[j].w))));
+    }
+    amax = wave_max_f(amax);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        const int c = lane + 64 * j;
+        if (c < K4) {
+            char4 q;
+            q.x = quant_i8(u[j].x, inv, false);
+            q.y = quant_i8(u[j].y, inv, false);
+            q.z = quant_i8(u[j].z, inv, false);
+            q.w = quant_i8(u[j].w, inv, false);
+            reinterpret_cast<char4*>(dst)[c] = q;
+        }
+    }
+    return a_scale;
+}
+
+// FQ: the activation rows come as f32 (xf [M][K], K <= kFqMaxK) and each
+// block quantizes them itself (after the RMSNorm with weight nw when nw is
+// set) while its weight loads are in flight — the separate norm / quantize
+// kernel and its kernel boundary go away. Every block computes the same bytes
+// and scales (the same operations in the same order), and they equal what
+// the quantize kernels give up to the f64 sum order of the norm.
+template <int CPW, bool FQ>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
-    const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out) {
+    const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out,
+    const float* __restrict__ xf, const float* __restrict__ nw, float eps) {
     extern __shared__ int4 lds_dyn[];  // x [M][K/16 + 1], then per-wave [16][16] chunks
     __shared__ v4i_m red[kThreads / 64][64];
     __shared__ float lds_as[16];
@@ -329,12 +386,51 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             rg[c][j] = make_int4(v.x & mm, v.y & mm, v.z & mm, v.w & mm);
         }
     }
-    const int4* x4 = reinterpret_cast<const int4*>(xq);
-    for (int i = threadIdx.x; i < M * C; i += kThreads) {  // only the M live rows; the rest read as zero
-        const int r = i / C, c = i - r * C;
-        lds_xv[r * xs + c] = x4[r * C + c];
+    if constexpr (FQ) {
+        constexpr int NF = kFqMaxK / 256;
+        const int K4 = K >> 2;
+        const float4* w4 = reinterpret_cast<const float4*>(nw);
+        float4 wv[NF];
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const int c = l + 64 * j;
+            wv[j] = nw ? w4[c < K4 ? c : K4 - 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // rows wave, wave + 4, ...: two rows' loads in flight at once
+        for (int r = wave; r < M; r += 2 * (kThreads / 64)) {
+            const int r2 = r + kThreads / 64;
+            const float4* x0 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r) * K);
+            const float4* x1 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r2 < M ? r2 : r) * K);
+            float4 v0[NF], v1[NF];
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                const int c = l + 64 * j;
+                const int cc = c < K4 ? c : K4 - 1;
+                const unsigned mk = c < K4 ? 0xFFFFFFFFu : 0u;
+                const float4 a = x0[cc], b = x1[cc];
+                v0[j] = make_float4(__uint_as_float(__float_as_uint(a.x) & mk), __uint_as_float(__float_as_uint(a.y) & mk),
+                                    __uint_as_float(__float_as_uint(a.z) & mk), __uint_as_float(__float_as_uint(a.w) & mk));
+                v1[j] = make_float4(__uint_as_float(__float_as_uint(b.x) & mk), __uint_as_float(__float_as_uint(b.y) & mk),
+                                    __uint_as_float(__float_as_uint(b.z) & mk), __uint_as_float(__float_as_uint(b.w) & mk));
+            }
+            const float s0 = fq_row_to_lds<NF>(v0, wv, nw != nullptr, eps, K, K4, l,
+                                               reinterpret_cast<int8_t*>(lds_xv + r * xs));
+            if (l == 0) lds_as[r] = s0;
+            if (r2 < M) {  // wave-uniform
+                const float s1 = fq_row_to_lds<NF>(v1, wv, nw != nullptr, eps, K, K4, l,
+                                                   reinterpret_cast<int8_t*>(lds_xv + r2 * xs));
+                if (l == 0) lds_as[r2] = s1;
+            }
+        }
+        if (threadIdx.x < 16 && threadIdx.x >= M) lds_as[threadIdx.x] = 0.0f;
+    } else {
+        const int4* x4 = reinterpret_cast<const int4*>(xq);
+        for (int i = threadIdx.x; i < M * C; i += kThreads) {  // only the M live rows; the rest read as zero
+            const int r = i / C, c = i - r * C;
+            lds_xv[r * xs + c] = x4[r * C + c];
+        }
+        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     }
-    if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     __syncthreads();
     v4i_m acc = {0, 0, 0, 0};
 #pragma unroll
@@ -468,6 +564,36 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int
     return hipGetLastError();
 }
 
+hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
+                              const float* norm_w, float eps, int m, float* y, int8_t* xq_tmp, float* xs_tmp,
+                              int cu_count) {
+    if (m < 1 || k <= 0) return hipErrorInvalidValue;
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    if (m >= kMfmaMinRows && k % 64 == 0 && k <= kFqMaxK && lds_splitk + lds_splitk_static <= max_lds_per_block() &&
+        (n + 15) / 16 < 4 * (cu_count > 0 ? cu_count : 256)) {
+        const int grid = (n + 15) / 16;
+        for (int r0 = 0; r0 < m; r0 += 16) {
+            const int mr = m - r0 < 16 ? m - r0 : 16;
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
+                        nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
+                        x + static_cast<size_t>(r0) * k, norm_w, eps);
+        }
+        return hipGetLastError();
+    }
+    // otherwise: the norm / quantize kernel, then the GEMV on the int8 rows
+    hipError_t e = norm_w ? launch_rms_norm_quant(s, x, norm_w, m, k, eps, xq_tmp, xs_tmp)
+                          : launch_quantize_rows(s, x, m, k, xq_tmp, xs_tmp, 0);
+    if (e != hipSuccess) return e;
+    for (int r0 = 0; r0 < m && e == hipSuccess; r0 += 32) {
+        const int mr = m - r0 < 32 ? m - r0 : 32;
+        e = launch_gemv_i8(s, w, ws, n, k, xq_tmp + static_cast<size_t>(r0) * k, xs_tmp + r0, mr,
+                           y + static_cast<size_t>(r0) * n, nullptr, nullptr, nullptr, cu_count);
+    }
+    return e;
+}
+
 hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
                           const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                           uint64_t* arg_keys, int* nparts_out, int cu_count) {
@@ -505,14 +631,14 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             float* y_r = y + static_cast<size_t>(r0) * n;
             int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
             if (cpw <= 2)
-                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<2>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
-                            xq_r, a_scales + r0, mr, y_r, acc_r);
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
             else if (cpw <= 4)
-                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<4>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
-                            xq_r, a_scales + r0, mr, y_r, acc_r);
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
             else
-                FOCR_LAUNCH(gemv_i8_mfma_splitk_kernel<8>, dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
-                            xq_r, a_scales + r0, mr, y_r, acc_r);
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
         }
         return hipGetLastError();
     }
