@@ -1236,7 +1236,7 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
         return fail(FOCR_HIP_E_SHAPE, fmt("decoder_layer_step: %zu streams outside 1..=%zu", B, max_b));
     const size_t I = L->gate ? L->gate->n : 0;
     // one scratch slot carved into the step's intermediates
-    const size_t fl = B * (3 * D + 3 * D + D + H + H + H) + (L->gate ? 3 * B * I : 0);
+    const size_t fl = B * (3 * D + D + D + H + H + H) + (L->gate ? 3 * B * I : 0);
     char* base = static_cast<char*>(ctx->scratch_get(kScrLayer, fl * 4 + B * H + B * I + 16 * 256));
     if (!base) return FOCR_HIP_E_OOM;
     auto take = [&](size_t bytes) {
@@ -1246,8 +1246,6 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     };
     float* qkv = reinterpret_cast<float*>(take(B * 3 * D * 4));
     float* q = reinterpret_cast<float*>(take(B * D * 4));
-    float* k = reinterpret_cast<float*>(take(B * D * 4));
-    float* v = reinterpret_cast<float*>(take(B * D * 4));
     float* cx = reinterpret_cast<float*>(take(B * D * 4));
     float* attn = reinterpret_cast<float*>(take(B * H * 4));
     float* h = reinterpret_cast<float*>(take(B * H * 4));
@@ -1268,12 +1266,23 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
         RopePositions rp{};
         for (size_t i = 0; i < B; ++i) rp.p[i] = positions[i];
         ProfScope ps(ctx, "layer_rope");
-        FOCR_HIP_TRY(launch_rope_split(s, qkv, rp, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, k, v),
+        // the ring write fused in: k and v go straight to each stream's next
+        // ring slot (the cursors advance as rswa_write_all's do)
+        for (size_t i = 0; i < B; ++i)
+            if (cache->prefill_len[i] < 0) return fail(FOCR_HIP_E_STATE, "rswa: write_decode_step before record_prefill");
+        RopeRing ring{};
+        ring.head_stride = static_cast<size_t>(kRingWindow) * kHeadDim;
+        for (size_t i = 0; i < B; ++i) {
+            const uint32_t slot = next_slot(cache, i);
+            ring.k[i] = cache->ring_k(i) + static_cast<size_t>(slot) * kHeadDim;
+            ring.v[i] = cache->ring_v(i) + static_cast<size_t>(slot) * kHeadDim;
+        }
+        FOCR_HIP_TRY(launch_rope_split(s, qkv, rp, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, nullptr,
+                                       nullptr, &ring),
                      "rope launch");
     }
-    int32_t st = rswa_write_all(ctx, cache, k, v, nullptr);
+    int32_t st = rswa_attend_all(ctx, cache, q, cx);
     if (st) return st;
-    if ((st = rswa_attend_all(ctx, cache, q, cx))) return st;
     // 4. quantize_row_i8 of the contexts + o_proj (one launch); 5. residual +
     //    post-attention RMSNorm
     {

@@ -275,8 +275,17 @@ struct RopePositions {
     static constexpr int kMax = 32;
     uint32_t p[kMax];
 };
+// Where the rotated k and the v rows go instead of contiguous k / v: stream
+// s's ring slot, head h at k[s] + h * head_stride (the R-SWA ring layout,
+// [head][W][head_dim] per stream, k[s] / v[s] already offset to the slot).
+struct RopeRing {
+    float* k[RopePositions::kMax];
+    float* v[RopePositions::kMax];
+    size_t head_stride;
+};
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
-                             int streams, int n_heads, int head_dim, float* q, float* k, float* v);
+                             int streams, int n_heads, int head_dim, float* q, float* k, float* v,
+                             const RopeRing* ring);
 hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n);
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n);
 // k_int4.hip

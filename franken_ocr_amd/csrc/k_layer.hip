@@ -95,12 +95,15 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __
 
 // One block per stream: the fused row qkv [3D] -> q, k rotated at
 // pos.p[s] (inv_freq [half], the reference's f64-then-f32 table) and v
-// copied, each [D] contiguous. Thread = (head, i < half) pairs. The
-// positions ride in the kernel arguments (no copy per step).
+// copied: q [D] contiguous; k and v [D] contiguous, or (ring.k[0] set)
+// straight into the stream's R-SWA ring slot — the ring write
+// (rswa.rs:451-466) fused in. Thread = (head, i < half) pairs. The positions
+// and slots ride in the kernel arguments (no copy per step).
 __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __restrict__ qkv, RopePositions pos,
                                                               const float* __restrict__ inv_freq, int n_heads,
                                                               int head_dim, float* __restrict__ q,
-                                                              float* __restrict__ k, float* __restrict__ v) {
+                                                              float* __restrict__ k, float* __restrict__ v,
+                                                              RopeRing ring) {
     const int s = blockIdx.x;
     const int D = n_heads * head_dim;
     const int half = head_dim >> 1;
@@ -115,10 +118,17 @@ __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __res
         const float ka = row[D + j0], kb = row[D + j1];
         q[static_cast<size_t>(s) * D + j0] = qa * cs - qb * sn;
         q[static_cast<size_t>(s) * D + j1] = qb * cs + qa * sn;
-        k[static_cast<size_t>(s) * D + j0] = ka * cs - kb * sn;
-        k[static_cast<size_t>(s) * D + j1] = kb * cs + ka * sn;
+        float* kr = ring.k[0] ? ring.k[s] + static_cast<size_t>(hd) * ring.head_stride
+                              : k + static_cast<size_t>(s) * D + static_cast<size_t>(hd) * head_dim;
+        kr[i] = ka * cs - kb * sn;
+        kr[i + half] = kb * cs + ka * sn;
     }
-    for (int j = threadIdx.x; j < D; j += kThreads) v[static_cast<size_t>(s) * D + j] = row[2 * D + j];
+    for (int j = threadIdx.x; j < D; j += kThreads) {
+        const int hd = j / head_dim, i = j - hd * head_dim;
+        float* vr = ring.v[0] ? ring.v[s] + static_cast<size_t>(hd) * ring.head_stride
+                              : v + static_cast<size_t>(s) * D + static_cast<size_t>(hd) * head_dim;
+        vr[i] = row[2 * D + j];
+    }
 }
 
 // act = silu(g) * u (decoder.rs:1746-1752), the dense MLP's SwiGLU.
@@ -160,10 +170,19 @@ hipError_t launch_rms_norm(hipStream_t s, const float* x, const float* w, int ro
 }
 
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
-                             int streams, int n_heads, int head_dim, float* q, float* k, float* v) {
+                             int streams, int n_heads, int head_dim, float* q, float* k, float* v,
+                             const RopeRing* ring) {
     if (head_dim % 2 || streams < 1 || streams > RopePositions::kMax) return hipErrorInvalidValue;
+    RopeRing r{};
+    if (ring) {
+        for (int i = 0; i < streams; ++i)
+            if (!ring->k[i] || !ring->v[i]) return hipErrorInvalidValue;
+        r = *ring;
+    } else if (!k || !v) {
+        return hipErrorInvalidValue;
+    }
     FOCR_LAUNCH(rope_split_kernel, dim3(streams), dim3(kThreads), 0, s, qkv, pos, inv_freq, n_heads, head_dim, q, k,
-                v);
+                v, r);
     return hipGetLastError();
 }
 
