@@ -1200,10 +1200,20 @@ int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n
     if (e == hipSuccess) e = hipMemcpy(L->input_ln, input_ln, hidden * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(L->post_ln, post_attn_ln, hidden * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(L->inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice);
+    // the qkv weights in RoPE pair order for the GEMV with the RoPE epilogue
+    const size_t qn = qkv->n, qk = qkv->k;
+    if (e == hipSuccess) e = hipMalloc(&L->qkv_rope_w, qn * qk);
+    if (e == hipSuccess) e = hipMalloc(&L->qkv_rope_s, qn * sizeof(float));
+    if (e == hipSuccess)
+        e = launch_permute_rows_i8(ctx->stream, qkv->w, qkv->scales, (int)qn, (int)qk, (int)(n_heads * head_dim),
+                                   (int)head_dim, L->qkv_rope_w, L->qkv_rope_s);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         hipFree(L->input_ln);
         hipFree(L->post_ln);
         hipFree(L->inv_freq);
+        hipFree(L->qkv_rope_w);
+        hipFree(L->qkv_rope_s);
         delete L;
         return hip_fail(e, "decoder_layer_create upload");
     }
@@ -1218,6 +1228,8 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* L) {
     hipFree(L->input_ln);
     hipFree(L->post_ln);
     hipFree(L->inv_freq);
+    hipFree(L->qkv_rope_w);
+    hipFree(L->qkv_rope_s);
     delete L;
     return FOCR_HIP_OK;
 }
@@ -1253,21 +1265,15 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     int8_t* xq = reinterpret_cast<int8_t*>(take(B * (H > D ? H : D)));
     float* xs = reinterpret_cast<float*>(take(B * 4));
     hipStream_t s = ctx->stream;
-    // 1. input RMSNorm + quantize_row_i8 and 2. the fused qkv GEMV, in one
-    //    launch whose blocks norm and quantize the rows themselves
-    {
-        ProfScope ps(ctx, "layer_qkv");
-        FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->qkv->w, L->qkv->scales, (int)(3 * D), (int)H, x, L->input_ln, L->eps,
-                                        (int)B, qkv, xq, xs, ctx->cu_count),
-                     "qkv gemv launch");
-    }
-    // 3. RoPE at each stream's position, ring write, attention
+    // 1. input RMSNorm + quantize_row_i8, 2. the fused qkv GEMV, 3. RoPE at
+    //    each stream's position and the ring write: k and v go straight to
+    //    each stream's next ring slot (the cursors advance as
+    //    rswa_write_all's do). One launch (blocks norm and quantize the rows
+    //    themselves, the epilogue rotates and scatters) where the shape
+    //    allows, else the GEMV and the RoPE kernel.
     {
         RopePositions rp{};
         for (size_t i = 0; i < B; ++i) rp.p[i] = positions[i];
-        ProfScope ps(ctx, "layer_rope");
-        // the ring write fused in: k and v go straight to each stream's next
-        // ring slot (the cursors advance as rswa_write_all's do)
         for (size_t i = 0; i < B; ++i)
             if (cache->prefill_len[i] < 0) return fail(FOCR_HIP_E_STATE, "rswa: write_decode_step before record_prefill");
         RopeRing ring{};
@@ -1277,9 +1283,26 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
             ring.k[i] = cache->ring_k(i) + static_cast<size_t>(slot) * kHeadDim;
             ring.v[i] = cache->ring_v(i) + static_cast<size_t>(slot) * kHeadDim;
         }
-        FOCR_HIP_TRY(launch_rope_split(s, qkv, rp, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q, nullptr,
-                                       nullptr, &ring),
-                     "rope launch");
+        hipError_t qe = hipErrorNotSupported;
+        if (L->qkv_rope_w) {
+            ProfScope ps(ctx, "layer_qkv_rope");
+            const RopeEpi epi{L->inv_freq, rp, ring, q, (int)D, (int)L->head_dim, 0};
+            qe = launch_qkv_rope_f32(s, L->qkv_rope_w, L->qkv_rope_s, (int)(3 * D), (int)H, x, L->input_ln, L->eps,
+                                     (int)B, epi, ctx->cu_count);
+            if (qe != hipErrorNotSupported) FOCR_HIP_TRY(qe, "qkv rope launch");
+        }
+        if (qe == hipErrorNotSupported) {
+            {
+                ProfScope ps(ctx, "layer_qkv");
+                FOCR_HIP_TRY(launch_gemv_i8_f32(s, L->qkv->w, L->qkv->scales, (int)(3 * D), (int)H, x, L->input_ln,
+                                                L->eps, (int)B, qkv, xq, xs, ctx->cu_count),
+                             "qkv gemv launch");
+            }
+            ProfScope ps(ctx, "layer_rope");
+            FOCR_HIP_TRY(launch_rope_split(s, qkv, rp, L->inv_freq, (int)B, (int)L->n_heads, (int)L->head_dim, q,
+                                           nullptr, nullptr, &ring),
+                         "rope launch");
+        }
     }
     int32_t st = rswa_attend_all(ctx, cache, q, cx);
     if (st) return st;

@@ -127,6 +127,10 @@ struct focr_hip_decoder_layer {
     const focr_hip_qint8* o_proj = nullptr;  // [hidden, n_heads * head_dim]
     const focr_hip_moe_layer* moe = nullptr;  // MoE MLP, or the dense one below
     const focr_hip_qint8 *gate = nullptr, *up = nullptr, *down = nullptr;
+    // qkv weights / scales with the q and k rows in RoPE pair order
+    // (qkv_rope_row), for the GEMV whose epilogue applies RoPE; owned
+    int8_t* qkv_rope_w = nullptr;
+    float* qkv_rope_s = nullptr;
 };
 
 struct focr_hip_moe_layer_i4 {
@@ -283,6 +287,34 @@ struct RopeRing {
     float* v[RopePositions::kMax];
     size_t head_stride;
 };
+// The qkv GEMV's RoPE epilogue: the weights' q and k rows are in the pair
+// order of qkv_rope_row (each 16-row tile holds 8 (i, i + half) pairs of one
+// head), rows >= 2 D in order; q goes to q [rows][D], k and v to the ring
+// slots; row i of the launch is stream r0 + i.
+struct RopeEpi {
+    const float* inv_freq;
+    RopePositions pos;
+    RopeRing ring;
+    float* q;
+    int d_model;   // D = n_heads * head_dim
+    int head_dim;
+    int r0;
+};
+// Original row of permuted qkv row p (p < 2 D: pairs; else p).
+__host__ __device__ inline int qkv_rope_row(int p, int D, int head_dim) {
+    if (p >= 2 * D) return p;
+    const int part = p / D, pl = p - part * D;
+    const int hd = pl / head_dim, pr = pl - hd * head_dim;
+    return part * D + hd * head_dim + (pr >> 1) + (pr & 1) * (head_dim >> 1);
+}
+hipError_t launch_permute_rows_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k, int D, int head_dim,
+                                  int8_t* w_out, float* ws_out);
+// qkv = quantized GEMV of the RMSNormed f32 rows (as launch_gemv_i8_f32) with
+// RoPE and the q / ring-slot scatter in the epilogue; hipErrorNotSupported
+// when the shape does not fit the one-launch form (the caller then runs the
+// GEMV and launch_rope_split).
+hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float* ws_perm, int n, int k,
+                               const float* x, const float* norm_w, float eps, int m, RopeEpi epi, int cu_count);
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
                              int streams, int n_heads, int head_dim, float* q, float* k, float* v,
                              const RopeRing* ring);

@@ -354,11 +354,15 @@ __device__ __forceinline__ float fq_row_to_lds(const float4 (&v)[NF], const floa
 // kernel and its kernel boundary go away. Every block computes the same bytes
 // and scales (the same operations in the same order), and they equal what
 // the quantize kernels give up to the f64 sum order of the norm.
-template <int CPW, bool FQ>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
+// ROPE (with FQ): W is the qkv weight in RoPE pair order; the epilogue
+// rotates each (i, i + half) pair — lanes col and col ^ 1 hold the two halves
+// of the same rows — with the RoPE kernel's expressions, and writes q to its
+// row and k / v to the streams' ring slots instead of y.
+template <int CPW, bool FQ, bool ROPE = false>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out,
-    const float* __restrict__ xf, const float* __restrict__ nw, float eps) {
+    const float* __restrict__ xf, const float* __restrict__ nw, float eps, RopeEpi re) {
     extern __shared__ int4 lds_dyn[];  // x [M][K/16 + 1], then per-wave [16][16] chunks
     __shared__ v4i_m red[kThreads / 64][64];
     __shared__ float lds_as[16];
@@ -463,6 +467,36 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         acc = v4i_m{acc[0] + o[0], acc[1] + o[1], acc[2] + o[2], acc[3] + o[3]};
     }
     const int n = n0 + col;
+    if constexpr (ROPE) {
+        const float wscale = ws[n < N ? n : N - 1];
+        const int D = re.d_model, hdim = re.head_dim, half = hdim >> 1;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = 4 * g + v;
+            const float yv = (static_cast<float>(acc[v]) * lds_as[i]) * wscale;
+            const float pv = __shfl_xor(yv, 1, 64);  // the pair partner: same rows, column col ^ 1
+            if (i >= M || n >= N) continue;
+            const int s = re.r0 + i;
+            if (n < 2 * D) {
+                const int part = n / D, pl = n - part * D;
+                const int hd = pl / hdim, pr = pl - hd * hdim;
+                const int ii = pr >> 1, b = pr & 1;
+                const float angle = static_cast<float>(re.pos.p[s]) * re.inv_freq[ii];
+                const float sn = sinf(angle), cs = cosf(angle);
+                // b = 0: a * cs - b * sn (a = mine); b = 1: b * cs + a * sn (b = mine)
+                const float o = b == 0 ? yv * cs - pv * sn : yv * cs + pv * sn;
+                const int j = ii + b * half;
+                if (part == 0)
+                    re.q[static_cast<size_t>(s) * D + hd * hdim + j] = o;
+                else
+                    re.ring.k[s][static_cast<size_t>(hd) * re.ring.head_stride + j] = o;
+            } else {
+                const int pl = n - 2 * D, hd = pl / hdim;
+                re.ring.v[s][static_cast<size_t>(hd) * re.ring.head_stride + (pl - hd * hdim)] = yv;
+            }
+        }
+        return;
+    }
     if (n >= N) return;
     const float wscale = ws[n];
 #pragma unroll
@@ -475,6 +509,20 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = av;
         }
     }
+}
+
+// Row p of the output = row qkv_rope_row(p) of w (and its scale): the qkv
+// weights in RoPE pair order, made once per decoder layer.
+__global__ __launch_bounds__(kThreads) void permute_rows_i8_kernel(const int8_t* __restrict__ w,
+                                                                  const float* __restrict__ ws, int k, int D,
+                                                                  int head_dim, int8_t* __restrict__ w_out,
+                                                                  float* __restrict__ ws_out) {
+    const int p = blockIdx.x;
+    const int src = qkv_rope_row(p, D, head_dim);
+    const int8_t* in = w + static_cast<size_t>(src) * k;
+    int8_t* out = w_out + static_cast<size_t>(p) * k;
+    for (int c = threadIdx.x; c < k; c += kThreads) out[c] = in[c];
+    if (threadIdx.x == 0) ws_out[p] = ws[src];
 }
 
 // One block per row: fold nparts keys -> the argmax index.
@@ -578,7 +626,7 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
             const int mr = m - r0 < 16 ? m - r0 : 16;
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
                         nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                        x + static_cast<size_t>(r0) * k, norm_w, eps);
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{});
         }
         return hipGetLastError();
     }
@@ -592,6 +640,37 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
                            y + static_cast<size_t>(r0) * n, nullptr, nullptr, nullptr, cu_count);
     }
     return e;
+}
+
+hipError_t launch_permute_rows_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k, int D, int head_dim,
+                                  int8_t* w_out, float* ws_out) {
+    if (n != 3 * D || head_dim % 2 || D % head_dim) return hipErrorInvalidValue;
+    FOCR_LAUNCH(permute_rows_i8_kernel, dim3(n), dim3(kThreads), 0, s, w, ws, k, D, head_dim, w_out, ws_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float* ws_perm, int n, int k,
+                               const float* x, const float* norm_w, float eps, int m, RopeEpi epi, int cu_count) {
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    const int D = epi.d_model;
+    if (m < kMfmaMinRows || m > RopePositions::kMax || k % 64 != 0 || k > kFqMaxK || n != 3 * D ||
+        epi.head_dim % 16 != 0 || D % epi.head_dim != 0 || !epi.q || !epi.inv_freq ||
+        lds_splitk + lds_splitk_static > max_lds_per_block() || (n + 15) / 16 >= 4 * (cu_count > 0 ? cu_count : 256))
+        return hipErrorNotSupported;
+    for (int i = 0; i < m; ++i)
+        if (!epi.ring.k[i] || !epi.ring.v[i]) return hipErrorInvalidValue;
+    const int grid = (n + 15) / 16;
+    for (int r0 = 0; r0 < m; r0 += 16) {
+        const int mr = m - r0 < 16 ? m - r0 : 16;
+        RopeEpi e = epi;
+        e.r0 = r0;
+        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w_perm,
+                    ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr, x + static_cast<size_t>(r0) * k, norm_w,
+                    eps, e);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
@@ -632,13 +711,13 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
             if (cpw <= 2)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
             else if (cpw <= 4)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f);
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
         }
         return hipGetLastError();
     }
