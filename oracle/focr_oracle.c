@@ -510,7 +510,7 @@ int oracle_s4s8_group_i32(const int8_t* a, const uint8_t* b_packed, size_t group
 }
 
 /* int4 prefill MoE: this build's composition (the reference has no int4
- * model wiring). Activations are quantized per row with the
+ * model wiring: no decoder layer loads int4 experts). Activations are quantized per row with the
  * prefill ties-even rule (decoder.rs:1647-1656); each projection is the int4
  * kernel contract (int4.rs:304-343) times the row's activation scale; the
  * grouped structure and ascending-expert scatter `out[t] += w * y` follow
