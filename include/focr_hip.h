@@ -363,8 +363,11 @@ int32_t focr_hip_rms_norm(focr_hip_ctx* ctx, const float* x, size_t rows, size_t
  * when one is set, or the dense SwiGLU MLP of layer 0), x = h + mlp.
  * RMSNorm: y = (x * rstd) * w, rstd from the f64 mean of squares + eps.
  * The layer borrows the weight handles (they must outlive it) and copies the
- * two norm weights (host pointers, [hidden]). Exactly one of moe or the three
- * dense handles. D = n_heads * head_dim must be 10 x 128 for the cache. */
+ * two norm weights (host pointers, [hidden]); it also keeps its own device
+ * copy of the qkv weights and scales with the q / k rows in RoPE pair order
+ * (3 D x hidden bytes), which the qkv GEMV with RoPE in its epilogue reads.
+ * Exactly one of moe or the three dense handles. D = n_heads * head_dim must
+ * be 10 x 128 for the cache. */
 int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n_heads, size_t head_dim,
                                       const float* input_ln, const float* post_attn_ln,
                                       const focr_hip_qint8* qkv, const focr_hip_qint8* o_proj,
