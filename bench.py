@@ -42,6 +42,20 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: logical CPUs (nproc) and the model
+    string from /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
 def traffic_for(kernel: str, workload: str):
     """HBM bytes per launch measured with rocprofv3 --pmc: FETCH_SIZE and
     WRITE_SIZE (one run each) scaled by what the same counters read for a
@@ -188,8 +202,10 @@ def cpu_moe(args, inputs):
         if time.perf_counter() - t0 >= args.cpu_seconds or n >= 2000:
             break
     el = time.perf_counter() - t0
+    st, want, want_idx, _ = pyoracle.moe_decode(hidden, router, wg, sg, wu, su, wd, sd, E, K, I, norm_topk=True)
+    same = st == 0 and np.array_equal(out, want.reshape(-1)) and np.array_equal(idx, want_idx.reshape(-1))
     return {"value": round(T * n / el, 2), "unit": "tokens/s", "cores": min(K, os.cpu_count() or 1),
-            "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+            "kind": "port", "tier": L.cpu_tier_feature(tier).decode(), "matches_oracle": bool(same),
             "sample": f"{n} MoE decode steps of T={T} tokens (first layer copy), {el:.1f} s; "
                       f"top-{K} experts as concurrent single-thread tasks, tokens sequential (decoder.rs:2231-2252)"}
 
@@ -271,8 +287,10 @@ def cpu_lm_head(args, inputs):
         L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am))
         n += 1
     el = time.perf_counter() - t0
+    want_l, want_a = pyoracle.lm_head_i8(x, w, s, N, Kd)
+    same = np.array_equal(logits, want_l.reshape(-1)) and np.array_equal(am, want_a)
     return {"value": round(M * n / el, 2), "unit": "tokens/s", "cores": int(L.cpu_threads()), "kind": "port",
-            "tier": L.cpu_tier_feature(tier).decode(),
+            "tier": L.cpu_tier_feature(tier).decode(), "matches_oracle": bool(same),
             "sample": f"{n} LM-head GEMV+argmax calls of M={M} rows, {el:.1f} s; 64-row blocks over all threads"}
 
 
@@ -831,6 +849,7 @@ def main() -> int:
     if cpu is not None and not args.no_cpu and cpu_inputs is not None:
         log("cpu baseline (reference x86 int8 tier restated in C) ...")
         line["cpu_baseline"] = cpu(args, cpu_inputs)
+        line["cpu_baseline"].update(host_cpu())
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

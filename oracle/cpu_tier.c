@@ -27,6 +27,23 @@ int cpu_detect_tier(void) {
     return CPU_TIER_SCALAR;
 }
 
+/* 1 if this host can run the given tier's kernels (each tier needs its own
+ * ISA extensions; a lower tier is not implied by a higher one for avxvnni). */
+int cpu_tier_available(int tier) {
+    __builtin_cpu_init();
+    switch (tier) {
+    case CPU_TIER_SCALAR: return 1;
+    case CPU_TIER_AVX2: return __builtin_cpu_supports("avx2") != 0;
+#if defined(__GNUC__) && (__GNUC__ >= 11)
+    case CPU_TIER_AVXVNNI: return __builtin_cpu_supports("avxvnni") != 0;
+#endif
+    case CPU_TIER_AVX512VNNI:
+        return __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw") &&
+               __builtin_cpu_supports("avx512f");
+    default: return 0;
+    }
+}
+
 const char* cpu_tier_tag(int tier) {
     static const char* t[] = {"scalar", "avx2", "avxvnni", "avx512vnni"};
     return (tier >= 0 && tier <= 3) ? t[tier] : "scalar";

@@ -26,6 +26,8 @@ enum { CPU_TIER_SCALAR = 0, CPU_TIER_AVX2 = 1, CPU_TIER_AVXVNNI = 2, CPU_TIER_AV
 
 /* Best tier available on this host, in the reference's order. */
 int cpu_detect_tier(void);
+/* 1 if this host supports the tier's instructions. */
+int cpu_tier_available(int tier);
 const char* cpu_tier_tag(int tier);          /* "avx512vnni", ... */
 const char* cpu_tier_feature(int tier);      /* "x86_64+avx512vnni", ... */
 /* Thread pool size (defaults to all logical CPUs; 0 keeps the default). */

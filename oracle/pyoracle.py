@@ -57,6 +57,7 @@ _SIGS = {
     "oracle_ring_write": ([_P, _P, _P, _P, _P, _P, _P], C.c_int),
     "oracle_decode_attention": ([_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P], C.c_int),
     "cpu_detect_tier": ([], C.c_int),
+    "cpu_tier_available": ([C.c_int], C.c_int),
     "cpu_tier_tag": ([C.c_int], C.c_char_p),
     "cpu_tier_feature": ([C.c_int], C.c_char_p),
     "cpu_set_threads": ([C.c_int], C.c_int),

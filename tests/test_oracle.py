@@ -414,16 +414,109 @@ def test_quantize_int8_known_answers():
     assert q.tolist() == [-127, 127]
 
 
-def test_pack_int4_roundtrip(rng):
-    n, k, g = 3, 64, 32
-    w = rng.standard_normal(n * k).astype(np.float32)
-    st, packed, s = O.pack_int4_f32(w, n, k, g)
+def _pack_codes(w, n, k, g):
+    st, packed, s = O.pack_int4_f32(np.asarray(w, np.float32), n, k, g)
     assert st == 0
-    _, q = O.unpack_to_i8(packed, n, k)
-    assert q.min() >= -8 and q.max() <= 7
-    deq = q.reshape(n, k // g, g).astype(np.float32) * s.reshape(n, k // g, 1)
-    err = np.abs(deq.reshape(-1) - w)
-    assert np.all(err <= np.repeat(s, g) * 0.5 + 1e-6)
+    return packed, s, O.unpack_to_i8(packed, n, k)[1]
+
+
+def test_pack_int4_known_answers():
+    # quant/int4.rs:344-360 exact_int4_values_roundtrip_with_unit_scale
+    vals = [7.0, -7.0, 0.0, 1.0, -1.0, 3.0, -3.0, 6.0, -6.0, 2.0, -2.0, 4.0, -4.0, 5.0, -5.0, 7.0]
+    packed, s, codes = _pack_codes(vals, 1, 16, 16)
+    assert s.tolist() == [1.0] and codes.tolist() == [int(v) for v in vals]
+    # :362-373 packed_and_scale_counts_match_layout
+    packed, s, _ = _pack_codes(np.ones(64), 2, 32, 16)
+    assert packed.size == 32 and s.size == 4
+    assert _pack_codes(np.ones(64), 2, 32, 32)[1].size == 2
+    # :375-390 per_group_scales_are_independent: -7/2 = -3.5 -> ties-even -> -4
+    w = np.zeros(32, np.float32)
+    w[0], w[16], w[17] = 7.0, 14.0, -7.0
+    _, s, codes = _pack_codes(w, 1, 32, 16)
+    assert s.tolist() == [1.0, 2.0] and (codes[0], codes[16], codes[17]) == (7, 7, -4)
+    # :392-399 all_zero_group_unit_scale_no_nan
+    _, s, codes = _pack_codes(np.zeros(16), 1, 16, 16)
+    assert s.tolist() == [1.0] and not codes.any()
+    # :401-414 clamps: 16/(16/7) -> 7, -16/(16/7) -> -7
+    w = np.zeros(16, np.float32)
+    w[0], w[1] = 16.0, -16.0
+    _, s, codes = _pack_codes(w, 1, 16, 16)
+    assert (codes[0], codes[1]) == (7, -7) and codes.min() >= -8 and codes.max() <= 7
+    # :425-439 unpack_is_exact_inverse_of_pack_nibbles: low nibble = even column
+    vals = [-8.0, 7.0, -1.0, 1.0, -8.0, -8.0, 7.0, 7.0, 0.0, 0.0, -4.0, 4.0, -2.0, 2.0, -6.0, 6.0]
+    packed, _, codes = _pack_codes(vals, 1, 16, 16)
+    for j in range(8):
+        assert packed[j] == ((int(codes[2 * j]) & 0xF) | ((int(codes[2 * j + 1]) & 0xF) << 4))
+    # :441-455 multi_row_packing_indexes_rows_correctly: -8/(8/7) = -7
+    w = np.concatenate([np.full(16, 7.0), np.full(16, -8.0)])
+    _, s, codes = _pack_codes(w, 2, 16, 16)
+    assert (codes[:16] == 7).all() and (codes[16:] == -7).all()
+    assert s[0] == 1.0 and s[1] == np.float32(8.0) / np.float32(7.0)
+    # ties at unit scale split the rounding rules: 2.5 -> 2 and 0.5 -> 0 (ties-even),
+    # where half-away-from-zero would give 3 and 1
+    w = np.zeros(16, np.float32)
+    w[:6] = [7.0, 2.5, 0.5, -0.5, -2.5, 1.5]
+    _, _, codes = _pack_codes(w, 1, 16, 16)
+    assert codes[:6].tolist() == [7, 2, 0, 0, -2, 2]
+    assert O.pack_int4_f32(np.zeros(16, np.float32), 1, 16, 8)[0] != 0  # :459 "must be 16 or 32"
+    assert O.pack_int4_f32(np.zeros(24, np.float32), 1, 24, 16)[0] != 0  # :465 "must divide k"
+
+
+def _np_pack_int4(w, n, k, g):
+    """pack_int4_f32 restated from its documented contract (int4.rs:130-205):
+    scale = max|group| / 7 (1.0 for an all-zero group), q = clamp(RNE(w / scale)
+    with true f32 division, -8, 7), low nibble = even column."""
+    w = np.asarray(w, np.float32).reshape(n, k // g, g)
+    mx = np.abs(w).max(axis=2)
+    s = np.where(mx == 0, np.float32(1), (mx / np.float32(7)).astype(np.float32)).astype(np.float32)
+    q = np.clip(np.rint((w / s[:, :, None]).astype(np.float32)), -8, 7).astype(np.int64).reshape(n, k)
+    nib = q & 0xF
+    return (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8).reshape(-1), s.reshape(-1)
+
+
+def _planted_division_ties(rng, count):
+    """Groups whose values sit exactly on a .5 code boundary under true division
+    but not under a reciprocal multiply (w * (1/s)): a reciprocal-multiply
+    packer gives a different code for at least one of them."""
+    found = []
+    while len(found) < count:
+        mx = np.float32(rng.uniform(0.5, 40.0))
+        s = np.float32(mx / np.float32(7))
+        inv = np.float32(np.float32(1) / s)
+        for c in range(-7, 7):
+            x = np.float32((c + 0.5) * s)
+            if np.float32(x / s) == np.float32(c + 0.5) and np.rint(np.float32(x * inv)) != np.rint(np.float32(x / s)):
+                found.append((mx, x))
+                break
+    return found
+
+
+@pytest.mark.parametrize("n,k,g", [(3, 64, 32), (5, 96, 16), (7, 1280, 32), (4, 896, 32)])
+def test_pack_int4_matches_numpy_restatement(n, k, g, rng):
+    w = (rng.standard_normal(n * k) * rng.uniform(0.01, 3.0)).astype(np.float32)
+    # plant exact .5 ties at unit scale (group max 7) and division-only ties in
+    # further groups, plus one all-zero group
+    w[:g] = 0.0
+    w[0], w[1], w[2] = 7.0, 2.5, -0.5
+    for i, (mx, x) in enumerate(_planted_division_ties(rng, 2)):
+        base = (i + 1) * g
+        w[base:base + g] = 0.0
+        w[base], w[base + 1] = mx, x
+    if n * k // g > 3:
+        w[3 * g:4 * g] = 0.0
+    st, packed, s = O.pack_int4_f32(w, n, k, g)
+    want_p, want_s = _np_pack_int4(w, n, k, g)
+    assert st == 0 and np.array_equal(s, want_s) and np.array_equal(packed, want_p)
+    # the planted cases discriminate: half-away or reciprocal rounding packs differently
+    grp = w.reshape(-1, g)
+    sc = want_s.reshape(-1)
+    half_away = np.clip(np.sign(grp / sc[:, None]) * np.floor(np.abs(grp / sc[:, None]) + 0.5), -8, 7)
+    recip = np.clip(np.rint(grp * (np.float32(1) / sc)[:, None].astype(np.float32)), -8, 7)
+    codes = O.unpack_to_i8(packed, n, k)[1].reshape(-1, g)
+    assert not np.array_equal(codes, half_away) and not np.array_equal(codes, recip)
+    # and the dequantized codes stay within half a step of the input
+    deq = codes.astype(np.float32) * sc[:, None]
+    assert np.all(np.abs(deq - grp) <= sc[:, None] * (0.5 + 1e-6))
 
 
 # ---- R-SWA ring + attention (src/native_engine/rswa.rs) ------------------------------------
@@ -615,6 +708,181 @@ def test_moe_prefill_i8_ascending_expert_scatter_and_shared(rng):
     bad = idx.copy()
     bad[0, 0] = E
     assert O.moe_prefill_i8(x, bad, gates, wg, sg, wu, su, wd, sd, E, inter)[0] != 0
+
+
+def _np_moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, E, inter):
+    """moe_block_i8's grouped structure (decoder.rs:2142-2181) over int4 experts,
+    restated in numpy from the pinned pieces' specs: ties-even reciprocal
+    quantize of x (decoder.rs:1647-1656), the packed int4 GEMM spec (int4.rs:
+    304-343, `_spec_s4s8`), f32 SiLU·up, act re-quantized ties-even, the down
+    product scaled by the act scale, and the scatter `out[t] += w·y` in
+    ascending expert order with a token's slots in slot order."""
+    t, h = x.shape
+    silu = np.vectorize(lambda v: O.lib().oracle_silu(float(v)), otypes=[np.float32])
+    xq = [_np_quant(x[r], ties_even=True) for r in range(t)]
+    gi, gh = inter // group, h // group
+    out = np.zeros((t, h), np.float32)
+    for e in range(E):
+        wg_e, wu_e = wg[e * inter * h // 2:(e + 1) * inter * h // 2], wu[e * inter * h // 2:(e + 1) * inter * h // 2]
+        wd_e = wd[e * h * inter // 2:(e + 1) * h * inter // 2]
+        for r in range(t):
+            slots = [j for j in range(idx.shape[1]) if idx[r, j] == e]
+            if not slots:
+                continue
+            q, xs = xq[r]
+            g = _spec_s4s8(q, wg_e, sg[e * inter * gh:(e + 1) * inter * gh], group, 1, h, inter)[0]
+            u = _spec_s4s8(q, wu_e, su[e * inter * gh:(e + 1) * inter * gh], group, 1, h, inter)[0]
+            act = (silu((g * xs).astype(np.float32)) * (u * xs).astype(np.float32)).astype(np.float32)
+            aq, as2 = _np_quant(act, ties_even=True)
+            y = _spec_s4s8(aq, wd_e, sd[e * h * gi:(e + 1) * h * gi], group, 1, inter, h)[0]
+            yv = (y * as2).astype(np.float32)
+            for j in slots:
+                out[r] = (out[r] + (np.float32(gates[r, j]) * yv).astype(np.float32)).astype(np.float32)
+    return out
+
+
+def _f64_moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, E, inter):
+    """The same layer in float64 from the integer codes (int64 dot products,
+    float64 group scaling, SwiGLU, down projection and gate-weighted sum):
+    catches a dropped scale or a transposed operand, independent of f32 order."""
+    t, h = x.shape
+
+    def codes(packed, n, k):
+        pk = packed.reshape(n, k // 2).astype(np.int64)
+        b = np.zeros((n, k), np.int64)
+        b[:, 0::2] = np.where((pk & 0xF) >= 8, (pk & 0xF) - 16, pk & 0xF)
+        b[:, 1::2] = np.where((pk >> 4) >= 8, (pk >> 4) - 16, pk >> 4)
+        return b
+
+    def gemv(a, packed, scales, k, n):
+        b = codes(packed, n, k).reshape(n, k // group, group)
+        parts = (b * a.astype(np.int64).reshape(1, k // group, group)).sum(axis=2)
+        return (parts * scales.reshape(n, k // group).astype(np.float64)).sum(axis=1)
+
+    def quant(v):
+        amax = np.abs(v).max()
+        s = amax / 127.0 if amax > 0 else 1.0
+        return np.clip(np.rint(v / s), -127, 127), s
+
+    out = np.zeros((t, h))
+    gi, gh = inter // group, h // group
+    for r in range(t):
+        q, xs = quant(x[r].astype(np.float64))
+        for j in range(idx.shape[1]):
+            e = int(idx[r, j])
+            g = gemv(q, wg[e * inter * h // 2:(e + 1) * inter * h // 2], sg[e * inter * gh:(e + 1) * inter * gh],
+                     h, inter) * xs
+            u = gemv(q, wu[e * inter * h // 2:(e + 1) * inter * h // 2], su[e * inter * gh:(e + 1) * inter * gh],
+                     h, inter) * xs
+            act = g / (1.0 + np.exp(-g)) * u
+            aq, as2 = quant(act)
+            y = gemv(aq, wd[e * h * inter // 2:(e + 1) * h * inter // 2], sd[e * h * gi:(e + 1) * h * gi], inter,
+                     h) * as2
+            out[r] += float(gates[r, j]) * y
+    return out
+
+
+@pytest.mark.parametrize("group", [16, 32])
+def test_moe_prefill_i4_matches_restatements(group, rng):
+    h, inter, E, K, t = 64, 32, 8, 3, 10
+    wg = rng.integers(0, 256, E * inter * h // 2).astype(np.uint8)
+    wu = rng.integers(0, 256, E * inter * h // 2).astype(np.uint8)
+    wd = rng.integers(0, 256, E * h * inter // 2).astype(np.uint8)
+    sg = rng.uniform(1e-3, 2e-2, E * inter * (h // group)).astype(np.float32)
+    su = rng.uniform(1e-3, 2e-2, E * inter * (h // group)).astype(np.float32)
+    sd = rng.uniform(1e-3, 2e-2, E * h * (inter // group)).astype(np.float32)
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    # row 2 has scale 1 (max 127) and exact .5 ties: ties-even codes 2, 0, -2, where
+    # half-away-from-zero gives 3, 1, -3
+    x[2, :5] = [127.0, 2.5, 0.5, -2.5, 1.5]
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(t)]).astype(np.uint32)
+    idx[4] = [6, 6, 1]  # a token routed twice to one expert: both slots are members
+    gates = rng.uniform(0.05, 1.0, (t, K)).astype(np.float32)
+    st, out, xq, xs = O.moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, E, inter)
+    assert st == 0
+    assert xq[2, :5].tolist() == [127, 2, 0, -2, 2] and xs[2] == 1.0
+    assert not np.array_equal(xq[2], _np_quant(x[2], ties_even=False)[0])
+    want = _np_moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, E, inter)
+    assert np.array_equal(out, want)
+    # the scatter order is observable: summing a token's experts in slot order
+    # instead of ascending expert order changes the f32 result somewhere
+    swapped = idx.copy()
+    order = np.argsort(-idx.astype(np.int64), axis=1, kind="stable")
+    swapped = np.take_along_axis(idx, order, axis=1)
+    swapped_g = np.take_along_axis(gates, order, axis=1)
+    by_slot = np.zeros_like(out)
+    for r in range(t):
+        one = [_np_moe_prefill_i4(x[r:r + 1], swapped[r:r + 1, j:j + 1], swapped_g[r:r + 1, j:j + 1], group, wg, sg,
+                                  wu, su, wd, sd, E, inter)[0] for j in range(K)]
+        for y in one:
+            by_slot[r] = (by_slot[r] + y).astype(np.float32)
+    assert not np.array_equal(by_slot, out)
+    want64 = _f64_moe_prefill_i4(x, idx, gates, group, wg, sg, wu, su, wd, sd, E, inter)
+    scale = np.abs(want64).max(axis=1, keepdims=True)
+    # f32 rounding plus an occasional one-code flip of a re-quantized act value
+    assert np.max(np.abs(out - want64) / scale) < 2e-2
+    bad = idx.copy()
+    bad[0, 0] = E
+    assert O.moe_prefill_i4(x, bad, gates, group, wg, sg, wu, su, wd, sd, E, inter)[0] != 0
+
+
+def test_moe_prefill_i4_hand_case():
+    # 1 token, 2 experts of width 16 (group 16), every weight nibble 1, unit
+    # group scales. x = [127, 0, ...] -> xq = x, scale 1: gate = up = 127 for
+    # every row; act = silu(127)*127 on every row -> aq = 127, as2 = act/127;
+    # down = 16 * 127 per output; y = 16 * act. Gates 0.25 and 0.5 on experts 1, 0
+    # -> out = 0.75 * 16 * act per column.
+    h = inter = 16
+    ones = np.full(inter * h // 2, 0x11, np.uint8)
+    wg = np.concatenate([ones, ones])
+    x = np.zeros((1, h), np.float32)
+    x[0, 0] = 127.0
+    s = np.ones(2 * inter, np.float32)
+    idx = np.array([[1, 0]], np.uint32)
+    gates = np.array([[0.25, 0.5]], np.float32)
+    st, out, xq, xs = O.moe_prefill_i4(x, idx, gates, 16, wg, s, wg, s, wg, s, 2, inter)
+    assert st == 0 and xs[0] == 1.0 and xq[0, 0] == 127
+    act = 127.0 / (1.0 + math.exp(-127.0)) * 127.0
+    np.testing.assert_allclose(out[0], np.full(h, 0.75 * 16 * act), rtol=1e-6)
+
+
+def test_moe_prefill_i4_act_requant_is_ties_even(rng):
+    # Exact .5 ties in the SiLU·up row, so the act re-quantization's rounding
+    # rule is observable. x = [127, 1, 0...] -> xq = x, scale 1; gate/up row i
+    # reads nibbles (n0, n1) of columns 0, 1, so acc = 127·n0 + n1 and, with
+    # power-of-two scales, g and u are exact. silu(g) == g in f32 for g >= 32.
+    # act = [127, 2.5, 0.5, -2.5, 1.5, 0...] -> scale 1, codes [127, 2, 0, -2, 2]
+    # (half-away-from-zero would give [127, 3, 1, -3, 2]).
+    h, inter, group = 32, 16, 16
+    gi, gh = inter // group, h // group
+    wg = np.zeros((inter, h // 2), np.uint8)
+    wu = np.zeros((inter, h // 2), np.uint8)
+    sg = np.ones((inter, gh), np.float32)
+    su = np.ones((inter, gh), np.float32)
+    wg[0, 0], wu[0, 0] = 0x01, 0x10  # g = 127, u = 1 -> act 127
+    for i, n1 in zip(range(1, 5), (5, 1, -5, 3)):
+        wg[i, 0] = 0x11  # acc 128, scale 1/4 -> g = 32
+        sg[i, 0] = 0.25
+        wu[i, 0] = (n1 & 0xF) << 4  # acc n1, scale 1/64
+        su[i, 0] = 1.0 / 64.0
+    wd = rng.integers(0, 256, h * inter // 2).astype(np.uint8)
+    sd = rng.uniform(1e-3, 2e-2, h * gi).astype(np.float32)
+    x = np.zeros((1, h), np.float32)
+    x[0, :2] = [127.0, 1.0]
+    idx = np.array([[0]], np.uint32)
+    gates = np.array([[0.5]], np.float32)
+    st, out, _, _ = O.moe_prefill_i4(x, idx, gates, group, wg.reshape(-1), sg.reshape(-1), wu.reshape(-1),
+                                     su.reshape(-1), wd, sd, 1, inter)
+    assert st == 0
+
+    def down(codes):
+        aq = np.zeros(inter, np.int8)
+        aq[:5] = codes
+        y = _spec_s4s8(aq, wd, sd, group, 1, inter, h)[0]
+        return (np.float32(0.5) * y).astype(np.float32)
+
+    assert np.array_equal(out[0], down([127, 2, 0, -2, 2]))
+    assert not np.array_equal(out[0], down([127, 3, 1, -3, 2]))
 
 
 # ---- decode-layer ops: RMSNorm, RoPE, the layer step ------------------------------------
