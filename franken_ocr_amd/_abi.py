@@ -76,6 +76,8 @@ _SIGS: dict[str, list] = {
     "focr_hip_moe_layer_set_shared": [_P, _SZ, _P, _P, _P, _P, _P, _P, _I32],
     "focr_hip_moe_layer_free": [_P],
     "focr_hip_moe_decode": [_P, _P, _P, _SZ, _I32, _F32, _I32, _P, _P, _P, _I32],
+    "focr_hip_moe_decode_noalloc": [_P, _P, _P, _SZ, _I32, _F32, _I32, _P, _P, _P, _I32],
+    "focr_hip_static_scratch_bytes": [],
     "focr_hip_moe_route": [_P, _P, _P, _SZ, _I32, _F32, _P, _P, _P],
     "focr_hip_moe_layer_i4_create": [_P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _I32, _P],
     "focr_hip_moe_layer_i4_free": [_P],
@@ -125,7 +127,8 @@ _SIGS: dict[str, list] = {
     "focr_hip_prof_read": [_P, C.c_char_p, _SZ],
 }
 
-_RESTYPE = {"focr_hip_last_error": C.c_char_p, "focr_hip_version": C.c_char_p}
+_RESTYPE = {"focr_hip_last_error": C.c_char_p, "focr_hip_version": C.c_char_p,
+            "focr_hip_static_scratch_bytes": C.c_size_t}
 
 
 class ExtensionMissing(RuntimeError):

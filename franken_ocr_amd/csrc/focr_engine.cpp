@@ -582,23 +582,41 @@ struct MoeScratch {
     void* sel;
 };
 
-int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
+// Where an entry point's intermediates live: the context's grow-only slots
+// (hipMalloc when a slot grows), or consecutive 256-byte aligned pieces of
+// the static per-device array (never allocates). In counting mode nothing is
+// handed out for use: `used` totals the bytes a call would carve.
+struct ScratchSource {
+    focr_hip_ctx* ctx = nullptr;
+    char* base = nullptr;  // the static array; null selects the context's slots
+    size_t cap = 0, used = 0;
+    bool counting = false;
+    void* get(int slot, size_t bytes) {
+        if (!base && !counting) return ctx->scratch_get(slot, bytes);
+        const size_t off = (used + 255) & ~static_cast<size_t>(255);
+        used = off + (bytes ? bytes : 16);
+        if (counting) return reinterpret_cast<void*>(static_cast<uintptr_t>(256));  // placeholder, never dereferenced
+        return used <= cap ? base + off : nullptr;
+    }
+};
+
+int32_t moe_scratch(ScratchSource& src, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
     const size_t pairs = t * L->top_k;
     const size_t sel_off = (pairs * 8 + 255) & ~static_cast<size_t>(255);
-    char* route = static_cast<char*>(ctx->scratch_get(kScrRoute, sel_off + moe_sel_bytes()));
-    s->xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
-    s->xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
-    s->act = static_cast<float*>(ctx->scratch_get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
-    char* shb = with_shared ? static_cast<char*>(ctx->scratch_get(
+    char* route = static_cast<char*>(src.get(kScrRoute, sel_off + moe_sel_bytes()));
+    s->xq = static_cast<int8_t*>(src.get(kScrXq, t * L->hidden));
+    s->xs = static_cast<float*>(src.get(kScrXs, t * sizeof(float)));
+    s->act = static_cast<float*>(src.get(kScrAct, (pairs * L->inter + (with_shared ? t * L->shared_inter : 0)) * sizeof(float)));
+    char* shb = with_shared ? static_cast<char*>(src.get(
                                   kScrShared, t * L->hidden * sizeof(float) + 256 + t * L->shared_inter + 256 + t * 4))
                             : nullptr;
     s->shared_y = reinterpret_cast<float*>(shb);
     s->shared_aq = shb ? reinterpret_cast<int8_t*>(shb + ((t * L->hidden * sizeof(float) + 255) & ~size_t(255))) : nullptr;
     s->shared_as = shb ? reinterpret_cast<float*>(reinterpret_cast<char*>(s->shared_aq) + ((t * L->shared_inter + 255) & ~size_t(255)))
                        : nullptr;
-    s->flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
+    s->flag = static_cast<int*>(src.get(kScrFlag, t * sizeof(int)));
     const bool grouped = static_cast<int>(t) >= kMoeGroupedDownT;
-    s->ybuf = grouped ? static_cast<float*>(ctx->scratch_get(kScrY, pairs * L->hidden * sizeof(float))) : nullptr;
+    s->ybuf = grouped ? static_cast<float*>(src.get(kScrY, pairs * L->hidden * sizeof(float))) : nullptr;
     if (!route || !s->xq || !s->xs || !s->act || !s->flag || (with_shared && !s->shared_y) || (grouped && !s->ybuf))
         return FOCR_HIP_E_OOM;
     s->idx = reinterpret_cast<uint32_t*>(route);
@@ -611,7 +629,8 @@ int32_t moe_scratch(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, size_t t, bo
 int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t with_shared) {
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("%s: null moe layer", name));
     if (!hidden) return fail(FOCR_HIP_E_ARG, fmt("%s: null hidden", name));
-    if (t < 1 || t > 64) return fail(FOCR_HIP_E_SHAPE, fmt("%s: t %zu outside 1..=64 for one call", name, t));
+    if (t < 1 || t > static_cast<size_t>(kMoeMaxT))
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: t %zu outside 1..=%d for one call", name, t, kMoeMaxT));
     if (with_shared && !L->swg) return fail(FOCR_HIP_E_ARG, fmt("%s: with_shared set but no shared expert uploaded", name));
     return FOCR_HIP_OK;
 }
@@ -619,8 +638,8 @@ int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* h
 // The route kernel writes flag[t] = 1 for a token with fewer than top_k
 // finite router scores (moe.rs:261-265). Reading it synchronises.
 int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
-    std::vector<int> flags(t, 0);
-    FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
+    int flags[kMoeMaxT] = {};  // t <= kMoeMaxT (moe_checks)
+    FOCR_HIP_TRY(hipMemcpyAsync(flags, dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
     FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (size_t i = 0; i < t; ++i)
         if (flags[i]) return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", i));
@@ -648,7 +667,8 @@ int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const
     int32_t st = moe_checks("moe_route", L, hidden, t, 0);
     if (st) return st;
     MoeScratch s;
-    if ((st = moe_scratch(ctx, L, t, false, &s))) return st;
+    ScratchSource src{ctx};
+    if ((st = moe_scratch(src, L, t, false, &s))) return st;
     if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, idx ? idx : s.idx, gates ? gates : s.gates,
                            probs, nullptr)))
         return st;
@@ -660,15 +680,31 @@ int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const
 namespace {
 
 // decode_mlp_i8 over t rows; with resid non-null, out = resid + the layer's
-// output (the decode layer's residual, decoder.rs:2625).
+// output (the decode layer's residual, decoder.rs:2625). With static_scratch
+// the intermediates are carved from the per-device static array instead of
+// the context's slots, and nothing is allocated.
 int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
                         int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
-                        float* gates, int32_t check_route, const float* resid) {
-    int32_t st = moe_checks("moe_decode", L, hidden, t, with_shared);
+                        float* gates, int32_t check_route, const float* resid, bool static_scratch = false) {
+    const char* name = static_scratch ? "moe_decode_noalloc" : "moe_decode";
+    int32_t st = moe_checks(name, L, hidden, t, with_shared);
     if (st) return st;
-    if (!out) return fail(FOCR_HIP_E_ARG, "moe_decode: null out");
+    if (!out) return fail(FOCR_HIP_E_ARG, fmt("%s: null out", name));
     MoeScratch s;
-    if ((st = moe_scratch(ctx, L, t, with_shared != 0, &s))) return st;
+    ScratchSource src{ctx};
+    if (static_scratch) {
+        if (!ctx->static_scratch)
+            return hip_fail(ctx->static_scratch_err != hipSuccess ? ctx->static_scratch_err : hipErrorInvalidSymbol,
+                            "moe_decode_noalloc: static scratch address");
+        ScratchSource count{ctx, nullptr, 0, 0, true};
+        moe_scratch(count, L, t, with_shared != 0, &s);
+        if (count.used > kStaticScratchBytes)
+            return fail(FOCR_HIP_E_SHAPE, fmt("moe_decode_noalloc: t %zu needs %zu bytes of scratch; the static "
+                                              "buffer holds %zu",
+                                              t, count.used, kStaticScratchBytes));
+        src = ScratchSource{ctx, static_cast<char*>(ctx->static_scratch), kStaticScratchBytes, 0, false};
+    }
+    if ((st = moe_scratch(src, L, t, with_shared != 0, &s))) return st;
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     uint32_t* di = idx ? idx : s.idx;
     float* dg = gates ? gates : s.gates;
@@ -730,6 +766,16 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, cons
     return moe_decode_impl(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
                            nullptr);
 }
+
+int32_t focr_hip_moe_decode_noalloc(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                                    int32_t norm_topk, float routed_scale, int32_t with_shared, float* out,
+                                    uint32_t* idx, float* gates, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    return moe_decode_impl(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
+                           nullptr, true);
+}
+
+size_t focr_hip_static_scratch_bytes(void) { return kStaticScratchBytes; }
 
 // ---- int4 MoE layer (chunked prefill) ------------------------------------------
 

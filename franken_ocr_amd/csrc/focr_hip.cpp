@@ -178,6 +178,10 @@ int32_t focr_hip_ctx_create(int32_t device, focr_hip_ctx** out) {
     c->arch = arch;
     // Default priority, non-blocking with respect to the legacy null stream.
     FOCR_HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+    // The allocation-free entry points' scratch: this device's address of the
+    // static array, resolved once per device with the device current. A
+    // failure here only disables those entry points (they report it).
+    c->static_scratch_err = static_scratch_init(device, &c->static_scratch);
     *out = c.release();
     return FOCR_HIP_OK;
 }

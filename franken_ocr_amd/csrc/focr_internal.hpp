@@ -54,6 +54,13 @@ enum ScratchSlot : int {
     kScrCount
 };
 
+// ---- static scratch of the allocation-free entry points ------------------
+// One array of this many bytes per GPU, held until the process ends.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+// With `device` current, the device address of that GPU's array (resolved
+// once per device; later calls return the cached address or error).
+hipError_t static_scratch_init(int device, void** out);
+
 struct ProfPending {
     std::string name;
     hipEvent_t start, stop;
@@ -71,6 +78,10 @@ struct focr_hip_ctx {
         void* p = nullptr;
         size_t cap = 0;
     } scratch[focr::kScrCount];
+    // this device's static scratch (focr::static_scratch_init), or null with
+    // the error that kept it from resolving
+    void* static_scratch = nullptr;
+    hipError_t static_scratch_err = hipSuccess;
     // profiling
     bool prof = false;
     std::vector<focr::ProfPending> pending;
@@ -260,6 +271,8 @@ hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf
 // Measured on MI355X: per token 30.9 / 43.9 / 56.9 us at T = 32 / 48 / 64,
 // grouped + combine 31.6 / 37.4 / 42.9 us.
 constexpr int kMoeGroupedDownT = 40;
+// Tokens per MoE decode call (the route kernel's selection matrices hold 64).
+constexpr int kMoeMaxT = 64;
 // down + slot-order combine in one launch, reading the routing from idx /
 // gates / flag ([t][top_k]) and the act rows of every pair (t*top_k + j).
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,

@@ -256,6 +256,27 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
                             const float* hidden, size_t t, int32_t norm_topk, float routed_scale,
                             int32_t with_shared, float* out, uint32_t* idx, float* gates,
                             int32_t check_route);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): focr_hip_moe_decode with the same arguments, kernels
+ * and results, but every intermediate (quantized rows, routing, selection
+ * matrices, act rows, expert outputs) lives in one statically allocated
+ * device array per GPU of focr_hip_static_scratch_bytes() bytes (8 MiB, held
+ * until the process ends), and the call makes no hipMalloc / hipFree or
+ * other allocating call. A call needing more scratch than that returns
+ * E_SHAPE (at hidden 1280, inter 896, top-6 every t <= 64 fits, with a
+ * shared expert up to 1792 wide). Nothing in the array must start at zero;
+ * it keeps the last call's contents. Every call on one GPU shares its
+ * array, so calls that overlap on one GPU (other contexts or streams) race.
+ * check_route = 1 synchronises (not capturable); 0 leaves the device flag
+ * unread. */
+int32_t focr_hip_moe_decode_noalloc(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
+                                    const float* hidden, size_t t, int32_t norm_topk,
+                                    float routed_scale, int32_t with_shared, float* out,
+                                    uint32_t* idx, float* gates, int32_t check_route);
+/* Size in bytes of the per-GPU static scratch of the allocation-free entry
+ * points. */
+size_t focr_hip_static_scratch_bytes(void);
 /* moe.rs:181-266 route alone: idx/gates [t, top_k] device pointers; probs
  * (nullable) receives the f32 softmax [t, E]. Synchronises to report
  * E_ROUTE. */
