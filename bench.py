@@ -402,6 +402,84 @@ def bench_rswa(args, ctx):
 
 
 # ---------------------------------------------------------------------------
+# chunked prefill attention (decoder.rs:1282-1340) on the f32 matrix cores
+# ---------------------------------------------------------------------------
+
+MFMA_F32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA, MI355X
+
+
+def attn_flops(seq: int, heads: int = 10, head_dim: int = 128) -> float:
+    # query t attends t + 1 keys: 2 * head_dim flops for its score and 2 *
+    # head_dim for its share of P.V, per key and head
+    return 4.0 * head_dim * heads * seq * (seq + 1) / 2
+
+
+def bench_prefill_attn(args, ctx):
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import RingCache, prefill_chunk_bounds
+
+    NH, D = 10, 128
+    seq, chunk = args.tokens, args.chunk
+    log(f"prefill_attn: seq={seq}, chunk={chunk} (one layer's chunked prefill into an R-SWA stream)")
+    q, k, v = (synth.f32_normal(synth.seed_of(3000 + i), seq * NH * D).reshape(seq, NH * D) for i in range(3))
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    bounds = prefill_chunk_bounds(seq, chunk)
+    cache = RingCache(1, seq, ctx)
+    out = ctx.empty((seq, NH * D), np.float32)
+    views = [(c0, dq.view_rows(c0, c1), dk.view_rows(c0, c1), dv.view_rows(c0, c1), out.view_rows(c0, c1))
+             for c0, c1 in bounds]
+
+    def step(i):
+        for c0, qc, kc, vc, oc in views:
+            cache.prefill_chunk(0, qc, kc, vc, c0, oc)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels = timed(ctx, step, args.steps)
+    a_us = kernel_us(prof, "attn_prefill")  # per chunk call (attention + key-range merge)
+    flops = attn_flops(seq, NH, D)
+    achieved = flops / (a_us * 1e-6 * len(bounds)) / 1e12
+    return {
+        "metric": f"chunked prefill attention tokens/s (one layer, {seq} tokens in chunks of {chunk}, 10x128, f32), 1 GPU",
+        "value": round(seq * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(el / args.steps * 1e3, 5),
+        "dtype": "f32",
+        "config": {"workload": "prefill_attn", "seq": seq, "chunk": chunk, "heads": NH, "head_dim": D,
+                   "chunks": len(bounds)},
+        "roofline": {"bound": "mfma", "kernel": "attn_prefill", "achieved": round(achieved, 2),
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
+                     "traffic": None, "algorithmic_flops_per_step": flops,
+                     "avg_launch_us": round(a_us, 3), "launches_per_step": len(bounds)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": (q, k, v, chunk),
+    }
+
+
+def cpu_prefill_attn(args, inputs):
+    from oracle import pyoracle
+
+    q, k, v, chunk = inputs
+    seq = q.shape[0]
+    L, P = pyoracle.lib(), pyoracle.p
+    qc = [(c0, c1, np.ascontiguousarray(q[c0:c1]), np.zeros((c1 - c0, q.shape[1]), np.float32))
+          for c0, c1 in [(c0, min(c0 + chunk, seq)) for c0 in range(0, seq, chunk)]]
+    kc, vc = np.ascontiguousarray(k), np.ascontiguousarray(v)
+    # whole chunked prefills of the sequence, repeated for a bounded time
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for c0, c1, qq, oo in qc:
+            L.oracle_chunk_prefill_attention_f32(P(qq), c1 - c0, P(kc), P(vc), c1, 10, 128, c0, P(oo))
+        n += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(seq * n / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n} chunked prefill attentions of {seq} tokens (chunks of {chunk}), {el:.1f} s; the f32 "
+                      f"restatement of decoder.rs:1282-1340 in the reference's described order, one thread (the "
+                      f"reference's ft-kernel-cpu sdpa is not in the reference tree)"}
+
+
+# ---------------------------------------------------------------------------
 # config 4: int4 chunked-prefill MoE expert GEMMs (matrix cores)
 # ---------------------------------------------------------------------------
 
@@ -796,6 +874,7 @@ WORKLOADS = {
     "linear_i8": (bench_linear_i8, None),
     "decode_layer": (bench_decode_layer, None),
     "decode_step": (bench_decode_step, None),
+    "prefill_attn": (bench_prefill_attn, cpu_prefill_attn),
 }
 
 
@@ -807,6 +886,7 @@ def main() -> int:
     ap.add_argument("--workload", default="moe_decode", choices=sorted(WORKLOADS))
     ap.add_argument("--tokens", type=int, default=None, help="T (moe), M (lm_head/igemm)")
     ap.add_argument("--copies", type=int, default=None, help="distinct weight copies rotated (defeats MALL)")
+    ap.add_argument("--chunk", type=int, default=256, help="prefill chunk (prefill_attn; DEFAULT_PREFILL_CHUNK)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -817,7 +897,7 @@ def main() -> int:
     defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
                 "copy": (1, 1),
                 "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
-                "decode_layer": (8, 6), "decode_step": (8, 1)}
+                "decode_layer": (8, 6), "decode_step": (8, 1), "prefill_attn": (1024, 1)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

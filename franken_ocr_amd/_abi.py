@@ -78,6 +78,9 @@ _SIGS: dict[str, list] = {
     "focr_hip_moe_decode": [_P, _P, _P, _SZ, _I32, _F32, _I32, _P, _P, _P, _I32],
     "focr_hip_moe_decode_noalloc": [_P, _P, _P, _SZ, _I32, _F32, _I32, _P, _P, _P, _I32],
     "focr_hip_static_scratch_bytes": [],
+    "focr_hip_chunk_prefill_attention": [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P],
+    "focr_hip_prefill_attention": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _P],
+    "focr_hip_rswa_prefill_chunk": [_P, _P, _SZ, _P, _P, _P, _SZ, _SZ, _P],
     "focr_hip_moe_route": [_P, _P, _P, _SZ, _I32, _F32, _P, _P, _P],
     "focr_hip_moe_layer_i4_create": [_P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _I32, _P],
     "focr_hip_moe_layer_i4_free": [_P],

@@ -1391,6 +1391,107 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     return FOCR_HIP_OK;
 }
 
+// ---- prefill attention (decoder.rs:568-640, :1282-1340) ------------------------
+
+}  // extern "C"
+
+namespace {
+
+// The shared body: causal attention of cs queries (positions c0 ..) over a
+// c1-key prefix, geometry as AttnGeom, on the context's stream.
+int32_t attn_run(focr_hip_ctx* ctx, const char* name, const AttnGeom& gm, const float* q, const float* k,
+                 const float* v, float* out, size_t cs, size_t c0, size_t c1, size_t heads) {
+    int split_len = 0;
+    const int nsplit = attn_pick_splits((int)cs, (int)c1, (int)heads, ctx->cu_count, &split_len);
+    float* part = nullptr;
+    if (nsplit > 1) {
+        part = static_cast<float*>(ctx->scratch_get(kScrAttn, attn_partials_bytes((int)cs, (int)heads, nsplit)));
+        if (!part) return FOCR_HIP_E_OOM;
+    }
+    ProfScope ps(ctx, "attn_prefill");
+    FOCR_HIP_TRY(launch_attn_prefill(ctx->stream, gm, q, k, v, out, (int)cs, (int)c0, (int)c1, (int)heads, kHeadDim,
+                                     nsplit, split_len, part),
+                 name);
+    return FOCR_HIP_OK;
+}
+
+int32_t attn_checks(const char* name, const void* q, const void* k, const void* v, const void* out, size_t cs,
+                    size_t c1, size_t heads, size_t head_dim) {
+    if (heads == 0 || head_dim == 0 || heads > (size_t(1) << 20) / head_dim)
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: num_heads*head_dim overflow or zero (%zu x %zu)", name, heads, head_dim));
+    if (head_dim != static_cast<size_t>(kHeadDim))
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: head_dim %zu unsupported (the gfx950 kernel takes %d)", name, head_dim,
+                                          kHeadDim));
+    if (c1 > static_cast<size_t>(1) << 24 || cs > c1)
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: %zu rows over a %zu-key prefix exceed the supported range", name, cs, c1));
+    if (cs && (!q || !k || !v || !out)) return fail(FOCR_HIP_E_ARG, fmt("%s: null device pointer", name));
+    return FOCR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t focr_hip_chunk_prefill_attention(focr_hip_ctx* ctx, const float* q_chunk, size_t cs, const float* k_prefix,
+                                         const float* v_prefix, size_t c1, size_t num_heads, size_t head_dim,
+                                         size_t c0, float* out) {
+    ENGINE_CTX(ctx);
+    const char* name = "chunk_prefill_attention";
+    if (c0 > c1 || c0 + cs != c1)  // decoder.rs:1320-1325
+        return fail(FOCR_HIP_E_SHAPE, fmt("chunk_prefill_attention: chunk [%zu, %zu) of %zu rows does not fit prefix %zu",
+                                          c0, c0 + cs, cs, c1));
+    int32_t st = attn_checks(name, q_chunk, k_prefix, v_prefix, out, cs, c1, num_heads, head_dim);
+    if (st || cs == 0) return st;
+    const int dim = static_cast<int>(num_heads * head_dim);
+    const AttnGeom gm{dim, kHeadDim, dim, kHeadDim, dim, kHeadDim, dim, kHeadDim};
+    return attn_run(ctx, name, gm, q_chunk, k_prefix, v_prefix, out, cs, c0, c1, num_heads);
+}
+
+int32_t focr_hip_prefill_attention(focr_hip_ctx* ctx, const float* q, const float* k, const float* v, size_t seq,
+                                   size_t num_heads, size_t head_dim, float* out) {
+    ENGINE_CTX(ctx);
+    const char* name = "prefill_attention";
+    int32_t st = attn_checks(name, q, k, v, out, seq, seq, num_heads, head_dim);
+    if (st || seq == 0) return st;
+    const int dim = static_cast<int>(num_heads * head_dim);
+    const AttnGeom gm{dim, kHeadDim, dim, kHeadDim, dim, kHeadDim, dim, kHeadDim};
+    return attn_run(ctx, name, gm, q, k, v, out, seq, 0, seq, num_heads);
+}
+
+int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
+                                    const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out) {
+    ENGINE_CTX(ctx);
+    const char* name = "rswa_prefill_chunk";
+    if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
+    if (stream >= c->n_streams)
+        return fail(FOCR_HIP_E_SHAPE, fmt("rswa: stream %zu >= num_streams %zu", stream, c->n_streams));
+    if (c0 != 0 && c->prefill_len[stream] != static_cast<int64_t>(c0))
+        return fail(FOCR_HIP_E_STATE, fmt("rswa_prefill_chunk: chunk starts at %zu but the stream holds %lld prefill "
+                                          "tokens",
+                                          c0, static_cast<long long>(c->prefill_len[stream])));
+    if (c0 + cs > c->ref_capacity)
+        return fail(FOCR_HIP_E_STATE, fmt("rswa: prefill seq %zu exceeds ref_capacity %zu", c0 + cs, c->ref_capacity));
+    int32_t st = attn_checks(name, q_chunk, k_chunk, v_chunk, out, cs, c0 + cs, kNumHeads, kHeadDim);
+    if (st) return st;
+    if (cs) {
+        FOCR_HIP_TRY(launch_attn_scatter_kv(ctx->stream, k_chunk, v_chunk, (int)cs, kNumHeads, c->ref_k(stream),
+                                            c->ref_v(stream), (int)c->ref_capacity, (int)c0),
+                     "rswa_prefill_chunk scatter");
+        const int dim = kNumHeads * kHeadDim;
+        const int hs = static_cast<int>(c->ref_capacity) * kHeadDim;
+        const AttnGeom gm{dim, kHeadDim, kHeadDim, hs, kHeadDim, hs, dim, kHeadDim};
+        if ((st = attn_run(ctx, name, gm, q_chunk, c->ref_k(stream), c->ref_v(stream), out, cs, c0, c0 + cs,
+                           kNumHeads)))
+            return st;
+    }
+    // the reference seeds the ring once from the whole prefix (record_prefill,
+    // decoder.rs:1438-1447): prefill_len = the prefix, ring empty
+    c->prefill_len[stream] = static_cast<int64_t>(c0 + cs);
+    c->ring_len[stream] = 0;
+    c->ring_pos[stream] = 0;
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,
                                 uint32_t* ring_pos) {
     if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");

@@ -51,6 +51,7 @@ enum ScratchSlot : int {
     kScrFlag,   // device status flags
     kScrBan,    // sampler ban bitmaps
     kScrLayer,  // decoder layer step intermediates
+    kScrAttn,   // prefill attention key-range partials
     kScrCount
 };
 
@@ -278,6 +279,24 @@ constexpr int kMoeMaxT = 64;
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
                                    const int* flag, const float* act, const int8_t* wd, const float* sd,
                                    const float* shared_y, const float* resid, float* out, int inter);
+// k_attn.hip — causal prefill attention on the f32 matrix cores (head_dim
+// 128). Element (row i, head h) of q / out and (key j, head h) of k / v sit at
+// base + i * ld + h * hstride (token-major: ld = heads * 128, hstride = 128).
+struct AttnGeom {
+    int ldq, hq, ldk, hk, ldv, hv, ldo, ho;
+};
+// Key ranges for a chunk of cs queries over a c1-key prefix: about two
+// blocks per CU, in whole 64-key tiles.
+int attn_pick_splits(int cs, int c1, int heads, int cu_count, int* split_len);
+size_t attn_partials_bytes(int cs, int heads, int nsplit);
+// part: attn_partials_bytes() of scratch when nsplit > 1 (unused otherwise).
+hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q, const float* k, const float* v,
+                               float* out, int cs, int c0, int c1, int heads, int head_dim, int nsplit,
+                               int split_len, float* part);
+// Token-major chunk rows [cs][heads*128] of K and V into head-major
+// reference blocks [heads][cap][128] at rows c0 .. c0 + cs - 1.
+hipError_t launch_attn_scatter_kv(hipStream_t s, const float* k_chunk, const float* v_chunk, int cs, int heads,
+                                  float* ref_k, float* ref_v, int cap, int c0);
 // k_layer.hip — the decode layer's ops around the GEMVs / attention / MoE.
 // xq, xs = quantize_row_i8(rms_norm(x) * w) per row (n <= 4096).
 hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, int rows, int n, float eps,

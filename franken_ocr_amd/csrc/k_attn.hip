@@ -1,0 +1,316 @@
+// k_attn.hip — causal prefill attention (decoder.rs:568-640 prefill_attention,
+// :1282-1340 chunk_prefill_attention) on the f32 matrix cores.
+//
+// A chunk's cs queries (global positions c0 .. c0 + cs - 1) attend keys
+// [0, t] of the f32 prefix, per head, softmax(q.k * 1/sqrt(128)) . v. The
+// scores and the P.V products are f32 MFMAs (v_mfma_f32_16x16x4_f32: exact
+// f32 products, f32 accumulation), so the result matches the reference's
+// f32 attention to rounding.
+//
+// Block = 4 waves on one head and 64 query rows (16 per wave); the block
+// walks its key range in tiles of 64 keys, staged in LDS and shared by the
+// waves. Per wave and 16-key subtile, S^T = K . Q^T (A = 16 keys x 4 dims from
+// LDS, B = 4 dims x 16 query rows from registers), so the accumulator lands
+// with lane (g = lane / 16, j = lane % 16) holding S[row j][keys 4g .. 4g + 3]
+// — exactly the B operand P^T[key][row j] the P.V product needs (keys taken in
+// the order 16n + 4g + r), with A = V^T from LDS: the softmax probabilities
+// never leave their registers. Output dims are taken in the order
+// 8 * (4g + r') + m, so each lane ends holding 32 consecutive dims of its row.
+// Dims of the score dot are taken in the order 32g + s (s = 0..31).
+//
+// Long prefixes are split into key ranges over more blocks (split-K); each
+// writes its running max, denominator and unnormalised output, and a merge
+// kernel folds them (log-sum-exp). A row whose keys all lie in other ranges
+// contributes max -inf and nothing else.
+#include "focr_internal.hpp"
+#include "k_common.hpp"
+
+namespace focr {
+namespace {
+
+constexpr int kD = 128;          // head_dim
+constexpr int kKT = 64;          // keys per LDS tile
+constexpr int kLdsRow = kD + 4;  // padded LDS row (floats)
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct AttnArgs {
+    const float* q;  // row i, head h at q + i * ldq + h * hq
+    const float* k;  // key j, head h at k + j * ldk + h * hk
+    const float* v;
+    float* out;      // single range: normalised context, out + i * ldo + h * ho
+    float* part_o;   // split: [split][head][row][kD] unnormalised
+    float* part_ml;  // split: [split][head][row][2] (max, denominator)
+    int ldq, hq, ldk, hk, ldv, hv, ldo, ho;
+    int cs, c0, c1, heads, split_len, nsplit;
+    float scale;
+};
+
+__device__ __forceinline__ float wave16_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float wave16_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_prefill_kernel(const AttnArgs a) {
+    extern __shared__ float4 lds_kv4[];  // K tile then V tile, [kKT][kLdsRow] floats each
+    float* lk = reinterpret_cast<float*>(lds_kv4);
+    float* lv = lk + kKT * kLdsRow;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int h = blockIdx.y;
+    const int split = blockIdx.z;
+    const int row0 = blockIdx.x * 64;            // block's first chunk row
+    const int wrow = row0 + wave * 16 + j;        // this lane's chunk row
+    const int qrow = wrow < a.cs ? wrow : a.cs - 1;
+    const int t = a.c0 + wrow;                    // its global position
+    // keys this block needs: [0, min(c1, c0 + row0 + 64)), this split's part
+    const int kmax = min(a.c1, a.c0 + row0 + 64);
+    const int ks = split * a.split_len;
+    const int ke = min(ks + a.split_len, kmax);
+
+    // Q fragment: qf[s] = q[row j][32g + s], s = 0..31
+    float qf[32];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(qrow) * a.ldq +
+                                                           static_cast<size_t>(h) * a.hq + 32 * g);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const v4f x = *reinterpret_cast<const v4f*>(qp + u);
+            qf[4 * u] = x.x;
+            qf[4 * u + 1] = x.y;
+            qf[4 * u + 2] = x.z;
+            qf[4 * u + 3] = x.w;
+        }
+    }
+    v4f oacc[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) oacc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // tile loads: 64 keys x 128 floats = 2048 float4 per matrix, 8 per thread
+    const int c4 = threadIdx.x & 31;  // float4 column
+    const int r8 = threadIdx.x >> 5;  // 8 rows per pass
+    const float* kh = a.k + static_cast<size_t>(h) * a.hk + 4 * c4;
+    const float* vh = a.v + static_cast<size_t>(h) * a.hv + 4 * c4;
+    // The tile after the current one is loaded into registers while the
+    // current one is consumed from LDS (key rows clamped into the prefix; a
+    // load past the range end is never used).
+    v4f pk[8], pv[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        int key = ks + r8 + 8 * p;
+        key = key < a.c1 ? key : a.c1 - 1;
+        pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
+        pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
+    }
+    for (int kb = ks; kb < ke; kb += kKT) {
+        __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            *reinterpret_cast<v4f*>(lk + (r8 + 8 * p) * kLdsRow + 4 * c4) = pk[p];
+            *reinterpret_cast<v4f*>(lv + (r8 + 8 * p) * kLdsRow + 4 * c4) = pv[p];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            int key = kb + kKT + r8 + 8 * p;
+            key = key < a.c1 ? key : a.c1 - 1;
+            pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
+            pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
+        }
+
+        // S^T for the 4 subtiles of 16 keys; each score dot runs as two
+        // 16-step MFMA chains (64 dims each) added at the end, halving the
+        // f32 accumulation chain of the 128-term dot
+        v4f sacc[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            v4f sc[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) sc[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const v4f kf = *reinterpret_cast<const v4f*>(lk + (16 * n + j) * kLdsRow + 32 * g + 4 * u);
+                v4f& acc = sc[u >> 2];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[4 * u], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[4 * u + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[4 * u + 2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[4 * u + 3], acc, 0, 0, 0);
+            }
+            sacc[n] = sc[0] + sc[1];
+        }
+        // scale, causal / range mask, online softmax (row j over 4 lanes)
+        float pr[4][4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kb + 16 * n + 4 * g + r;
+                const float sv = sacc[n][r] * a.scale;
+                const bool ok = key <= t && key < ke;
+                pr[n][r] = ok ? sv : -INFINITY;
+                tmax = fmaxf(tmax, pr[n][r]);
+            }
+        tmax = wave16_max(tmax);
+        const float m_new = fmaxf(m_run, tmax);
+        const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        float tsum = 0.0f;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = pr[n][r] == -INFINITY ? 0.0f : expf(pr[n][r] - m_new);
+                pr[n][r] = p;
+                tsum += p;
+            }
+        tsum = wave16_sum(tsum);
+        l_run = l_run * corr + tsum;
+        m_run = m_new;
+        // this tile's V^T . P^T in fresh accumulators (step (n, r) is key
+        // kb + 16n + 4g + r), folded into the running output once per tile:
+        // 64-term sums then a per-tile sum, not one long f32 chain
+        v4f otile[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) otile[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* vr = lv + (16 * n + 4 * g + r) * kLdsRow + 8 * j;
+                const v4f v0 = *reinterpret_cast<const v4f*>(vr);
+                const v4f v1 = *reinterpret_cast<const v4f*>(vr + 4);
+                const float b = pr[n][r];
+                otile[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.x, b, otile[0], 0, 0, 0);
+                otile[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.y, b, otile[1], 0, 0, 0);
+                otile[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.z, b, otile[2], 0, 0, 0);
+                otile[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.w, b, otile[3], 0, 0, 0);
+                otile[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.x, b, otile[4], 0, 0, 0);
+                otile[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.y, b, otile[5], 0, 0, 0);
+                otile[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.z, b, otile[6], 0, 0, 0);
+                otile[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.w, b, otile[7], 0, 0, 0);
+            }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) oacc[m] = oacc[m] * corr + otile[m];
+    }
+    if (wrow >= a.cs) return;
+    // lane (g, j) holds O[row j][32g + 8r' + m] in oacc[m][r']
+    if (a.nsplit == 1) {
+        const float inv = 1.0f / l_run;
+        float* op = a.out + static_cast<size_t>(wrow) * a.ldo + static_cast<size_t>(h) * a.ho + 32 * g;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            float4 x0, x1;
+            x0.x = oacc[0][rr] * inv;
+            x0.y = oacc[1][rr] * inv;
+            x0.z = oacc[2][rr] * inv;
+            x0.w = oacc[3][rr] * inv;
+            x1.x = oacc[4][rr] * inv;
+            x1.y = oacc[5][rr] * inv;
+            x1.z = oacc[6][rr] * inv;
+            x1.w = oacc[7][rr] * inv;
+            *reinterpret_cast<float4*>(op + 8 * rr) = x0;
+            *reinterpret_cast<float4*>(op + 8 * rr + 4) = x1;
+        }
+        return;
+    }
+    const size_t pidx = (static_cast<size_t>(split) * a.heads + h) * a.cs + wrow;
+    float* op = a.part_o + pidx * kD + 32 * g;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        *reinterpret_cast<float4*>(op + 8 * rr) = make_float4(oacc[0][rr], oacc[1][rr], oacc[2][rr], oacc[3][rr]);
+        *reinterpret_cast<float4*>(op + 8 * rr + 4) = make_float4(oacc[4][rr], oacc[5][rr], oacc[6][rr], oacc[7][rr]);
+    }
+    if (g == 0) *reinterpret_cast<float2*>(a.part_ml + pidx * 2) = make_float2(m_run, l_run);
+}
+
+// Fold the key ranges: out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,
+// M = max_s m_s (a range with no key of the row has m = -inf, l = 0, O = 0).
+// Thread = one dim of one (row, head).
+__global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
+    const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; ++s)
+        M = fmaxf(M, a.part_ml[((static_cast<size_t>(s) * a.heads + h) * a.cs + row) * 2]);
+    float den = 0.0f, acc = 0.0f;
+    for (int s = 0; s < a.nsplit; ++s) {
+        const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
+        const float ms = a.part_ml[pidx * 2];
+        if (ms == -INFINITY) continue;
+        const float w = expf(ms - M);
+        den += w * a.part_ml[pidx * 2 + 1];
+        acc += w * a.part_o[pidx * kD + d];
+    }
+    a.out[static_cast<size_t>(row) * a.ldo + static_cast<size_t>(h) * a.ho + d] = acc / den;
+}
+
+// Chunk rows [cs][heads*128] (token-major) into a cache's head-major
+// reference block: ref[h][c0 + i][:] = chunk[i][h*128 ..]. Thread = one
+// float4 of one (row, head), K and V together.
+__global__ __launch_bounds__(256) void attn_scatter_kv_kernel(const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, int cs, int heads,
+                                                              float* __restrict__ ref_k, float* __restrict__ ref_v,
+                                                              int cap, int c0) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;  // (row, head, float4)
+    const int per_row = heads * (kD / 4);
+    if (idx >= cs * per_row) return;
+    const int i = idx / per_row;
+    const int rem = idx - i * per_row;
+    const int h = rem / (kD / 4), c = rem - h * (kD / 4);
+    const size_t src = static_cast<size_t>(i) * heads * kD + h * kD + 4 * c;
+    const size_t dst = (static_cast<size_t>(h) * cap + c0 + i) * kD + 4 * c;
+    *reinterpret_cast<v4f*>(ref_k + dst) = *reinterpret_cast<const v4f*>(kc + src);
+    *reinterpret_cast<v4f*>(ref_v + dst) = *reinterpret_cast<const v4f*>(vc + src);
+}
+
+}  // namespace
+
+hipError_t launch_attn_scatter_kv(hipStream_t s, const float* k_chunk, const float* v_chunk, int cs, int heads,
+                                  float* ref_k, float* ref_v, int cap, int c0) {
+    if (cs < 1 || heads < 1 || c0 < 0 || c0 + cs > cap) return hipErrorInvalidValue;
+    const int n = cs * heads * (kD / 4);
+    FOCR_LAUNCH(attn_scatter_kv_kernel, dim3((n + 255) / 256), dim3(256), 0, s, k_chunk, v_chunk, cs, heads, ref_k,
+                ref_v, cap, c0);
+    return hipGetLastError();
+}
+
+size_t attn_partials_bytes(int cs, int heads, int nsplit) {
+    return static_cast<size_t>(nsplit) * heads * cs * (kD + 2) * sizeof(float);
+}
+
+int attn_pick_splits(int cs, int c1, int heads, int cu_count, int* split_len) {
+    const int qtiles = (cs + 63) / 64;
+    const int want = (2 * cu_count + qtiles * heads - 1) / (qtiles * heads);  // about two blocks per CU
+    int nsplit = want < 1 ? 1 : want;
+    int len = (c1 + nsplit - 1) / nsplit;
+    len = ((len + kKT - 1) / kKT) * kKT;  // whole tiles per range
+    nsplit = (c1 + len - 1) / len;
+    *split_len = len;
+    return nsplit;
+}
+
+hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q, const float* k, const float* v,
+                               float* out, int cs, int c0, int c1, int heads, int head_dim, int nsplit,
+                               int split_len, float* part) {
+    if (head_dim != kD || cs < 1 || c1 < 1 || c0 < 0 || c0 + cs != c1 || heads < 1 || nsplit < 1 ||
+        split_len % kKT != 0 || static_cast<long long>(nsplit) * split_len < c1)
+        return hipErrorInvalidValue;
+    AttnArgs a{q, k, v, out, nullptr, nullptr, gm.ldq, gm.hq, gm.ldk, gm.hk, gm.ldv, gm.hv, gm.ldo, gm.ho,
+               cs, c0, c1, heads, split_len, nsplit, 1.0f / sqrtf(static_cast<float>(head_dim))};
+    if (nsplit > 1) {
+        a.part_o = part;
+        a.part_ml = part + static_cast<size_t>(nsplit) * heads * cs * kD;
+    }
+    const dim3 grid((cs + 63) / 64, heads, nsplit);
+    FOCR_LAUNCH(attn_prefill_kernel, grid, dim3(256), 2 * kKT * kLdsRow * sizeof(float), s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || nsplit == 1) return e;
+    FOCR_LAUNCH(attn_merge_kernel, dim3(cs, heads), dim3(kD), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace focr

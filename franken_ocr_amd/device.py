@@ -132,11 +132,6 @@ class DeviceArray:
     def c_ptr(self) -> C.c_void_p:
         return self._p
 
-    def free(self) -> None:
-        if self._p:
-            _abi.lib().focr_hip_dfree(self.ctx.handle, self._p)
-            self._p = C.c_void_p()
-
     def __del__(self):  # pragma: no cover
         try:
             if self._p and self.ctx._h:
@@ -161,6 +156,24 @@ class DeviceArray:
         out = np.empty(self.shape, dtype=self.dtype)
         _abi.call("focr_hip_d2h", self.ctx.handle, out.ctypes.data_as(C.c_void_p), self._p, self.nbytes)
         return out
+
+    def view_rows(self, r0: int, r1: int) -> "DeviceArray":
+        """Rows [r0, r1) of a 2-D array as a DeviceArray that borrows this
+        allocation (it frees nothing; keep the parent alive while using it)."""
+        if len(self.shape) != 2 or not 0 <= r0 <= r1 <= self.shape[0]:
+            raise ValueError("row view out of range")
+        row = self.shape[1] * self.dtype.itemsize
+        v = DeviceArray.__new__(DeviceArray)
+        v.ctx, v.shape, v.dtype = self.ctx, (r1 - r0, self.shape[1]), self.dtype
+        v.nbytes = (r1 - r0) * row
+        v._p = C.c_void_p(self.ptr + r0 * row)
+        v._borrowed = self
+        return v
+
+    def free(self) -> None:
+        if self._p and not getattr(self, "_borrowed", None):
+            _abi.lib().focr_hip_dfree(self.ctx.handle, self._p)
+        self._p = C.c_void_p()
 
     def offset(self, nbytes: int) -> C.c_void_p:
         """A raw pointer nbytes into this allocation (for sub-views)."""

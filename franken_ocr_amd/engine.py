@@ -334,6 +334,15 @@ class RingCache:
     def step(self, q: DeviceArray, k_steps: DeviceArray, v_steps: DeviceArray, out: DeviceArray) -> None:
         _abi.call("focr_hip_rswa_step", self.ctx.handle, self._h, q.c_ptr, k_steps.c_ptr, v_steps.c_ptr, out.c_ptr)
 
+    def prefill_chunk(self, stream: int, q_chunk: DeviceArray, k_chunk: DeviceArray, v_chunk: DeviceArray,
+                      c0: int, out: DeviceArray) -> None:
+        """One chunk of prefill_with_cache_chunked (decoder.rs:1400-1447) for one
+        layer: the chunk's K/V [cs, 1280] go to the stream's reference block at
+        [c0, c0 + cs) and its queries attend causally over ref[0 .. c0 + cs)."""
+        cs = q_chunk.shape[0]
+        _abi.call("focr_hip_rswa_prefill_chunk", self.ctx.handle, self._h, stream, q_chunk.c_ptr, k_chunk.c_ptr,
+                  v_chunk.c_ptr, cs, c0, out.c_ptr)
+
     def state(self, stream: int) -> tuple:
         p, rl, rp = C.c_uint32(), C.c_uint32(), C.c_uint32()
         _abi.call("focr_hip_rswa_get_state", self._h, stream, C.byref(p), C.byref(rl), C.byref(rp))
@@ -357,6 +366,28 @@ class RingCache:
             self.free()
         except Exception:
             pass
+
+
+def prefill_chunk_bounds(seq: int, chunk: int) -> list:
+    """decoder.rs:1246-1256: contiguous ascending [c0, c1) tiles of at most
+    `chunk` tokens covering [0, seq) (chunk clamped to >= 1)."""
+    chunk = max(int(chunk), 1)
+    return [(c0, min(c0 + chunk, seq)) for c0 in range(0, seq, chunk)]
+
+
+def chunk_prefill_attention(q_chunk: DeviceArray, k_prefix: DeviceArray, v_prefix: DeviceArray, num_heads: int,
+                            head_dim: int, c0: int, out: DeviceArray) -> None:
+    """decoder.rs:1282-1340: the chunk's queries (positions [c0, c0 + cs)) attend
+    causally over the prefix [c1 = c0 + cs, num_heads*head_dim]; out [cs, dim]."""
+    _abi.call("focr_hip_chunk_prefill_attention", q_chunk.ctx.handle, q_chunk.c_ptr, q_chunk.shape[0],
+              k_prefix.c_ptr, v_prefix.c_ptr, k_prefix.shape[0], num_heads, head_dim, c0, out.c_ptr)
+
+
+def prefill_attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, num_heads: int, head_dim: int,
+                      out: DeviceArray) -> None:
+    """decoder.rs:568-640: full causal multi-head attention over the sequence."""
+    _abi.call("focr_hip_prefill_attention", q.ctx.handle, q.c_ptr, k.c_ptr, v.c_ptr, q.shape[0], num_heads, head_dim,
+              out.c_ptr)
 
 
 def rms_norm(x: DeviceArray, y: DeviceArray, w: DeviceArray | None = None, eps: float = 1e-6) -> None:

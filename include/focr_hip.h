@@ -331,6 +331,24 @@ int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* lay
                                 size_t t, const uint32_t* idx, const float* gates,
                                 int32_t with_shared, float* out, int32_t check_idx);
 
+/* ---- prefill attention on the f32 matrix cores -----------------------------
+ * decoder.rs:1282-1340 chunk_prefill_attention: the cs = c1 - c0 queries
+ * q_chunk [cs, num_heads*head_dim] (global positions [c0, c1), RoPE applied)
+ * attend over the prefix k_prefix / v_prefix [c1, num_heads*head_dim] under
+ * the causal mask — query t sees keys [0, t] — with scale 1/sqrt(head_dim):
+ * ctx [cs, num_heads*head_dim] (pre-o_proj). Token-major (head h in columns
+ * h*head_dim ..). E_SHAPE with the reference's message when c0 > c1 or
+ * c0 + cs != c1 ("chunk_prefill_attention: chunk [c0, c0+cs) of cs rows does
+ * not fit prefix c1"); head_dim must be 128 (E_SHAPE otherwise). f32
+ * throughout (f32 MFMAs); agrees with the reference's f32 attention to
+ * rounding (rel 1e-4). Device pointers. */
+int32_t focr_hip_chunk_prefill_attention(focr_hip_ctx* ctx, const float* q_chunk, size_t cs,
+                                         const float* k_prefix, const float* v_prefix, size_t c1,
+                                         size_t num_heads, size_t head_dim, size_t c0, float* out);
+/* decoder.rs:568-640 prefill_attention: the whole sequence, c0 = 0. */
+int32_t focr_hip_prefill_attention(focr_hip_ctx* ctx, const float* q, const float* k, const float* v,
+                                   size_t seq, size_t num_heads, size_t head_dim, float* out);
+
 /* ---- R-SWA ring KV cache (rswa.rs:121-152 RingCache, :645-824 batched) ---
  * n_streams independent caches of one layer, f32, head-major per stream:
  * ref K/V [NUM_HEADS=10][ref_capacity][HEAD_DIM=128], ring K/V
@@ -357,6 +375,19 @@ int32_t focr_hip_rswa_decode_attention(focr_hip_ctx* ctx, const focr_hip_rswa* c
 /* rswa.rs:1184-1200 convenience step: write this token's K/V, then attend. */
 int32_t focr_hip_rswa_step(focr_hip_ctx* ctx, focr_hip_rswa* cache, const float* q,
                            const float* k_steps, const float* v_steps, float* out);
+/* Chunked prefill of one stream straight into its cache (decoder.rs:
+ * 1400-1447 prefill_with_cache_chunked, one layer): the chunk's k / v rows,
+ * token-major [cs][10*128] at positions [c0, c0 + cs), are written to the
+ * stream's reference block — the reference appends them to its running K/V
+ * and seeds the ring from the whole prefix once, which gives the same block
+ * — prefill_len becomes c0 + cs and the ring is emptied; then the chunk's
+ * queries q_chunk [cs][10*128] attend causally over ref[0 .. c0 + cs)
+ * (chunk_prefill_attention) into ctx_out [cs][10*128]. Chunks come in
+ * ascending order: c0 is 0 or the stream's current prefill length (E_STATE
+ * otherwise); c0 + cs <= ref_capacity (E_STATE). Device pointers. */
+int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* cache, size_t stream,
+                                    const float* q_chunk, const float* k_chunk,
+                                    const float* v_chunk, size_t cs, size_t c0, float* ctx_out);
 /* Cursor reflection / speculative roll-back (rswa.rs:219-283, :524-579). */
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* cache, size_t stream, uint32_t* prefill_len,
                                 uint32_t* ring_len, uint32_t* ring_pos);

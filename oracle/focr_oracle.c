@@ -842,3 +842,114 @@ int oracle_decode_attention(const float* ref_k, const float* ref_v, size_t ref_c
     }
     return ORACLE_OK;
 }
+
+/* ---- decoder.rs:1282-1340 chunk_prefill_attention (and :568-640 prefill_attention)
+ * The reference front-pads the chunk's queries to the prefix length and runs
+ * nn::sdpa (ft_kernel_cpu::sdpa_forward_f32, un-vendored) with the top-left
+ * causal mask, so the kept row t (= c0 + i) attends keys [0, t]; the padded
+ * rows are discarded. The kept row is restated directly: per head, the score
+ * q.k over head_dim times scale = 1/sqrt(head_dim) (rswa.rs:52-55 form), a
+ * max-subtracted softmax over [0, t], P.V over the keys.
+ *
+ * ft-kernel-cpu's f32 summation order is unknowable here, and any f32 order
+ * lands about 1e-4 (relative to 1% of a row's largest output) from the exact
+ * result at 1024 keys — the 128-term f32 score dots dominate. So the oracle
+ * evaluates this math in float64 from the f32 inputs and rounds once to f32:
+ * the attention every f32 implementation, the reference's included,
+ * approximates (parity with the reference's exact bits unpinned). The f32
+ * restatement in the order the reference's comments give
+ * (decoder.rs:1274-1279: ascending dims, ascending keys) is kept beside it
+ * as oracle_chunk_prefill_attention_f32, to measure that spread. Either way a
+ * row is a pure function of (q_t, k[0..t], v[0..t]), so a chunked schedule
+ * equals the monolithic one bit for bit. */
+static int attention_shape_ok(size_t cs, size_t c1, size_t num_heads, size_t head_dim, size_t c0) {
+    return num_heads != 0 && head_dim != 0 && c0 <= c1 && c0 + cs == c1;
+}
+
+int oracle_chunk_prefill_attention(const float* q_chunk, size_t cs, const float* k_prefix,
+                                   const float* v_prefix, size_t c1, size_t num_heads,
+                                   size_t head_dim, size_t c0, float* out) {
+    if (!attention_shape_ok(cs, c1, num_heads, head_dim, c0)) return ORACLE_E_SHAPE;
+    const size_t dim = num_heads * head_dim;
+    const double scale = 1.0 / sqrt((double)head_dim);
+    double* s = (double*)malloc((c1 ? c1 : 1) * sizeof(double));
+    double* o = (double*)malloc(head_dim * sizeof(double));
+    if (!s || !o) {
+        free(s);
+        free(o);
+        return ORACLE_E_SHAPE;
+    }
+    for (size_t i = 0; i < cs; ++i) {
+        const size_t t = c0 + i;
+        for (size_t h = 0; h < num_heads; ++h) {
+            const float* q = q_chunk + i * dim + h * head_dim;
+            double mx = -INFINITY;
+            for (size_t j = 0; j <= t; ++j) {
+                const float* k = k_prefix + j * dim + h * head_dim;
+                double acc = 0.0;
+                for (size_t d = 0; d < head_dim; ++d) acc += (double)q[d] * (double)k[d];
+                s[j] = acc * scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            double sum = 0.0;
+            for (size_t j = 0; j <= t; ++j) {
+                s[j] = exp(s[j] - mx);
+                sum += s[j];
+            }
+            for (size_t d = 0; d < head_dim; ++d) o[d] = 0.0;
+            for (size_t j = 0; j <= t; ++j) {
+                const double p = s[j] / sum;
+                const float* v = v_prefix + j * dim + h * head_dim;
+                for (size_t d = 0; d < head_dim; ++d) o[d] += p * (double)v[d];
+            }
+            float* orow = out + i * dim + h * head_dim;
+            for (size_t d = 0; d < head_dim; ++d) orow[d] = (float)o[d];
+        }
+    }
+    free(s);
+    free(o);
+    return ORACLE_OK;
+}
+
+int oracle_chunk_prefill_attention_f32(const float* q_chunk, size_t cs, const float* k_prefix,
+                                       const float* v_prefix, size_t c1, size_t num_heads,
+                                       size_t head_dim, size_t c0, float* out) {
+    if (!attention_shape_ok(cs, c1, num_heads, head_dim, c0)) return ORACLE_E_SHAPE;
+    const size_t dim = num_heads * head_dim;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* s = (float*)malloc((c1 ? c1 : 1) * sizeof(float));
+    if (!s) return ORACLE_E_SHAPE;
+    for (size_t i = 0; i < cs; ++i) {
+        const size_t t = c0 + i;
+        for (size_t h = 0; h < num_heads; ++h) {
+            const float* q = q_chunk + i * dim + h * head_dim;
+            float mx = -INFINITY;
+            for (size_t j = 0; j <= t; ++j) {
+                const float* k = k_prefix + j * dim + h * head_dim;
+                float acc = 0.0f;
+                for (size_t d = 0; d < head_dim; ++d) acc += q[d] * k[d];
+                s[j] = acc * scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            float sum = 0.0f;
+            for (size_t j = 0; j <= t; ++j) {
+                s[j] = expf(s[j] - mx);
+                sum += s[j];
+            }
+            float* o = out + i * dim + h * head_dim;
+            for (size_t d = 0; d < head_dim; ++d) o[d] = 0.0f;
+            for (size_t j = 0; j <= t; ++j) {
+                const float p = s[j] / sum;
+                const float* v = v_prefix + j * dim + h * head_dim;
+                for (size_t d = 0; d < head_dim; ++d) o[d] += p * v[d];
+            }
+        }
+    }
+    free(s);
+    return ORACLE_OK;
+}
+
+int oracle_prefill_attention(const float* q, const float* k, const float* v, size_t seq,
+                             size_t num_heads, size_t head_dim, float* out) {
+    return oracle_chunk_prefill_attention(q, seq, k, v, seq, num_heads, head_dim, 0, out);
+}

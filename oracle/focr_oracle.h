@@ -173,6 +173,23 @@ int oracle_decode_attention(const float* ref_k, const float* ref_v, size_t ref_c
                             size_t prefill_len, const float* ring_k, const float* ring_v,
                             size_t ring_len, const float* q, float* out);
 
+/* ---- decoder.rs:568-640 prefill_attention / :1282-1340 chunk_prefill_attention
+ * Causal multi-head attention over token-major f32 [rows, num_heads*head_dim]
+ * matrices (head h in columns h*head_dim ..). Query row i of a chunk sits at
+ * global position t = c0 + i and attends keys [0, t]; scale = 1/sqrt(head_dim).
+ * chunk: q_chunk [cs, dim], k_prefix / v_prefix [c1, dim], c0 + cs == c1
+ * (ORACLE_E_SHAPE otherwise). prefill_attention is the chunk with c0 = 0.
+ * Evaluated in float64 and rounded once; the _f32 variant is the f32
+ * restatement in the reference's described order (ascending dims and keys). */
+int oracle_chunk_prefill_attention(const float* q_chunk, size_t cs, const float* k_prefix,
+                                   const float* v_prefix, size_t c1, size_t num_heads,
+                                   size_t head_dim, size_t c0, float* out);
+int oracle_chunk_prefill_attention_f32(const float* q_chunk, size_t cs, const float* k_prefix,
+                                       const float* v_prefix, size_t c1, size_t num_heads,
+                                       size_t head_dim, size_t c0, float* out);
+int oracle_prefill_attention(const float* q, const float* k, const float* v, size_t seq,
+                             size_t num_heads, size_t head_dim, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,9 @@ _SIGS = {
     "oracle_pack_int4_f32": ([_P, _SZ, _SZ, _SZ, _P, _P], C.c_int),
     "oracle_ring_write": ([_P, _P, _P, _P, _P, _P, _P], C.c_int),
     "oracle_decode_attention": ([_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P], C.c_int),
+    "oracle_chunk_prefill_attention": ([_P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_prefill_attention": ([_P, _P, _P, _SZ, _SZ, _SZ, _P], C.c_int),
+    "oracle_chunk_prefill_attention_f32": ([_P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P], C.c_int),
     "cpu_detect_tier": ([], C.c_int),
     "cpu_tier_available": ([C.c_int], C.c_int),
     "cpu_tier_tag": ([C.c_int], C.c_char_p),
@@ -411,3 +414,32 @@ class Ring:
                                            p(self.ring_k), p(self.ring_v), self.ring_len.value,
                                            p(_c(q, np.float32)), p(out))
         return st, out
+
+
+def chunk_prefill_attention(q_chunk, k_prefix, v_prefix, num_heads, head_dim, c0):
+    """decoder.rs:1282-1340: context [cs, num_heads*head_dim] of the chunk's queries."""
+    q_chunk = _c(q_chunk, np.float32)
+    cs = q_chunk.shape[0]
+    c1 = k_prefix.shape[0]
+    out = np.zeros((cs, num_heads * head_dim), np.float32)
+    st = lib().oracle_chunk_prefill_attention(p(q_chunk), cs, p(_c(k_prefix, np.float32)), p(_c(v_prefix, np.float32)),
+                                              c1, num_heads, head_dim, c0, p(out))
+    return st, out
+
+
+def prefill_attention_f32(q, k, v, num_heads, head_dim):
+    """The f32 restatement in the reference's described order (ascending dims, keys)."""
+    q = _c(q, np.float32)
+    out = np.zeros(q.shape, np.float32)
+    st = lib().oracle_chunk_prefill_attention_f32(p(q), q.shape[0], p(_c(k, np.float32)), p(_c(v, np.float32)),
+                                                  q.shape[0], num_heads, head_dim, 0, p(out))
+    return st, out
+
+
+def prefill_attention(q, k, v, num_heads, head_dim):
+    """decoder.rs:568-640: full causal multi-head attention [seq, num_heads*head_dim]."""
+    q = _c(q, np.float32)
+    out = np.zeros(q.shape, np.float32)
+    st = lib().oracle_prefill_attention(p(q), p(_c(k, np.float32)), p(_c(v, np.float32)), q.shape[0], num_heads,
+                                        head_dim, p(out))
+    return st, out

@@ -116,6 +116,15 @@ def test_cfg5_fixture():
 
 # ---- GPU: device path vs fixtures ---------------------------------------------------
 
+def _rel_floored(got, want):
+    """max |got - want| / max(|want|, 1% of the row's largest |want|): the GPU
+    tests' relative-error rule (a pure relative error is meaningless for
+    elements that a sum with cancellation leaves near zero)."""
+    want = np.asarray(want, np.float64)
+    floor = np.max(np.abs(want), axis=-1, keepdims=True) * 1e-2
+    return float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), floor)))
+
+
 @pytest.mark.gpu
 def test_gpu_matches_golden(ctx):
     from franken_ocr_amd import simd, synth
@@ -153,7 +162,7 @@ def test_gpu_matches_golden(ctx):
     L.decode(ctx.to_device(d["x"]), dout, didx, dg, norm_topk=True)
     assert np.array_equal(didx.numpy(), d["idx"])
     np.testing.assert_allclose(dg.numpy(), d["gates"], rtol=1e-6)
-    np.testing.assert_allclose(dout.numpy(), d["out"], rtol=1e-3, atol=1e-3 * float(np.abs(d["out"]).max()))
+    assert _rel_floored(dout.numpy(), d["out"]) <= 1e-3
 
     print("[gpu-golden] cfg4", flush=True)
     d = load("cfg4_int4_small.npz")
@@ -177,4 +186,4 @@ def test_gpu_matches_golden(ctx):
     assert cache.state(0) == (Gr, int(d["ring_len"]), int(d["ring_pos"]))
     dout = ctx.empty((1, 1280), np.float32)
     cache.decode_attention(ctx.to_device(d["q"]), dout)
-    np.testing.assert_allclose(dout.numpy()[0], d["out"], rtol=1e-4, atol=1e-4 * float(np.abs(d["out"]).max()))
+    assert _rel_floored(dout.numpy(), d["out"].reshape(1, -1)) <= 1e-4

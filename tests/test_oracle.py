@@ -992,3 +992,100 @@ def test_decoder_layer_step_zero_projections_is_identity(rng):
     r.record_prefill(np.ones(10 * 4 * 128, np.float32), np.ones(10 * 4 * 128, np.float32), 4)
     x = rng.standard_normal((1, 1280)).astype(np.float32)
     assert np.array_equal(O.decoder_layer_step(x, [4], [r], lw), x)
+
+
+# ---- prefill attention (decoder.rs:568-640) and chunked prefill attention (:1282-1340) ----
+
+def _sin_fill(seq, dim, salt):
+    # decoder.rs:3508-3513: ((i + salt) * 0.37).sin() * 1.7 - 0.2, in f32
+    i = np.arange(seq * dim, dtype=np.float32)
+    x = ((i + np.float32(salt)) * np.float32(0.37)).astype(np.float32)
+    return (np.sin(x).astype(np.float32) * np.float32(1.7) - np.float32(0.2)).astype(np.float32).reshape(seq, dim)
+
+
+def _f64_attention(q, k, v, num_heads, head_dim, c0=0):
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    out = np.zeros(q.shape)
+    for i in range(q.shape[0]):
+        t = c0 + i
+        for h in range(num_heads):
+            sl = slice(h * head_dim, (h + 1) * head_dim)
+            s = k[: t + 1, sl] @ q[i, sl] / math.sqrt(head_dim)
+            p = np.exp(s - s.max())
+            out[i, sl] = (p / p.sum()) @ v[: t + 1, sl]
+    return out
+
+
+def test_prefill_attention_known_answers():
+    # decoder.rs:4104-4126: row 0 attends only to itself -> v[0]; row 1 is a
+    # convex blend strictly between v[0] and v[1]
+    q = np.array([[1, 0], [0, 1]], np.float32)
+    v = np.array([[5, 6], [7, 8]], np.float32)
+    st, out = O.prefill_attention(q, q.copy(), v, 1, 2)
+    assert st == 0 and out[0].tolist() == [5.0, 6.0]
+    assert 5.0 < out[1, 0] < 7.0 and 6.0 < out[1, 1] < 8.0
+    # one key -> its value; equal scores -> the mean (rswa.rs:1475-1510 pattern)
+    k = np.zeros((3, 4), np.float32)
+    vv = np.array([[1, 2, 3, 4], [3, 4, 5, 6], [8, 0, 1, 2]], np.float32)
+    st, out = O.prefill_attention(np.ones((3, 4), np.float32), k, vv, 1, 4)
+    assert out[0].tolist() == vv[0].tolist()
+    np.testing.assert_allclose(out[2], vv.mean(axis=0), rtol=1e-6)
+
+
+def test_chunked_attention_is_byte_identical_to_monolithic():
+    # decoder.rs:3503-3535: 3 heads x 4 dims, seq 11, chunks 1, 2, 3 and the full length
+    nh, hd, seq = 3, 4, 11
+    dim = nh * hd
+    q, k, v = _sin_fill(seq, dim, 0.0), _sin_fill(seq, dim, 11.0), _sin_fill(seq, dim, 23.0)
+    st, mono = O.prefill_attention(q, k, v, nh, hd)
+    assert st == 0
+    for chunk in (1, 2, 3, seq):
+        got = np.zeros_like(mono)
+        for c0 in range(0, seq, chunk):
+            c1 = min(c0 + chunk, seq)
+            st, ctx = O.chunk_prefill_attention(q[c0:c1], k[:c1], v[:c1], nh, hd, c0)
+            assert st == 0
+            got[c0:c1] = ctx
+        assert np.array_equal(got.view(np.uint32), mono.view(np.uint32)), chunk
+
+
+@pytest.mark.parametrize("seq,nh,hd", [(17, 2, 8), (40, 10, 128)])
+def test_prefill_attention_vs_float64_and_causal_mask(seq, nh, hd, rng):
+    q, k, v = (rng.standard_normal((seq, nh * hd)).astype(np.float32) for _ in range(3))
+    st, out = O.prefill_attention(q, k, v, nh, hd)
+    assert st == 0
+    want = _f64_attention(q, k, v, nh, hd)
+    # evaluated in float64 and rounded once: within f32 rounding of the numpy restatement
+    np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-7)
+    # the f32 restatement of the reference's order: same math to f32 rounding
+    st, o32 = O.prefill_attention_f32(q, k, v, nh, hd)
+    assert st == 0
+    np.testing.assert_allclose(o32, want, rtol=1e-3, atol=2e-5)
+    assert not np.array_equal(o32, out)
+    # the mask: changing keys / values at positions > r leaves rows <= r unchanged
+    r = seq // 2
+    k2, v2 = k.copy(), v.copy()
+    k2[r + 1:] += 3.0
+    v2[r + 1:] -= 5.0
+    st, out2 = O.prefill_attention(q, k2, v2, nh, hd)
+    assert np.array_equal(out2[: r + 1], out[: r + 1]) and not np.array_equal(out2[r + 1:], out[r + 1:])
+    # heads are independent: a change confined to head 0's columns leaves head 1 unchanged
+    k3 = k.copy()
+    k3[:, :hd] *= -1.0
+    st, out3 = O.prefill_attention(q, k3, v, nh, hd)
+    assert np.array_equal(out3[:, hd:], out[:, hd:]) and not np.array_equal(out3[:, :hd], out[:, :hd])
+
+
+def test_prefill_attention_f32_variant_known_answers():
+    # the f32 restatement obeys the same known answers (decoder.rs:4104-4126)
+    q = np.array([[1, 0], [0, 1]], np.float32)
+    v = np.array([[5, 6], [7, 8]], np.float32)
+    st, out = O.prefill_attention_f32(q, q.copy(), v, 1, 2)
+    assert st == 0 and out[0].tolist() == [5.0, 6.0] and 5.0 < out[1, 0] < 7.0 and 6.0 < out[1, 1] < 8.0
+
+
+def test_chunk_prefill_attention_rejects_bad_chunks():
+    # decoder.rs:1320-1325: c0 > c1 or c0 + cs != c1
+    z = np.zeros((4, 8), np.float32)
+    assert O.chunk_prefill_attention(z[:2], z, z, 2, 4, 1)[0] != 0
+    assert O.chunk_prefill_attention(z[:2], z, z, 2, 4, 2)[0] == 0
