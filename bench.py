@@ -56,11 +56,19 @@ def host_cpu() -> dict:
     return {"nproc": os.cpu_count(), "cpu_model": model}
 
 
+TRAFFIC_NOTE = ("stored: profiles/traffic.json, rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 512 MiB "
+                "copy; null when the kernel's source changed since it was measured")
+
+
 def traffic_for(kernel: str, workload: str):
     """HBM bytes per launch measured with rocprofv3 --pmc: FETCH_SIZE and
     WRITE_SIZE (one run each) scaled by what the same counters read for a
     512 MiB device-to-device copy (profiles/traffic.json, written by
-    franken_ocr_amd.rocprof_summary traffic), or None if not recorded."""
+    franken_ocr_amd.rocprof_summary traffic). A stored value is returned only
+    while the hash of the kernel source it was measured on matches the file
+    as it is now; otherwise (or if not recorded) None."""
+    from franken_ocr_amd.rocprof_summary import source_sha16
+
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
@@ -68,7 +76,11 @@ def traffic_for(kernel: str, workload: str):
         rec = json.loads(f.read_text()).get(f"{kernel}@{workload}")
     except (OSError, ValueError):
         return None
-    return None if rec is None else rec.get("bytes_per_dispatch")
+    if rec is None or "source" not in rec or not (ROOT / rec["source"]).exists():
+        return None
+    if source_sha16(ROOT / rec["source"]) != rec.get("source_sha256_16"):
+        return None
+    return rec.get("bytes_per_dispatch")
 
 
 def timed(ctx, step, steps: int):
@@ -168,7 +180,7 @@ def bench_moe(args, ctx):
                    "norm_topk": True, "layer_copies_rotated": args.copies, "distinct_experts_mean": mean_u},
         "roofline": {"bound": "hbm", "kernel": "moe_gate_up", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_for("moe_gate_up", "moe_decode_t%d" % T),
+                     "traffic": traffic_for("moe_gate_up", "moe_decode_t%d" % T), "traffic_note": TRAFFIC_NOTE,
                      "algorithmic_bytes_per_launch": int(gate_up_bytes), "avg_launch_us": round(gu_ms * 1e3, 3)},
         "layer_roofline": {"achieved": round(layer_gbs, 1), "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                            "algorithmic_bytes_per_step": int(layer_bytes)},
@@ -263,7 +275,7 @@ def bench_lm_head(args, ctx, sampler=False):
         "config": cfg,
         "roofline": {"bound": "hbm", "kernel": "lm_head_gemv", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_for("lm_head_gemv", f"lm_head_m{M}"),
+                     "traffic": traffic_for("lm_head_gemv", f"lm_head_m{M}"), "traffic_note": TRAFFIC_NOTE,
                      "algorithmic_bytes_per_launch": int(gemv_bytes), "avg_launch_us": round(g_ms * 1e3, 3)},
         "step_achieved_gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1),
         "kernel_avg_us": kernels,
@@ -394,7 +406,7 @@ def bench_rswa(args, ctx):
                                    "cache_copies_rotated": copies},
         "roofline": {"bound": "hbm", "kernel": "rswa_chunk", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_for("rswa_chunk", "rswa"),
+                     "traffic": traffic_for("rswa_chunk", "rswa"), "traffic_note": TRAFFIC_NOTE,
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
         "kernel_avg_us": kernels,
         "_cpu_inputs": None,

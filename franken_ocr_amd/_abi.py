@@ -11,7 +11,11 @@ import ctypes as C
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libfocr_hip.so"
+import os
+
+# FOCR_HIP_LIB selects another build of the same library (the host-sanitized
+# copy that franken_ocr_amd/sanitize.py runs the CPU checks against).
+LIB_PATH = Path(os.environ.get("FOCR_HIP_LIB") or Path(__file__).resolve().parent / "libfocr_hip.so")
 
 OK = 0
 E_SHAPE = -1

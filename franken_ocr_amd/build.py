@@ -63,31 +63,46 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, "-x", "hip", "-c", str(src), "-o", str(obj)]
+# Host-side sanitizers for the CPU-only checks of the host code (the .focrq
+# parser, the ABI's argument checks): every -fsanitize= applies to the host
+# pass only, the gfx950 code is built as usual. The result loads into a
+# process that preloads the clang ASan runtime (franken_ocr_amd/sanitize.py).
+SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
+            "-Xarch_host", "-shared-libsan"]
+SAN_BUILD = PKG / "_build_san"
+SAN_OUT = SAN_BUILD / "libfocr_hip_san.so"
+
+
+def _compile(src: Path, sanitize: bool = False) -> Path:
+    obj = (SAN_BUILD if sanitize else BUILD) / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON, *(SANITIZE if sanitize else []), "-x", "hip", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel/host source for gfx950 and link the shared library."""
-    BUILD.mkdir(exist_ok=True)
+def build(verbose: bool = False, sanitize: bool = False) -> Path:
+    """Compile every kernel/host source for gfx950 and link the shared library
+    (with sanitize: the host-sanitized copy in _build_san/ instead)."""
+    out_dir = SAN_BUILD if sanitize else BUILD
+    out_dir.mkdir(exist_ok=True)
+    out = SAN_OUT if sanitize else OUT
     srcs = sources()
     jobs = min(8, len(srcs), os.cpu_count() or 1)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+        objs = list(ex.map(lambda src: _compile(src, sanitize), srcs))
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", *(SANITIZE if sanitize else []), "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT} from {len(srcs)} sources", file=sys.stderr)
-    return OUT
+        print(f"built {out} from {len(srcs)} sources", file=sys.stderr)
+    return out
 
 
 if __name__ == "__main__":

@@ -118,6 +118,14 @@ def _pick(means: dict, kernel: str, counter: str) -> float:
     return hits[0] if len(hits) == 1 else st.mean(hits)
 
 
+def source_sha16(path) -> str:
+    """First 16 hex digits of a source file's SHA-256 (ties a stored
+    measurement to the kernel source it was taken on)."""
+    import hashlib
+
+    return hashlib.sha256(Path(path).read_bytes()).hexdigest()[:16]
+
+
 def traffic(args) -> dict:
     fetch_kib = _pick(counter_means(args.fetch), args.kernel, "FETCH_SIZE")
     write_kib = _pick(counter_means(args.write), args.kernel, "WRITE_SIZE")
@@ -136,6 +144,7 @@ def traffic(args) -> dict:
         "fetch_scale": round(f_fetch, 4),
         "write_scale": round(f_write, 4),
         "bytes_per_dispatch": int(bytes_per),
+        **({"source": args.source, "source_sha256_16": source_sha16(args.source)} if args.source else {}),
     }
 
 
@@ -155,6 +164,7 @@ def main(argv=None) -> int:
         t.add_argument(name, required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--copy-kernel", default="copyBuffer")
+    t.add_argument("--source", default=None, help="the kernel's source file (its hash is stored with the result)")
     t.add_argument("--json", default=None, help="merge the result into this JSON file under --key")
     a = ap.parse_args(argv)
     if a.what == "kernels":

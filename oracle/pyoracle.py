@@ -7,13 +7,15 @@ bench.py's cpu_baseline leg — never by the product package.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# FOCR_ORACLE_LIB selects another build of the oracle (the sanitized one in _san/).
+LIB_PATH = Path(os.environ.get("FOCR_ORACLE_LIB") or HERE / "liboracle.so")
 
 _P = C.c_void_p
 _SZ = C.c_size_t
