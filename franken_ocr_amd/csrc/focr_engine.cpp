@@ -200,7 +200,7 @@ int32_t focr_hip_qint8_from_device(focr_hip_ctx* ctx, const int8_t* w, const flo
 
 int32_t focr_hip_qint8_free(focr_hip_qint8* w) {
     if (!w) return FOCR_HIP_OK;
-    if (w->owned || w->w_mfma) {
+    if (w->owned || w->w_mfma || w->w_tiled) {
         hipSetDevice(w->ctx->device);
         hipStreamSynchronize(w->ctx->stream);
     }
@@ -209,6 +209,7 @@ int32_t focr_hip_qint8_free(focr_hip_qint8* w) {
         hipFree(w->scales);
     }
     hipFree(w->w_mfma);
+    hipFree(w->w_tiled);
     delete w;
     return FOCR_HIP_OK;
 }
@@ -954,19 +955,48 @@ int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
     if (!i8_mfma_supported(static_cast<int>(w->k)))
         return fail(FOCR_HIP_E_SHAPE,
                     fmt("linear_int8_dynamic: k %zu is not a multiple of 64 (the matrix-core K stage)", w->k));
-    int32_t st = ensure_tiled(ctx, &w->w_mfma, w->w, 1, w->n, w->k, "linear_int8_dynamic");
-    if (st) return st;
-    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+    // 256 rows and up: 256 x 128 LDS-staged tiles on the tiled operands;
+    // fewer: 64-row tiles on the fragment-order weight copy
+    const bool big = i8_gemm256_supported((int)m, (int)w->n, (int)w->k);
+    if (big) {
+        if (!w->w_tiled) {
+            const size_t bytes = i8_gemm256_b_bytes((int)w->n, (int)w->k);
+            int8_t* p = nullptr;
+            if (hipMalloc(&p, bytes) != hipSuccess)
+                return fail(FOCR_HIP_E_OOM, fmt("linear_int8_dynamic: tiled weight copy of %zu bytes", bytes));
+            hipError_t e = launch_i8_gemm256_retile_b(ctx->stream, w->w, (int)w->n, (int)w->k, p);
+            if (e != hipSuccess) {
+                hipFree(p);
+                return hip_fail(e, "retile launch");
+            }
+            w->w_tiled = p;
+        }
+    } else {
+        int32_t st = ensure_tiled(ctx, &w->w_mfma, w->w, 1, w->n, w->k, "linear_int8_dynamic");
+        if (st) return st;
+    }
+    int8_t* xq = static_cast<int8_t*>(
+        ctx->scratch_get(kScrXq, big ? i8_gemm256_a_bytes((int)m, (int)w->k) : m * w->k));
     float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
     if (!xq || !xs) return FOCR_HIP_E_OOM;
     {
         ProfScope ps(ctx, "quantize_rows_dyn");
-        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
-                     "quantize launch");
+        if (big)
+            FOCR_HIP_TRY(launch_quantize_rows_tiled(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
+                         "quantize launch");
+        else
+            FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
+                         "quantize launch");
     }
     ProfScope ps(ctx, "linear_i8");
-    FOCR_HIP_TRY(launch_linear_i8(ctx->stream, xq, xs, (int)m, (int)w->k, w->w_mfma, w->scales, (int)w->n, bias, y),
-                 "linear_i8 launch");
+    if (big)
+        FOCR_HIP_TRY(launch_i8_gemm256(ctx->stream, xq, xs, (int)m, (int)w->k, w->w_tiled, w->scales, (int)w->n,
+                                       bias, y),
+                     "linear_i8 launch");
+    else
+        FOCR_HIP_TRY(launch_linear_i8(ctx->stream, xq, xs, (int)m, (int)w->k, w->w_mfma, w->scales, (int)w->n, bias,
+                                      y),
+                     "linear_i8 launch");
     return FOCR_HIP_OK;
 }
 

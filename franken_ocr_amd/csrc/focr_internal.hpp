@@ -105,6 +105,9 @@ struct focr_hip_qint8 {
     // the weights in the matrix-core fragment order (launch_retile_i8), built
     // the first time the handle is used for prefill; always owned
     mutable int8_t* w_mfma = nullptr;
+    // the weights in the large-row GEMM's tiled order (launch_i8_gemm256_retile_b),
+    // built the first time the handle multiplies 256 rows or more; always owned
+    mutable int8_t* w_tiled = nullptr;
 };
 
 struct focr_hip_moe_layer {
@@ -222,6 +225,8 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
                           const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                           uint64_t* arg_keys, int* nparts_out, int cu_count);
 int gemv_i8_nparts(int n, int cu_count);
+// The current device's dynamic-LDS limit per block (160 KB on gfx950).
+size_t max_lds_per_block();
 // The same GEMV with a per-row ban bitmap (ban_words u32 per row): a set bit
 // n writes y[i][n] = -inf and keys see -inf.
 // y = dequant(W . quantize_row_i8(x)) for m f32 rows x [m][k] (after
@@ -429,6 +434,16 @@ hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, in
 // wg, wu in fragment order.
 hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
                             const float* sg, const int8_t* wu, const float* su, int n, float* act);
+// k_i8gemm.hip — the same product for large row counts: 256 x 128 block
+// tiles, both operands in a tiled order (the activations written so by the
+// quantizer, the weights retiled once). Needs m >= 256 and k a multiple of 64.
+bool i8_gemm256_supported(int m, int n, int k);
+size_t i8_gemm256_a_bytes(int m, int k);  // tiled activation buffer
+size_t i8_gemm256_b_bytes(int n, int k);  // tiled weight buffer
+hipError_t launch_i8_gemm256_retile_b(hipStream_t s, const int8_t* w, int n, int k, int8_t* wt);
+hipError_t launch_quantize_rows_tiled(hipStream_t s, const float* x, int m, int k, int8_t* xt, float* xs, int rule);
+hipError_t launch_i8_gemm256(hipStream_t s, const int8_t* xt, const float* xs, int m, int k, const int8_t* wt,
+                             const float* ws, int n, const float* bias, float* y);
 struct MoeI8Scratch {
     int8_t* xq;       // [t][hidden]
     float* xs;        // [t]

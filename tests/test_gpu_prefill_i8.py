@@ -35,7 +35,9 @@ def assert_rel(got, want, rtol):
 
 @pytest.mark.parametrize("m,k,n,bias", [(1, 64, 8, False), (5, 128, 33, True), (64, 1280, 256, False),
                                         (100, 1280, 3840, True), (513, 896, 1280, False), (7, 6848, 64, True),
-                                        (130, 1792, 300, False)])
+                                        (130, 1792, 300, False), (256, 1280, 256, True), (700, 960, 1000, True),
+                                        (300, 6848, 96, False), (512, 1280, 6848, True), (257, 192, 33, True),
+                                        (256, 8256, 40, True)])
 def test_linear_i8_dynamic_bit_exact(ctx, m, k, n, bias):
     from franken_ocr_amd.engine import QInt8, linear_i8_dynamic
 
