@@ -345,6 +345,41 @@ def bench_igemm(args, ctx):
     }
 
 
+def bench_igemm_batched(args, ctx):
+    """cfg1 batched: 64 distinct experts' gate projections (896 x 1280 each,
+    73.4 MB) in one launch, each against its own M activation rows, i32 out
+    accumulated (+=)."""
+    from franken_ocr_amd import _abi, synth
+
+    M, N, Kd, B = args.tokens, 896, 1280, 64
+    w = synth.int8_uniform(synth.seed_of(1), B * N * Kd)
+    a = synth.int8_uniform(synth.seed_of(3), B * M * Kd)
+    dw, da = ctx.to_device(w), ctx.to_device(a)
+    dout = ctx.to_device(np.zeros(B * M * N, np.int32))
+
+    def step(i):
+        _abi.call("focr_hip_igemm_s8s8_batched_dev", ctx.handle, da.c_ptr, dw.c_ptr, B, M, Kd, N, dout.c_ptr)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels = timed(ctx, step, args.steps)
+    g_us = kernel_us(prof, "igemm_i8_batched")
+    nbytes = B * (N * Kd + M * Kd + 2 * M * N * 4)
+    achieved = nbytes / (g_us * 1e-6) / 1e9
+    return {
+        "metric": "int8 igemm, 64 experts' gate-proj (896x1280) in one launch, launches/s, 1 GPU",
+        "value": round(args.steps / el, 1), "unit": "launches/s", "ms_per_step": round(el / args.steps * 1e3, 5),
+        "dtype": "int8", "config": {"workload": "igemm_batched", "m": M, "n": N, "k": Kd, "instances": B,
+                                    "weight_bytes": B * N * Kd},
+        "roofline": {"bound": "hbm", "kernel": "igemm_i8_batched", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_us, 3)},
+        "kernel_avg_us": kernels,
+        "_cpu_inputs": None,
+    }
+
+
 def cpu_igemm(args, inputs):
     from oracle import pyoracle
 
@@ -510,6 +545,40 @@ def make_i4_layer(seed: int, group: int = 32):
     return wg, sg, wu, su, wd, sd
 
 
+def h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, steps, gu_name, dn_name, per_expert_bytes):
+    """SURVEY H5's views of the prefill MoE's int8 MFMA utilisation (ops /
+    time / 5.0 POPS): cold (rotating layer copies, the measured step), warm
+    (one layer, MALL-resident) and the compute-bound bucket (every expert at
+    M_e >= 195, where ops/byte ~ 3.2 M_e: token t routes to hot[(t + j) % 8],
+    j < top_k, so each of the 8 most-hit experts gets T * top_k / 8 rows;
+    rotating copies). Returns (views, warm ms, warm / bucket per-kernel us)."""
+    pairs = T * K
+    gu_ops, dn_ops = 2.0 * pairs * 2 * I * H, 2.0 * pairs * H * I
+    nw = max(steps // 2, 10)
+    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False), nw)
+    counts = np.bincount(idx.ravel(), minlength=E)
+    hot = np.sort(np.argsort(-counts, kind="stable")[:8]).astype(np.uint32)
+    bidx = np.ascontiguousarray(np.stack([hot[(np.arange(T) + j) % 8] for j in range(K)], axis=1))
+    dbi = ctx.to_device(bidx)
+    el_b, prof_b, kernels_b = timed(ctx, lambda i: layers[i % len(layers)].prefill(dx, dbi, dg, dout,
+                                                                                  check_idx=False), nw)
+    ms_w, ms_b = el_w / nw * 1e3, el_b / nw * 1e3
+
+    def frac(ops, us):
+        return round(ops / (us * 1e-6) / 1e12 / MFMA_INT8_PEAK_TOPS, 4)
+
+    ku = kernel_us
+    views = {
+        "cold_layer": frac(gu_ops + dn_ops, ms * 1e3), "warm_layer": frac(gu_ops + dn_ops, ms_w * 1e3),
+        "cold_gate_up": frac(gu_ops, ku(prof, gu_name)), "warm_gate_up": frac(gu_ops, ku(prof_w, gu_name)),
+        "cold_down": frac(dn_ops, ku(prof, dn_name)), "warm_down": frac(dn_ops, ku(prof_w, dn_name)),
+        "bucket": {"experts": 8, "rows_per_expert": pairs // 8, "layer": frac(gu_ops + dn_ops, ms_b * 1e3),
+                   "gate_up": frac(gu_ops, ku(prof_b, gu_name)), "down": frac(dn_ops, ku(prof_b, dn_name)),
+                   "weight_bytes_per_step": 8 * per_expert_bytes},
+    }
+    return views, ms_w, kernels_w, kernels_b
+
+
 def bench_prefill_i4(args, ctx):
     from franken_ocr_amd import synth
     from franken_ocr_amd.engine import MoeLayerI4
@@ -538,11 +607,11 @@ def bench_prefill_i4(args, ctx):
     gu_tops = gu_ops / (gu_us * 1e-6) / 1e12
     layer_tops = (gu_ops + dn_ops) / (ms * 1e-3) / 1e12
     counts = np.bincount(idx.ravel(), minlength=E)
-    wbytes = int((counts > 0).sum()) * (2 * I * H // 2 + H * I // 2 + 4 * (2 * I * (H // group) + H * (I // group)))
-    # warm: one layer, its 137.6 MB resident in the 256 MB Infinity Cache
-    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False),
-                                    max(args.steps // 2, 10))
-    log(f"per-kernel avg us {kernels}; warm {kernels_w}")
+    per_expert_bytes = 2 * I * H // 2 + H * I // 2 + 4 * (2 * I * (H // group) + H * (I // group))
+    wbytes = int((counts > 0).sum()) * per_expert_bytes
+    views, ms_w, kernels_w, kernels_b = h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps,
+                                                 "i4_gate_up", "i4_down", per_expert_bytes)
+    log(f"per-kernel avg us {kernels}; warm {kernels_w}; bucket {kernels_b}")
     return {
         "metric": "int4 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
         "value": round(T * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int4xint8",
@@ -556,9 +625,12 @@ def bench_prefill_i4(args, ctx):
         "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
-                       "warm_ms_per_step": round(el_w / max(args.steps // 2, 10) * 1e3, 5)},
+                       "warm_ms_per_step": round(ms_w, 5)},
+        # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
+        "mfma_utilisation": views,
         "kernel_avg_us": kernels,
         "kernel_avg_us_warm": kernels_w,
+        "kernel_avg_us_bucket": kernels_b,
         "_cpu_inputs": (x, idx, gates, host),
     }
 
@@ -655,10 +727,11 @@ def bench_prefill_i8(args, ctx):
     gu_tops = gu_ops / (gu_us * 1e-6) / 1e12
     layer_tops = (gu_ops + dn_ops) / (ms * 1e-3) / 1e12
     counts = np.bincount(idx.ravel(), minlength=E)
-    wbytes = int((counts > 0).sum()) * (3 * I * H + 4 * (2 * I + H))
-    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False),
-                                    max(args.steps // 2, 10))
-    log(f"per-kernel avg us {kernels}; warm {kernels_w}")
+    per_expert_bytes = 3 * I * H + 4 * (2 * I + H)
+    wbytes = int((counts > 0).sum()) * per_expert_bytes
+    views, ms_w, kernels_w, kernels_b = h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps,
+                                                 "i8_gate_up", "i8_down", per_expert_bytes)
+    log(f"per-kernel avg us {kernels}; warm {kernels_w}; bucket {kernels_b}")
     return {
         "metric": "int8 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
         "value": round(T * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
@@ -672,9 +745,12 @@ def bench_prefill_i8(args, ctx):
         "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
-                       "warm_ms_per_step": round(el_w / max(args.steps // 2, 10) * 1e3, 5)},
+                       "warm_ms_per_step": round(ms_w, 5)},
+        # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
+        "mfma_utilisation": views,
         "kernel_avg_us": kernels,
         "kernel_avg_us_warm": kernels_w,
+        "kernel_avg_us_bucket": kernels_b,
         "_cpu_inputs": None,
     }
 
@@ -879,6 +955,7 @@ WORKLOADS = {
     "lm_head": (bench_lm_head, cpu_lm_head),
     "lm_head_sample": (lambda args, ctx: bench_lm_head(args, ctx, sampler=True), None),
     "igemm": (bench_igemm, cpu_igemm),
+    "igemm_batched": (bench_igemm_batched, None),
     "rswa": (bench_rswa, None),
     "copy": (bench_copy, None),
     "moe_prefill_i4": (bench_prefill_i4, cpu_prefill_i4),
@@ -888,6 +965,52 @@ WORKLOADS = {
     "decode_step": (bench_decode_step, None),
     "prefill_attn": (bench_prefill_attn, cpu_prefill_attn),
 }
+
+
+# Secondary configurations measured after the headline in the default run and
+# reported under "extra" (key, workload, tokens, copies, steps, warmup): the
+# other SURVEY configs and the prefill paths, each timed the same way as its
+# own --workload run, with fewer steps.
+EXTRAS = [
+    ("cfg1_igemm_m16", "igemm", 16, 64, 200, 20),
+    ("cfg1_igemm_batched64_m16", "igemm_batched", 16, 1, 50, 5),
+    ("cfg2_lm_head_m1", "lm_head", 1, 3, 50, 5),
+    ("cfg2_lm_head_m8", "lm_head", 8, 3, 50, 5),
+    ("cfg3_moe_decode_t1", "moe_decode", 1, 8, 100, 10),
+    ("cfg3_moe_decode_t32", "moe_decode", 32, 8, 100, 10),
+    ("cfg4_moe_prefill_i4_m512", "moe_prefill_i4", 512, 3, 20, 3),
+    ("cfg5_rswa_b8", "rswa", 8, 4, 100, 10),
+    ("prefill_attn_1024", "prefill_attn", 1024, 1, 20, 3),
+    ("linear_i8_m8192", "linear_i8", 8192, 3, 20, 3),
+    ("decode_layer_b8", "decode_layer", 8, 6, 50, 5),
+]
+_EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us")
+
+
+def run_extras(ctx, base_args) -> dict:
+    import gc
+
+    out = {}
+    for key, wl, tokens, copies, steps, warmup in EXTRAS:
+        if wl not in WORKLOADS:
+            continue
+        a = argparse.Namespace(**vars(base_args))
+        a.workload, a.tokens, a.copies, a.steps, a.warmup, a.no_cpu = wl, tokens, copies, steps, warmup, True
+        log(f"extra {key}")
+        res = WORKLOADS[wl][0](a, ctx)
+        res.pop("_cpu_inputs", None)
+        rl = res.get("roofline") or {}
+        ent = {"metric": res["metric"], "value": res["value"], "unit": res["unit"],
+               "ms_per_step": res["ms_per_step"], "steps": steps, "config": res["config"],
+               "roofline": {k: rl.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit", "frac",
+                                                   "avg_launch_us")}}
+        for k in _EXTRA_KEYS:
+            if k in res:
+                ent[k] = res[k]
+        out[key] = ent
+        del res
+        gc.collect()
+    return out
 
 
 def main() -> int:
@@ -901,12 +1024,15 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=256, help="prefill chunk (prefill_attn; DEFAULT_PREFILL_CHUNK)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the secondary configurations the default (moe_decode) run reports under 'extra'")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
               file=sys.stderr)
         return 2
     defaults = {"moe_decode": (8, 8), "lm_head": (1, 3), "lm_head_sample": (8, 3), "igemm": (1, 64), "rswa": (8, 4),
+                "igemm_batched": (1, 1),
                 "copy": (1, 1),
                 "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
                 "decode_layer": (8, 6), "decode_step": (8, 1), "prefill_attn": (1024, 1)}
@@ -944,6 +1070,8 @@ def main() -> int:
         line["cpu_baseline"].update(host_cpu())
     else:
         line["cpu_baseline"] = None
+    if args.workload == "moe_decode" and args.tokens == 8 and not args.no_extras:
+        line["extra"] = run_extras(ctx, args)
     print(json.dumps(line), flush=True)
     return 0
 

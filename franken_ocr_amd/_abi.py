@@ -62,6 +62,7 @@ _SIGS: dict[str, list] = {
     "focr_hip_debug_s4s8_group_i32": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _SZ],
     "focr_hip_selftest": [_P, C.c_char_p, _SZ, _P],
     "focr_hip_igemm_s8s8_dev": [_P, _P, _P, _SZ, _SZ, _SZ, _P],
+    "focr_hip_igemm_s8s8_batched_dev": [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P],
     "focr_hip_igemm_u8s8_dev": [_P, _P, _P, _SZ, _SZ, _SZ, _P],
     "focr_hip_igemm_s4s8_packed_dev": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P],
     "focr_hip_qint8_upload": [_P, _P, _P, _SZ, _SZ, _P],

@@ -515,6 +515,28 @@ int32_t focr_hip_igemm_u8s8_dev(focr_hip_ctx* ctx, const uint8_t* a, const int8_
     return FOCR_HIP_OK;
 }
 
+int32_t focr_hip_igemm_s8s8_batched_dev(focr_hip_ctx* ctx, const int8_t* a, const int8_t* b, size_t batch,
+                                        size_t m, size_t k, size_t n, int32_t* out) {
+    CTX_GUARD(ctx);
+    int32_t st = FOCR_HIP_OK;
+    if (!fits_i32("igemm_s8s8_batched", m, "m", &st) || !fits_i32("igemm_s8s8_batched", k, "k", &st) ||
+        !fits_i32("igemm_s8s8_batched", n, "n", &st))
+        return st;
+    if (batch > 65535)
+        return fail(FOCR_HIP_E_SHAPE, fmt("igemm_s8s8_batched: batch %zu exceeds 65535", batch));
+    if (batch * m * n == 0) return FOCR_HIP_OK;
+    if (k == 0 || k % 16 || k > 65536)
+        return fail(FOCR_HIP_E_SHAPE,
+                    fmt("igemm_s8s8_batched: k %zu must be a positive multiple of 16, at most 65536", k));
+    if (!a || !b || !out) return fail(FOCR_HIP_E_ARG, "igemm_s8s8_batched: null device pointer");
+    if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16)
+        return fail(FOCR_HIP_E_ARG, "igemm_s8s8_batched: a and b must be 16-byte aligned");
+    ProfScope ps(ctx, "igemm_i8_batched");
+    FOCR_HIP_TRY(launch_igemm_i8_batched(ctx->stream, a, b, out, (int)batch, (int)m, (int)k, (int)n),
+                 "igemm kernel launch");
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_igemm_s4s8_packed_dev(focr_hip_ctx* ctx, const int8_t* a, const uint8_t* b_packed,
                                        const float* scales, size_t group, size_t m, size_t k, size_t n, float* out) {
     CTX_GUARD(ctx);

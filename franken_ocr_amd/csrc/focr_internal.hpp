@@ -212,6 +212,11 @@ constexpr int kRingWindow = 128;
 // k_igemm.hip: drop-in tier i32 GEMM, out[M,N] += A[M,K] . B[N,K]^T.
 hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const int8_t* b,
                            int32_t* out, int m, int k, int n);
+// batch independent s8s8 products in one launch: instance b reads
+// a + b*m*k, b + b*n*k and accumulates into out + b*m*n. Needs k a multiple
+// of 16 (<= 65536) and 16-byte aligned a and b.
+hipError_t launch_igemm_i8_batched(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int batch, int m,
+                                   int k, int n);
 
 // k_gemv.hip
 // rule: 0 quantize_row_i8 (half away), 1 quantize_row_i8_te (ties even), 2

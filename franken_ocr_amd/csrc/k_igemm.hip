@@ -17,12 +17,18 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kGroups = kThreads / 16;
 
+// blockIdx.y selects one of a batch of independent instances, A, B and out
+// advanced by sa, sb, so elements (0 for a single product).
 template <bool kU8, int MC>
 __global__ __launch_bounds__(kThreads) void igemm_vec_kernel(const int8_t* __restrict__ A,
                                                              const int8_t* __restrict__ B,
                                                              int32_t* __restrict__ out, int M,
-                                                             int K, int N) {
+                                                             int K, int N, size_t sa, size_t sb,
+                                                             size_t so) {
     extern __shared__ int4 lds_a[];  // [MC][K/16]
+    A += blockIdx.y * sa;
+    B += blockIdx.y * sb;
+    out += blockIdx.y * so;
     const int group = threadIdx.x >> 4;
     const int lane = threadIdx.x & 15;
     const int C = K >> 4;
@@ -102,7 +108,7 @@ __global__ __launch_bounds__(kThreads) void igemm_byte_kernel(const int8_t* __re
 
 template <bool kU8>
 hipError_t launch_vec(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int m, int k,
-                      int n) {
+                      int n, int batch = 1) {
     const int tiles = (n + kGroups - 1) / kGroups;
     const int grid = tiles < 4096 ? tiles : 4096;
     // Stage up to 32 rows, keeping LDS at or under 64 KiB.
@@ -116,8 +122,9 @@ hipError_t launch_vec(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* 
     const size_t lds = static_cast<size_t>(mc) * k;
 #define FOCR_IGEMM_CASE(MCV)                                                                   \
     case MCV:                                                                                  \
-        FOCR_LAUNCH((igemm_vec_kernel<kU8, MCV>), dim3(grid), dim3(kThreads), lds, s, a, \
-                           b, out, m, k, n);                                                   \
+        FOCR_LAUNCH((igemm_vec_kernel<kU8, MCV>), dim3(grid, batch), dim3(kThreads), lds, s, a, \
+                    b, out, m, k, n, static_cast<size_t>(m) * k, static_cast<size_t>(n) * k,      \
+                    static_cast<size_t>(m) * n);                                                  \
         break;
     switch (mc) {
         FOCR_IGEMM_CASE(1)
@@ -134,6 +141,15 @@ hipError_t launch_vec(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* 
 }
 
 }  // namespace
+
+hipError_t launch_igemm_i8_batched(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int batch, int m,
+                                   int k, int n) {
+    if (batch == 0 || m == 0 || n == 0) return hipSuccess;
+    if (batch < 0 || batch > 65535 || k <= 0 || k % 16 || k > 65536 ||
+        reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16)
+        return hipErrorInvalidValue;
+    return launch_vec<false>(s, a, b, out, m, k, n, batch);
+}
 
 hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const int8_t* b,
                            int32_t* out, int m, int k, int n) {

@@ -153,6 +153,15 @@ int32_t focr_hip_igemm_s8s8_dev(focr_hip_ctx* ctx, const int8_t* a, const int8_t
                                 size_t k, size_t n, int32_t* out);
 int32_t focr_hip_igemm_u8s8_dev(focr_hip_ctx* ctx, const uint8_t* a, const int8_t* b, size_t m,
                                 size_t k, size_t n, int32_t* out);
+/* `batch` independent s8s8 products in one launch (device pointers): for
+ * instance i, out[i] (m x n, i32) += a[i] (m x k) . b[i] (n x k)^T, with
+ * a = [batch][m][k], b = [batch][n][k], out = [batch][m][n]. The per-instance
+ * contract is simd::igemm_s8s8 (scalar.rs:78-116); the reference makes these
+ * calls one expert at a time (decoder.rs:1634, :1920, :2358), this entry
+ * takes all of them at once (e.g. 64 experts' gate projections). k must be a
+ * positive multiple of 16 (<= 65536), a and b 16-byte aligned, batch <= 65535. */
+int32_t focr_hip_igemm_s8s8_batched_dev(focr_hip_ctx* ctx, const int8_t* a, const int8_t* b,
+                                        size_t batch, size_t m, size_t k, size_t n, int32_t* out);
 int32_t focr_hip_igemm_s4s8_packed_dev(focr_hip_ctx* ctx, const int8_t* a,
                                        const uint8_t* b_packed, const float* scales, size_t group,
                                        size_t m, size_t k, size_t n, float* out);

@@ -26,6 +26,12 @@ def test_host_code_clean_under_asan_and_ubsan():
     oracle_san = ROOT / "oracle" / "_san" / "liboracle_san.so"
     if not B.SAN_OUT.exists() or not oracle_san.exists():
         pytest.skip("sanitized builds absent (run __graft_entry__.build())")
+    # a library older than its sources would test stale host code (and miss
+    # entry points the ABI binds): rebuild it first
+    newest = max(p.stat().st_mtime for p in B.sources() + list(B.CSRC.glob("*.hpp")))
+    if B.SAN_OUT.stat().st_mtime < newest:
+        B.build(sanitize=True)
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle"), "san"], check=True)
     env = dict(os.environ)
     env.update({
         "LD_PRELOAD": S.asan_runtime(),
