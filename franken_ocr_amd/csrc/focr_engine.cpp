@@ -1576,8 +1576,10 @@ static void drain_prof(focr_hip_ctx* ctx) {
             t.first += 1;
             t.second += ms;
         }
-        ctx->event_pool.push_back(p.start);
-        ctx->event_pool.push_back(p.stop);
+        // not recycled: an event reused for a later dispatch has read back
+        // elapsed times several times the kernel's (same step throughput)
+        hipEventDestroy(p.start);
+        hipEventDestroy(p.stop);
     }
     ctx->pending.clear();
 }

@@ -82,9 +82,9 @@ ProfScope::~ProfScope() {
     if (!start || !stop) return;
     if (used) {
         ctx->pending.push_back({name, start, stop});
-    } else {  // nothing launched (an error path): return the events
-        ctx->event_pool.push_back(start);
-        ctx->event_pool.push_back(stop);
+    } else {  // nothing launched (an error path)
+        hipEventDestroy(start);
+        hipEventDestroy(stop);
     }
 }
 
@@ -114,12 +114,8 @@ void* focr_hip_ctx::scratch_get(int slot, size_t bytes) {
     return b.p;
 }
 
+// A fresh event per profiled scope, destroyed once read (drain_prof).
 hipEvent_t focr_hip_ctx::take_event() {
-    if (!event_pool.empty()) {
-        hipEvent_t e = event_pool.back();
-        event_pool.pop_back();
-        return e;
-    }
     hipEvent_t e = nullptr;
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
@@ -196,7 +192,6 @@ int32_t focr_hip_ctx_destroy(focr_hip_ctx* ctx) {
         hipEventDestroy(p.start);
         hipEventDestroy(p.stop);
     }
-    for (auto e : ctx->event_pool) hipEventDestroy(e);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return FOCR_HIP_OK;

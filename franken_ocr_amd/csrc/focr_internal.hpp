@@ -86,7 +86,6 @@ struct focr_hip_ctx {
     // profiling
     bool prof = false;
     std::vector<focr::ProfPending> pending;
-    std::vector<hipEvent_t> event_pool;
     std::map<std::string, std::pair<long, double>> prof_totals;
 
     // Grow-only scratch. Returns nullptr (and sets the error) on failure.
