@@ -804,9 +804,10 @@ def bench_decode_layer(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    U = [len(np.unique(b.numpy())) for b in idx]
     el, prof, kernels = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
+    # distinct experts of each copy's last step (every copy has run by now)
+    U = [len(np.unique(b.numpy())) for b in idx[:min(n, args.warmup + 2 * args.steps)]]
     ring = min(128, (args.warmup + 2 * args.steps) // n)  # about where the rings are during the timed passes
     keys = G + ring
     mean_u = float(np.mean(U))
