@@ -713,16 +713,14 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
     if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.sel))) return st;
     hipError_t e = hipSuccess;
     {
+        // the shared expert's gate/up rows ride in the same launch as extra blocks
+        const MoeSharedGateUp shgu{L->swg, L->swu, L->ssg, L->ssu, s.shared_act, (int)L->shared_inter};
         ProfScope ps(ctx, "moe_gate_up");
-        e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false);
+        e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false,
+                               with_shared ? &shgu : nullptr);
     }
     if (e == hipSuccess && with_shared) {
         {
-            ProfScope ps(ctx, "moe_shared_gate_up");
-            e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->swg, L->ssg, L->swu, L->ssu, s.shared_act,
-                                   (int)L->shared_inter, true);
-        }
-        if (e == hipSuccess) {
             // quantize_row_i8 of the act rows, then the int8 GEMV: the same
             // products, scales and rounding as the expert's down projection
             // (decoder.rs:1753-1754), with the GEMV's full-grid weight stream

@@ -265,9 +265,17 @@ size_t moe_sel_bytes();
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, void* sel);
+// The shared expert's gate/up weights, folded into the routed gate/up launch
+// as extra blocks (every token a pair, act rows [t][inter]).
+struct MoeSharedGateUp {
+    const int8_t *wg, *wu;
+    const float *sg, *su;
+    float* act;
+    int inter;
+};
 hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
                               const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, bool shared);
+                              int inter, bool shared, const MoeSharedGateUp* with_shared = nullptr);
 hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
                            const float* sd, float* ybuf, int inter, bool shared);
 // out[t] = slot-order sum of ybuf[t*top_k + j] (+ shared_y[t]); zero for a

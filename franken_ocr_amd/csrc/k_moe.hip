@@ -256,8 +256,9 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
 // apart in load.
 // Shared mode is one expert whose pairs are the tokens. Slots past the number
 // of active experts get -1.
-__device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T) {
+__device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T, int slot = -1) {
     if (shared_T > 0) return 0;
+    if (slot < 0) slot = static_cast<int>(blockIdx.y);
     const int lane = threadIdx.x & 63;
     const uint4* row = reinterpret_cast<const uint4*>(sel.slot + lane * kMaxT);
     const uint4 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3];
@@ -265,7 +266,7 @@ __device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T) {
                          (r3.x | r3.y | r3.z | r3.w);
     const unsigned long long m = __ballot(any != 0u);
     const int below = __popcll(m & ((1ull << lane) - 1ull));
-    const unsigned long long hit = __ballot(any != 0u && below == static_cast<int>(blockIdx.y));
+    const unsigned long long hit = __ballot(any != 0u && below == slot);
     return hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
 }
 
@@ -360,24 +361,47 @@ constexpr int kAllTok = 32;  // stage every token row when T <= kAllTok
 // kAllTok) stages every token row once; its own instantiation, without the
 // per-pass staging path, fits 64 VGPRs, i.e. 8 waves per SIMD, so about
 // every block of a T = 8 step is resident at once.
+// The shared expert folded into the routed launch: grid rows y < nslots are
+// its blocks (each covering gridDim.x * G of its I rows), every token a pair
+// with gate 1, and y - nslots is the routed slot. Its blocks come first in
+// the dispatch order: each takes every token, so dispatched last they would
+// be the launch's tail. nslots = 0: none.
+struct SharedGU {
+    const int8_t *wg, *wu;
+    const float *sg, *su;
+    float* act;  // [T][I]
+    int I, nslots;
+};
+
 template <int LPR, int JC, bool ALLTOK>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     const MoeSel sel, int T, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, const int8_t* __restrict__ wg,
     const float* __restrict__ sg, const int8_t* __restrict__ wu, const float* __restrict__ su,
-    float* __restrict__ act, int H, int I, int shared_T) {
+    float* __restrict__ act, int H, int I, int shared_T, const SharedGU sh) {
     extern __shared__ int4 lds_x[];  // [rows staged][H/16]
     __shared__ int s_pid[kMaxT];
     __shared__ int s_tok[kMaxT];
     __shared__ float s_xs[64];  // one per lane of the staging wave
     __shared__ int s_np;
     constexpr int G = 256 / LPR;  // rows per block
-    const int e = block_expert(sel, shared_T);
+    const bool shb = static_cast<int>(blockIdx.y) < sh.nslots;  // block-uniform
+    if (shb) {
+        shared_T = T;
+        wg = sh.wg;
+        wu = sh.wu;
+        sg = sh.sg;
+        su = sh.su;
+        act = sh.act;
+        I = sh.I;
+    }
+    const int e = shb ? 0 : block_expert(sel, shared_T, static_cast<int>(blockIdx.y) - sh.nslots);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int C = H >> 4;
-    const int r = blockIdx.x * G + grp;
+    const int r = (shb ? static_cast<int>(blockIdx.y) * static_cast<int>(gridDim.x) * G : 0) +
+                  static_cast<int>(blockIdx.x) * G + grp;
     const bool live = r < I;  // rows past I compute unused values from row 0
     const size_t row = static_cast<size_t>(e) * I + (live ? r : 0);
     int4 wgv[JC], wuv[JC];
@@ -686,15 +710,15 @@ struct GemvArgs {
 template <int LPR>
 hipError_t launch_gate_up_lpr(hipStream_t s, dim3 grid, size_t lds, int JC, const GemvArgs& a, const int8_t* xq,
                               const float* xs, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
-                              float* act) {
+                              float* act, const SharedGU& sh) {
 #define FOCR_GU(J)                                                                                              \
     case J:                                                                                                     \
         if (a.T <= kAllTok)                                                                                     \
             FOCR_LAUNCH((moe_gate_up_kernel<LPR, J, true>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs, wg, \
-                        sg, wu, su, act, a.H, a.I, a.shared_T);                                                 \
+                        sg, wu, su, act, a.H, a.I, a.shared_T, sh);                                             \
         else                                                                                                    \
             FOCR_LAUNCH((moe_gate_up_kernel<LPR, J, false>), grid, dim3(256), lds, s, a.sel, a.T, a.K, xq, xs,    \
-                        wg, sg, wu, su, act, a.H, a.I, a.shared_T);                                             \
+                        wg, sg, wu, su, act, a.H, a.I, a.shared_T, sh);                                         \
         break;
     switch (JC) {
         FOCR_GU(1) FOCR_GU(2) FOCR_GU(3) FOCR_GU(4) FOCR_GU(5) FOCR_GU(6) FOCR_GU(7) FOCR_GU(8)
@@ -761,18 +785,25 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
 
 hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
                               const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, bool shared) {
+                              int inter, bool shared, const MoeSharedGateUp* with_shared) {
     int lpr, jc;
     pick_lpr(d.hidden, &lpr, &jc);
     if (!dims_ok(d) || !sel || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
     const int rows_per_block = 256 / lpr;
     const int max_active = shared ? 1 : (d.n_experts < d.t * d.top_k ? d.n_experts : d.t * d.top_k);
-    const dim3 grid((inter + rows_per_block - 1) / rows_per_block, max_active);
+    const int gx = (inter + rows_per_block - 1) / rows_per_block;
+    SharedGU sh{};
+    if (with_shared && !shared) {
+        const int per = gx * rows_per_block;
+        sh = SharedGU{with_shared->wg, with_shared->wu, with_shared->sg, with_shared->su, with_shared->act,
+                      with_shared->inter, (with_shared->inter + per - 1) / per};
+    }
+    const dim3 grid(gx, max_active + sh.nslots);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
     const size_t lds = (static_cast<size_t>(staged) * d.hidden + 1023) & ~static_cast<size_t>(1023);
     const GemvArgs a{sel_of(const_cast<void*>(sel)), d.t, d.top_k, d.hidden, inter, shared ? d.t : 0};
-    if (lpr == 16) return launch_gate_up_lpr<16>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
-    return launch_gate_up_lpr<8>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act);
+    if (lpr == 16) return launch_gate_up_lpr<16>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act, sh);
+    return launch_gate_up_lpr<8>(s, grid, lds, jc, a, xq, xs, wg, sg, wu, su, act, sh);
 }
 
 hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
