@@ -649,11 +649,11 @@ int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
 
 int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t, int32_t norm_topk,
                      float routed_scale, const MoeScratch& s, uint32_t* idx, float* gates, float* probs,
-                     void* sel) {
+                     void* sel, const MoeRouteNorm* norm = nullptr) {
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     ProfScope ps(ctx, "moe_route");
     FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
-                                  probs, s.flag, sel),
+                                  probs, s.flag, sel, norm),
                  "route launch");
     return FOCR_HIP_OK;
 }
@@ -684,9 +684,13 @@ namespace {
 // output (the decode layer's residual, decoder.rs:2625). With static_scratch
 // the intermediates are carved from the per-device static array instead of
 // the context's slots, and nothing is allocated.
+// norm: route rms_norm(hidden + norm->attn) * norm->w instead of hidden (the
+// decoder layer's residual + post-attention norm, folded into the route
+// kernel, which writes hidden + attn to norm->h_out; resid is then that).
 int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
                         int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
-                        float* gates, int32_t check_route, const float* resid, bool static_scratch = false) {
+                        float* gates, int32_t check_route, const float* resid, bool static_scratch = false,
+                        const MoeRouteNorm* norm = nullptr) {
     const char* name = static_scratch ? "moe_decode_noalloc" : "moe_decode";
     int32_t st = moe_checks(name, L, hidden, t, with_shared);
     if (st) return st;
@@ -710,7 +714,7 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
     uint32_t* di = idx ? idx : s.idx;
     float* dg = gates ? gates : s.gates;
     hipStream_t str = ctx->stream;
-    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.sel))) return st;
+    if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, di, dg, nullptr, s.sel, norm))) return st;
     hipError_t e = hipSuccess;
     {
         // the shared expert's gate/up rows ride in the same launch as extra blocks
@@ -1388,17 +1392,22 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
                                         attn, xq, xs, ctx->cu_count),
                      "o_proj gemv launch");
     }
+    // 6. decode_mlp_i8 (decoder.rs:2199-2268) and the residual
+    if (L->moe && H <= 1280) {
+        // route_default (moe.rs:53-76: norm_topk_prob false, scaling 1.0) + the shared expert; the
+        // route kernel computes h = x + attn and routes rms_norm(h) * post_ln itself
+        const MoeRouteNorm rn{attn, L->post_ln, L->eps, h};
+        return moe_decode_impl(ctx, L->moe, x, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, route_idx, nullptr, check_route,
+                               h, false, &rn);
+    }
     {
         ProfScope ps(ctx, "layer_residual_norm");
         FOCR_HIP_TRY(launch_residual_rms_norm(s, x, attn, L->post_ln, (int)B, (int)H, L->eps, h, nrm),
                      "residual rms_norm launch");
     }
-    // 6. decode_mlp_i8 (decoder.rs:2199-2268) and the residual
-    if (L->moe) {
-        // route_default (moe.rs:53-76: norm_topk_prob false, scaling 1.0) + the shared expert
+    if (L->moe)
         return moe_decode_impl(ctx, L->moe, nrm, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, route_idx, nullptr, check_route,
                                h);
-    }
     // dense (layer 0): expert_gemv_i8 (decoder.rs:1711-1720)
     float* g = reinterpret_cast<float*>(take(B * I * 4));
     float* u = reinterpret_cast<float*>(take(B * I * 4));

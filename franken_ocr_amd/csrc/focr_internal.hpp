@@ -262,9 +262,18 @@ struct MoeDims {
 // layout the expert kernels read (moe_sel_bytes() of device scratch: token
 // masks, per-expert slot and gate columns). Nothing is carried between calls.
 size_t moe_sel_bytes();
+// The decoder layer's residual + post-attention RMSNorm folded into the route
+// kernel: it routes rms_norm(hidden + attn) * w and writes hidden + attn to
+// h_out (hidden <= 1280).
+struct MoeRouteNorm {
+    const float* attn;
+    const float* w;
+    float eps;
+    float* h_out;
+};
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel);
+                            float* probs, int* flag, void* sel, const MoeRouteNorm* norm = nullptr);
 // The shared expert's gate/up weights, folded into the routed gate/up launch
 // as extra blocks (every token a pair, act rows [t][inter]).
 struct MoeSharedGateUp {

@@ -75,11 +75,24 @@ constexpr int kRouteNC = 5;   // float4 chunks per lane per batch: 64 x 5 x 4 = 
 // block has its whole 327 KB router request in flight at once (H = 1280 is
 // one batch). Every wave holds the whole token row, so each computes max|x|
 // for quantize_row_i8 itself; there is no barrier before the logits.
+// NORM: the decoder layer's residual + post-attention RMSNorm first
+// (decoder.rs:2596-2600): the token row is h = x + attn (h written to h_out
+// for the layer's final residual) and the routed row is rms_norm(h) * w, as
+// rms_norm_rows_kernel<1> computes it (f32 h, f64 sum of squares, f32
+// rstd); every wave holds the whole row, so each reduces it itself.
+struct RouteNorm {
+    const float* attn;  // [T][H]
+    const float* w;     // [H]
+    float eps;
+    float* h_out;       // [T][H]
+};
+
+template <bool NORM>
 __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void moe_route_kernel(
     const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
-    MoeSel sel) {
+    MoeSel sel, const RouteNorm rn) {
     __shared__ float s_logit[kMaxE];
     __shared__ __align__(16) float s_p[kMaxE];
     __shared__ int s_sel_e[kMaxK];
@@ -104,6 +117,56 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
                            __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
     };
 
+    // NORM: the residual row and the norm factor, from a per-wave copy of the
+    // whole row (NORM requires H <= 64 * 4 * kRouteNC: one batch below)
+    const float4* ar = NORM ? reinterpret_cast<const float4*>(rn.attn + static_cast<size_t>(t) * H) : nullptr;
+    const float4* wr = NORM ? reinterpret_cast<const float4*>(rn.w) : nullptr;
+    float rstd = 1.0f;
+    float4 nv[kRouteNC];  // NORM: this lane's chunks of the normed row (the batch below is one pass)
+    if constexpr (NORM) {
+        float4 hv[kRouteNC];
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const int c = lane + 64 * i;
+            const float4 a = xr[c < H4 ? c : H4 - 1], b = ar[c < H4 ? c : H4 - 1];
+            hv[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            if (lane + 64 * i < H4) {
+                ss = fma(static_cast<double>(hv[i].x), static_cast<double>(hv[i].x), ss);
+                ss = fma(static_cast<double>(hv[i].y), static_cast<double>(hv[i].y), ss);
+                ss = fma(static_cast<double>(hv[i].z), static_cast<double>(hv[i].z), ss);
+                ss = fma(static_cast<double>(hv[i].w), static_cast<double>(hv[i].w), ss);
+            }
+        }
+        ss = wave_sum_d(ss);
+        rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(H) + static_cast<double>(rn.eps)));
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < kRouteNC; ++i) {
+                const int c = lane + 64 * i;
+                if (c < H4) reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[c] = hv[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const int c = lane + 64 * i;
+            const float4 g = wr[c < H4 ? c : H4 - 1];
+            nv[i] = make_float4((hv[i].x * rstd) * g.x, (hv[i].y * rstd) * g.y, (hv[i].z * rstd) * g.z,
+                                (hv[i].w * rstd) * g.w);
+        }
+    }
+    // chunk c of the routed row: x itself, or (NORM) ((x + attn) * rstd) * w
+    auto row_chunk4 = [&](int c) {
+        const float4 a = xr[c];
+        if constexpr (!NORM) return a;
+        const float4 b = ar[c], g = wr[c];
+        return make_float4(((a.x + b.x) * rstd) * g.x, ((a.y + b.y) * rstd) * g.y, ((a.z + b.z) * rstd) * g.z,
+                           ((a.w + b.w) * rstd) * g.w);
+    };
+
     // 1. logits as f64 dot products (rounded to f32 below) and max|x|
     double acc[kRouteEPW];
 #pragma unroll
@@ -118,7 +181,8 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
         for (int i = 0; i < kRouteNC; ++i) {
             const int c = c0 + 64 * i;
             m[i] = c < H4 ? 0xFFFFFFFFu : 0u;
-            xv[i] = xr[c < H4 ? c : H4 - 1];
+            if constexpr (NORM) xv[i] = nv[i];
+            else xv[i] = xr[c < H4 ? c : H4 - 1];
         }
 #pragma unroll
         for (int k = 0; k < kRouteEPW; ++k)
@@ -157,7 +221,7 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     if (threadIdx.x < H4) {
         const float inv = 1.0f / a_scale;
-        const float4 xv = xr[threadIdx.x];
+        const float4 xv = row_chunk4(threadIdx.x);
         char4 q;
         q.x = quant_i8(xv.x, inv, false);
         q.y = quant_i8(xv.y, inv, false);
@@ -776,10 +840,19 @@ size_t moe_sel_bytes() { return kMaxE * kMaxT + kMaxE * kMaxT * 4; }
 
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel) {
+                            float* probs, int* flag, void* sel, const MoeRouteNorm* norm) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
-    FOCR_LAUNCH(moe_route_kernel, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden, d.n_experts,
-                d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel));
+    if (norm) {
+        // one batch of kRouteNC float4 per lane holds the whole row
+        if (d.hidden > 64 * 4 * kRouteNC || !norm->attn || !norm->w || !norm->h_out) return hipErrorInvalidValue;
+        const RouteNorm rn{norm->attn, norm->w, norm->eps, norm->h_out};
+        FOCR_LAUNCH(moe_route_kernel<true>, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn);
+    } else {
+        FOCR_LAUNCH(moe_route_kernel<false>, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel),
+                    RouteNorm{});
+    }
     return hipGetLastError();
 }
 
