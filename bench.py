@@ -495,7 +495,7 @@ def bench_prefill_attn(args, ctx):
                    "chunks": len(bounds)},
         "roofline": {"bound": "mfma", "kernel": "attn_prefill", "achieved": round(achieved, 2),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
-                     "traffic": None, "algorithmic_flops_per_step": flops,
+                     "traffic": traffic_for("attn_prefill", f"prefill_attn_{seq}"), "algorithmic_flops_per_step": flops,
                      "avg_launch_us": round(a_us, 3), "launches_per_step": len(bounds)},
         "kernel_avg_us": kernels,
         "_cpu_inputs": (q, k, v, chunk),
@@ -609,8 +609,8 @@ def bench_prefill_i4(args, ctx):
     counts = np.bincount(idx.ravel(), minlength=E)
     per_expert_bytes = 2 * I * H // 2 + H * I // 2 + 4 * (2 * I * (H // group) + H * (I // group))
     wbytes = int((counts > 0).sum()) * per_expert_bytes
-    views, ms_w, kernels_w, kernels_b = h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps,
-                                                 "i4_gate_up", "i4_down", per_expert_bytes)
+    views, ms_w, kernels_w, kernels_b = (None, float("nan"), {}, {}) if args.no_views else h5_views(
+        ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps, "i4_gate_up", "i4_down", per_expert_bytes)
     log(f"per-kernel avg us {kernels}; warm {kernels_w}; bucket {kernels_b}")
     return {
         "metric": "int4 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
@@ -729,8 +729,8 @@ def bench_prefill_i8(args, ctx):
     counts = np.bincount(idx.ravel(), minlength=E)
     per_expert_bytes = 3 * I * H + 4 * (2 * I + H)
     wbytes = int((counts > 0).sum()) * per_expert_bytes
-    views, ms_w, kernels_w, kernels_b = h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps,
-                                                 "i8_gate_up", "i8_down", per_expert_bytes)
+    views, ms_w, kernels_w, kernels_b = (None, float("nan"), {}, {}) if args.no_views else h5_views(
+        ctx, layers, dx, di, dg, dout, idx, T, prof, ms, args.steps, "i8_gate_up", "i8_down", per_expert_bytes)
     log(f"per-kernel avg us {kernels}; warm {kernels_w}; bucket {kernels_b}")
     return {
         "metric": "int8 chunked-prefill MoE (M=512, top-6, Zipf routing) tokens/s + int8 MFMA utilisation, 1 GPU",
@@ -1027,6 +1027,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations the default (moe_decode) run reports under 'extra'")
+    ap.add_argument("--no-views", action="store_true",
+                    help="prefill MoE workloads: skip the warm and bucket re-runs (profile the cold step alone)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",

@@ -92,13 +92,18 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
-    MoeSel sel, const RouteNorm rn) {
+    MoeSel sel, const RouteNorm rn, int spread) {
     __shared__ float s_logit[kMaxE];
     __shared__ __align__(16) float s_p[kMaxE];
     __shared__ int s_sel_e[kMaxK];
     __shared__ float s_sel_w[kMaxK];
     __shared__ int s_nvalid;
-    const int t = blockIdx.x;
+    // Token t runs as block t * spread; the blocks between exit at once.
+    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8), so with
+    // spread 8 every token block lands on XCD 0 and the 327 KB router comes
+    // from HBM once into that XCD's L2, not once per XCD.
+    if (blockIdx.x % spread) return;
+    const int t = blockIdx.x / spread;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int H4 = H >> 2;
@@ -299,7 +304,7 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     // writes them as one word unless a token block owns some of them
     static_assert(kMaxE * kMaxT == 4 * kRouteThreads, "one slot word per thread");
     if (sel.slot && t == 0) {
-        const int T = static_cast<int>(gridDim.x);
+        const int T = static_cast<int>(gridDim.x) / spread;
         const int ei = threadIdx.x / (kMaxT / 4), t0 = 4 * (threadIdx.x % (kMaxT / 4));
         uint8_t* w = sel.slot + 4 * threadIdx.x;
         if (ei >= E || t0 >= T) {
@@ -842,16 +847,20 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, void* sel, const MoeRouteNorm* norm) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
+    // token blocks on as few XCDs as hold them (32 CUs each): one router fetch per XCD used
+    const int spread = d.t <= 32 ? 8 : 4;
+    const dim3 grid(static_cast<unsigned>(d.t * spread));
     if (norm) {
         // one batch of kRouteNC float4 per lane holds the whole row
         if (d.hidden > 64 * 4 * kRouteNC || !norm->attn || !norm->w || !norm->h_out) return hipErrorInvalidValue;
         const RouteNorm rn{norm->attn, norm->w, norm->eps, norm->h_out};
-        FOCR_LAUNCH(moe_route_kernel<true>, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
-                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn);
+        FOCR_LAUNCH(moe_route_kernel<true>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn,
+                    spread);
     } else {
-        FOCR_LAUNCH(moe_route_kernel<false>, dim3(d.t), dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+        FOCR_LAUNCH(moe_route_kernel<false>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
                     d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel),
-                    RouteNorm{});
+                    RouteNorm{}, spread);
     }
     return hipGetLastError();
 }
