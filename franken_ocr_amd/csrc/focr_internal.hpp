@@ -214,6 +214,11 @@ hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const 
 // batch independent s8s8 products in one launch: instance b reads
 // a + b*m*k, b + b*n*k and accumulates into out + b*m*n. Needs k a multiple
 // of 16 (<= 65536) and 16-byte aligned a and b.
+// k_gemv.hip: the same products on the matrix cores (split-K GEMV, 16 rows
+// per pass, out += wrapping); hipErrorNotSupported where the shape does not
+// fit (m < 2, k < 64, not a multiple of 64 or > 8192, unaligned operands).
+hipError_t launch_igemm_i8_mfma(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int batch, int m,
+                                int k, int n);
 hipError_t launch_igemm_i8_batched(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int batch, int m,
                                    int k, int n);
 

@@ -358,12 +358,26 @@ __device__ __forceinline__ float fq_row_to_lds(const float4 (&v)[NF], const floa
 // rotates each (i, i + half) pair — lanes col and col ^ 1 hold the two halves
 // of the same rows — with the RoPE kernel's expressions, and writes q to its
 // row and k / v to the streams' ring slots instead of y.
+// The igemm form (simd::igemm_s8s8 on device buffers): y and the scales
+// unused, acc_out += the i32 sums (wrapping, as the reference's i32 adds);
+// grid row y advances W, xq and acc_out by sw, sx, so elements (a batch of
+// independent products in one launch).
+struct IgemmMode {
+    int accumulate;
+    size_t sw, sx, so;
+};
+
 template <int CPW, bool FQ, bool ROPE = false>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out,
-    const float* __restrict__ xf, const float* __restrict__ nw, float eps, RopeEpi re) {
+    const float* __restrict__ xf, const float* __restrict__ nw, float eps, RopeEpi re, const IgemmMode im) {
     extern __shared__ int4 lds_dyn[];  // x [M][K/16 + 1], then per-wave [16][16] chunks
+    if (gridDim.y > 1) {
+        W += blockIdx.y * im.sw;
+        xq += blockIdx.y * im.sx;
+        acc_out += blockIdx.y * im.so;
+    }
     __shared__ v4i_m red[kThreads / 64][64];
     __shared__ float lds_as[16];
     const int C = K >> 4;
@@ -433,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             const int r = i / C, c = i - r * C;
             lds_xv[r * xs + c] = x4[r * C + c];
         }
-        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M && a_scales ? a_scales[threadIdx.x] : 0.0f;
     }
     __syncthreads();
     v4i_m acc = {0, 0, 0, 0};
@@ -498,15 +512,18 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         return;
     }
     if (n >= N) return;
-    const float wscale = ws[n];
+    const float wscale = ws ? ws[n] : 0.0f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int i = 4 * g + v;
         if (i < M) {
             const int av = acc[v];
             const float t0 = static_cast<float>(av) * lds_as[i];
-            y[static_cast<size_t>(i) * N + n] = t0 * wscale;
-            if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = av;
+            if (y) y[static_cast<size_t>(i) * N + n] = t0 * wscale;
+            if (acc_out) {
+                int32_t* o = acc_out + static_cast<size_t>(i) * N + n;
+                *o = im.accumulate ? static_cast<int32_t>(static_cast<uint32_t>(*o) + static_cast<uint32_t>(av)) : av;
+            }
         }
     }
 }
@@ -626,7 +643,7 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
             const int mr = m - r0 < 16 ? m - r0 : 16;
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
                         nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                        x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{});
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
         }
         return hipGetLastError();
     }
@@ -655,7 +672,7 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
         (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
     const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
     const int D = epi.d_model;
-    if (m < kMfmaMinRows || m > RopePositions::kMax || k % 64 != 0 || k > kFqMaxK || n != 3 * D ||
+    if (m < kMfmaMinRows || m > RopePositions::kMax || k < 64 || k % 64 != 0 || k > kFqMaxK || n != 3 * D ||
         epi.head_dim % 16 != 0 || D % epi.head_dim != 0 || !epi.q || !epi.inv_freq ||
         lds_splitk + lds_splitk_static > max_lds_per_block() || (n + 15) / 16 >= 4 * (cu_count > 0 ? cu_count : 256))
         return hipErrorNotSupported;
@@ -668,7 +685,7 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
         e.r0 = r0;
         FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w_perm,
                     ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr, x + static_cast<size_t>(r0) * k, norm_w,
-                    eps, e);
+                    eps, e, IgemmMode{});
     }
     return hipGetLastError();
 }
@@ -711,13 +728,13 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
             if (cpw <= 2)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
             else if (cpw <= 4)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
         }
         return hipGetLastError();
     }
@@ -800,6 +817,42 @@ hipError_t launch_argmax_partial(hipStream_t s, const float* logits, int m, int 
                                  const uint32_t* ban_bits, int ban_words) {
     if (m == 0) return hipSuccess;
     FOCR_LAUNCH(argmax_partial_kernel, dim3(nparts, m), dim3(kThreads), 0, s, logits, n, keys, ban_bits, ban_words);
+    return hipGetLastError();
+}
+
+// simd::igemm_s8s8 on device buffers through the matrix-core split-K GEMV:
+// out (+)= a . b^T for batch instances (a [batch][m][k], b [batch][n][k],
+// out [batch][m][n]), 16 rows per pass. hipErrorNotSupported where the shape
+// does not fit it (k below 64, not a multiple of 64 or above 8192, m < 2, or
+// the rows' LDS stage too large).
+hipError_t launch_igemm_i8_mfma(hipStream_t s, const int8_t* a, const int8_t* b, int32_t* out, int batch, int m,
+                                int k, int n) {
+    // k >= 64: the kernel clamps its loads to the row's last 16-byte piece,
+    // which k = 0 does not have
+    if (batch < 1 || batch > 65535 || m < kMfmaMinRows || n < 1 || k < 64 || k % 64 || k > 256 * 4 * kSplitKMaxChunks)
+        return hipErrorNotSupported;
+    if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16) return hipErrorNotSupported;
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    if (lds_splitk + lds_splitk_static > max_lds_per_block()) return hipErrorNotSupported;
+    const int cpw = ((k + 255) / 256 + 3) / 4;
+    const dim3 grid(static_cast<unsigned>((n + 15) / 16), static_cast<unsigned>(batch));
+    const IgemmMode im{1, static_cast<size_t>(n) * k, static_cast<size_t>(m) * k, static_cast<size_t>(m) * n};
+    for (int r0 = 0; r0 < m; r0 += 16) {
+        const int mr = m - r0 < 16 ? m - r0 : 16;
+        const int8_t* ar = a + static_cast<size_t>(r0) * k;
+        int32_t* orow = out + static_cast<size_t>(r0) * n;
+        if (cpw <= 2)
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+        else if (cpw <= 4)
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+        else
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+    }
     return hipGetLastError();
 }
 

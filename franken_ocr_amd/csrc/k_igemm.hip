@@ -16,6 +16,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kGroups = kThreads / 16;
+// s8s8 products of up to this many rows (two 16-row passes) go to the
+// matrix-core split-K GEMV (each pass reads the weights once; the sdot4
+// kernel below spends one VALU dot per 4 weight bytes per row)
+constexpr int kMfmaMaxRows = 32;
 
 // blockIdx.y selects one of a batch of independent instances, A, B and out
 // advanced by sa, sb, so elements (0 for a single product).
@@ -148,6 +152,10 @@ hipError_t launch_igemm_i8_batched(hipStream_t s, const int8_t* a, const int8_t*
     if (batch < 0 || batch > 65535 || k <= 0 || k % 16 || k > 65536 ||
         reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16)
         return hipErrorInvalidValue;
+    if (m <= kMfmaMaxRows) {  // 2..32 rows: the matrix-core split-K GEMV
+        const hipError_t e = launch_igemm_i8_mfma(s, a, b, out, batch, m, k, n);
+        if (e != hipErrorNotSupported) return e;
+    }
     return launch_vec<false>(s, a, b, out, m, k, n, batch);
 }
 
@@ -157,6 +165,10 @@ hipError_t launch_igemm_i8(hipStream_t s, const void* a, bool a_unsigned, const 
     const int8_t* a8 = static_cast<const int8_t*>(a);
     const bool aligned = (reinterpret_cast<uintptr_t>(a8) % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(b) % 16 == 0);
+    if (!a_unsigned && aligned && m <= kMfmaMaxRows) {  // 2..32 rows: the matrix-core split-K GEMV
+        const hipError_t e = launch_igemm_i8_mfma(s, a8, b, out, 1, m, k, n);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (k > 0 && k % 16 == 0 && aligned && k <= 65536) {
         return a_unsigned ? launch_vec<true>(s, a8, b, out, m, k, n)
                           : launch_vec<false>(s, a8, b, out, m, k, n);
