@@ -1133,18 +1133,21 @@ int32_t focr_hip_rswa_record_prefill(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t
 
 namespace {
 
-// rswa.rs:467-494: slot and cursor update for one stream.
-uint32_t next_slot(focr_hip_rswa* c, size_t s) {
-    uint32_t slot;
+// rswa.rs:467-494: the slot one stream's next K/V row goes to, and the
+// cursor update after it is written. Callers take the slots first and advance
+// the cursors only once the launch that writes the rows has been accepted, so
+// a failed step leaves the ring as it was.
+uint32_t peek_slot(const focr_hip_rswa* c, size_t s) {
+    return c->ring_len[s] < static_cast<uint32_t>(kRingWindow) ? c->ring_len[s] : c->ring_pos[s];
+}
+
+void advance_slot(focr_hip_rswa* c, size_t s) {
     if (c->ring_len[s] < static_cast<uint32_t>(kRingWindow)) {
-        slot = c->ring_len[s];
         c->ring_len[s] += 1;
         c->ring_pos[s] = c->ring_len[s] % kRingWindow;
     } else {
-        slot = c->ring_pos[s];
         c->ring_pos[s] = (c->ring_pos[s] + 1) % kRingWindow;
     }
-    return slot;
 }
 
 int32_t rswa_write_all(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* k_steps, const float* v_steps,
@@ -1156,12 +1159,13 @@ int32_t rswa_write_all(focr_hip_ctx* ctx, focr_hip_rswa* c, const float* k_steps
         RswaStepArgs a{};
         a.n = static_cast<uint32_t>(std::min<size_t>(RswaStepArgs::kMax, c->n_streams - s0));
         for (uint32_t i = 0; i < a.n; ++i) {
-            a.slot[i] = next_slot(c, s0 + i);
+            a.slot[i] = peek_slot(c, s0 + i);
             if (slots) slots[s0 + i] = a.slot[i];
         }
         const size_t off = s0 * kNumHeads * kHeadDim;
         ProfScope ps(ctx, "rswa_write");
         FOCR_HIP_TRY(launch_rswa_write(ctx->stream, c, s0, a, k_steps + off, v_steps + off), "ring write launch");
+        for (uint32_t i = 0; i < a.n; ++i) advance_slot(c, s0 + i);
     }
     return FOCR_HIP_OK;
 }
@@ -1346,7 +1350,7 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
     // 1. input RMSNorm + quantize_row_i8, 2. the fused qkv GEMV, 3. RoPE at
     //    each stream's position and the ring write: k and v go straight to
     //    each stream's next ring slot (the cursors advance as
-    //    rswa_write_all's do). One launch (blocks norm and quantize the rows
+    //    rswa_write_all's do, once that launch is accepted). One launch (blocks norm and quantize the rows
     //    themselves, the epilogue rotates and scatters) where the shape
     //    allows, else the GEMV and the RoPE kernel.
     {
@@ -1357,7 +1361,7 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
         RopeRing ring{};
         ring.head_stride = static_cast<size_t>(kRingWindow) * kHeadDim;
         for (size_t i = 0; i < B; ++i) {
-            const uint32_t slot = next_slot(cache, i);
+            const uint32_t slot = peek_slot(cache, i);
             ring.k[i] = cache->ring_k(i) + static_cast<size_t>(slot) * kHeadDim;
             ring.v[i] = cache->ring_v(i) + static_cast<size_t>(slot) * kHeadDim;
         }
@@ -1381,6 +1385,7 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
                                            nullptr, nullptr, &ring),
                          "rope launch");
         }
+        for (size_t i = 0; i < B; ++i) advance_slot(cache, i);  // k and v are in their slots
     }
     int32_t st = rswa_attend_all(ctx, cache, q, cx);
     if (st) return st;
