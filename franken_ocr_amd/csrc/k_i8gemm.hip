@@ -192,10 +192,14 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(WPE, WPE))
         for (int s = 0; s < NS - 1; ++s) {
             read_step(sa, s + 1, (s + 1) & 1);
             mfma_step(s & 1);
-            // keep the reads ahead of the MFMAs (the scheduler would sink
-            // them below to reuse the fragment registers)
+            // one MFMA, then the next step's reads, then the other MFMAs:
+            // the wait for this step's fragments (issued a whole step ago)
+            // comes before the new reads, not after them (the compiler's
+            // wait there is lgkmcnt(0)); the order is pinned because the
+            // scheduler would sink the reads below to reuse registers
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, TI + TJ, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ - 1, 0);
         }
     };
     // every stage but the last (peeled, so the loop body has no branch)

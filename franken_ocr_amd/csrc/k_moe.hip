@@ -189,10 +189,12 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
             if constexpr (NORM) xv[i] = nv[i];
             else xv[i] = xr[c < H4 ? c : H4 - 1];
         }
+        // chunk-major: the dot products below take chunk i of all four rows
+        // at once, so they can start as soon as the first chunks arrive
 #pragma unroll
-        for (int k = 0; k < kRouteEPW; ++k)
+        for (int i = 0; i < kRouteNC; ++i)
 #pragma unroll
-            for (int i = 0; i < kRouteNC; ++i) {
+            for (int k = 0; k < kRouteEPW; ++k) {
                 const int c = c0 + 64 * i;
                 gv[k][i] = gr[k][c < H4 ? c : H4 - 1];
             }
@@ -325,14 +327,24 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
 // apart in load.
 // Shared mode is one expert whose pairs are the tokens. Slots past the number
 // of active experts get -1.
-__device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T, int slot = -1) {
+// Route zeroes every entry t >= T, so for T <= 16 the first 16 bytes of a
+// row decide it: one load per lane instead of four (every wave of the
+// launch reads the 64 rows before its first weight load; T = 8 gate/up
+// 16.8 -> 15.7 us).
+__device__ __forceinline__ int block_expert(const MoeSel& sel, int shared_T, int T, int slot = -1) {
     if (shared_T > 0) return 0;
     if (slot < 0) slot = static_cast<int>(blockIdx.y);
     const int lane = threadIdx.x & 63;
     const uint4* row = reinterpret_cast<const uint4*>(sel.slot + lane * kMaxT);
-    const uint4 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3];
-    const unsigned any = (r0.x | r0.y | r0.z | r0.w) | (r1.x | r1.y | r1.z | r1.w) | (r2.x | r2.y | r2.z | r2.w) |
-                         (r3.x | r3.y | r3.z | r3.w);
+    unsigned any;
+    if (T <= 16) {  // kernel argument: a uniform branch
+        const uint4 r0 = row[0];
+        any = r0.x | r0.y | r0.z | r0.w;
+    } else {
+        const uint4 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3];
+        any = (r0.x | r0.y | r0.z | r0.w) | (r1.x | r1.y | r1.z | r1.w) | (r2.x | r2.y | r2.z | r2.w) |
+              (r3.x | r3.y | r3.z | r3.w);
+    }
     const unsigned long long m = __ballot(any != 0u);
     const int below = __popcll(m & ((1ull << lane) - 1ull));
     const unsigned long long hit = __ballot(any != 0u && below == slot);
@@ -464,7 +476,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
         act = sh.act;
         I = sh.I;
     }
-    const int e = shb ? 0 : block_expert(sel, shared_T, static_cast<int>(blockIdx.y) - sh.nslots);
+    const int e = shb ? 0 : block_expert(sel, shared_T, T, static_cast<int>(blockIdx.y) - sh.nslots);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -542,7 +554,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     __shared__ float s_gate[kMaxT];
     __shared__ int s_np;
     constexpr int G = 256 / LPR;
-    const int e = block_expert(sel, shared_T);
+    const int e = block_expert(sel, shared_T, T);
     if (e < 0) return;
     const int grp = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
