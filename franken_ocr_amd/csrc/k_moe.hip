@@ -643,7 +643,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // caches.
 constexpr int DC_THREADS = 512;
 
-template <int LPR, int JC>
+template <int LPR, int JC, int RPG>
 __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     const uint32_t* __restrict__ idx, const float* __restrict__ gates, const int* __restrict__ flag, int T, int K,
     const float* __restrict__ act, const int8_t* __restrict__ wd, const float* __restrict__ sd,
@@ -651,8 +651,8 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     int E) {
     extern __shared__ int4 lds_q[];  // [K][I/16] quantized act rows of token t
     __shared__ float s_as[kMaxK];
-    __shared__ float s_y[DC_THREADS / LPR];
     constexpr int NG = DC_THREADS / LPR;
+    __shared__ float s_y[RPG * NG];
     // XCD-aware order: blocks are dispatched to the 8 XCDs round-robin
     // (block b to XCD b % 8, each with its own L2), and block b takes row
     // block rb = b % 8 + 8 * (b / (8 T)) of token t = (b / 8) % T, so every
@@ -662,20 +662,29 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
     const int b = static_cast<int>(blockIdx.x);
     const int t = (b >> 3) % T;
     const int rb = (b & 7) + 8 * ((b >> 3) / T);
-    const int R = NG / K;
+    // lane group g owns the RPG (slot, row) pairs p = g + NG q: slot
+    // j = p % K, row rb * R + p / K
+    const int R = RPG * NG / K;
     const int g = threadIdx.x / LPR;
     const int ln = threadIdx.x % LPR;
     const int wave = threadIdx.x >> 6;
     const int wl = threadIdx.x & 63;
-    const int j = g % K;
-    const int r = rb * R + g / K;
-    const bool live = g < K * R && r < H;  // dead groups compute unused values from valid addresses
     const int C = I >> 4;
-    // 1. expert id and gate of slot j, the token's flag, and (wave w < K) act
-    //    row t*K + w — all issued before anything waits
-    const int pid = t * K + (live ? j : 0);
-    const uint32_t eid = idx[pid];
-    const float gate = gates[pid];
+    int jq[RPG];
+    bool liveq[RPG];
+    uint32_t eid[RPG];
+    float gate[RPG];
+    // 1. expert ids and gates of the group's slots, the token's flag, and
+    //    (wave w < K) act row t*K + w — all issued before anything waits
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+        const int p = g + NG * q;
+        jq[q] = p % K;
+        liveq[q] = p < K * R && rb * R + p / K < H;  // dead pairs compute unused values from valid addresses
+        const int pid = t * K + (liveq[q] ? jq[q] : 0);
+        eid[q] = idx[pid];
+        gate[q] = gates[pid];
+    }
     const int bad = flag[t];
     const bool qwave = wave < K;  // wave-uniform
     const float* ar = act + static_cast<size_t>(t * K + (qwave ? wave : 0)) * I;
@@ -688,16 +697,18 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
             v[q] = ar[i < I ? i : I - 1];  // a duplicate of the last value past I: max unchanged
         }
     }
-    // 2. the down row of (slot j, row r)
-    const uint32_t e = eid < static_cast<uint32_t>(E) ? eid : 0u;
-    const size_t row = static_cast<size_t>(e) * H + (live ? r : 0);
-    int4 wv[JC];
-    {
+    // 2. the down rows of the group's pairs
+    int4 wv[RPG][JC];
+    float sdr[RPG];
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+        const uint32_t e = eid[q] < static_cast<uint32_t>(E) ? eid[q] : 0u;
+        const size_t row = static_cast<size_t>(e) * H + (liveq[q] ? rb * R + (g + NG * q) / K : 0);
         const int4* drow = reinterpret_cast<const int4*>(wd + row * I);
 #pragma unroll
-        for (int c = 0; c < JC; ++c) wv[c] = row_chunk(drow, ln + LPR * c, C);
+        for (int c = 0; c < JC; ++c) wv[q][c] = row_chunk(drow, ln + LPR * c, C);
+        sdr[q] = sd[row];
     }
-    const float sdr = sd[row];
     // 3. quantize_row_i8 of the act rows into LDS
     if (qwave) {
         int8_t* qrow = reinterpret_cast<int8_t*>(lds_q) + wave * I;
@@ -723,14 +734,17 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
         }
     }
     __syncthreads();
-    int d = 0;
 #pragma unroll
-    for (int c = 0; c < JC; ++c) {
-        const int cc = ln + LPR * c;
-        if (cc < C) d = dot16_i8(wv[c], lds_q[j * C + cc], d);
+    for (int q = 0; q < RPG; ++q) {
+        int d = 0;
+#pragma unroll
+        for (int c = 0; c < JC; ++c) {
+            const int cc = ln + LPR * c;
+            if (cc < C) d = dot16_i8(wv[q][c], lds_q[jq[q] * C + cc], d);
+        }
+        d = reduce_lanes<LPR>(d);
+        if (ln == 0) s_y[g + NG * q] = ((static_cast<float>(d) * s_as[jq[q]]) * sdr[q]) * gate[q];
     }
-    d = reduce_lanes<LPR>(d);
-    if (ln == 0 && g < NG) s_y[g] = ((static_cast<float>(d) * s_as[j]) * sdr) * gate;
     __syncthreads();
     // 4. slot-order sum of the token's K results for each row
     if (threadIdx.x < R) {
@@ -928,19 +942,30 @@ hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32
     int lpr, jc;
     pick_lpr(inter, &lpr, &jc);
     if (!dims_ok(d) || inter % 16 != 0 || jc > 8) return hipErrorInvalidValue;
-    const int R = (DC_THREADS / lpr) / d.top_k;
-    const int nrb8 = (((d.hidden + R - 1) / R) + 7) & ~7;  // row blocks, a multiple of 8 (the extra ones have no rows)
+    // row blocks per token, a multiple of 8 (the extra ones have no rows)
+    auto row_blocks = [&](int rpg) {
+        const int R = rpg * (DC_THREADS / lpr) / d.top_k;
+        return (((d.hidden + R - 1) / R) + 7) & ~7;
+    };
+    // two rows per lane group where one row each would need more blocks than
+    // fit at once (768: three 8-wave blocks per CU at the one-row kernel's
+    // registers; T = 8 needs 1024), so no second round of blocks pays the
+    // whole id -> weight -> act latency chain again at the kernel's end
+    const bool two_ok = (lpr == 8 && jc == 7) || (lpr == 16 && jc == 5);
+    const int rpg = two_ok && d.t * row_blocks(1) > 768 ? 2 : 1;
+    const int nrb8 = row_blocks(rpg);
     const dim3 grid(static_cast<unsigned>(d.t * nrb8));
     const size_t lds = static_cast<size_t>(d.top_k) * inter;
-#define FOCR_DC(L, J)                                                                                             \
-    if (lpr == L && jc == J) {                                                                                   \
-        FOCR_LAUNCH((moe_down_combine_kernel<L, J>), grid, dim3(DC_THREADS), lds, s, idx, gates, flag, d.t,      \
+#define FOCR_DC(L, J, P)                                                                                          \
+    if (lpr == L && jc == J && rpg == P) {                                                                       \
+        FOCR_LAUNCH((moe_down_combine_kernel<L, J, P>), grid, dim3(DC_THREADS), lds, s, idx, gates, flag, d.t,   \
                     d.top_k, act, wd, sd, shared_y, resid, out, d.hidden, inter, d.n_experts);                   \
         return hipGetLastError();                                                                                \
     }
-    FOCR_DC(8, 1) FOCR_DC(8, 2) FOCR_DC(8, 3) FOCR_DC(8, 4) FOCR_DC(8, 5) FOCR_DC(8, 6) FOCR_DC(8, 7) FOCR_DC(8, 8)
-    FOCR_DC(16, 1) FOCR_DC(16, 2) FOCR_DC(16, 3) FOCR_DC(16, 4) FOCR_DC(16, 5) FOCR_DC(16, 6) FOCR_DC(16, 7)
-    FOCR_DC(16, 8)
+    FOCR_DC(8, 1, 1) FOCR_DC(8, 2, 1) FOCR_DC(8, 3, 1) FOCR_DC(8, 4, 1) FOCR_DC(8, 5, 1) FOCR_DC(8, 6, 1)
+    FOCR_DC(8, 7, 1) FOCR_DC(8, 8, 1) FOCR_DC(16, 1, 1) FOCR_DC(16, 2, 1) FOCR_DC(16, 3, 1) FOCR_DC(16, 4, 1)
+    FOCR_DC(16, 5, 1) FOCR_DC(16, 6, 1) FOCR_DC(16, 7, 1) FOCR_DC(16, 8, 1)
+    FOCR_DC(8, 7, 2) FOCR_DC(16, 5, 2)
 #undef FOCR_DC
     return hipErrorInvalidValue;
 }
