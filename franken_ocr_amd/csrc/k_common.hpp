@@ -36,13 +36,7 @@ __device__ __forceinline__ int4 ld_stream(const int4* p) {
 }
 
 // Sum across the 16 lanes of a row group (all 16 lanes end with the total).
-__device__ __forceinline__ int reduce16_add(int v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
-    return v;
-}
+
 
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
@@ -54,6 +48,68 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// The same reductions through DPP row moves (VALU, a few cycles a step)
+// and four v_readlane_b32, for call sites that run with every lane of the
+// wave active; the shuffles above go through ds_bpermute at LDS latency, six
+// dependent round trips per reduction. The max is exact in any order; the
+// f64 sum adds pairs, quads, 8- and 16-lane rows, then the four rows, which
+// is another order than the butterfly above (a different last bit at most).
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_d(double v) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(dpp_mov<CTRL>(static_cast<int>(u & 0xffffffffu)));
+    const unsigned hi = static_cast<unsigned>(dpp_mov<CTRL>(static_cast<int>(u >> 32)));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), lane));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// Sum over aligned groups of LPR lanes (2, 4, 8 or 16), every lane of a
+// group getting its sum, as an xor butterfly of width LPR would (integers:
+// exact in any order). A disabled source lane reads as 0.
+template <int LPR>
+__device__ __forceinline__ int reduce_lanes(int v) {
+    static_assert(LPR == 2 || LPR == 4 || LPR == 8 || LPR == 16, "groups within one 16-lane DPP row");
+    v += dpp_mov<0xB1>(v);
+    if constexpr (LPR >= 4) v += dpp_mov<0x4E>(v);
+    if constexpr (LPR >= 8) v += dpp_mov<0x141>(v);
+    if constexpr (LPR >= 16) v += dpp_mov<0x140>(v);
+    return v;
+}
+
+__device__ __forceinline__ int reduce16_add(int v) { return reduce_lanes<16>(v); }
+
+// DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
+__device__ __forceinline__ float wave_max_f_full(float v) {
+    v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));  // every lane: its 16-lane row's max
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ double wave_sum_d_full(double v) {
+    v += dpp_mov_d<0xB1>(v);
+    v += dpp_mov_d<0x4E>(v);
+    v += dpp_mov_d<0x141>(v);
+    v += dpp_mov_d<0x140>(v);  // every lane: its 16-lane row's sum
+    return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
 }
 
 __device__ __forceinline__ double wave_max_d(double v) {

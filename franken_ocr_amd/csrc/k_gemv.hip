@@ -300,52 +300,78 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
 constexpr int kSplitKMaxChunks = 8;  // per wave: K <= 32 * 256
 constexpr int kFqMaxK = 2048;  // f32-input form: a row's float4s held by one wave's lanes (8 per lane)
 
-// quantize_row_i8 (half away, reciprocal) of one f32 row held as float4
-// chunks c = lane + 64 j (zero past K4), after an RMSNorm when nw is set
+// quantize_row_i8 (half away, reciprocal) of two f32 rows held as float4
+// chunks c = lane + 64 j (zero past K4), after an RMSNorm when norm is set
 // (y = (x * rstd) * w, the sum of squares in f64), written as int8 into the
-// LDS stage row `dst`; returns the row's activation scale.
+// LDS stage rows dst0 / dst1 (row 1 stored only when has1); s0 / s1 get the
+// activation scales. The two rows run in lockstep, their dependent
+// chains (f64 sum and reduction, sqrt, amax, division) interleaved, which one
+// wave per SIMD cannot hide otherwise (one row took ~1.6 us of a block's
+// time), and the reductions through DPP (the call is wave-uniform: every lane
+// of the wave takes part).
 template <int NF>
-__device__ __forceinline__ float fq_row_to_lds(const float4 (&v)[NF], const float4 (&wv)[NF], bool norm, float eps,
-                                               int K, int K4, int lane, int8_t* dst) {
-    float rstd = 1.0f;
+__device__ __forceinline__ void fq_rows2_to_lds(const float4 (&v0)[NF], const float4 (&v1)[NF],
+                                                const float4 (&wv)[NF], bool norm, float eps, int K, int K4,
+                                                int lane, int8_t* dst0, int8_t* dst1, bool has1, float& s0,
+                                                float& s1) {
+    float rstd0 = 1.0f, rstd1 = 1.0f;
     if (norm) {
-        double ss = 0.0;
+        double ss0 = 0.0, ss1 = 0.0;
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
-            const double a = v[j].x, b = v[j].y, c = v[j].z, d = v[j].w;
-            ss = fma(a, a, ss);
-            ss = fma(b, b, ss);
-            ss = fma(c, c, ss);
-            ss = fma(d, d, ss);
+            const double a0 = v0[j].x, b0 = v0[j].y, c0 = v0[j].z, d0 = v0[j].w;
+            const double a1 = v1[j].x, b1 = v1[j].y, c1 = v1[j].z, d1 = v1[j].w;
+            ss0 = fma(a0, a0, ss0);
+            ss1 = fma(a1, a1, ss1);
+            ss0 = fma(b0, b0, ss0);
+            ss1 = fma(b1, b1, ss1);
+            ss0 = fma(c0, c0, ss0);
+            ss1 = fma(c1, c1, ss1);
+            ss0 = fma(d0, d0, ss0);
+            ss1 = fma(d1, d1, ss1);
         }
-        ss = wave_sum_d(ss);
-        rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(K) + static_cast<double>(eps)));
+        ss0 = wave_sum_d_full(ss0);
+        ss1 = wave_sum_d_full(ss1);
+        rstd0 = static_cast<float>(1.0 / sqrt(ss0 / static_cast<double>(K) + static_cast<double>(eps)));
+        rstd1 = static_cast<float>(1.0 / sqrt(ss1 / static_cast<double>(K) + static_cast<double>(eps)));
     }
-    float4 u[NF];
-    float amax = 0.0f;
+    float4 u0[NF], u1[NF];
+    float amax0 = 0.0f, amax1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
-        u[j] = norm ? make_float4((v[j].x * rstd) * wv[j].x, (v[j].y * rstd) * wv[j].y, (v[j].z * rstd) * wv[j].z,
-                                  (v[j].w * rstd) * wv[j].w)
-                    : v[j];
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(u[j].x), fabsf(u[j].y)), fmaxf(fabsf(u[j].z), fabsf(u[j].w))));
+        u0[j] = norm ? make_float4((v0[j].x * rstd0) * wv[j].x, (v0[j].y * rstd0) * wv[j].y,
+                                   (v0[j].z * rstd0) * wv[j].z, (v0[j].w * rstd0) * wv[j].w)
+                     : v0[j];
+        u1[j] = norm ? make_float4((v1[j].x * rstd1) * wv[j].x, (v1[j].y * rstd1) * wv[j].y,
+                                   (v1[j].z * rstd1) * wv[j].z, (v1[j].w * rstd1) * wv[j].w)
+                     : v1[j];
+        amax0 = fmaxf(amax0, fmaxf(fmaxf(fabsf(u0[j].x), fabsf(u0[j].y)), fmaxf(fabsf(u0[j].z), fabsf(u0[j].w))));
+        amax1 = fmaxf(amax1, fmaxf(fmaxf(fabsf(u1[j].x), fabsf(u1[j].y)), fmaxf(fabsf(u1[j].z), fabsf(u1[j].w))));
     }
-    amax = wave_max_f(amax);
-    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    const float inv = 1.0f / a_scale;
+    amax0 = wave_max_f_full(amax0);
+    amax1 = wave_max_f_full(amax1);
+    const float a_scale0 = amax0 > 0.0f ? amax0 / 127.0f : 1.0f;
+    const float a_scale1 = amax1 > 0.0f ? amax1 / 127.0f : 1.0f;
+    const float inv0 = 1.0f / a_scale0, inv1 = 1.0f / a_scale1;
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
         const int c = lane + 64 * j;
         if (c < K4) {
-            char4 q;
-            q.x = quant_i8(u[j].x, inv, false);
-            q.y = quant_i8(u[j].y, inv, false);
-            q.z = quant_i8(u[j].z, inv, false);
-            q.w = quant_i8(u[j].w, inv, false);
-            reinterpret_cast<char4*>(dst)[c] = q;
+            char4 q0, q1;
+            q0.x = quant_i8(u0[j].x, inv0, false);
+            q0.y = quant_i8(u0[j].y, inv0, false);
+            q0.z = quant_i8(u0[j].z, inv0, false);
+            q0.w = quant_i8(u0[j].w, inv0, false);
+            q1.x = quant_i8(u1[j].x, inv1, false);
+            q1.y = quant_i8(u1[j].y, inv1, false);
+            q1.z = quant_i8(u1[j].z, inv1, false);
+            q1.w = quant_i8(u1[j].w, inv1, false);
+            reinterpret_cast<char4*>(dst0)[c] = q0;
+            if (has1) reinterpret_cast<char4*>(dst1)[c] = q1;
         }
     }
-    return a_scale;
+    s0 = a_scale0;
+    s1 = a_scale1;
 }
 
 // FQ: the activation rows come as f32 (xf [M][K], K <= kFqMaxK) and each
@@ -367,7 +393,9 @@ struct IgemmMode {
     size_t sw, sx, so;
 };
 
-template <int CPW, bool FQ, bool ROPE = false>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
+// NF (FQ): float4 chunks of a row per lane, 64 NF >= K / 4 (5 for K = 1280,
+// so the norm / quantize work covers no dead chunks)
+template <int CPW, bool FQ, bool ROPE = false, int NF = kFqMaxK / 256>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out,
@@ -390,22 +418,24 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int nch = (K + 255) >> 8;
     const int n0 = blockIdx.x * 16;
     int4 rg[CPW][4];
+    auto issue_weights = [&]() {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-        const int kc = wave + 4 * c;
-        const int kcl = kc < nch ? kc : nch - 1;  // loads past this wave's chunks re-read its last one (unused)
-        const int pc = kcl * 16 + col;            // this lane's 16-byte piece of the row
+        for (int c = 0; c < CPW; ++c) {
+            const int kc = wave + 4 * c;
+            const int kcl = kc < nch ? kc : nch - 1;  // loads past this wave's chunks re-read its last one (unused)
+            const int pc = kcl * 16 + col;            // this lane's 16-byte piece of the row
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 4 * j + g;
-            const int4 v = ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n < N ? n : N - 1) * K) +
-                                     (pc < C ? pc : C - 1));
-            const int mm = (n < N && pc < C) ? -1 : 0;  // past N or past K: zero
-            rg[c][j] = make_int4(v.x & mm, v.y & mm, v.z & mm, v.w & mm);
+            for (int j = 0; j < 4; ++j) {
+                const int n = n0 + 4 * j + g;
+                const int4 v = ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n < N ? n : N - 1) * K) +
+                                         (pc < C ? pc : C - 1));
+                const int mm = (n < N && pc < C) ? -1 : 0;  // past N or past K: zero
+                rg[c][j] = make_int4(v.x & mm, v.y & mm, v.z & mm, v.w & mm);
+            }
         }
-    }
+    };
     if constexpr (FQ) {
-        constexpr int NF = kFqMaxK / 256;
+        static_assert(64 * NF <= kFqMaxK / 4, "a row's chunks fit the lanes");
         const int K4 = K >> 2;
         const float4* w4 = reinterpret_cast<const float4*>(nw);
         float4 wv[NF];
@@ -414,12 +444,15 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             const int c = l + 64 * j;
             wv[j] = nw ? w4[c < K4 ? c : K4 - 1] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        // rows wave, wave + 4, ...: two rows' loads in flight at once
-        for (int r = wave; r < M; r += 2 * (kThreads / 64)) {
+        // rows wave, wave + 4, ...: two rows' loads in flight at once. The
+        // first pair's rows are requested before the weights (loads complete
+        // in issue order, so rows issued after the weights would wait for
+        // them); a wave past the last row loads row M - 1 and drops it.
+        auto load_pair = [&](int r, float4 (&v0)[NF], float4 (&v1)[NF]) {
+            const int ra = r < M ? r : M - 1;
             const int r2 = r + kThreads / 64;
-            const float4* x0 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r) * K);
-            const float4* x1 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r2 < M ? r2 : r) * K);
-            float4 v0[NF], v1[NF];
+            const float4* x0 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(ra) * K);
+            const float4* x1 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r2 < M ? r2 : ra) * K);
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
                 const int c = l + 64 * j;
@@ -431,17 +464,33 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
                 v1[j] = make_float4(__uint_as_float(__float_as_uint(b.x) & mk), __uint_as_float(__float_as_uint(b.y) & mk),
                                     __uint_as_float(__float_as_uint(b.z) & mk), __uint_as_float(__float_as_uint(b.w) & mk));
             }
-            const float s0 = fq_row_to_lds<NF>(v0, wv, nw != nullptr, eps, K, K4, l,
-                                               reinterpret_cast<int8_t*>(lds_xv + r * xs));
-            if (l == 0) lds_as[r] = s0;
-            if (r2 < M) {  // wave-uniform
-                const float s1 = fq_row_to_lds<NF>(v1, wv, nw != nullptr, eps, K, K4, l,
-                                                   reinterpret_cast<int8_t*>(lds_xv + r2 * xs));
-                if (l == 0) lds_as[r2] = s1;
+        };
+        auto quant_pair = [&](int r, const float4 (&v0)[NF], const float4 (&v1)[NF]) {
+            const int r2 = r + kThreads / 64;
+            if (r >= M) return;  // wave-uniform
+            const bool has1 = r2 < M;  // wave-uniform; without it row 1 repeats row 0 and is dropped
+            float s0, s1;
+            fq_rows2_to_lds<NF>(v0, v1, wv, nw != nullptr, eps, K, K4, l, reinterpret_cast<int8_t*>(lds_xv + r * xs),
+                                reinterpret_cast<int8_t*>(lds_xv + (has1 ? r2 : r) * xs), has1, s0, s1);
+            if (l == 0) {
+                lds_as[r] = s0;
+                if (has1) lds_as[r2] = s1;
             }
+        };
+        {
+            float4 v0[NF], v1[NF];
+            load_pair(wave, v0, v1);
+            issue_weights();
+            quant_pair(wave, v0, v1);
+        }
+        for (int r = wave + 2 * (kThreads / 64); r < M; r += 2 * (kThreads / 64)) {
+            float4 v0[NF], v1[NF];
+            load_pair(r, v0, v1);
+            quant_pair(r, v0, v1);
         }
         if (threadIdx.x < 16 && threadIdx.x >= M) lds_as[threadIdx.x] = 0.0f;
     } else {
+        issue_weights();
         const int4* x4 = reinterpret_cast<const int4*>(xq);
         for (int i = threadIdx.x; i < M * C; i += kThreads) {  // only the M live rows; the rest read as zero
             const int r = i / C, c = i - r * C;
@@ -496,7 +545,8 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
                 const int hd = pl / hdim, pr = pl - hd * hdim;
                 const int ii = pr >> 1, b = pr & 1;
                 const float angle = static_cast<float>(re.pos.p[s]) * re.inv_freq[ii];
-                const float sn = sinf(angle), cs = cosf(angle);
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
                 // b = 0: a * cs - b * sn (a = mine); b = 1: b * cs + a * sn (b = mine)
                 const float o = b == 0 ? yv * cs - pv * sn : yv * cs + pv * sn;
                 const int j = ii + b * half;
@@ -641,9 +691,14 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
         const int grid = (n + 15) / 16;
         for (int r0 = 0; r0 < m; r0 += 16) {
             const int mr = m - r0 < 16 ? m - r0 : 16;
-            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n, k,
-                        nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                        x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+            if (k <= 64 * 4 * 5)  // rows of <= 5 float4 per lane
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 5>), dim3(grid), dim3(kThreads), lds_splitk,
+                            s, w, ws, n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+            else
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
+                            n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
         }
         return hipGetLastError();
     }
@@ -683,9 +738,14 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
         const int mr = m - r0 < 16 ? m - r0 : 16;
         RopeEpi e = epi;
         e.r0 = r0;
-        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w_perm,
-                    ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr, x + static_cast<size_t>(r0) * k, norm_w,
-                    eps, e, IgemmMode{});
+        if (k <= 64 * 4 * 5)  // rows of <= 5 float4 per lane
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true, 5>), dim3(grid), dim3(kThreads), lds_splitk, s,
+                        w_perm, ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr,
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{});
+        else
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true>), dim3(grid), dim3(kThreads), lds_splitk, s,
+                        w_perm, ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr,
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{});
     }
     return hipGetLastError();
 }

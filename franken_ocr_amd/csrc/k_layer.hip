@@ -112,7 +112,8 @@ __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __res
     for (int t = threadIdx.x; t < n_heads * half; t += kThreads) {
         const int hd = t / half, i = t - hd * half;
         const float angle = p * inv_freq[i];
-        const float sn = sinf(angle), cs = cosf(angle);
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
         const int j0 = hd * head_dim + i, j1 = j0 + half;
         const float qa = row[j0], qb = row[j1];
         const float ka = row[D + j0], kb = row[D + j1];

@@ -50,12 +50,6 @@ struct MoeSel {
     float* gate;    // [kMaxE][kMaxT]
 };
 
-template <int LPR>
-__device__ __forceinline__ int reduce_lanes(int v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
-    return v;
-}
 
 // Index of the a-th set bit of m (a is block-uniform), or -1.
 __device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
@@ -129,11 +123,13 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     float rstd = 1.0f;
     float4 nv[kRouteNC];  // NORM: this lane's chunks of the normed row (the batch below is one pass)
     if constexpr (NORM) {
-        float4 hv[kRouteNC];
+        float4 hv[kRouteNC], gw[kRouteNC];
+        // the norm weights load with the two rows (one round trip, not two)
 #pragma unroll
         for (int i = 0; i < kRouteNC; ++i) {
             const int c = lane + 64 * i;
             const float4 a = xr[c < H4 ? c : H4 - 1], b = ar[c < H4 ? c : H4 - 1];
+            gw[i] = wr[c < H4 ? c : H4 - 1];
             hv[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
         }
         double ss = 0.0;
@@ -146,19 +142,11 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
                 ss = fma(static_cast<double>(hv[i].w), static_cast<double>(hv[i].w), ss);
             }
         }
-        ss = wave_sum_d(ss);
+        ss = wave_sum_d_full(ss);
         rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(H) + static_cast<double>(rn.eps)));
-        if (wave == 0) {
-#pragma unroll
-            for (int i = 0; i < kRouteNC; ++i) {
-                const int c = lane + 64 * i;
-                if (c < H4) reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[c] = hv[i];
-            }
-        }
 #pragma unroll
         for (int i = 0; i < kRouteNC; ++i) {
-            const int c = lane + 64 * i;
-            const float4 g = wr[c < H4 ? c : H4 - 1];
+            const float4 g = gw[i];
             nv[i] = make_float4((hv[i].x * rstd) * g.x, (hv[i].y * rstd) * g.y, (hv[i].z * rstd) * g.z,
                                 (hv[i].w * rstd) * g.w);
         }
@@ -215,7 +203,7 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
         }
     }
 #pragma unroll
-    for (int k = 0; k < kRouteEPW; ++k) acc[k] = wave_sum_d(acc[k]);
+    for (int k = 0; k < kRouteEPW; ++k) acc[k] = wave_sum_d_full(acc[k]);
     if (lane < kRouteEPW) {
         const int e = wave * kRouteEPW + lane;
         const double a = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
@@ -224,11 +212,18 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
 
     // 2. quantize_row_i8 of the token row (thread c owns chunk c; its wave
     //    holds max|x| of the whole row)
-    amax = wave_max_f(amax);
+    amax = wave_max_f_full(amax);
     const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     if (threadIdx.x < H4) {
         const float inv = 1.0f / a_scale;
         const float4 xv = row_chunk4(threadIdx.x);
+        if constexpr (NORM) {
+            // h = x + attn for the residual, stored here rather than before
+            // the router loads: a store ahead of them makes their wait cover it
+            const float4 a = xr[threadIdx.x], b = ar[threadIdx.x];
+            reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[threadIdx.x] =
+                make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        }
         char4 q;
         q.x = quant_i8(xv.x, inv, false);
         q.y = quant_i8(xv.y, inv, false);
@@ -244,11 +239,10 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     if (wave == 0) {
         const bool valid = lane < E;
         const float lg = valid ? s_logit[lane] : -INFINITY;
-        const double mx = static_cast<double>(wave_max_f(lg));
+        const double mx = static_cast<double>(wave_max_f_full(lg));
         double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
         double sum = ex;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        sum = wave_sum_d_full(sum);
         const float p = static_cast<float>(ex / sum);
         if (valid) {
             s_p[lane] = p;
@@ -586,7 +580,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
             if (I > 64 * NQ) {  // long rows (a wide shared expert): two passes over L2
                 float amax = 0.0f;
                 for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
-                amax = wave_max_f(amax);
+                amax = wave_max_f_full(amax);
                 const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
                 const float inv = 1.0f / a_scale;
                 for (int i = wl; i < I; i += 64) lds_b[pp * I + i] = quant_i8(ar[i], inv, false);
@@ -602,7 +596,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < NQ; ++q) amax = fmaxf(amax, fabsf(v[q]));
-            amax = wave_max_f(amax);
+            amax = wave_max_f_full(amax);
             const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const float inv = 1.0f / a_scale;
 #pragma unroll
@@ -716,7 +710,7 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < NQ; ++q) amax = fmaxf(amax, fabsf(v[q]));
-            amax = wave_max_f(amax);
+            amax = wave_max_f_full(amax);
             const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const float inv = 1.0f / a_scale;
 #pragma unroll
@@ -726,7 +720,7 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(
         } else {  // long rows: two passes over L2
             float amax = 0.0f;
             for (int i = wl; i < I; i += 64) amax = fmaxf(amax, fabsf(ar[i]));
-            amax = wave_max_f(amax);
+            amax = wave_max_f_full(amax);
             const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const float inv = 1.0f / a_scale;
             for (int i = wl; i < I; i += 64) qrow[i] = quant_i8(ar[i], inv, false);
