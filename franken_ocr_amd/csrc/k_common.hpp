@@ -104,6 +104,25 @@ __device__ __forceinline__ float wave_max_f_full(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// f32 sum over each 16-lane DPP row (every lane gets its row's sum; pairs,
+// quads, halves, then the row), for the full-wave reductions below.
+__device__ __forceinline__ float row16_sum_f(float v) {
+    v += __int_as_float(dpp_mov<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x140>(__float_as_int(v)));
+    return v;
+}
+
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float wave_sum_f_full(float v) {
+    v = row16_sum_f(v);
+    return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
+}
+
 __device__ __forceinline__ double wave_sum_d_full(double v) {
     v += dpp_mov_d<0xB1>(v);
     v += dpp_mov_d<0x4E>(v);

@@ -86,12 +86,10 @@ __global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, Rswa
     for (int i = 0; i < 8; ++i) {
         const int j = wave * 16 + 2 * i + half;
         const int key = chunk * KC + j;
-        float d = qv.x * kv[i].x + qv.y * kv[i].y + qv.z * kv[i].z + qv.w * kv[i].w;
-        d += __shfl_xor(d, 16, 32);
-        d += __shfl_xor(d, 8, 32);
-        d += __shfl_xor(d, 4, 32);
-        d += __shfl_xor(d, 2, 32);
-        d += __shfl_xor(d, 1, 32);
+        // the 32-lane dot: 16-lane row sums by DPP, then the two rows of each
+        // half wave read back as scalars (every lane is active here)
+        const float d16 = row16_sum_f(qv.x * kv[i].x + qv.y * kv[i].y + qv.z * kv[i].z + qv.w * kv[i].w);
+        const float d = half ? lane_f(d16, 32) + lane_f(d16, 48) : lane_f(d16, 0) + lane_f(d16, 16);
         if (dl == 0) sc[j] = key < N ? d * scale : -INFINITY;
     }
     // p . V: 8 key groups x 32 lanes (float4 of the head dim each); the V
@@ -108,11 +106,9 @@ __global__ __launch_bounds__(256) void rswa_chunk_kernel(Geom g, size_t s0, Rswa
     __syncthreads();
     if (wave == 0) {
         const float v = sc[lane];
-        const float m = wave_max_f(v);
+        const float m = wave_max_f_full(v);
         const float p = v == -INFINITY ? 0.0f : expf(v - m);
-        float l = p;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        const float l = wave_sum_f_full(p);
         sc[lane] = p;
         if (lane == 0) {
             s_ml[0] = m;
@@ -162,7 +158,7 @@ __global__ __launch_bounds__(D) void rswa_merge_kernel(RswaStepArgs a, const flo
     const float* base = partials + (static_cast<size_t>(si) * H + h) * max_chunks * kPart;
     float m = -INFINITY;
     for (int c = threadIdx.x; c < nch; c += D) m = fmaxf(m, base[c * kPart]);
-    m = wave_max_f(m);
+    m = wave_max_f_full(m);
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6][0] = m;
     __syncthreads();
     const float M = fmaxf(s_red[0][0], s_red[1][0]);
