@@ -45,13 +45,34 @@ struct AttnArgs {
     float scale;
 };
 
+// Combine lane l's value with lanes l ^ 16, l ^ 32, l ^ 48 (the four 16-lane
+// rows): gfx950's v_permlane16_swap / v_permlane32_swap of a value with itself
+// put both partners of an xor-16 (xor-32) pair in each lane (VALU; the
+// shuffle form went through ds_bpermute at LDS latency). The pairs combine as
+// the xor butterfly did: (r0 op r1) op (r2 op r3) in every lane.
+__device__ __forceinline__ float perm16_lo(float v, float& hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    hi = __uint_as_float(r[1]);
+    return __uint_as_float(r[0]);
+}
+__device__ __forceinline__ float perm32_lo(float v, float& hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    hi = __uint_as_float(r[1]);
+    return __uint_as_float(r[0]);
+}
 __device__ __forceinline__ float wave16_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    float b;
+    const float a = perm16_lo(v, b);
+    v = fmaxf(a, b);
+    const float c = perm32_lo(v, b);
+    return fmaxf(c, b);
 }
 __device__ __forceinline__ float wave16_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    float b;
+    const float a = perm16_lo(v, b);
+    v = a + b;
+    const float c = perm32_lo(v, b);
+    return c + b;
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_prefill_kernel(const AttnArgs a) {

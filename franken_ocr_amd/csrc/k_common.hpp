@@ -131,6 +131,35 @@ __device__ __forceinline__ double wave_sum_d_full(double v) {
     return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_mov_u64(uint64_t v) {
+    const unsigned lo = static_cast<unsigned>(dpp_mov<CTRL>(static_cast<int>(v & 0xffffffffu)));
+    const unsigned hi = static_cast<unsigned>(dpp_mov<CTRL>(static_cast<int>(v >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// max over each 16-lane DPP row, every lane getting its row's max (keys
+// ordered as u64, 0 the identity)
+__device__ __forceinline__ uint64_t row16_max_u64(uint64_t v) {
+    v = umax64(v, dpp_mov_u64<0xB1>(v));
+    v = umax64(v, dpp_mov_u64<0x4E>(v));
+    v = umax64(v, dpp_mov_u64<0x141>(v));
+    return umax64(v, dpp_mov_u64<0x140>(v));
+}
+
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int lane) {
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffu), lane));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64_full(uint64_t v) {
+    v = row16_max_u64(v);
+    return umax64(umax64(lane_u64(v, 0), lane_u64(v, 16)), umax64(lane_u64(v, 32), lane_u64(v, 48)));
+}
+
 __device__ __forceinline__ double wave_max_d(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));

@@ -269,12 +269,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
     if (keys) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            uint64_t bk = best[v];
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) {
-                const uint64_t w2 = __shfl_xor(bk, o, 16);
-                bk = w2 > bk ? w2 : bk;
-            }
+            const uint64_t bk = row16_max_u64(best[v]);
             if (col == 0) lds_keys[wave][4 * g + v] = bk;
         }
         __syncthreads();
@@ -537,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         for (int v = 0; v < 4; ++v) {
             const int i = 4 * g + v;
             const float yv = (static_cast<float>(acc[v]) * lds_as[i]) * wscale;
-            const float pv = __shfl_xor(yv, 1, 64);  // the pair partner: same rows, column col ^ 1
+            const float pv = __int_as_float(dpp_mov<0xB1>(__float_as_int(yv)));  // lane col ^ 1: the pair partner
             if (i >= M || n >= N) continue;
             const int s = re.r0 + i;
             if (n < 2 * D) {
@@ -603,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void argmax_reduce_kernel(const uint64_t*
         const uint64_t k = keys[static_cast<size_t>(row) * nparts + i];
         b = k > b ? k : b;
     }
-    b = wave_max_u64(b);
+    b = wave_max_u64_full(b);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -631,7 +626,7 @@ __global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float* _
         const uint64_t k = argmax_key(v, static_cast<uint32_t>(i));
         b = k > b ? k : b;
     }
-    b = wave_max_u64(b);
+    b = wave_max_u64_full(b);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
         for (int j = 0; j < F4L; ++j) v[j] = l + 64 * j < nf ? xr[l + 64 * j] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < F4L; ++j) amax = absmax(amax, v[j]);
-        amax = wave_max_f(amax);
+        amax = wave_max_f_full(amax);
         const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
         const float inv = 1.0f / a_scale;
 #pragma unroll
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
         if (l == 0) xs[row] = a_scale;
     } else {
         for (int f = l; f < nf; f += 64) amax = absmax(amax, xr[f]);
-        amax = wave_max_f(amax);
+        amax = wave_max_f_full(amax);
         const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
         const float inv = 1.0f / a_scale;
         for (int f = l; f < nf; f += 64) put(f, xr[f], a_scale, inv);

@@ -30,7 +30,7 @@ __device__ __forceinline__ double block_sum_sq(const float* __restrict__ r, int 
         const double v = static_cast<double>(r[i]);
         ss = fma(v, v, ss);
     }
-    ss = wave_sum_d(ss);
+    ss = wave_sum_d_full(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     double t = 0.0;
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __
         s_row[i] = v;  // each thread rewrites only its own elements
         amax = fmaxf(amax, fabsf(v));
     }
-    amax = wave_max_f(amax);
+    amax = wave_max_f_full(amax);
     if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = amax;
     __syncthreads();
     amax = s_max[0];

@@ -502,7 +502,7 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         const float* xr = x + static_cast<size_t>(ok ? row : 0) * H;
         float amax = 0.0f;
         for (int i = st; i < H; i += 256) amax = fmaxf(amax, fabsf(xr[i]));
-        amax = wave_max_f(amax);
+        amax = wave_max_f_full(amax);
         if (lane == 0) s_red[wave] = amax;
         __syncthreads();
         const int w0 = sub * 4;

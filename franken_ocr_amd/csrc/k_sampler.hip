@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(const uint64_t*
         const uint64_t k = keys[static_cast<size_t>(r) * nparts + i];
         b = k > b ? k : b;
     }
-    b = wave_max_u64(b);
+    b = wave_max_u64_full(b);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
     __syncthreads();
     if (threadIdx.x != 0) return;
