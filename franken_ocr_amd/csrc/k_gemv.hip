@@ -690,6 +690,10 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 5>), dim3(grid), dim3(kThreads), lds_splitk,
                             s, w, ws, n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
                             x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+            else if (k <= 64 * 4 * 7)  // <= 7 (the shared expert's 1792-wide act rows)
+                FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 7>), dim3(grid), dim3(kThreads), lds_splitk,
+                            s, w, ws, n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
                             n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
