@@ -235,7 +235,8 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
     __syncthreads();
 
     // 4. softmax in f64 over the f32 logits (wave 0, lane = expert): max,
-    //    exp, butterfly sum, divide, round to f32
+    //    exp, DPP-tree sum (the oracle's wave_tree_sum64 order), divide, round
+    //    to f32
     if (wave == 0) {
         const bool valid = lane < E;
         const float lg = valid ? s_logit[lane] : -INFINITY;

@@ -277,25 +277,33 @@ int oracle_sample(const float* row, size_t n, const uint32_t* seq, size_t len, s
  * optional renormalisation w /= (sum_f32(w) + 1e-20), then w *= scale.
  * Router numerics (documented definition of this build): each logit is an
  * f64 dot product rounded to f32; the softmax is computed in f64 from those
- * f32 logits (max-subtracted, exp, the sum taken in the order of a 64-lane
- * xor butterfly, butterfly_sum64 below, divide) and each probability rounded
+ * f32 logits (max-subtracted, exp, the sum taken in the order of the GPU's
+ * full-wave DPP reduction, wave_tree_sum64 below, divide) and each probability rounded
  * to f32. Any f64 summation order of a 1280-term dot product or a 64-term sum
  * rounds to the same f32 except when the f64 value lies within ~2^-29
  * (relative) of an f32 rounding boundary, so the increasing-q dot order here
  * and the GPU's strided partial sums agree bit for bit in practice; the
  * softmax sum order is fixed exactly. `probs` (optional) receives the f32
  * probabilities [t][n_experts]. */
-/* Sum of v[0..n), n <= 64, in 64-lane xor-butterfly order: lanes i >= n hold
- * +0; for o = 32, 16, 8, 4, 2, 1 every lane i takes v[i] + v[i ^ o]. All lanes
- * end equal (each step adds the same two operands in both partner lanes). */
-static double butterfly_sum64(const double* v, size_t n) {
-    double a[64], b[64];
+/* Sum of v[0..n), n <= 64, in the order of the GPU's full-wave DPP
+ * reduction (lane i holds v[i], lanes i >= n hold +0): within each 16-lane
+ * row the pairs (i, i+1), then the two pairs of each quad, then the two quads
+ * of each 8-lane half, then the two halves (each step adds the same two
+ * operands in both lanes that meet, and f64 addition is commutative, so every
+ * lane of a row ends with the same value), then the four rows as
+ * ((row0 + row1) + row2) + row3. */
+static double wave_tree_sum64(const double* v, size_t n) {
+    double a[64], row[4];
     for (size_t i = 0; i < 64; ++i) a[i] = i < n ? v[i] : 0.0;
-    for (size_t o = 32; o > 0; o >>= 1) {
-        for (size_t i = 0; i < 64; ++i) b[i] = a[i] + a[i ^ o];
-        memcpy(a, b, sizeof(a));
+    for (size_t r = 0; r < 4; ++r) {
+        double q[4];
+        for (size_t k = 0; k < 4; ++k) {
+            const double* b = a + 16 * r + 4 * k;
+            q[k] = (b[0] + b[1]) + (b[2] + b[3]);
+        }
+        row[r] = (q[0] + q[1]) + (q[2] + q[3]);
     }
-    return a[0];
+    return ((row[0] + row[1]) + row[2]) + row[3];
 }
 
 int oracle_route(const float* hidden, size_t t, size_t h, const float* gate, size_t n_experts,
@@ -318,7 +326,7 @@ int oracle_route(const float* hidden, size_t t, size_t h, const float* gate, siz
         for (size_t e = 0; e < n_experts; ++e)
             if ((double)logit[e] > mx) mx = (double)logit[e];
         for (size_t e = 0; e < n_experts; ++e) ex[e] = exp((double)logit[e] - mx);
-        const double sum = butterfly_sum64(ex, n_experts);
+        const double sum = wave_tree_sum64(ex, n_experts);
         for (size_t e = 0; e < n_experts; ++e) p[e] = (float)(ex[e] / sum);
         if (probs) memcpy(probs + tok * n_experts, p, n_experts * sizeof(float));
 
