@@ -658,6 +658,39 @@ def cpu_prefill_i4(args, inputs):
 # prefill on int8 weights (int8 matrix cores): the dense linear and the MoE block
 # ---------------------------------------------------------------------------
 
+_INT_MM_CHILD = """
+import sys, torch
+M, N, K, steps = map(int, sys.argv[1:5])
+a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+b = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda").t()  # [K, N], K contiguous
+for _ in range(3):
+    torch._int_mm(a, b)
+torch.cuda.synchronize()
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+e0.record()
+for _ in range(steps):
+    torch._int_mm(a, b)
+e1.record()
+torch.cuda.synchronize()
+print(e0.elapsed_time(e1) * 1e3 / steps)
+"""
+
+
+def library_int_mm_us(M: int, N: int, K: int, steps: int) -> float:
+    """The platform library's int8 GEMM at the same shape, as a reference
+    point: torch._int_mm (hipBLASLt; int8 x int8 -> int32, no scales), timed
+    with torch's events. It runs in a child process: torch ships its own HIP
+    runtime, which finds no device in a process where this library's runtime
+    already holds it. Not the product path."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, "-c", _INT_MM_CHILD, str(M), str(N), str(K), str(steps)],
+                       capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(f"library int8 GEMM child failed ({r.returncode}): {r.stderr[-500:]}")
+    return float(r.stdout.strip().splitlines()[-1])
+
+
 def bench_linear_i8(args, ctx):
     """nn::linear_int8_dynamic at the dense layer-0 MLP gate shape (N = 6848,
     K = 1280) over M prefill rows: dynamic-rule quantize + int8 MFMA GEMM."""
@@ -684,6 +717,12 @@ def bench_linear_i8(args, ctx):
     g_us = kernel_us(prof, "linear_i8")
     tops = ops / (g_us * 1e-6) / 1e12
     log(f"per-kernel avg us {kernels}")
+    lib = None
+    if args.library_ref:
+        lib_us = library_int_mm_us(M, N, Kd, args.steps)
+        lib = {"impl": "torch._int_mm (hipBLASLt), int8 x int8 -> int32", "avg_launch_us": round(lib_us, 3),
+               "frac": round(ops / (lib_us * 1e-6) / 1e12 / MFMA_INT8_PEAK_TOPS, 4)}
+        log(f"library int8 GEMM at the same shape: {lib}")
     return {
         "metric": "prefill int8 linear (linear_int8_dynamic) rows/s + int8 MFMA utilisation, 1 GPU",
         "value": round(M * args.steps / el, 1), "unit": "rows/s", "ms_per_step": round(ms, 5), "dtype": "int8",
@@ -693,6 +732,7 @@ def bench_linear_i8(args, ctx):
                      "traffic": traffic_for("linear_i8", f"linear_i8_m{M}"),
                      "algorithmic_ops_per_launch": ops, "avg_launch_us": round(g_us, 3)},
         "kernel_avg_us": kernels,
+        **({"library_ref": lib} if lib else {}),
         "_cpu_inputs": None,
     }
 
@@ -1027,6 +1067,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations the default (moe_decode) run reports under 'extra'")
+    ap.add_argument("--library-ref", action="store_true",
+                    help="linear_i8: also time the platform library's int8 GEMM (torch._int_mm) at the same shape")
     ap.add_argument("--no-views", action="store_true",
                     help="prefill MoE workloads: skip the warm and bucket re-runs (profile the cold step alone)")
     args = ap.parse_args()
