@@ -1289,6 +1289,22 @@ int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n
     if (e == hipSuccess)
         e = launch_permute_rows_i8(ctx->stream, qkv->w, qkv->scales, (int)qn, (int)qk, (int)(n_heads * head_dim),
                                    (int)head_dim, L->qkv_rope_w, L->qkv_rope_s);
+    if (dense) {
+        // gate rows then up rows, so one GEMV launch computes both
+        const size_t gi = dense_gate->n, gh = dense_gate->k;
+        if (e == hipSuccess) e = hipMalloc(&L->gate_up_w, 2 * gi * gh);
+        if (e == hipSuccess) e = hipMalloc(&L->gate_up_s, 2 * gi * sizeof(float));
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L->gate_up_w, dense_gate->w, gi * gh, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L->gate_up_w + gi * gh, dense_up->w, gi * gh, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L->gate_up_s, dense_gate->scales, gi * sizeof(float), hipMemcpyDeviceToDevice,
+                               ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L->gate_up_s + gi, dense_up->scales, gi * sizeof(float), hipMemcpyDeviceToDevice,
+                               ctx->stream);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         hipFree(L->input_ln);
@@ -1296,6 +1312,8 @@ int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n
         hipFree(L->inv_freq);
         hipFree(L->qkv_rope_w);
         hipFree(L->qkv_rope_s);
+        hipFree(L->gate_up_w);
+        hipFree(L->gate_up_s);
         delete L;
         return hip_fail(e, "decoder_layer_create upload");
     }
@@ -1312,6 +1330,8 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* L) {
     hipFree(L->inv_freq);
     hipFree(L->qkv_rope_w);
     hipFree(L->qkv_rope_s);
+    hipFree(L->gate_up_w);
+    hipFree(L->gate_up_s);
     delete L;
     return FOCR_HIP_OK;
 }
@@ -1404,6 +1424,25 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
         const MoeRouteNorm rn{attn, L->post_ln, L->eps, h};
         return moe_decode_impl(ctx, L->moe, x, B, 0, 1.0f, L->moe->swg ? 1 : 0, x, route_idx, nullptr, check_route,
                                h, false, &rn);
+    }
+    // dense (layer 0) in three launches where the shapes allow: the residual,
+    // the post-attention norm, quantize, the gate and up GEMVs and SiLU(g) * u
+    // in one (h = x + attn stored by it); quantize_row_i8 of act; the down
+    // GEMV with the residual add in its epilogue (x = h + down(act))
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    if (!L->moe && L->gate_up_w && B >= 2 && H % 64 == 0 && H <= 1280 && I % 64 == 0 && I <= 8192 &&
+        (I + 15) / 16 < static_cast<size_t>(4 * cu) && (H + 15) / 16 < static_cast<size_t>(4 * cu)) {
+        float* act = reinterpret_cast<float*>(take(B * I * 4));
+        int8_t* aq = reinterpret_cast<int8_t*>(take(B * I));
+        ProfScope ps(ctx, "layer_dense_mlp");
+        FOCR_HIP_TRY(launch_swiglu_i8_f32_add(s, L->gate_up_w, L->gate_up_s, (int)I, (int)H, x, attn, h, L->post_ln,
+                                              L->eps, (int)B, act, ctx->cu_count),
+                     "dense residual + norm + gate/up + silu launch");
+        FOCR_HIP_TRY(launch_quantize_rows(s, act, (int)B, (int)I, aq, xs, 0), "dense quantize launch");
+        FOCR_HIP_TRY(launch_gemv_i8_resid(s, L->down->w, L->down->scales, (int)H, (int)I, aq, xs, (int)B, h, x,
+                                          ctx->cu_count),
+                     "dense down + residual launch");
+        return FOCR_HIP_OK;
     }
     {
         ProfScope ps(ctx, "layer_residual_norm");

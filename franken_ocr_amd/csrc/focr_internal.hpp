@@ -145,6 +145,10 @@ struct focr_hip_decoder_layer {
     // (qkv_rope_row), for the GEMV whose epilogue applies RoPE; owned
     int8_t* qkv_rope_w = nullptr;
     float* qkv_rope_s = nullptr;
+    // dense MLP: gate rows then up rows [2 * inter, hidden] and their scales,
+    // for the one GEMV launch that computes both; owned
+    int8_t* gate_up_w = nullptr;
+    float* gate_up_s = nullptr;
 };
 
 struct focr_hip_moe_layer_i4 {
@@ -250,6 +254,17 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
                                  const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                                  uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,
                                  int ban_words);
+// The dense SwiGLU MLP in three launches (decode_layer step, layer 0): act =
+// silu(g) * u with [g; u] = dequant(W_gu . quantize_row_i8(rms_norm(x + x2) *
+// norm_w)) (W_gu: n gate rows then n up rows, k <= 1280), h = x + x2 written
+// to h_out, in one launch; the quantize kernel; y = dequant(W . xq) + resid.
+// Each returns hipErrorNotSupported where its shape is outside the one-launch
+// form (the caller then runs the separate kernels).
+hipError_t launch_swiglu_i8_f32_add(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
+                                    const float* x, const float* x2, float* h_out, const float* norm_w, float eps,
+                                    int m, float* act, int cu_count);
+hipError_t launch_gemv_i8_resid(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
+                                const float* a_scales, int m, const float* resid, float* y, int cu_count);
 hipError_t launch_argmax_reduce(hipStream_t s, const uint64_t* keys, int m, int nparts,
                                 uint32_t* argmax);
 // Per-block argmax keys [m][nparts] of a logits matrix (ban_bits nullable).

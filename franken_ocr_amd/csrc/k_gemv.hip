@@ -433,14 +433,31 @@ struct IgemmMode {
     int accumulate;
     size_t sw, sx, so;
 };
+// ADD (with FQ): the activation row is xf + xf2 (add_residual, decoder.rs:
+// 529-546, ahead of the post-attention norm); block 0 writes that sum to
+// h_out for the layer's final residual. resid (no ROPE): the epilogue returns
+// y + resid[i][n] (the residual folded into the projection's store; f32 adds
+// commute, so it equals the separate add bit for bit).
+struct RowAdd {
+    const float* xf2;
+    float* h_out;
+    const float* resid;
+};
 
 // NF (FQ): float4 chunks of a row per lane, 64 NF >= K / 4 (5 for K = 1280,
 // so the norm / quantize work covers no dead chunks)
-template <int CPW, bool FQ, bool ROPE = false, int NF = kFqMaxK / 256>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
+// SWIGLU: W is [gate rows; up rows] (2N rows) and ws their 2N scales; a block
+// computes the same 16 columns of both and its epilogue returns
+// y = silu(g) * u (decoder.rs:1711-1752: the dense MLP's gate and up GEMVs and
+// silu_mul_kernel, the same expressions in the same order).
+template <int CPW, bool FQ, bool ROPE = false, int NF = kFqMaxK / 256, bool ADD = false, bool SWIGLU = false>  // chunks per wave: 4 * CPW >= the row's 256-byte chunks
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K, const int8_t* __restrict__ xq,
     const float* __restrict__ a_scales, int M, float* __restrict__ y, int32_t* __restrict__ acc_out,
-    const float* __restrict__ xf, const float* __restrict__ nw, float eps, RopeEpi re, const IgemmMode im) {
+    const float* __restrict__ xf, const float* __restrict__ nw, float eps, RopeEpi re, const IgemmMode im,
+    const RowAdd radd) {
+    static_assert(!ADD || (FQ && !ROPE), "ADD is an f32-input form");
+    static_assert(!SWIGLU || !ROPE, "one epilogue");
     extern __shared__ int4 lds_dyn[];  // x [M][K/16 + 1], then per-wave [16][16] chunks
     if (gridDim.y > 1) {
         W += blockIdx.y * im.sw;
@@ -448,6 +465,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         acc_out += blockIdx.y * im.so;
     }
     __shared__ v4i_m red[kThreads / 64][64];
+    __shared__ v4i_m red_u[SWIGLU ? kThreads / 64 : 1][64];  // SWIGLU: the up tile's partials
     __shared__ float lds_as[16];
     const int C = K >> 4;
     const int xs = C + 1;
@@ -459,6 +477,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     const int nch = (K + 255) >> 8;
     const int n0 = blockIdx.x * 16;
     int4 rg[CPW][4];
+    int4 rgu[SWIGLU ? CPW : 1][4];  // SWIGLU: the up rows n + N
     auto issue_weights = [&]() {
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
@@ -468,10 +487,14 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int n = n0 + 4 * j + g;
-                const int4 v = ld_stream(reinterpret_cast<const int4*>(W + static_cast<size_t>(n < N ? n : N - 1) * K) +
-                                         (pc < C ? pc : C - 1));
+                const size_t row = static_cast<size_t>(n < N ? n : N - 1);
+                const int4 v = ld_stream(reinterpret_cast<const int4*>(W + row * K) + (pc < C ? pc : C - 1));
                 const int mm = (n < N && pc < C) ? -1 : 0;  // past N or past K: zero
                 rg[c][j] = make_int4(v.x & mm, v.y & mm, v.z & mm, v.w & mm);
+                if constexpr (SWIGLU) {
+                    const int4 u = ld_stream(reinterpret_cast<const int4*>(W + (row + N) * K) + (pc < C ? pc : C - 1));
+                    rgu[c][j] = make_int4(u.x & mm, u.y & mm, u.z & mm, u.w & mm);
+                }
             }
         }
     };
@@ -494,12 +517,20 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             const int r2 = r + kThreads / 64;
             const float4* x0 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(ra) * K);
             const float4* x1 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r2 < M ? r2 : ra) * K);
+            const float4* y0 = ADD ? reinterpret_cast<const float4*>(radd.xf2 + static_cast<size_t>(ra) * K) : nullptr;
+            const float4* y1 =
+                ADD ? reinterpret_cast<const float4*>(radd.xf2 + static_cast<size_t>(r2 < M ? r2 : ra) * K) : nullptr;
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
                 const int c = l + 64 * j;
                 const int cc = c < K4 ? c : K4 - 1;
                 const unsigned mk = c < K4 ? 0xFFFFFFFFu : 0u;
-                const float4 a = x0[cc], b = x1[cc];
+                float4 a = x0[cc], b = x1[cc];
+                if constexpr (ADD) {
+                    const float4 a2 = y0[cc], b2 = y1[cc];
+                    a = make_float4(a.x + a2.x, a.y + a2.y, a.z + a2.z, a.w + a2.w);
+                    b = make_float4(b.x + b2.x, b.y + b2.y, b.z + b2.z, b.w + b2.w);
+                }
                 v0[j] = make_float4(__uint_as_float(__float_as_uint(a.x) & mk), __uint_as_float(__float_as_uint(a.y) & mk),
                                     __uint_as_float(__float_as_uint(a.z) & mk), __uint_as_float(__float_as_uint(a.w) & mk));
                 v1[j] = make_float4(__uint_as_float(__float_as_uint(b.x) & mk), __uint_as_float(__float_as_uint(b.y) & mk),
@@ -510,6 +541,20 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             const int r2 = r + kThreads / 64;
             if (r >= M) return;  // wave-uniform
             const bool has1 = r2 < M;  // wave-uniform; without it row 1 repeats row 0 and is dropped
+            if constexpr (ADD) {
+                if (blockIdx.x == 0) {  // h = x + xf2 for the residual, once
+                    float4* h0 = reinterpret_cast<float4*>(radd.h_out + static_cast<size_t>(r) * K);
+                    float4* h1 = reinterpret_cast<float4*>(radd.h_out + static_cast<size_t>(r2) * K);
+#pragma unroll
+                    for (int j = 0; j < NF; ++j) {
+                        const int c = l + 64 * j;
+                        if (c < K4) {
+                            h0[c] = v0[j];
+                            if (has1) h1[c] = v1[j];
+                        }
+                    }
+                }
+            }
             float s0, s1;
             fq_rows2_to_lds<NF>(v0, v1, wv, nw != nullptr, eps, K, K4, l, reinterpret_cast<int8_t*>(lds_xv + r * xs),
                                 reinterpret_cast<int8_t*>(lds_xv + (has1 ? r2 : r) * xs), has1, s0, s1);
@@ -539,16 +584,26 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         }
         if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M && a_scales ? a_scales[threadIdx.x] : 0.0f;
     }
-    __syncthreads();
-    v4i_m acc = {0, 0, 0, 0};
+    // the epilogue's residual values, requested now so they arrive under the
+    // MFMAs (wave 0 writes the outputs)
+    float rsd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (!ROPE && !SWIGLU && radd.resid && wave == 0) {
+        const int nn = n0 + col < N ? n0 + col : N - 1;
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-        const int kc = wave + 4 * c;
-        if (kc >= nch) break;  // wave-uniform
+        for (int v = 0; v < 4; ++v) {
+            const int i = 4 * g + v;
+            rsd[v] = radd.resid[static_cast<size_t>(i < M ? i : 0) * N + nn];
+        }
+    }
+    __syncthreads();
+    v4i_m acc = {0, 0, 0, 0}, accu = {0, 0, 0, 0};
+    // one 16-row tile of chunk kc: the rows through the wave's LDS tile (one
+    // wave writes and reads it, in order), 4 MFMA steps into a
+    auto tile_mfma = [&](const int4 (&rgc)[4], int kc, v4i_m& a_acc) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int r = 4 * j + g;
-            wbuf[r * 16 + (col ^ r)] = rg[c][j];
+            wbuf[r * 16 + (col ^ r)] = rgc[j];
         }
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
@@ -559,18 +614,44 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
             const int ma = (pa < C && col < M) ? -1 : 0;
             const v4i_m bv = {bw.x, bw.y, bw.z, bw.w};
             const v4i_m av = {a.x & ma, a.y & ma, a.z & ma, a.w & ma};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc, 0, 0, 0);
+            a_acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, a_acc, 0, 0, 0);
         }
+    };
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int kc = wave + 4 * c;
+        if (kc >= nch) break;  // wave-uniform
+        tile_mfma(rg[c], kc, acc);
+        if constexpr (SWIGLU) tile_mfma(rgu[c], kc, accu);
     }
     red[wave][l] = acc;
+    if constexpr (SWIGLU) red_u[wave][l] = accu;
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (int w2 = 1; w2 < kThreads / 64; ++w2) {
         const v4i_m o = red[w2][l];
         acc = v4i_m{acc[0] + o[0], acc[1] + o[1], acc[2] + o[2], acc[3] + o[3]};
+        if constexpr (SWIGLU) {
+            const v4i_m ou = red_u[w2][l];
+            accu = v4i_m{accu[0] + ou[0], accu[1] + ou[1], accu[2] + ou[2], accu[3] + ou[3]};
+        }
     }
     const int n = n0 + col;
+    if constexpr (SWIGLU) {
+        if (n >= N) return;
+        const float sg = ws[n], su = ws[N + n];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = 4 * g + v;
+            if (i < M) {
+                const float gv = (static_cast<float>(acc[v]) * lds_as[i]) * sg;
+                const float uv = (static_cast<float>(accu[v]) * lds_as[i]) * su;
+                y[static_cast<size_t>(i) * N + n] = silu_f(gv) * uv;
+            }
+        }
+        return;
+    }
     if constexpr (ROPE) {
         const float wscale = ws[n < N ? n : N - 1];
         const int D = re.d_model, hdim = re.head_dim, half = hdim >> 1;
@@ -610,7 +691,10 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         if (i < M) {
             const int av = acc[v];
             const float t0 = static_cast<float>(av) * lds_as[i];
-            if (y) y[static_cast<size_t>(i) * N + n] = t0 * wscale;
+            if (y) {
+                const float o = t0 * wscale;
+                y[static_cast<size_t>(i) * N + n] = radd.resid ? o + rsd[v] : o;
+            }
             if (acc_out) {
                 int32_t* o = acc_out + static_cast<size_t>(i) * N + n;
                 *o = im.accumulate ? static_cast<int32_t>(static_cast<uint32_t>(*o) + static_cast<uint32_t>(av)) : av;
@@ -748,15 +832,15 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
             if (k <= 64 * 4 * 5)  // rows of <= 5 float4 per lane
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 5>), dim3(grid), dim3(kThreads), lds_splitk,
                             s, w, ws, n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{}, RowAdd{});
             else if (k <= 64 * 4 * 7)  // <= 7 (the shared expert's 1792-wide act rows)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 7>), dim3(grid), dim3(kThreads), lds_splitk,
                             s, w, ws, n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{}, RowAdd{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
                             n, k, nullptr, nullptr, mr, y + static_cast<size_t>(r0) * n, nullptr,
-                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{});
+                            x + static_cast<size_t>(r0) * k, norm_w, eps, RopeEpi{}, IgemmMode{}, RowAdd{});
         }
         return hipGetLastError();
     }
@@ -770,6 +854,56 @@ hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, i
                            y + static_cast<size_t>(r0) * n, nullptr, nullptr, nullptr, cu_count);
     }
     return e;
+}
+
+hipError_t launch_swiglu_i8_f32_add(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
+                                    const float* x, const float* x2, float* h_out, const float* norm_w, float eps,
+                                    int m, float* act, int cu_count) {
+    if (m < 1 || !x2 || !h_out) return hipErrorInvalidValue;
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    if (m < kMfmaMinRows || k < 64 || k % 64 != 0 || k > 64 * 4 * 5 ||
+        lds_splitk + lds_splitk_static > max_lds_per_block() || (n + 15) / 16 >= 4 * (cu_count > 0 ? cu_count : 256))
+        return hipErrorNotSupported;
+    const int grid = (n + 15) / 16;
+    for (int r0 = 0; r0 < m; r0 += 16) {
+        const int mr = m - r0 < 16 ? m - r0 : 16;
+        const size_t off = static_cast<size_t>(r0) * k;
+        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, false, 5, true, true>), dim3(grid), dim3(kThreads),
+                    lds_splitk, s, w_gu, ws_gu, n, k, nullptr, nullptr, mr, act + static_cast<size_t>(r0) * n, nullptr,
+                    x + off, norm_w, eps, RopeEpi{}, IgemmMode{}, RowAdd{x2 + off, h_out + off, nullptr});
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_i8_resid(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
+                                const float* a_scales, int m, const float* resid, float* y, int cu_count) {
+    if (m < 1 || !resid) return hipErrorInvalidValue;
+    const size_t lds_splitk =
+        (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_splitk_static = (kThreads / 64) * 64 * sizeof(int4) + 16 * sizeof(float);
+    if (m < kMfmaMinRows || k < 64 || k % 64 != 0 || k > 256 * 4 * kSplitKMaxChunks ||
+        lds_splitk + lds_splitk_static > max_lds_per_block() || (n + 15) / 16 >= 4 * (cu_count > 0 ? cu_count : 256))
+        return hipErrorNotSupported;
+    const int grid = (n + 15) / 16;
+    const int cpw = ((k + 255) / 256 + 3) / 4;
+    for (int r0 = 0; r0 < m; r0 += 16) {
+        const int mr = m - r0 < 16 ? m - r0 : 16;
+        const int8_t* xq_r = xq + static_cast<size_t>(r0) * k;
+        float* y_r = y + static_cast<size_t>(r0) * n;
+        const RowAdd ra{nullptr, nullptr, resid + static_cast<size_t>(r0) * n};
+        if (cpw <= 2)
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n,
+                        k, xq_r, a_scales + r0, mr, y_r, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, ra);
+        else if (cpw <= 4)
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n,
+                        k, xq_r, a_scales + r0, mr, y_r, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, ra);
+        else
+            FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws, n,
+                        k, xq_r, a_scales + r0, mr, y_r, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, ra);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_permute_rows_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k, int D, int head_dim,
@@ -799,11 +933,11 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
         if (k <= 64 * 4 * 5)  // rows of <= 5 float4 per lane
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true, 5>), dim3(grid), dim3(kThreads), lds_splitk, s,
                         w_perm, ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr,
-                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{});
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{}, RowAdd{});
         else
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, true, true>), dim3(grid), dim3(kThreads), lds_splitk, s,
                         w_perm, ws_perm, n, k, nullptr, nullptr, mr, nullptr, nullptr,
-                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{});
+                        x + static_cast<size_t>(r0) * k, norm_w, eps, e, IgemmMode{}, RowAdd{});
     }
     return hipGetLastError();
 }
@@ -846,13 +980,13 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             int32_t* acc_r = acc ? acc + static_cast<size_t>(r0) * n : nullptr;
             if (cpw <= 2)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, RowAdd{});
             else if (cpw <= 4)
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, RowAdd{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), dim3(grid), dim3(kThreads), lds_splitk, s, w, ws,
-                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{});
+                            n, k, xq_r, a_scales + r0, mr, y_r, acc_r, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, RowAdd{});
         }
         return hipGetLastError();
     }
@@ -963,13 +1097,13 @@ hipError_t launch_igemm_i8_mfma(hipStream_t s, const int8_t* a, const int8_t* b,
         int32_t* orow = out + static_cast<size_t>(r0) * n;
         if (cpw <= 2)
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
-                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
         else if (cpw <= 4)
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
-                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
         else
             FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false>), grid, dim3(kThreads), lds_splitk, s, b, nullptr, n, k,
-                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im);
+                        ar, nullptr, mr, nullptr, orow, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
     }
     return hipGetLastError();
 }

@@ -98,7 +98,9 @@ def _prefill(ctx, B, seed):
     return cache, rings, kv
 
 
-@pytest.mark.parametrize("kind,B", [("moe", 4), ("dense", 2), ("moe", 20)])  # 20: a second 16-row qkv pass
+# moe 20: a second 16-row qkv pass; dense 2 / 8 (its stream limit): the
+# three-launch dense MLP; dense 1: the separate kernels it replaces
+@pytest.mark.parametrize("kind,B", [("moe", 4), ("dense", 2), ("moe", 20), ("dense", 8), ("dense", 1)])
 def test_decoder_layer_steps_match_oracle(ctx, kind, B):
     _say(f"{kind} layer, {B} streams, 3 steps")
     lw = _weights(12000 if kind == "moe" else 12500, None if kind == "moe" else 6848)
