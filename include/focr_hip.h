@@ -426,7 +426,10 @@ int32_t focr_hip_rms_norm(focr_hip_ctx* ctx, const float* x, size_t rows, size_t
  * The layer borrows the weight handles (they must outlive it) and copies the
  * two norm weights (host pointers, [hidden]); it also keeps its own device
  * copy of the qkv weights and scales with the q / k rows in RoPE pair order
- * (3 D x hidden bytes), which the qkv GEMV with RoPE in its epilogue reads.
+ * (3 D x hidden bytes), which the qkv GEMV with RoPE in its epilogue reads,
+ * and, for the dense MLP, a copy of the gate rows followed by the up rows
+ * with their scales (2 x inter x hidden bytes), which the one launch that
+ * computes both and silu(gate) * up reads.
  * Exactly one of moe or the three dense handles. D = n_heads * head_dim must
  * be 10 x 128 for the cache. */
 int32_t focr_hip_decoder_layer_create(focr_hip_ctx* ctx, size_t hidden, size_t n_heads, size_t head_dim,
