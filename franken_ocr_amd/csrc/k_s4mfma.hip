@@ -276,8 +276,30 @@ __device__ __forceinline__ void s4_tile(const int8_t* __restrict__ A, int K, int
     constexpr int APT = (BM * QC * 2 + 255) / 256;  // pieces per thread and chunk
     int4 va[APT];
     int vat[APT];
+    // a full chunk's pieces of this thread: the same rows, columns and LDS
+    // offsets in every full chunk, so they are worked out once per tile (the
+    // division by the pieces per row is a software division)
+    const int8_t* fsrc[APT];
+    int fvat[APT];
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+        constexpr int cpr = 2 * QC;
+        const int i = u * 256 + tid, nch = rows_staged * cpr;
+        const int ic = i < nch ? i : nch - 1;  // past the end: a duplicate of the last piece
+        const int m = ic / cpr, c = ic - m * cpr;
+        fvat[u] = m * KS + 16 * c;
+        fsrc[u] = A + static_cast<size_t>(s_arow[m]) * K + 16 * c;
+    }
     auto load_a = [&](int c0) {
         const int cpr = min(QC, Q - c0) * 2;  // 16-byte pieces per row in the chunk
+        if (cpr == 2 * QC) {
+#pragma unroll
+            for (int u = 0; u < APT; ++u) {
+                vat[u] = fvat[u];
+                va[u] = *reinterpret_cast<const int4*>(fsrc[u] + c0 * 32);
+            }
+            return;
+        }
         const int nch = rows_staged * cpr;
 #pragma unroll
         for (int u = 0; u < APT; ++u) {
