@@ -67,6 +67,29 @@ def test_route_bit_exact(ctx, gpu_layer, layer_w, t, norm_topk):
     np.testing.assert_allclose(dp.numpy(), probs, rtol=1e-6, atol=1e-12)
 
 
+def test_route_ties_at_the_cutoff_pick_lower_indices(ctx):
+    """Seven identical router rows that dominate every token: their logits and
+    probabilities are bit-identical, so the greedy top-6 (moe.rs:215-240: rank
+    by probability, then index) must take the six lowest of them, in index
+    order, with equal gates."""
+    from franken_ocr_amd.engine import MoeLayer
+
+    router, wg, sg, wu, su, wd, sd = make_layer(700)
+    tied = [2, 11, 19, 33, 47, 52, 60]
+    router[tied, :] = np.abs(synth.f32_normal(synth.seed_of(701), H, 0.0, 0.02)) * 5.0
+    t = 8
+    x = np.abs(synth.f32_normal(synth.seed_of(702), t * H)).reshape(t, H)
+    L = MoeLayer(H, I, E, K, router, wg, sg, wu, su, wd, sd, ctx=ctx)
+    didx, dg, dp = ctx.empty((t, K), np.uint32), ctx.empty((t, K), np.float32), ctx.empty((t, E), np.float32)
+    L.route(ctx.to_device(x), didx, dg, dp, norm_topk=True)
+    st, idx, w, probs = O.route(x, router, E, K, norm_topk=True)
+    assert st == 0
+    assert idx.tolist() == [tied[:6]] * t  # the oracle itself resolves the tie this way
+    assert np.array_equal(didx.numpy(), idx)
+    np.testing.assert_allclose(dg.numpy(), w, rtol=1e-6, atol=0)
+    assert (dg.numpy() == dg.numpy()[:, :1]).all()  # tied probabilities: equal gates
+
+
 @pytest.mark.parametrize("t", [1, 8, 32])
 def test_moe_decode_matches_oracle(ctx, gpu_layer, layer_w, t):
     _say(f"moe_decode t={t}")
