@@ -242,6 +242,50 @@ __device__ __forceinline__ void block_quantize_row(const float* __restrict__ xr,
     if (threadIdx.x == 0) *a_scale_out = a_scale;
 }
 
+// The same with the row held in registers: thread t takes float4 chunks
+// t + THREADS j (j < NC; K % 4 == 0, 4 THREADS NC >= K, xr 16-byte and q
+// 4-byte aligned), every load issued before the first use, the amax from
+// registers (DPP wave max), the codes stored four to a word. Same quant_rule,
+// same amax (order-free), so the same bytes and scale as block_quantize_row,
+// whose strided loop waits for each load in turn.
+template <int THREADS, int NC>
+__device__ __forceinline__ void block_quantize_row_vec(const float* __restrict__ xr, int K, int8_t* __restrict__ q,
+                                                       float* __restrict__ a_scale_out, int rule, float* red) {
+    const int K4 = K >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    float4 v[NC];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + THREADS * j;
+        const float4 t = x4[c < K4 ? c : K4 - 1];  // past the row: its last chunk again (unused)
+        v[j] = t;
+        if (c < K4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+    }
+    amax = wave_max_f_full(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < THREADS / 64; ++w) amax = fmaxf(amax, red[w]);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+    char4* q4 = reinterpret_cast<char4*>(q);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + THREADS * j;
+        if (c < K4) {
+            char4 o;
+            o.x = quant_rule(v[j].x, a_scale, inv, rule);
+            o.y = quant_rule(v[j].y, a_scale, inv, rule);
+            o.z = quant_rule(v[j].z, a_scale, inv, rule);
+            o.w = quant_rule(v[j].w, a_scale, inv, rule);
+            q4[c] = o;
+        }
+    }
+    if (threadIdx.x == 0) *a_scale_out = a_scale;
+}
+
 // decoder.rs:1079-1083 silu(x) = x / (1 + e^-x), accurate expf (no fast math).
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 

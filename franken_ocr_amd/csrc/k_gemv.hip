@@ -42,39 +42,8 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_vec_kernel(const float
                                                                      float* __restrict__ a_scales, int rule) {
     __shared__ float red[kThreads / 64];
     const int row = blockIdx.x;
-    const int K4 = K >> 2;
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * K);
-    float4 v[NC];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const int c = static_cast<int>(threadIdx.x) + kThreads * j;
-        const float4 t = xr[c < K4 ? c : K4 - 1];  // past the row: its last chunk again (unused)
-        v[j] = t;
-        if (c < K4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
-    }
-    amax = wave_max_f_full(amax);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = red[0];
-#pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) amax = fmaxf(amax, red[w]);
-    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    const float inv = 1.0f / a_scale;
-    char4* q = reinterpret_cast<char4*>(xq + static_cast<size_t>(row) * K);
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const int c = static_cast<int>(threadIdx.x) + kThreads * j;
-        if (c < K4) {
-            char4 o;
-            o.x = quant_rule(v[j].x, a_scale, inv, rule);
-            o.y = quant_rule(v[j].y, a_scale, inv, rule);
-            o.z = quant_rule(v[j].z, a_scale, inv, rule);
-            o.w = quant_rule(v[j].w, a_scale, inv, rule);
-            q[c] = o;
-        }
-    }
-    if (threadIdx.x == 0) a_scales[row] = a_scale;
+    block_quantize_row_vec<kThreads, NC>(x + static_cast<size_t>(row) * K, K, xq + static_cast<size_t>(row) * K,
+                                         a_scales + row, rule, red);
 }
 
 // JB = row chunks (16 B) a lane holds in flight per batch; R = weight rows a

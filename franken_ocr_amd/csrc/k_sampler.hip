@@ -22,8 +22,19 @@ __global__ __launch_bounds__(kThreads) void sampler_prep_kernel(const float* __r
                                                                 SamplerArgs a) {
     __shared__ float red[kThreads / 64];
     const int r = blockIdx.x;
-    if (x) block_quantize_row<kThreads>(x + static_cast<size_t>(r) * K, K, xq + static_cast<size_t>(r) * K, xs + r,
-                                        false, red);
+    if (x) {
+        const float* xr = x + static_cast<size_t>(r) * K;
+        int8_t* qr = xq + static_cast<size_t>(r) * K;
+        // the row in registers (all loads in flight at once) where it fits
+        const bool vec = K % 4 == 0 && reinterpret_cast<uintptr_t>(xr) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(qr) % 4 == 0;  // uniform
+        if (vec && K <= 2 * 4 * kThreads)
+            block_quantize_row_vec<kThreads, 2>(xr, K, qr, xs + r, false, red);
+        else if (vec && K <= 8 * 4 * kThreads)
+            block_quantize_row_vec<kThreads, 8>(xr, K, qr, xs + r, false, red);
+        else
+            block_quantize_row<kThreads>(xr, K, qr, xs + r, false, red);
+    }
 
     uint32_t* bits = a.ban_bits + static_cast<size_t>(r) * a.ban_words;
     for (int w = threadIdx.x; w < a.ban_words; w += kThreads) bits[w] = 0u;
