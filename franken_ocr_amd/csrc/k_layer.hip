@@ -93,6 +93,113 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const float* __
     if (threadIdx.x == 0) xs[blockIdx.x] = a_scale;
 }
 
+// The same three modes with the row held in registers: thread t takes
+// float4 chunks t + 256 j (j < NC; n % 4 == 0, 1024 NC >= n, 16-byte aligned
+// rows), every load issued before the first use (the strided loops above wait
+// for each load in turn). Sum of squares: per thread over its chunks, the
+// wave by DPP, the four waves in order (f64 throughout, another order than
+// the loop above: rstd, rounded to f32, can differ in the last bit only when
+// the f64 value sits on an f32 rounding boundary).
+template <int MODE, int NC>
+__global__ __launch_bounds__(kThreads) void rms_norm_rows_vec_kernel(const float* __restrict__ x,
+                                                                     const float* __restrict__ a,
+                                                                     const float* __restrict__ w, int n, float eps,
+                                                                     float* __restrict__ h, float* __restrict__ y,
+                                                                     int8_t* __restrict__ xq, float* __restrict__ xs) {
+    __shared__ double s_red[kThreads / 64];
+    __shared__ float s_max[kThreads / 64];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    const int n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x + base);
+    const float4* a4 = MODE == 1 ? reinterpret_cast<const float4*>(a + base) : nullptr;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[NC], g[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + kThreads * j;
+        const int cc = c < n4 ? c : n4 - 1;  // past the row: its last chunk again (unused)
+        v[j] = x4[cc];
+        if (MODE == 1) {
+            const float4 b = a4[cc];
+            v[j] = make_float4(v[j].x + b.x, v[j].y + b.y, v[j].z + b.z, v[j].w + b.w);
+        }
+        g[j] = w ? w4[cc] : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        if (static_cast<int>(threadIdx.x) + kThreads * j < n4) {
+            ss = fma(static_cast<double>(v[j].x), static_cast<double>(v[j].x), ss);
+            ss = fma(static_cast<double>(v[j].y), static_cast<double>(v[j].y), ss);
+            ss = fma(static_cast<double>(v[j].z), static_cast<double>(v[j].z), ss);
+            ss = fma(static_cast<double>(v[j].w), static_cast<double>(v[j].w), ss);
+        }
+    }
+    ss = wave_sum_d_full(ss);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int wv = 0; wv < kThreads / 64; ++wv) tot += s_red[wv];
+    const float rstd = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(n) + static_cast<double>(eps)));
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + kThreads * j;
+        if (c >= n4) continue;
+        const float4 t = v[j];
+        float4 o = make_float4(t.x * rstd, t.y * rstd, t.z * rstd, t.w * rstd);
+        if (MODE != 2 || w) o = make_float4(o.x * g[j].x, o.y * g[j].y, o.z * g[j].z, o.w * g[j].w);
+        if (MODE == 1) reinterpret_cast<float4*>(h + base)[c] = t;
+        if (MODE != 0) {
+            reinterpret_cast<float4*>(y + base)[c] = o;
+        } else {
+            v[j] = o;
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+        }
+    }
+    if (MODE != 0) return;
+    amax = wave_max_f_full(amax);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = s_max[0];
+#pragma unroll
+    for (int wv = 1; wv < kThreads / 64; ++wv) amax = fmaxf(amax, s_max[wv]);
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + kThreads * j;
+        if (c >= n4) continue;
+        char4 q;
+        q.x = quant_i8(v[j].x, inv, false);
+        q.y = quant_i8(v[j].y, inv, false);
+        q.z = quant_i8(v[j].z, inv, false);
+        q.w = quant_i8(v[j].w, inv, false);
+        reinterpret_cast<char4*>(xq + base)[c] = q;
+    }
+    if (threadIdx.x == 0) xs[blockIdx.x] = a_scale;
+}
+
+// Launch MODE over rows: the register form where the shape and alignment
+// allow, else the staged-row kernel.
+template <int MODE>
+hipError_t launch_rms_norm_mode(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
+                                float eps, float* h, float* y, int8_t* xq, float* xs) {
+    auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool vec = n % 4 == 0 && n <= 4 * 4 * kThreads && al16(x) && al16(a) && al16(w) && al16(h) && al16(y) &&
+                     (xq == nullptr || reinterpret_cast<uintptr_t>(xq) % 4 == 0);
+    if (vec && n <= 2 * 4 * kThreads)
+        FOCR_LAUNCH((rms_norm_rows_vec_kernel<MODE, 2>), dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, xq,
+                    xs);
+    else if (vec)
+        FOCR_LAUNCH((rms_norm_rows_vec_kernel<MODE, 4>), dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, xq,
+                    xs);
+    else
+        FOCR_LAUNCH(rms_norm_rows_kernel<MODE>, dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, xq, xs);
+    return hipGetLastError();
+}
+
 // One block per stream: the fused row qkv [3D] -> q, k rotated at
 // pos.p[s] (inv_freq [half], the reference's f64-then-f32 table) and v
 // copied: q [D] contiguous; k and v [D] contiguous, or (ring.k[0] set)
@@ -150,24 +257,18 @@ __global__ __launch_bounds__(kThreads) void add_rows_kernel(const float* __restr
 hipError_t launch_rms_norm_quant(hipStream_t s, const float* x, const float* w, int rows, int n, float eps,
                                  int8_t* xq, float* xs) {
     if (n > 4096 || rows < 1) return hipErrorInvalidValue;
-    FOCR_LAUNCH(rms_norm_rows_kernel<0>, dim3(rows), dim3(kThreads), 0, s, x, nullptr, w, n, eps, nullptr, nullptr,
-                xq, xs);
-    return hipGetLastError();
+    return launch_rms_norm_mode<0>(s, x, nullptr, w, rows, n, eps, nullptr, nullptr, xq, xs);
 }
 
 hipError_t launch_residual_rms_norm(hipStream_t s, const float* x, const float* a, const float* w, int rows, int n,
                                     float eps, float* h, float* y) {
     if (n > 4096 || rows < 1) return hipErrorInvalidValue;
-    FOCR_LAUNCH(rms_norm_rows_kernel<1>, dim3(rows), dim3(kThreads), 0, s, x, a, w, n, eps, h, y, nullptr,
-                nullptr);
-    return hipGetLastError();
+    return launch_rms_norm_mode<1>(s, x, a, w, rows, n, eps, h, y, nullptr, nullptr);
 }
 
 hipError_t launch_rms_norm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
     if (n > 4096 || rows < 1) return hipErrorInvalidValue;
-    FOCR_LAUNCH(rms_norm_rows_kernel<2>, dim3(rows), dim3(kThreads), 0, s, x, nullptr, w, n, eps, nullptr, y, nullptr,
-                nullptr);
-    return hipGetLastError();
+    return launch_rms_norm_mode<2>(s, x, nullptr, w, rows, n, eps, nullptr, y, nullptr, nullptr);
 }
 
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
