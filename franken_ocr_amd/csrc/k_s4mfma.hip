@@ -478,6 +478,7 @@ __global__ __launch_bounds__(256) void retile_s_kernel(const float* __restrict__
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kQRows = kPlanThreads / 256;  // token rows per quantize block
+constexpr int kPlanPre = 4;  // rounds of pairs whose expert ids the plan block loads up front
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane) {
     int x = v;
@@ -522,8 +523,23 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         const int row = blockIdx.x * kQRows + sub;
         const bool ok = row < T;
         const float* xr = x + static_cast<size_t>(ok ? row : 0) * H;
+        // the row in registers (float4 loads all issued before the first use)
+        // where it fits; the strided loop waits for each load in turn
+        const int H4 = H >> 2;
+        const bool vec = (H & 3) == 0 && H4 <= 2 * 256 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(xq) % 4 == 0;  // uniform
+        float4 v[2] = {};
         float amax = 0.0f;
-        for (int i = st; i < H; i += 256) amax = fmaxf(amax, fabsf(xr[i]));
+        if (vec) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int c = st + 256 * j;
+                v[j] = reinterpret_cast<const float4*>(xr)[c < H4 ? c : H4 - 1];
+                if (c < H4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+            }
+        } else {
+            for (int i = st; i < H; i += 256) amax = fmaxf(amax, fabsf(xr[i]));
+        }
         amax = wave_max_f_full(amax);
         if (lane == 0) s_red[wave] = amax;
         __syncthreads();
@@ -533,11 +549,44 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         const float inv = 1.0f / a_scale;
         if (ok) {
             int8_t* q = xq + static_cast<size_t>(row) * H;
-            for (int i = st; i < H; i += 256) q[i] = quant_rule(xr[i], a_scale, inv, rule);
+            if (vec) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int c = st + 256 * j;
+                    if (c < H4) {
+                        char4 o;
+                        o.x = quant_rule(v[j].x, a_scale, inv, rule);
+                        o.y = quant_rule(v[j].y, a_scale, inv, rule);
+                        o.z = quant_rule(v[j].z, a_scale, inv, rule);
+                        o.w = quant_rule(v[j].w, a_scale, inv, rule);
+                        reinterpret_cast<char4*>(q)[c] = o;
+                    }
+                }
+            } else {
+                for (int i = st; i < H; i += 256) q[i] = quant_rule(xr[i], a_scale, inv, rule);
+            }
             if (st == 0) xs[row] = a_scale;
         }
         return;
     }
+    // the plan block: the expert ids of the first kPlanPre rounds of pairs are
+    // requested once, up front (the counting and the scatter pass each read
+    // every round; loaded per round, each round waited on its own load)
+    uint32_t epre[kPlanPre];
+#pragma unroll
+    for (int r = 0; r < kPlanPre; ++r) {
+        const int p = r * kPlanThreads + tid;
+        epre[r] = p < TK ? idx[p] : 127u;
+    }
+    auto expert_of = [&](int c0) {  // c0: the round's first pair (uniform)
+        const int r = c0 / kPlanThreads, p = c0 + tid;
+        uint32_t e = 127u;
+#pragma unroll
+        for (int q = 0; q < kPlanPre; ++q)
+            if (r == q) e = epre[q];
+        if (r >= kPlanPre) e = p < TK ? idx[p] : 127u;
+        return e;
+    };
     if (tid < kMaxE) s_cnt[tid] = 0;
     for (int i = tid; i < kPlanWaves * kMaxE; i += kPlanThreads) (&s_wc[0][0])[i] = 0;
     if (tid == 0) s_err = 0;
@@ -545,7 +594,7 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
     // counts: one LDS add per distinct expert per wave and round
     for (int c0 = 0; c0 < TK; c0 += kPlanThreads) {
         const int p = c0 + tid;
-        uint32_t e = p < TK ? idx[p] : 127u;
+        uint32_t e = expert_of(c0);
         if (p < TK && e >= static_cast<uint32_t>(E)) s_err = 1;
         if (e >= static_cast<uint32_t>(E)) e = 127u;
         const unsigned long long same = match7(e);
@@ -575,7 +624,7 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
     // expert ids with ballots, wave offsets from per-wave counts
     for (int c0 = 0; c0 < TK; c0 += kPlanThreads) {
         const int p = c0 + tid;
-        uint32_t e = p < TK ? idx[p] : 127u;
+        uint32_t e = expert_of(c0);
         if (e >= static_cast<uint32_t>(E)) e = 127u;  // invalid: never placed
         const unsigned long long same = match7(e);
         const unsigned long long lt = (1ull << lane) - 1ull;
