@@ -278,12 +278,20 @@ int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const fl
     uint64_t* keys = static_cast<uint64_t*>(ctx->scratch_get(kScrArg, m * nparts * sizeof(uint64_t)));
     float* y = logits ? logits : static_cast<float*>(ctx->scratch_get(kScrLogits, m * w->n * sizeof(float)));
     if (!xq || !xs || !keys || !y) return FOCR_HIP_E_OOM;
-    {
-        ProfScope ps(ctx, "quantize_rows");
-        FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, false), "quantize launch");
-    }
     int np = 0;
-    {
+    // one row: the GEMV blocks quantize it themselves (one launch fewer)
+    hipError_t fe = hipErrorNotSupported;
+    if (m == 1) {
+        ProfScope ps(ctx, "lm_head_gemv");
+        fe = launch_gemv_i8_f32_row(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, x, y, keys, &np,
+                                    ctx->cu_count);
+        if (fe != hipErrorNotSupported) FOCR_HIP_TRY(fe, "lm_head gemv launch");
+    }
+    if (fe == hipErrorNotSupported) {
+        {
+            ProfScope ps(ctx, "quantize_rows");
+            FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, false), "quantize launch");
+        }
         ProfScope ps(ctx, "lm_head_gemv");
         FOCR_HIP_TRY(launch_gemv_i8(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y, nullptr,
                                     keys, &np, ctx->cu_count),

@@ -53,12 +53,16 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_vec_kernel(const float
 // wave covers four adjacent rows, 256 contiguous bytes each. BAN: output
 // channel n of row i is written -inf when bit n of ban_bits[i] is set (the
 // no-repeat-ngram ban folded into the dequant epilogue, decoder.rs:2319-2357).
-template <int MC, int JB, int R, bool BAN>
+// FQ (MC = 1): the row comes as f32 (xf, K % 4 == 0, K <= 2048) and each
+// block quantizes it itself (quantize_row_i8, half away: the bytes and scale
+// of quantize_rows_vec_kernel) — the separate quantize launch goes away.
+template <int MC, int JB, int R, bool BAN, bool FQ = false>
 __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
     float* __restrict__ y, int32_t* __restrict__ acc_out, uint64_t* __restrict__ keys,
-    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words) {
+    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words, const float* __restrict__ xf) {
+    static_assert(!FQ || MC == 1, "f32 input: one row");
     extern __shared__ int4 lds_x[];  // [MC][K/16]
     __shared__ uint64_t lds_keys[kGroups][MC];
     __shared__ float lds_as[MC];
@@ -66,9 +70,45 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     const int group = threadIdx.x >> 4;
     const int lane = threadIdx.x & 15;
     const int C = K >> 4;
-    const int4* x4 = reinterpret_cast<const int4*>(xq);
-    for (int i = threadIdx.x; i < M * C; i += kThreads) lds_x[i] = x4[i];
-    if (threadIdx.x < MC) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+    if constexpr (FQ) {
+        __shared__ float red[kThreads / 64];
+        const int K4 = K >> 2;
+        const float4* xr4 = reinterpret_cast<const float4*>(xf);
+        float4 v[2];
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = static_cast<int>(threadIdx.x) + kThreads * j;
+            v[j] = xr4[c < K4 ? c : K4 - 1];
+            if (c < K4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+        }
+        amax = wave_max_f_full(amax);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        amax = red[0];
+#pragma unroll
+        for (int wv = 1; wv < kThreads / 64; ++wv) amax = fmaxf(amax, red[wv]);
+        const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const float inv = 1.0f / a_scale;
+        char4* q4 = reinterpret_cast<char4*>(lds_x);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = static_cast<int>(threadIdx.x) + kThreads * j;
+            if (c < K4) {
+                char4 o;
+                o.x = quant_i8(v[j].x, inv, false);
+                o.y = quant_i8(v[j].y, inv, false);
+                o.z = quant_i8(v[j].z, inv, false);
+                o.w = quant_i8(v[j].w, inv, false);
+                q4[c] = o;
+            }
+        }
+        if (threadIdx.x == 0) lds_as[0] = a_scale;
+    } else {
+        const int4* x4 = reinterpret_cast<const int4*>(xq);
+        for (int i = threadIdx.x; i < M * C; i += kThreads) lds_x[i] = x4[i];
+        if (threadIdx.x < MC) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+    }
     __syncthreads();
 
     // the argmax key of row i is kept by lane i & 15 only: best[i >> 4]
@@ -918,6 +958,23 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
                                  0);
 }
 
+hipError_t launch_gemv_i8_f32_row(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
+                                  float* y, uint64_t* arg_keys, int* nparts_out, int cu_count) {
+    // one f32 row, quantized by every block: the sdot4 kernel's one-row form
+    if (k <= 0 || k % 16 != 0 || k > 2 * 4 * kThreads || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+        return hipErrorNotSupported;
+    const int rows_per_tile = kGroups;  // R = 1
+    const int tiles = (n + rows_per_tile - 1) / rows_per_tile;
+    const int target_blocks = (cu_count > 0 ? cu_count : 256) * 8;
+    int tpb = (tiles + target_blocks - 1) / target_blocks;
+    tpb = tpb < 1 ? 1 : tpb;
+    const int grid = (tiles + tpb - 1) / tpb;
+    if (nparts_out) *nparts_out = grid;
+    FOCR_LAUNCH((gemv_i8_kernel<1, 8, 1, false, true>), dim3(grid), dim3(kThreads), static_cast<size_t>(k), s, w, ws,
+                n, k, nullptr, nullptr, 1, y, nullptr, arg_keys, tpb, nullptr, 0, x);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
                                  const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                                  uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,
@@ -1000,10 +1057,10 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
     case MCV:                                                                                             \
         if (ban_bits)                                                                                     \
             FOCR_LAUNCH((gemv_i8_kernel<MCV, JBV, RV, true>), dim3(grid), dim3(kThreads), lds, s, w, ws, n, \
-                        k, xq, a_scales, m, y, acc, arg_keys, tpb, ban_bits, ban_words);                  \
+                        k, xq, a_scales, m, y, acc, arg_keys, tpb, ban_bits, ban_words, nullptr);         \
         else                                                                                              \
             FOCR_LAUNCH((gemv_i8_kernel<MCV, JBV, RV, false>), dim3(grid), dim3(kThreads), lds, s, w, ws, n,\
-                        k, xq, a_scales, m, y, acc, arg_keys, tpb, nullptr, 0);                           \
+                        k, xq, a_scales, m, y, acc, arg_keys, tpb, nullptr, 0, nullptr);                  \
         break;
     switch (mc) {
         FOCR_GEMV_CASE(1, 8, 1)
