@@ -286,6 +286,25 @@ __device__ __forceinline__ void block_quantize_row_vec(const float* __restrict__
     if (threadIdx.x == 0) *a_scale_out = a_scale;
 }
 
+// This thread's maximum over keys kr[t + THREADS i] (i >= 0, < n): U loads
+// in flight at once (a strided loop waits for each in turn); past the end a
+// key is read again, which leaves a maximum as it is.
+template <int THREADS, int U = 8>
+__device__ __forceinline__ uint64_t thread_max_keys(const uint64_t* __restrict__ kr, int n) {
+    uint64_t b = 0ull;
+    for (int i0 = static_cast<int>(threadIdx.x); i0 < n; i0 += U * THREADS) {
+        uint64_t k[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + u * THREADS;
+            k[u] = kr[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) b = k[u] > b ? k[u] : b;
+    }
+    return b;
+}
+
 // decoder.rs:1079-1083 silu(x) = x / (1 + e^-x), accurate expf (no fast math).
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 

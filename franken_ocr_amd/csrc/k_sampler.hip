@@ -71,11 +71,7 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(const uint64_t*
                                                                  uint8_t* __restrict__ is_eos, SamplerArgs a) {
     __shared__ uint64_t red[kThreads / 64];
     const int r = blockIdx.x;
-    uint64_t b = 0ull;
-    for (int i = threadIdx.x; i < nparts; i += kThreads) {
-        const uint64_t k = keys[static_cast<size_t>(r) * nparts + i];
-        b = k > b ? k : b;
-    }
+    uint64_t b = thread_max_keys<kThreads>(keys + static_cast<size_t>(r) * nparts, nparts);
     b = wave_max_u64_full(b);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
     __syncthreads();
