@@ -279,12 +279,13 @@ int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const fl
     float* y = logits ? logits : static_cast<float*>(ctx->scratch_get(kScrLogits, m * w->n * sizeof(float)));
     if (!xq || !xs || !keys || !y) return FOCR_HIP_E_OOM;
     int np = 0;
-    // one row: the GEMV blocks quantize it themselves (one launch fewer)
-    hipError_t fe = hipErrorNotSupported;
-    if (m == 1) {
+    // the GEMV blocks quantize the rows themselves where the shape allows (one
+    // launch fewer)
+    hipError_t fe;
+    {
         ProfScope ps(ctx, "lm_head_gemv");
-        fe = launch_gemv_i8_f32_row(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, x, y, keys, &np,
-                                    ctx->cu_count);
+        fe = launch_gemv_i8_f32_keys(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, x, (int)m, y, keys, &np,
+                                     ctx->cu_count);
         if (fe != hipErrorNotSupported) FOCR_HIP_TRY(fe, "lm_head gemv launch");
     }
     if (fe == hipErrorNotSupported) {

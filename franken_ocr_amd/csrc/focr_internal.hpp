@@ -250,11 +250,12 @@ size_t max_lds_per_block();
 hipError_t launch_gemv_i8_f32(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
                               const float* norm_w, float eps, int m, float* y, int8_t* xq_tmp, float* xs_tmp,
                               int cu_count);
-// The same for one f32 row x [k] (m = 1), quantized (quantize_row_i8) inside
-// every block: no separate quantize launch. hipErrorNotSupported outside
-// k % 16 == 0, k <= 2048, 16-byte aligned x.
-hipError_t launch_gemv_i8_f32_row(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
-                                  float* y, uint64_t* arg_keys, int* nparts_out, int cu_count);
+// The same (with per-block argmax keys) for m f32 rows x [m][k], quantized
+// (quantize_row_i8) inside every block: no separate quantize launch. m = 1:
+// k % 16 == 0, k <= 2048; m = 2..16: k % 256 == 0, k <= 1280 (the
+// matrix-core form); x 16-byte aligned. hipErrorNotSupported outside those.
+hipError_t launch_gemv_i8_f32_keys(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
+                                   int m, float* y, uint64_t* arg_keys, int* nparts_out, int cu_count);
 hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws, int n, int k,
                                  const int8_t* xq, const float* a_scales, int m, float* y, int32_t* acc,
                                  uint64_t* arg_keys, int* nparts_out, int cu_count, const uint32_t* ban_bits,

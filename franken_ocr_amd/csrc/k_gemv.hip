@@ -217,12 +217,81 @@ typedef int v4i_m __attribute__((ext_vector_type(4)));
 constexpr int kMfmaMinRows = 2;  // below this the sdot4 kernel is already HBM-bound
 constexpr int kMfmaTileBytes = 16 * 256;  // one chunk of one tile
 
-template <bool BAN>
+template <int NF>
+__device__ __forceinline__ void fq_rows2_to_lds(const float4 (&v0)[NF], const float4 (&v1)[NF],
+                                                const float4 (&wv)[NF], bool norm, float eps, int K, int K4,
+                                                int lane, int8_t* dst0, int8_t* dst1, bool has1, float& s0,
+                                                float& s1) {
+    float rstd0 = 1.0f, rstd1 = 1.0f;
+    if (norm) {
+        double ss0 = 0.0, ss1 = 0.0;
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const double a0 = v0[j].x, b0 = v0[j].y, c0 = v0[j].z, d0 = v0[j].w;
+            const double a1 = v1[j].x, b1 = v1[j].y, c1 = v1[j].z, d1 = v1[j].w;
+            ss0 = fma(a0, a0, ss0);
+            ss1 = fma(a1, a1, ss1);
+            ss0 = fma(b0, b0, ss0);
+            ss1 = fma(b1, b1, ss1);
+            ss0 = fma(c0, c0, ss0);
+            ss1 = fma(c1, c1, ss1);
+            ss0 = fma(d0, d0, ss0);
+            ss1 = fma(d1, d1, ss1);
+        }
+        ss0 = wave_sum_d_full(ss0);
+        ss1 = wave_sum_d_full(ss1);
+        rstd0 = static_cast<float>(1.0 / sqrt(ss0 / static_cast<double>(K) + static_cast<double>(eps)));
+        rstd1 = static_cast<float>(1.0 / sqrt(ss1 / static_cast<double>(K) + static_cast<double>(eps)));
+    }
+    float4 u0[NF], u1[NF];
+    float amax0 = 0.0f, amax1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        u0[j] = norm ? make_float4((v0[j].x * rstd0) * wv[j].x, (v0[j].y * rstd0) * wv[j].y,
+                                   (v0[j].z * rstd0) * wv[j].z, (v0[j].w * rstd0) * wv[j].w)
+                     : v0[j];
+        u1[j] = norm ? make_float4((v1[j].x * rstd1) * wv[j].x, (v1[j].y * rstd1) * wv[j].y,
+                                   (v1[j].z * rstd1) * wv[j].z, (v1[j].w * rstd1) * wv[j].w)
+                     : v1[j];
+        amax0 = fmaxf(amax0, fmaxf(fmaxf(fabsf(u0[j].x), fabsf(u0[j].y)), fmaxf(fabsf(u0[j].z), fabsf(u0[j].w))));
+        amax1 = fmaxf(amax1, fmaxf(fmaxf(fabsf(u1[j].x), fabsf(u1[j].y)), fmaxf(fabsf(u1[j].z), fabsf(u1[j].w))));
+    }
+    amax0 = wave_max_f_full(amax0);
+    amax1 = wave_max_f_full(amax1);
+    const float a_scale0 = amax0 > 0.0f ? amax0 / 127.0f : 1.0f;
+    const float a_scale1 = amax1 > 0.0f ? amax1 / 127.0f : 1.0f;
+    const float inv0 = 1.0f / a_scale0, inv1 = 1.0f / a_scale1;
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        const int c = lane + 64 * j;
+        if (c < K4) {
+            char4 q0, q1;
+            q0.x = quant_i8(u0[j].x, inv0, false);
+            q0.y = quant_i8(u0[j].y, inv0, false);
+            q0.z = quant_i8(u0[j].z, inv0, false);
+            q0.w = quant_i8(u0[j].w, inv0, false);
+            q1.x = quant_i8(u1[j].x, inv1, false);
+            q1.y = quant_i8(u1[j].y, inv1, false);
+            q1.z = quant_i8(u1[j].z, inv1, false);
+            q1.w = quant_i8(u1[j].w, inv1, false);
+            reinterpret_cast<char4*>(dst0)[c] = q0;
+            if (has1) reinterpret_cast<char4*>(dst1)[c] = q1;
+        }
+    }
+    s0 = a_scale0;
+    s1 = a_scale1;
+}
+
+// FQ: the <= 16 activation rows come as f32 (xf [M][K], K % 64 == 0,
+// K <= 1280) and every block quantizes them (quantize_row_i8, two rows per
+// wave in lockstep, while the first weight chunks are in flight) — the same
+// bytes and scales as the quantize kernel, whose launch goes away.
+template <bool BAN, bool FQ = false>
 __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
     float* __restrict__ y, int32_t* __restrict__ acc_out, uint64_t* __restrict__ keys,
-    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words) {
+    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words, const float* __restrict__ xf) {
     extern __shared__ int4 lds_dyn[];  // x [16][K/16 + 1] then per-wave [16][16] chunks
     __shared__ uint64_t lds_keys[kThreads / 64][16];
     __shared__ float lds_as[16];
@@ -264,12 +333,54 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
     int4 rg0[4], rg1[4];
     if (nq > 0) load(0, rg0);
     if (nq > 1) load(1, rg1);
-    const int4* x4 = reinterpret_cast<const int4*>(xq);
-    for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
-        const int r = i / C, c = i - r * C;
-        lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+    if constexpr (FQ) {
+        constexpr int NF = 5;  // float4 chunks of a row per lane: K <= 1280
+        const int K4 = K >> 2;
+        const float4 wv[NF] = {};  // no norm weight
+        // rows r and r + 4 per wave and pass; rows >= M are zero
+        for (int r = wave; r < 16; r += 8) {
+            const int r2 = r + 4;
+            if (r >= M) {  // wave-uniform
+                for (int c = l; c < C; c += 64) {
+                    lds_xv[r * xs + c] = make_int4(0, 0, 0, 0);
+                    lds_xv[r2 * xs + c] = make_int4(0, 0, 0, 0);
+                }
+                if (l == 0) lds_as[r] = lds_as[r2] = 0.0f;
+                continue;
+            }
+            const bool has1 = r2 < M;  // wave-uniform
+            const float4* x0 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(r) * K);
+            const float4* x1 = reinterpret_cast<const float4*>(xf + static_cast<size_t>(has1 ? r2 : r) * K);
+            float4 v0[NF], v1[NF];
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                const int c = l + 64 * j;
+                const int cc = c < K4 ? c : K4 - 1;
+                const unsigned mk = c < K4 ? 0xFFFFFFFFu : 0u;
+                const float4 a = x0[cc], b = x1[cc];
+                v0[j] = make_float4(__uint_as_float(__float_as_uint(a.x) & mk), __uint_as_float(__float_as_uint(a.y) & mk),
+                                    __uint_as_float(__float_as_uint(a.z) & mk), __uint_as_float(__float_as_uint(a.w) & mk));
+                v1[j] = make_float4(__uint_as_float(__float_as_uint(b.x) & mk), __uint_as_float(__float_as_uint(b.y) & mk),
+                                    __uint_as_float(__float_as_uint(b.z) & mk), __uint_as_float(__float_as_uint(b.w) & mk));
+            }
+            float s0, s1;
+            fq_rows2_to_lds<NF>(v0, v1, wv, false, 0.0f, K, K4, l, reinterpret_cast<int8_t*>(lds_xv + r * xs),
+                                reinterpret_cast<int8_t*>(lds_xv + r2 * xs), has1, s0, s1);
+            if (!has1)
+                for (int c = l; c < C; c += 64) lds_xv[r2 * xs + c] = make_int4(0, 0, 0, 0);
+            if (l == 0) {
+                lds_as[r] = s0;
+                lds_as[r2] = has1 ? s1 : 0.0f;
+            }
+        }
+    } else {
+        const int4* x4 = reinterpret_cast<const int4*>(xq);
+        for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
+            const int r = i / C, c = i - r * C;
+            lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+        }
+        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     }
-    if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     __syncthreads();
     if (nq > 0) store(rg0);
 
@@ -359,70 +470,6 @@ constexpr int kFqMaxK = 2048;  // f32-input form: a row's float4s held by one wa
 // wave per SIMD cannot hide otherwise (one row took ~1.6 us of a block's
 // time), and the reductions through DPP (the call is wave-uniform: every lane
 // of the wave takes part).
-template <int NF>
-__device__ __forceinline__ void fq_rows2_to_lds(const float4 (&v0)[NF], const float4 (&v1)[NF],
-                                                const float4 (&wv)[NF], bool norm, float eps, int K, int K4,
-                                                int lane, int8_t* dst0, int8_t* dst1, bool has1, float& s0,
-                                                float& s1) {
-    float rstd0 = 1.0f, rstd1 = 1.0f;
-    if (norm) {
-        double ss0 = 0.0, ss1 = 0.0;
-#pragma unroll
-        for (int j = 0; j < NF; ++j) {
-            const double a0 = v0[j].x, b0 = v0[j].y, c0 = v0[j].z, d0 = v0[j].w;
-            const double a1 = v1[j].x, b1 = v1[j].y, c1 = v1[j].z, d1 = v1[j].w;
-            ss0 = fma(a0, a0, ss0);
-            ss1 = fma(a1, a1, ss1);
-            ss0 = fma(b0, b0, ss0);
-            ss1 = fma(b1, b1, ss1);
-            ss0 = fma(c0, c0, ss0);
-            ss1 = fma(c1, c1, ss1);
-            ss0 = fma(d0, d0, ss0);
-            ss1 = fma(d1, d1, ss1);
-        }
-        ss0 = wave_sum_d_full(ss0);
-        ss1 = wave_sum_d_full(ss1);
-        rstd0 = static_cast<float>(1.0 / sqrt(ss0 / static_cast<double>(K) + static_cast<double>(eps)));
-        rstd1 = static_cast<float>(1.0 / sqrt(ss1 / static_cast<double>(K) + static_cast<double>(eps)));
-    }
-    float4 u0[NF], u1[NF];
-    float amax0 = 0.0f, amax1 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NF; ++j) {
-        u0[j] = norm ? make_float4((v0[j].x * rstd0) * wv[j].x, (v0[j].y * rstd0) * wv[j].y,
-                                   (v0[j].z * rstd0) * wv[j].z, (v0[j].w * rstd0) * wv[j].w)
-                     : v0[j];
-        u1[j] = norm ? make_float4((v1[j].x * rstd1) * wv[j].x, (v1[j].y * rstd1) * wv[j].y,
-                                   (v1[j].z * rstd1) * wv[j].z, (v1[j].w * rstd1) * wv[j].w)
-                     : v1[j];
-        amax0 = fmaxf(amax0, fmaxf(fmaxf(fabsf(u0[j].x), fabsf(u0[j].y)), fmaxf(fabsf(u0[j].z), fabsf(u0[j].w))));
-        amax1 = fmaxf(amax1, fmaxf(fmaxf(fabsf(u1[j].x), fabsf(u1[j].y)), fmaxf(fabsf(u1[j].z), fabsf(u1[j].w))));
-    }
-    amax0 = wave_max_f_full(amax0);
-    amax1 = wave_max_f_full(amax1);
-    const float a_scale0 = amax0 > 0.0f ? amax0 / 127.0f : 1.0f;
-    const float a_scale1 = amax1 > 0.0f ? amax1 / 127.0f : 1.0f;
-    const float inv0 = 1.0f / a_scale0, inv1 = 1.0f / a_scale1;
-#pragma unroll
-    for (int j = 0; j < NF; ++j) {
-        const int c = lane + 64 * j;
-        if (c < K4) {
-            char4 q0, q1;
-            q0.x = quant_i8(u0[j].x, inv0, false);
-            q0.y = quant_i8(u0[j].y, inv0, false);
-            q0.z = quant_i8(u0[j].z, inv0, false);
-            q0.w = quant_i8(u0[j].w, inv0, false);
-            q1.x = quant_i8(u1[j].x, inv1, false);
-            q1.y = quant_i8(u1[j].y, inv1, false);
-            q1.z = quant_i8(u1[j].z, inv1, false);
-            q1.w = quant_i8(u1[j].w, inv1, false);
-            reinterpret_cast<char4*>(dst0)[c] = q0;
-            if (has1) reinterpret_cast<char4*>(dst1)[c] = q1;
-        }
-    }
-    s0 = a_scale0;
-    s1 = a_scale1;
-}
 
 // FQ: the activation rows come as f32 (xf [M][K], K <= kFqMaxK) and each
 // block quantizes them itself (after the RMSNorm with weight nw when nw is
@@ -954,20 +1001,35 @@ hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n
                                  0);
 }
 
-hipError_t launch_gemv_i8_f32_row(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
-                                  float* y, uint64_t* arg_keys, int* nparts_out, int cu_count) {
-    // one f32 row, quantized by every block: the sdot4 kernel's one-row form
-    if (k <= 0 || k % 16 != 0 || k > 2 * 4 * kThreads || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+hipError_t launch_gemv_i8_f32_keys(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const float* x,
+                                   int m, float* y, uint64_t* arg_keys, int* nparts_out, int cu_count) {
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return hipErrorNotSupported;
+    if (m == 1) {
+        // one f32 row, quantized by every block: the sdot4 kernel's one-row form
+        if (k <= 0 || k % 16 != 0 || k > 2 * 4 * kThreads) return hipErrorNotSupported;
+        const int tiles = (n + kGroups - 1) / kGroups;  // R = 1
+        const int target_blocks = (cu_count > 0 ? cu_count : 256) * 8;
+        int tpb = (tiles + target_blocks - 1) / target_blocks;
+        tpb = tpb < 1 ? 1 : tpb;
+        const int grid = (tiles + tpb - 1) / tpb;
+        if (nparts_out) *nparts_out = grid;
+        FOCR_LAUNCH((gemv_i8_kernel<1, 8, 1, false, true>), dim3(grid), dim3(kThreads), static_cast<size_t>(k), s, w,
+                    ws, n, k, nullptr, nullptr, 1, y, nullptr, arg_keys, tpb, nullptr, 0, x);
+        return hipGetLastError();
+    }
+    // 2..16 f32 rows on the matrix-core kernel, quantized by every block
+    const size_t lds_mfma = (static_cast<size_t>(16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) *
+                            sizeof(int4);
+    if (m < kMfmaMinRows || m > 16 || k < 256 || k % 256 != 0 || k > 64 * 4 * 5 || lds_mfma > 65536)
         return hipErrorNotSupported;
-    const int rows_per_tile = kGroups;  // R = 1
-    const int tiles = (n + rows_per_tile - 1) / rows_per_tile;
-    const int target_blocks = (cu_count > 0 ? cu_count : 256) * 8;
+    const int tiles = (n + 15) / 16;
+    const int target_blocks = (cu_count > 0 ? cu_count : 256) * 4;  // as launch_gemv_i8's matrix-core form
     int tpb = (tiles + target_blocks - 1) / target_blocks;
-    tpb = tpb < 1 ? 1 : tpb;
+    tpb = (tpb + 3) & ~3;
     const int grid = (tiles + tpb - 1) / tpb;
     if (nparts_out) *nparts_out = grid;
-    FOCR_LAUNCH((gemv_i8_kernel<1, 8, 1, false, true>), dim3(grid), dim3(kThreads), static_cast<size_t>(k), s, w, ws,
-                n, k, nullptr, nullptr, 1, y, nullptr, arg_keys, tpb, nullptr, 0, x);
+    FOCR_LAUNCH((gemv_i8_mfma_kernel<false, true>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k, nullptr,
+                nullptr, m, y, nullptr, arg_keys, tpb, nullptr, 0, x);
     return hipGetLastError();
 }
 
@@ -1032,10 +1094,10 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             if (ban_bits)
                 FOCR_LAUNCH((gemv_i8_mfma_kernel<true>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k, xq_r,
                             a_scales + r0, mr, y_r, acc_r, keys_r, tpb, ban_bits + static_cast<size_t>(r0) * ban_words,
-                            ban_words);
+                            ban_words, nullptr);
             else
                 FOCR_LAUNCH((gemv_i8_mfma_kernel<false>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k,
-                            xq_r, a_scales + r0, mr, y_r, acc_r, keys_r, tpb, nullptr, 0);
+                            xq_r, a_scales + r0, mr, y_r, acc_r, keys_r, tpb, nullptr, 0, nullptr);
         }
         return hipGetLastError();
     }
