@@ -634,9 +634,24 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
     } else {
         issue_weights();
         const int4* x4 = reinterpret_cast<const int4*>(xq);
-        for (int i = threadIdx.x; i < M * C; i += kThreads) {  // only the M live rows; the rest read as zero
-            const int r = i / C, c = i - r * C;
-            lds_xv[r * xs + c] = x4[r * C + c];
+        // only the M live rows (the rest read as zero): wave w stages rows
+        // w, w + 4, ..., lane l its 16-byte chunks l + 64 j, all of a row's
+        // loads issued before its stores (a loop of single loads waits for
+        // each in turn); past the row's end: its padding chunk, never read
+        constexpr int J = CPW;  // C <= 64 CPW: the kernel's K <= 256 * 4 * CPW
+        for (int r = wave; r < M; r += kThreads / 64) {
+            const int4* xr = x4 + static_cast<size_t>(r) * C;
+            int4 v[J];
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int c = l + 64 * j;
+                v[j] = xr[c < C ? c : C - 1];
+            }
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int c = l + 64 * j;
+                lds_xv[r * xs + (c < C ? c : C)] = v[j];
+            }
         }
         if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M && a_scales ? a_scales[threadIdx.x] : 0.0f;
     }
