@@ -375,9 +375,28 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
         }
     } else {
         const int4* x4 = reinterpret_cast<const int4*>(xq);
-        for (int i = threadIdx.x; i < 16 * C; i += kThreads) {
-            const int r = i / C, c = i - r * C;
-            lds_xv[r * xs + c] = r < M ? x4[r * C + c] : make_int4(0, 0, 0, 0);
+        // wave w stages rows w, w + 4, ... (rows >= M zero), lane l its chunks
+        // l + 64 j, all of a row's loads issued before its stores; past the
+        // row's end: its padding chunk, never read
+        constexpr int J = 4;  // C <= 256 (the launch's LDS bound keeps K below 3840)
+        for (int r = wave; r < 16; r += kThreads / 64) {
+            int4 v[J];
+            if (r < M) {  // wave-uniform
+                const int4* xr = x4 + static_cast<size_t>(r) * C;
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const int c = l + 64 * j;
+                    v[j] = xr[c < C ? c : C - 1];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < J; ++j) v[j] = make_int4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int c = l + 64 * j;
+                lds_xv[r * xs + (c < C ? c : C)] = v[j];
+            }
         }
         if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
     }
