@@ -64,10 +64,10 @@ def traffic_for(kernel: str, workload: str):
     """HBM bytes per launch measured with rocprofv3 --pmc: FETCH_SIZE and
     WRITE_SIZE (one run each) scaled by what the same counters read for a
     512 MiB device-to-device copy (profiles/traffic.json, written by
-    franken_ocr_amd.rocprof_summary traffic). A stored value is returned only
+    rocprof_summary.py traffic). A stored value is returned only
     while the hash of the kernel source it was measured on matches the file
     as it is now; otherwise (or if not recorded) None."""
-    from franken_ocr_amd.rocprof_summary import source_sha16
+    from rocprof_summary import source_sha16
 
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
@@ -83,27 +83,94 @@ def traffic_for(kernel: str, workload: str):
     return rec.get("bytes_per_dispatch")
 
 
+STAT_STEPS = 100  # the statistics passes run at least this many steps
+
+
 def timed(ctx, step, steps: int):
-    """Time `steps` steps between two device synchronisations, then run the
-    same steps again with per-kernel HIP events. The events ride in each
-    kernel's dispatch packet (hipExtLaunchKernelGGL), so they measure the
-    kernel's own execution — they agree with rocprofv3's kernel trace — but
-    the completion signals they add slow the step as a whole, which is why
-    the throughput comes from the first, unprofiled pass."""
+    """Three passes over the same steps.
+
+    1. Throughput: exactly `steps` steps between two device synchronisations
+       (wall clock); `value` and `ms_per_step` come from this pass.
+    2. Per-kernel HIP events over max(steps, STAT_STEPS) steps. The events
+       ride in each kernel's dispatch packet (hipExtLaunchKernelGGL), so they
+       time the kernel's own execution (they agree with rocprofv3's kernel
+       trace); their completion signals slow the step as a whole, which is why
+       throughput comes from pass 1. Per launch: mean, min, median, p90.
+    3. Step marks (an event recorded on the stream between steps) over
+       max(steps, STAT_STEPS) steps: the GPU-clock time of each step,
+       summarised as min / median / p90 / CoV (the reference's statistics,
+       perf_harness.rs:186-282, nearest-rank percentiles)."""
     ctx.device_synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i)
     ctx.device_synchronize()
     el = time.perf_counter() - t0
+    n_stat = max(steps, STAT_STEPS)
     ctx.prof_reset()
     ctx.prof_enable(True)
-    for i in range(steps):
+    for i in range(n_stat):
         step(i)
     prof = ctx.prof_read()
     ctx.prof_enable(False)
     kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
-    return el, prof, kernels
+    ctx.device_synchronize()
+    ctx.mark()
+    for i in range(n_stat):
+        step(i)
+        ctx.mark()
+    step_ms = ctx.marks_read()
+    return el, prof, kernels, sample_stats([v * 1e-3 for v in step_ms], scale=1e6, unit="us")
+
+
+def nearest_rank(sorted_asc, q: float) -> float:
+    """perf_harness.rs:276-282: rank = ceil(q * n) clamped to [1, n]."""
+    n = len(sorted_asc)
+    rank = min(max(int(np.ceil(q * n)), 1), n)
+    return sorted_asc[rank - 1]
+
+
+def sample_stats(secs, scale: float = 1e3, unit: str = "ms") -> dict:
+    """perf_harness.rs:186-263 SampleStats over per-iteration seconds: n,
+    min (best-of-N), p50, p90 (nearest rank), mean and the coefficient of
+    variation in percent (sample standard deviation / mean), in `unit`."""
+    v = sorted(secs)
+    n = len(v)
+    mean = sum(v) / n
+    var = sum((x - mean) ** 2 for x in v) / (n - 1) if n > 1 else 0.0
+    return {"n": n, "unit": unit, "min": round(v[0] * scale, 3), "p50": round(nearest_rank(v, 0.5) * scale, 3),
+            "p90": round(nearest_rank(v, 0.9) * scale, 3), "mean": round(mean * scale, 3),
+            "cv_pct": round(100.0 * var ** 0.5 / mean, 2) if mean > 0 else 0.0}
+
+
+def launch_stats(prof: dict, name: str) -> dict:
+    """Median, p90 and minimum launch time (us) of one profiled scope."""
+    g = prof.get(name) or {}
+    if not g.get("count"):
+        return {}
+    return {"p50_launch_us": round(g["p50_ms"] * 1e3, 3), "p90_launch_us": round(g["p90_ms"] * 1e3, 3),
+            "min_launch_us": round(g["min_ms"] * 1e3, 3), "launches_timed": g["count"]}
+
+
+def cpu_stats(call, units_per_call: float, unit: str, seconds: float, min_iters: int = 3,
+              max_iters: int = 100000) -> dict:
+    """The CPU baseline's timing, after the reference's bench harness
+    (perf_harness.rs:186-263): one warm-up call discarded, then one
+    wall-clock sample per call until `seconds` have passed (at least
+    `min_iters` calls). `value` is the throughput of the median call; `best`
+    that of the fastest (best-of-N); the per-call times' p50 / p90 / min and
+    CoV are kept beside them."""
+    call()
+    secs = []
+    t_end = time.perf_counter() + seconds
+    while len(secs) < max_iters and (len(secs) < min_iters or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        call()
+        secs.append(time.perf_counter() - t0)
+    st = sample_stats(secs)
+    return {"value": round(units_per_call / (st["p50"] * 1e-3), 2), "unit": unit,
+            "best": round(units_per_call / (st["min"] * 1e-3), 2), "call_ms": st,
+            "cov_pct": st["cv_pct"], "calls": len(secs), "seconds": round(sum(secs), 2)}
 
 
 def kernel_us(prof: dict, name: str) -> float:
@@ -158,7 +225,7 @@ def bench_moe(args, ctx):
     ctx.device_synchronize()
     # distinct experts actually routed, per copy (for algorithmic bytes)
     U = [len(np.unique(b.numpy())) for b in idx_bufs]
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     tok_s = T * args.steps / el
 
@@ -178,23 +245,30 @@ def bench_moe(args, ctx):
         "dtype": "int8",
         "config": {"workload": "moe_decode", "tokens": T, "hidden": H, "inter": I, "experts": E, "top_k": K,
                    "norm_topk": True, "layer_copies_rotated": args.copies, "distinct_experts_mean": mean_u},
+        # the dominant kernel's roofline, and beside it the whole layer's (the
+        # metric and the >= 60% target are layer-level: every byte of the step
+        # over the step's wall-clock time, route and kernel boundaries included)
         "roofline": {"bound": "hbm", "kernel": "moe_gate_up", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("moe_gate_up", "moe_decode_t%d" % T), "traffic_note": TRAFFIC_NOTE,
-                     "algorithmic_bytes_per_launch": int(gate_up_bytes), "avg_launch_us": round(gu_ms * 1e3, 3)},
+                     "algorithmic_bytes_per_launch": int(gate_up_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
+                     **launch_stats(prof, "moe_gate_up"),
+                     "layer_achieved": round(layer_gbs, 1), "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                     "layer_algorithmic_bytes_per_step": int(layer_bytes),
+                     "layer_frac_at_p50_step": round(layer_bytes / (sstats["p50"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         "layer_roofline": {"achieved": round(layer_gbs, 1), "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                            "algorithmic_bytes_per_step": int(layer_bytes)},
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "_cpu_inputs": (hidden, layers[0], base),
     }
 
 
 def cpu_moe(args, inputs):
     from oracle import pyoracle
-
-    hidden, layer0, base = inputs
     from franken_ocr_amd import synth
 
+    hidden, layer0, base = inputs
     router = synth.f32_normal(synth.seed_of(1000), E * H, 0.0, 0.02).reshape(E, H)
     _, wg, sg, wu, su, wd, sd = base
     L = pyoracle.lib()
@@ -206,20 +280,14 @@ def cpu_moe(args, inputs):
     P = pyoracle.p
     args_c = [P(np.ascontiguousarray(hidden)), T, H, I, E, K, P(router), P(wg), P(sg), P(wu), P(su), P(wd), P(sd),
               1, 1.0, P(out), P(idx), P(gates)]
-    L.cpu_moe_decode(tier, *args_c)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        L.cpu_moe_decode(tier, *args_c)
-        n += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds or n >= 2000:
-            break
-    el = time.perf_counter() - t0
+    res = cpu_stats(lambda: L.cpu_moe_decode(tier, *args_c), T, "tokens/s", args.cpu_seconds)
     st, want, want_idx, _ = pyoracle.moe_decode(hidden, router, wg, sg, wu, su, wd, sd, E, K, I, norm_topk=True)
     same = st == 0 and np.array_equal(out, want.reshape(-1)) and np.array_equal(idx, want_idx.reshape(-1))
-    return {"value": round(T * n / el, 2), "unit": "tokens/s", "cores": min(K, os.cpu_count() or 1),
-            "kind": "port", "tier": L.cpu_tier_feature(tier).decode(), "matches_oracle": bool(same),
-            "sample": f"{n} MoE decode steps of T={T} tokens (first layer copy), {el:.1f} s; "
-                      f"top-{K} experts as concurrent single-thread tasks, tokens sequential (decoder.rs:2231-2252)"}
+    res.update({"cores": min(K, os.cpu_count() or 1), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "matches_oracle": bool(same),
+                "sample": f"MoE decode steps of T={T} tokens (first layer copy); top-{K} experts as concurrent "
+                          f"single-thread tasks, tokens sequential (decoder.rs:2231-2252)"})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -256,7 +324,7 @@ def bench_lm_head(args, ctx, sampler=False):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     g_ms = kernel_us(prof, "lm_head_gemv") * 1e-3
     gemv_bytes = N * Kd + N * 4 + M * Kd + M * 4 + M * N * 4
@@ -276,9 +344,10 @@ def bench_lm_head(args, ctx, sampler=False):
         "roofline": {"bound": "hbm", "kernel": "lm_head_gemv", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("lm_head_gemv", f"lm_head_m{M}"), "traffic_note": TRAFFIC_NOTE,
-                     "algorithmic_bytes_per_launch": int(gemv_bytes), "avg_launch_us": round(g_ms * 1e3, 3)},
+                     "algorithmic_bytes_per_launch": int(gemv_bytes), "avg_launch_us": round(g_ms * 1e3, 3), **launch_stats(prof, "lm_head_gemv")},
         "step_achieved_gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1),
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "_cpu_inputs": (x, w, s),
     }
 
@@ -293,54 +362,69 @@ def cpu_lm_head(args, inputs):
     logits = np.zeros(M * N, np.float32)
     am = np.zeros(M, np.uint32)
     P = pyoracle.p
-    L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am))
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < args.cpu_seconds and n < 10000:
-        L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am))
-        n += 1
-    el = time.perf_counter() - t0
+    res = cpu_stats(lambda: L.cpu_lm_head_i8(tier, P(x), M, P(w), P(s), N, Kd, P(logits), P(am)), M, "tokens/s",
+                    args.cpu_seconds)
     want_l, want_a = pyoracle.lm_head_i8(x, w, s, N, Kd)
     same = np.array_equal(logits, want_l.reshape(-1)) and np.array_equal(am, want_a)
-    return {"value": round(M * n / el, 2), "unit": "tokens/s", "cores": int(L.cpu_threads()), "kind": "port",
-            "tier": L.cpu_tier_feature(tier).decode(), "matches_oracle": bool(same),
-            "sample": f"{n} LM-head GEMV+argmax calls of M={M} rows, {el:.1f} s; 64-row blocks over all threads"}
+    res.update({"cores": int(L.cpu_threads()), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "matches_oracle": bool(same),
+                "sample": f"LM-head GEMV+argmax calls of M={M} rows; 64-row blocks over all threads "
+                          f"(decoder.rs:1621-1640)"})
+    return res
 
 
 # ---------------------------------------------------------------------------
 # config 1: single igemm at the gate-proj shape
 # ---------------------------------------------------------------------------
 
+IGEMM_SETS = 8  # distinct 64-expert weight sets (8 x 73.4 MB = 587 MB, over twice the 256 MB MALL)
+
+
+def igemm_weight_sets(ctx, N, Kd):
+    """IGEMM_SETS device copies of 64 experts' gate-proj weights (one seeded
+    host set uploaded to distinct allocations: the Infinity Cache holds lines
+    by address, so every copy is read from HBM once the rotation has cycled)."""
+    from franken_ocr_amd import synth
+
+    w = synth.int8_uniform(synth.seed_of(1), 64 * N * Kd)
+    return w, [ctx.to_device(w) for _ in range(IGEMM_SETS)]
+
+
 def bench_igemm(args, ctx):
     from franken_ocr_amd import _abi, synth
 
     M, N, Kd = args.tokens, 896, 1280
-    copies = 64  # 64 distinct experts' gate-proj weights (73 MB), rotated
-    w = synth.int8_uniform(synth.seed_of(1), copies * N * Kd)
+    w, sets = igemm_weight_sets(ctx, N, Kd)
+    copies = 64 * len(sets)  # distinct 1.15 MB gate-proj matrices, rotated
+    log(f"igemm: M={M}, {copies} distinct weight matrices ({copies * N * Kd / 1e6:.0f} MB) rotated")
     a = synth.int8_uniform(synth.seed_of(2), M * Kd)
-    dw = ctx.to_device(w)
     da = ctx.to_device(a)
     dout = ctx.empty((M, N), np.int32)
-    import ctypes as C
 
     def step(i):
-        off = (i % copies) * N * Kd
-        _abi.call("focr_hip_igemm_s8s8_dev", ctx.handle, da.c_ptr, dw.offset(off), M, Kd, N, dout.c_ptr)
+        c = i % copies
+        _abi.call("focr_hip_igemm_s8s8_dev", ctx.handle, da.c_ptr, sets[c % len(sets)].offset((c // len(sets)) * N * Kd),
+                  M, Kd, N, dout.c_ptr)
 
-    for i in range(args.warmup):
+    for i in range(max(args.warmup, copies)):  # every matrix once: the timed pass starts from a cycled MALL
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     g_ms = kernel_us(prof, "igemm_i8") * 1e-3
     nbytes = N * Kd + M * Kd + 2 * M * N * 4
     achieved = nbytes / (g_ms * 1e-3) / 1e9
     return {
         "metric": "int8 igemm (gate-proj 896x1280) launches/s, 1 GPU",
         "value": round(args.steps / el, 1), "unit": "launches/s", "ms_per_step": round(el / args.steps * 1e3, 5),
-        "dtype": "int8", "config": {"workload": "igemm", "m": M, "n": N, "k": Kd, "weight_copies_rotated": copies},
+        "dtype": "int8", "config": {"workload": "igemm", "m": M, "n": N, "k": Kd, "weight_copies_rotated": copies,
+                                    "rotated_weight_bytes": copies * N * Kd},
         "roofline": {"bound": "hbm", "kernel": "igemm_i8", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("igemm_i8", f"igemm_m{M}"), "traffic_note": TRAFFIC_NOTE,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3),
+                     **launch_stats(prof, "igemm_i8")},
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "_cpu_inputs": (a, w[: N * Kd]),
     }
 
@@ -348,22 +432,25 @@ def bench_igemm(args, ctx):
 def bench_igemm_batched(args, ctx):
     """cfg1 batched: 64 distinct experts' gate projections (896 x 1280 each,
     73.4 MB) in one launch, each against its own M activation rows, i32 out
-    accumulated (+=)."""
+    accumulated (+=). The timed launches rotate over IGEMM_SETS distinct
+    64-expert weight sets (587 MB), so the weights come from HBM."""
     from franken_ocr_amd import _abi, synth
 
     M, N, Kd, B = args.tokens, 896, 1280, 64
-    w = synth.int8_uniform(synth.seed_of(1), B * N * Kd)
+    w, sets = igemm_weight_sets(ctx, N, Kd)
+    log(f"igemm_batched: M={M}, {B} instances per launch, {len(sets)} weight sets rotated")
     a = synth.int8_uniform(synth.seed_of(3), B * M * Kd)
-    dw, da = ctx.to_device(w), ctx.to_device(a)
+    da = ctx.to_device(a)
     dout = ctx.to_device(np.zeros(B * M * N, np.int32))
 
     def step(i):
-        _abi.call("focr_hip_igemm_s8s8_batched_dev", ctx.handle, da.c_ptr, dw.c_ptr, B, M, Kd, N, dout.c_ptr)
+        _abi.call("focr_hip_igemm_s8s8_batched_dev", ctx.handle, da.c_ptr, sets[i % len(sets)].c_ptr, B, M, Kd, N,
+                  dout.c_ptr)
 
-    for i in range(args.warmup):
+    for i in range(max(args.warmup, len(sets))):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     g_us = kernel_us(prof, "igemm_i8_batched")
     nbytes = B * (N * Kd + M * Kd + 2 * M * N * 4)
     achieved = nbytes / (g_us * 1e-6) / 1e9
@@ -371,12 +458,15 @@ def bench_igemm_batched(args, ctx):
         "metric": "int8 igemm, 64 experts' gate-proj (896x1280) in one launch, launches/s, 1 GPU",
         "value": round(args.steps / el, 1), "unit": "launches/s", "ms_per_step": round(el / args.steps * 1e3, 5),
         "dtype": "int8", "config": {"workload": "igemm_batched", "m": M, "n": N, "k": Kd, "instances": B,
-                                    "weight_bytes": B * N * Kd},
+                                    "weight_bytes": B * N * Kd, "weight_sets_rotated": len(sets)},
         "roofline": {"bound": "hbm", "kernel": "igemm_i8_batched", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_us, 3)},
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("igemm_i8_batched", f"igemm_batched_m{M}"), "traffic_note": TRAFFIC_NOTE,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_us, 3),
+                     **launch_stats(prof, "igemm_i8_batched")},
         "kernel_avg_us": kernels,
-        "_cpu_inputs": None,
+        "step_us": sstats,
+        "_cpu_inputs": (a, w, M),
     }
 
 
@@ -389,13 +479,36 @@ def cpu_igemm(args, inputs):
     M, N, Kd = args.tokens, 896, 1280
     out = np.zeros(M * N, np.int32)
     P = pyoracle.p
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < args.cpu_seconds and n < 200000:
-        L.cpu_igemm_s8s8(tier, P(a), P(w), M, Kd, N, P(out))
-        n += 1
-    el = time.perf_counter() - t0
-    return {"value": round(n / el, 1), "unit": "launches/s", "cores": 1, "kind": "port",
-            "tier": L.cpu_tier_feature(tier).decode(), "sample": f"{n} single-thread igemm calls, {el:.1f} s"}
+    res = cpu_stats(lambda: L.cpu_igemm_s8s8(tier, P(a), P(w), M, Kd, N, P(out)), 1, "launches/s", args.cpu_seconds)
+    want = pyoracle.igemm_s8s8(a, w, M, Kd, N)
+    got = np.zeros(M * N, np.int32)
+    L.cpu_igemm_s8s8(tier, P(a), P(w), M, Kd, N, P(got))
+    res.update({"cores": 1, "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "matches_oracle": bool(np.array_equal(got, want)),
+                "sample": f"single-thread igemm_s8s8 calls at M={M} (the tier kernel is single-threaded, x86.rs)"})
+    return res
+
+
+def cpu_igemm_batched(args, inputs):
+    from oracle import pyoracle
+
+    a, w, M = inputs
+    L = pyoracle.lib()
+    tier = L.cpu_detect_tier()
+    N, Kd, B = 896, 1280, 64
+    out = np.zeros(B * M * N, np.int32)
+    P = pyoracle.p
+    res = cpu_stats(lambda: L.cpu_igemm_s8s8_batched(tier, P(a), P(w), B, M, Kd, N, P(out)), 1, "launches/s",
+                    args.cpu_seconds)
+    got = np.zeros(B * M * N, np.int32)
+    L.cpu_igemm_s8s8_batched(tier, P(a), P(w), B, M, Kd, N, P(got))
+    same = all(np.array_equal(got[i * M * N:(i + 1) * M * N],
+                              pyoracle.igemm_s8s8(a[i * M * Kd:(i + 1) * M * Kd], w[i * N * Kd:(i + 1) * N * Kd],
+                                                  M, Kd, N)) for i in (0, B - 1))
+    res.update({"cores": int(L.cpu_threads()), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "matches_oracle": bool(same),
+                "sample": f"the 64 instances' igemm_s8s8 at M={M} as one task each over all threads"})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -406,21 +519,35 @@ def bench_rswa(args, ctx):
     from franken_ocr_amd import synth
     from franken_ocr_amd.engine import RingCache
 
-    B, G, NH, D = 8, 1024, 10, 128
+    import ctypes as C
+
+    from franken_ocr_amd import _abi
+
+    B, G, NH, D, W = 8, 1024, 10, 128, 128
     copies = args.copies
     caches = []
     rng = np.random.default_rng(7)
     ring_lens = [int(x) for x in rng.integers(0, 129, B)]
+    host = []  # per stream: ref K, ref V, ring K, ring V (head-major), ring_len
+    for s in range(B):
+        host.append((synth.f32_normal(synth.seed_of(2000 + s), NH * G * D),
+                     synth.f32_normal(synth.seed_of(2100 + s), NH * G * D),
+                     synth.f32_normal(synth.seed_of(2300 + s), NH * W * D),
+                     synth.f32_normal(synth.seed_of(2400 + s), NH * W * D), ring_lens[s]))
+    ring_pos = [rl % W if rl < W else int(rng.integers(0, W)) for rl in ring_lens]
     for c in range(copies):
         cache = RingCache(B, G, ctx)
         for s in range(B):
-            k = synth.f32_normal(synth.seed_of(2000 + s), NH * G * D)
-            v = synth.f32_normal(synth.seed_of(2100 + s), NH * G * D)
-            cache.record_prefill(s, ctx.to_device(k), ctx.to_device(v), G)
-            rl = ring_lens[s]
-            cache.set_state(s, rl, rl % 128 if rl < 128 else int(rng.integers(0, 128)))
+            rk, rv, gk, gv, rl = host[s]
+            cache.record_prefill(s, ctx.to_device(rk), ctx.to_device(rv), G)
+            reg = cache.regions(s)
+            for key, arr in (("ring_k", gk), ("ring_v", gv)):
+                _abi.call("focr_hip_h2d", ctx.handle, C.c_void_p(reg[key]), arr.ctypes.data_as(C.c_void_p),
+                          arr.nbytes)
+            cache.set_state(s, rl, ring_pos[s])
         caches.append(cache)
-    q = ctx.to_device(synth.f32_normal(synth.seed_of(2200), B * NH * D).reshape(B, NH * D))
+    q_host = synth.f32_normal(synth.seed_of(2200), B * NH * D).reshape(B, NH * D)
+    q = ctx.to_device(q_host)
     out = ctx.empty((B, NH * D), np.float32)
 
     def step(i):
@@ -429,8 +556,10 @@ def bench_rswa(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     g_ms = kernel_us(prof, "rswa_chunk") * 1e-3
+    caches[0].decode_attention(q, out)
+    gpu_out = out.numpy()
     keys = sum(G + r for r in ring_lens)
     nbytes = 2 * NH * keys * D * 4 + 2 * B * NH * D * 4
     achieved = nbytes / (g_ms * 1e-3) / 1e9
@@ -442,10 +571,36 @@ def bench_rswa(args, ctx):
         "roofline": {"bound": "hbm", "kernel": "rswa_chunk", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("rswa_chunk", "rswa"), "traffic_note": TRAFFIC_NOTE,
-                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3)},
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(g_ms * 1e3, 3), **launch_stats(prof, "rswa_chunk")},
         "kernel_avg_us": kernels,
-        "_cpu_inputs": None,
+        "step_us": sstats,
+        "_cpu_inputs": (host, q_host, gpu_out, G),
     }
+
+
+def cpu_rswa(args, inputs):
+    """decode_attention_scalar (rswa.rs:894-939) per stream, one thread,
+    the 8 streams one after another (rswa.rs:1359-1366), on the same caches
+    and queries as the GPU step (the oracle's restatement, oracle/)."""
+    from oracle import pyoracle
+
+    host, q, gpu_out, G = inputs
+    L, P = pyoracle.lib(), pyoracle.p
+    B, NH, D, W = len(host), 10, 128, 128
+    out = np.zeros((B, NH * D), np.float32)
+    qs = [np.ascontiguousarray(q[s]) for s in range(B)]
+
+    def call():
+        for s, (rk, rv, gk, gv, rl) in enumerate(host):
+            st = L.oracle_decode_attention(P(rk), P(rv), G, G, P(gk), P(gv), rl, P(qs[s]), P(out[s]))
+            assert st == 0
+
+    res = cpu_stats(call, 1, "steps/s", args.cpu_seconds)
+    err = float(np.max(np.abs(gpu_out - out) / np.maximum(np.abs(out), np.abs(out).max() * 1e-2)))
+    res.update({"cores": 1, "kind": "port", "gpu_max_rel_err": err,
+                "sample": f"decode attention steps over {B} streams (ref {G} rows + ring), the streams one after "
+                          f"another, one thread; gpu_max_rel_err: the GPU step's output against this one"})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -483,7 +638,7 @@ def bench_prefill_attn(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     a_us = kernel_us(prof, "attn_prefill")  # per chunk call (attention + key-range merge)
     flops = attn_flops(seq, NH, D)
     achieved = flops / (a_us * 1e-6 * len(bounds)) / 1e12
@@ -496,8 +651,9 @@ def bench_prefill_attn(args, ctx):
         "roofline": {"bound": "mfma", "kernel": "attn_prefill", "achieved": round(achieved, 2),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
                      "traffic": traffic_for("attn_prefill", f"prefill_attn_{seq}"), "algorithmic_flops_per_step": flops,
-                     "avg_launch_us": round(a_us, 3), "launches_per_step": len(bounds)},
+                     "avg_launch_us": round(a_us, 3), "launches_per_step": len(bounds), **launch_stats(prof, "attn_prefill")},
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "_cpu_inputs": (q, k, v, chunk),
     }
 
@@ -511,19 +667,17 @@ def cpu_prefill_attn(args, inputs):
     qc = [(c0, c1, np.ascontiguousarray(q[c0:c1]), np.zeros((c1 - c0, q.shape[1]), np.float32))
           for c0, c1 in [(c0, min(c0 + chunk, seq)) for c0 in range(0, seq, chunk)]]
     kc, vc = np.ascontiguousarray(k), np.ascontiguousarray(v)
-    # whole chunked prefills of the sequence, repeated for a bounded time
-    n, t0 = 0, time.perf_counter()
-    while True:
+
+    def call():
         for c0, c1, qq, oo in qc:
             L.oracle_chunk_prefill_attention_f32(P(qq), c1 - c0, P(kc), P(vc), c1, 10, 128, c0, P(oo))
-        n += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    el = time.perf_counter() - t0
-    return {"value": round(seq * n / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n} chunked prefill attentions of {seq} tokens (chunks of {chunk}), {el:.1f} s; the f32 "
-                      f"restatement of decoder.rs:1282-1340 in the reference's described order, one thread (the "
-                      f"reference's ft-kernel-cpu sdpa is not in the reference tree)"}
+
+    res = cpu_stats(call, seq, "tokens/s", args.cpu_seconds, min_iters=2)
+    res.update({"cores": 1, "kind": "port",
+                "sample": f"whole chunked prefills of {seq} tokens (chunks of {chunk}); the f32 restatement of "
+                          f"decoder.rs:1282-1340 in the reference's described order, one thread (the reference's "
+                          f"ft-kernel-cpu sdpa is not in the reference tree)"})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -555,12 +709,12 @@ def h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, steps, gu_name, dn
     pairs = T * K
     gu_ops, dn_ops = 2.0 * pairs * 2 * I * H, 2.0 * pairs * H * I
     nw = max(steps // 2, 10)
-    el_w, prof_w, kernels_w = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False), nw)
+    el_w, prof_w, kernels_w, _ = timed(ctx, lambda i: layers[0].prefill(dx, di, dg, dout, check_idx=False), nw)
     counts = np.bincount(idx.ravel(), minlength=E)
     hot = np.sort(np.argsort(-counts, kind="stable")[:8]).astype(np.uint32)
     bidx = np.ascontiguousarray(np.stack([hot[(np.arange(T) + j) % 8] for j in range(K)], axis=1))
     dbi = ctx.to_device(bidx)
-    el_b, prof_b, kernels_b = timed(ctx, lambda i: layers[i % len(layers)].prefill(dx, dbi, dg, dout,
+    el_b, prof_b, kernels_b, _ = timed(ctx, lambda i: layers[i % len(layers)].prefill(dx, dbi, dg, dout,
                                                                                   check_idx=False), nw)
     ms_w, ms_b = el_w / nw * 1e3, el_b / nw * 1e3
 
@@ -598,7 +752,7 @@ def bench_prefill_i4(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     pairs = T * K
     gu_ops = 2.0 * pairs * 2 * I * H
@@ -621,7 +775,7 @@ def bench_prefill_i4(args, ctx):
         "roofline": {"bound": "mfma", "kernel": "i4_gate_up", "achieved": round(gu_tops, 2),
                      "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(gu_tops / MFMA_INT8_PEAK_TOPS, 4),
                      "traffic": traffic_for("i4_gate_up", f"moe_prefill_i4_m{T}"),
-                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3)},
+                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3), **launch_stats(prof, "i4_gate_up")},
         "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
@@ -629,6 +783,7 @@ def bench_prefill_i4(args, ctx):
         # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
         "mfma_utilisation": views,
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "kernel_avg_us_warm": kernels_w,
         "kernel_avg_us_bucket": kernels_b,
         "_cpu_inputs": (x, idx, gates, host),
@@ -636,22 +791,44 @@ def bench_prefill_i4(args, ctx):
 
 
 def cpu_prefill_i4(args, inputs):
+    """The reference's two x86 int4 paths (int4.rs:454-460: no x86 int4 MAC
+    kernel): s4s8_packed_kernel_scalar and igemm_s4s8 (AVX2 nibble unpack,
+    then the per-group loop), both built -O3 by LLVM for the baseline x86-64
+    ISA as rustc's release profile builds them (oracle/cpu_int4.c), run in
+    moe_block's structure (experts one after another, each expert's members
+    as one GEMM call). Both are timed on the first 64 tokens; the faster is
+    then timed on the whole M = 512 layer and reported."""
     from oracle import pyoracle
 
     x, idx, gates, host = inputs
-    n, t0, chunk = 0, time.perf_counter(), 8
-    while True:
-        lo = (n * chunk) % x.shape[0]
-        st, _, _, _ = pyoracle.moe_prefill_i4(x[lo:lo + chunk], idx[lo:lo + chunk], gates[lo:lo + chunk], 32, *host,
-                                              E, I)
+    wg, sg, wu, su, wd, sd = host
+    L, P = pyoracle.lib(), pyoracle.p
+    T = x.shape[0]
+    idx, gates = np.ascontiguousarray(idx), np.ascontiguousarray(gates)
+    out = np.zeros(T * H, np.float32)
+
+    def run(kind, t):
+        st = L.cpu_moe_prefill_i4(kind, P(np.ascontiguousarray(x[:t])), t, H, I, E, K, P(idx), P(gates), 32, P(wg),
+                                  P(sg), P(wu), P(su), P(wd), P(sd), P(out))
         assert st == 0
-        n += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    el = time.perf_counter() - t0
-    return {"value": round(n * chunk / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "tier": "scalar (the reference has no x86 int4 kernel, int4.rs:454-460)",
-            "sample": f"{n} chunks of {chunk} tokens of the same layer and routing, {el:.1f} s, single thread"}
+
+    sample_t = min(64, T)
+    names = ("s4s8_packed_kernel_scalar", "igemm_s4s8 (avx2 unpack + per-group loop)")
+    probe = {}
+    for kind, name in enumerate(names):
+        t0 = time.perf_counter()
+        run(kind, sample_t)
+        probe[name] = round(sample_t / (time.perf_counter() - t0), 2)
+    kind = max(range(len(names)), key=lambda k_: probe[names[k_]])
+    res = cpu_stats(lambda: run(kind, T), T, "tokens/s", args.cpu_seconds, min_iters=2)
+    n_check = min(16, T)
+    st, want, _, _ = pyoracle.moe_prefill_i4(x[:n_check], idx[:n_check], gates[:n_check], 32, *host, E, I)
+    same = st == 0 and np.array_equal(out.reshape(T, H)[:n_check], want)
+    res.update({"cores": 1, "kind": "port", "tier": names[kind],
+                "paths_probed_tokens_per_s": probe, "matches_oracle": bool(same),
+                "sample": f"whole M={T} int4 MoE layers with the faster path (both probed on {sample_t} tokens); "
+                          f"one thread, experts one after another; matches_oracle on the first {n_check} rows"})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -711,7 +888,7 @@ def bench_linear_i8(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     ops = 2.0 * M * N * Kd
     g_us = kernel_us(prof, "linear_i8")
@@ -730,11 +907,36 @@ def bench_linear_i8(args, ctx):
         "roofline": {"bound": "mfma", "kernel": "linear_i8", "achieved": round(tops, 2),
                      "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4),
                      "traffic": traffic_for("linear_i8", f"linear_i8_m{M}"),
-                     "algorithmic_ops_per_launch": ops, "avg_launch_us": round(g_us, 3)},
+                     "algorithmic_ops_per_launch": ops, "avg_launch_us": round(g_us, 3), **launch_stats(prof, "linear_i8")},
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         **({"library_ref": lib} if lib else {}),
-        "_cpu_inputs": None,
+        "_cpu_inputs": (x, w, ws),
     }
+
+
+def cpu_linear_i8(args, inputs):
+    """nn::linear_int8_dynamic (nn.rs:151-173) on the best int8 tier: the
+    dynamic-rule row quantize, then the i32 products in 64-output-row blocks
+    over all host threads and the dequant (oracle/cpu_tier.c; ft-kernel-cpu's
+    own kernel is not in the reference tree). Timed on 512-row slices."""
+    from oracle import pyoracle
+
+    x, w, ws = inputs
+    L, P = pyoracle.lib(), pyoracle.p
+    tier = L.cpu_detect_tier()
+    N, Kd = ws.shape[0], x.shape[1]
+    rows = min(512, x.shape[0])
+    xs = np.ascontiguousarray(x[:rows])
+    y = np.zeros((rows, N), np.float32)
+    res = cpu_stats(lambda: L.cpu_linear_i8_dynamic(tier, P(xs), rows, Kd, P(w), P(ws), N, P(y)), rows, "rows/s",
+                    args.cpu_seconds)
+    st, want, _, _ = pyoracle.linear_i8_dynamic(xs[:8], w, ws, N)
+    res.update({"cores": int(L.cpu_threads()), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "matches_oracle": bool(st == 0 and np.array_equal(y[:8], want)),
+                "sample": f"linear_int8_dynamic over {rows}-row slices of the {x.shape[0]}-row input, "
+                          f"{N}x{Kd} weights; matches_oracle on the first 8 rows"})
+    return res
 
 
 def bench_prefill_i8(args, ctx):
@@ -758,7 +960,7 @@ def bench_prefill_i8(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     pairs = T * K
     gu_ops = 2.0 * pairs * 2 * I * H
@@ -781,7 +983,7 @@ def bench_prefill_i8(args, ctx):
         "roofline": {"bound": "mfma", "kernel": "i8_gate_up", "achieved": round(gu_tops, 2),
                      "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(gu_tops / MFMA_INT8_PEAK_TOPS, 4),
                      "traffic": traffic_for("i8_gate_up", f"moe_prefill_i8_m{T}"),
-                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3)},
+                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3), **launch_stats(prof, "i8_gate_up")},
         "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
@@ -789,6 +991,7 @@ def bench_prefill_i8(args, ctx):
         # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
         "mfma_utilisation": views,
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "kernel_avg_us_warm": kernels_w,
         "kernel_avg_us_bucket": kernels_b,
         "_cpu_inputs": None,
@@ -820,7 +1023,8 @@ def bench_decode_layer(args, ctx):
     so = synth.f32_uniform(synth.seed_of(809), H, 1e-3, 2e-2)
     ln1 = synth.f32_uniform(synth.seed_of(810), H, 0.5, 1.5)
     ln2 = synth.f32_uniform(synth.seed_of(811), H, 0.5, 1.5)
-    kv = [ctx.to_device(synth.f32_normal(synth.seed_of(820 + i), 10 * G * 128)) for i in range(2)]
+    kv_host = [synth.f32_normal(synth.seed_of(820 + i), 10 * G * 128) for i in range(2)]
+    kv = [ctx.to_device(a) for a in kv_host]
     layers, caches = [], []
     for c in range(args.copies):
         router = synth.f32_normal(synth.seed_of(1000 + c), E * H, 0.0, 0.02).reshape(E, H)
@@ -832,7 +1036,8 @@ def bench_decode_layer(args, ctx):
         for s in range(B):
             cache.record_prefill(s, kv[0], kv[1], G)
         caches.append(cache)
-    x = ctx.to_device(synth.f32_normal(synth.seed_of(830), B * H).reshape(B, H))
+    x_host = synth.f32_normal(synth.seed_of(830), B * H).reshape(B, H)
+    x = ctx.to_device(x_host)
     idx = [ctx.empty((B, K), np.uint32) for _ in layers]
     pos = np.full(B, G, np.uint32)
     n = len(layers)
@@ -844,7 +1049,7 @@ def bench_decode_layer(args, ctx):
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     # distinct experts of each copy's last step (every copy has run by now)
     U = [len(np.unique(b.numpy())) for b in idx[:min(n, args.warmup + 2 * args.steps)]]
@@ -867,8 +1072,61 @@ def bench_decode_layer(args, ctx):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_step": int(layer_bytes), "avg_step_us": round(ms * 1e3, 3)},
         "kernel_avg_us": kernels,
-        "_cpu_inputs": None,
+        "step_us": sstats,
+        "_cpu_inputs": dict(x=x_host, kv=kv_host, G=G, base=base, sh=sh, wqkv=wqkv, sqkv=sqkv, wo=wo, so=so, ln1=ln1, ln2=ln2, SI=SI),
     }
+
+
+def cpu_decode_layer(args, inputs):
+    """One layer of batched_decode_step_i8_streams (decoder.rs:2812-2933) on
+    the host: M = B GEMVs on the best int8 tier over all threads, RoPE, ring
+    write and R-SWA decode attention per stream (single thread, streams one
+    after another), the MoE (top-6 + shared expert as concurrent serial
+    tasks, tokens one after another) — oracle/cpu_tier.c
+    cpu_decoder_layer_step, the same weights as layer copy 0 and 1024-token
+    reference blocks."""
+    import ctypes as C
+
+    from franken_ocr_amd import synth
+    from oracle import pyoracle
+
+    d = inputs
+    L, P = pyoracle.lib(), pyoracle.p
+    tier = L.cpu_detect_tier()
+    x0, G = d["x"], d["G"]
+    B = x0.shape[0]
+    _, wg, sg, wu, su, wd, sd = d["base"]
+    router = synth.f32_normal(synth.seed_of(1000), E * H, 0.0, 0.02).reshape(E, H)
+    rings = [pyoracle.Ring(G) for _ in range(B)]
+    for r in rings:
+        r.record_prefill(d["kv"][0], d["kv"][1], G)
+
+    def ptrs(name):
+        return (C.c_void_p * B)(*[getattr(r, name).ctypes.data for r in rings])
+
+    refk, refv, ringk, ringv = ptrs("ref_k"), ptrs("ref_v"), ptrs("ring_k"), ptrs("ring_v")
+    plen = np.full(B, G, np.uint32)
+    rlen = np.zeros(B, np.uint32)
+    rpos = np.zeros(B, np.uint32)
+    x = np.array(x0, np.float32)
+    sh = [P(a) for a in d["sh"]]
+    step = [0]
+
+    def call():
+        x[:] = x0
+        pos = np.full(B, G + step[0], np.uint32)
+        step[0] += 1
+        st = L.cpu_decoder_layer_step(tier, P(x), B, P(pos), refk, refv, G, P(plen), ringk, ringv, P(rlen), P(rpos),
+                                      P(d["ln1"]), P(d["ln2"]), 1e-6, 10000.0, P(d["wqkv"]), P(d["sqkv"]),
+                                      P(d["wo"]), P(d["so"]), P(router), E, K, I, P(wg), P(sg), P(wu), P(su), P(wd),
+                                      P(sd), *sh, d["SI"])
+        assert st == 0
+
+    res = cpu_stats(call, B, "tokens/s", args.cpu_seconds)
+    res.update({"cores": int(L.cpu_threads()), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "sample": f"decoder-layer decode steps over {B} streams (1024-token reference blocks, rings "
+                          f"filling); parity of this composition with the oracle's: tests/test_cpu_baseline.py"})
+    return res
 
 
 def bench_decode_step(args, ctx):
@@ -933,7 +1191,7 @@ def bench_decode_step(args, ctx):
         step(i)
     ctx.device_synchronize()
     U = [len(np.unique(idx[l].numpy())) for l in range(1, NL)]
-    el, prof, kernels = timed(ctx, step, args.steps)
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     keys = G + min(128, args.warmup + args.steps)  # the rings' fill during the timed pass
     attn = B * 2 * 10 * keys * 128 * 4
@@ -953,6 +1211,7 @@ def bench_decode_step(args, ctx):
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_step": int(step_bytes), "avg_step_us": round(ms * 1e3, 3)},
         "kernel_avg_us": kernels,
+        "step_us": sstats,
         "_cpu_inputs": None,
     }
 
@@ -996,13 +1255,13 @@ WORKLOADS = {
     "lm_head": (bench_lm_head, cpu_lm_head),
     "lm_head_sample": (lambda args, ctx: bench_lm_head(args, ctx, sampler=True), None),
     "igemm": (bench_igemm, cpu_igemm),
-    "igemm_batched": (bench_igemm_batched, None),
-    "rswa": (bench_rswa, None),
+    "igemm_batched": (bench_igemm_batched, cpu_igemm_batched),
+    "rswa": (bench_rswa, cpu_rswa),
     "copy": (bench_copy, None),
     "moe_prefill_i4": (bench_prefill_i4, cpu_prefill_i4),
     "moe_prefill_i8": (bench_prefill_i8, None),
-    "linear_i8": (bench_linear_i8, None),
-    "decode_layer": (bench_decode_layer, None),
+    "linear_i8": (bench_linear_i8, cpu_linear_i8),
+    "decode_layer": (bench_decode_layer, cpu_decode_layer),
     "decode_step": (bench_decode_step, None),
     "prefill_attn": (bench_prefill_attn, cpu_prefill_attn),
 }
@@ -1025,10 +1284,13 @@ EXTRAS = [
     ("linear_i8_m8192", "linear_i8", 8192, 3, 20, 3),
     ("decode_layer_b8", "decode_layer", 8, 6, 50, 5),
 ]
-_EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us")
+_EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us", "step_us")
 
 
 def run_extras(ctx, base_args) -> dict:
+    """Each secondary configuration timed like its own --workload run, then
+    its CPU baseline on the host (base_args.extra_cpu_seconds each, unless
+    --no-cpu)."""
     import gc
 
     out = {}
@@ -1036,20 +1298,28 @@ def run_extras(ctx, base_args) -> dict:
         if wl not in WORKLOADS:
             continue
         a = argparse.Namespace(**vars(base_args))
-        a.workload, a.tokens, a.copies, a.steps, a.warmup, a.no_cpu = wl, tokens, copies, steps, warmup, True
+        a.workload, a.tokens, a.copies, a.steps, a.warmup = wl, tokens, copies, steps, warmup
+        a.cpu_seconds = base_args.extra_cpu_seconds
         log(f"extra {key}")
-        res = WORKLOADS[wl][0](a, ctx)
-        res.pop("_cpu_inputs", None)
+        run, cpu = WORKLOADS[wl]
+        res = run(a, ctx)
+        cpu_inputs = res.pop("_cpu_inputs", None)
         rl = res.get("roofline") or {}
         ent = {"metric": res["metric"], "value": res["value"], "unit": res["unit"],
                "ms_per_step": res["ms_per_step"], "steps": steps, "config": res["config"],
-               "roofline": {k: rl.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit", "frac",
-                                                   "avg_launch_us")}}
+               "roofline": {k: rl.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit", "frac", "traffic",
+                                                   "avg_launch_us", "p50_launch_us", "p90_launch_us")}}
         for k in _EXTRA_KEYS:
             if k in res:
                 ent[k] = res[k]
+        if cpu is not None and not base_args.no_cpu and cpu_inputs is not None:
+            log(f"extra {key}: cpu baseline")
+            ent["cpu_baseline"] = cpu(a, cpu_inputs)
+            ent["cpu_baseline"].update(host_cpu())
+        else:
+            ent["cpu_baseline"] = None
         out[key] = ent
-        del res
+        del res, cpu_inputs
         gc.collect()
     return out
 
@@ -1063,7 +1333,10 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=None, help="T (moe), M (lm_head/igemm)")
     ap.add_argument("--copies", type=int, default=None, help="distinct weight copies rotated (defeats MALL)")
     ap.add_argument("--chunk", type=int, default=256, help="prefill chunk (prefill_attn; DEFAULT_PREFILL_CHUNK)")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="CPU baseline sample of the headline workload (seconds of timed calls)")
+    ap.add_argument("--extra-cpu-seconds", type=float, default=4.0,
+                    help="CPU baseline sample of each secondary configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations the default (moe_decode) run reports under 'extra'")

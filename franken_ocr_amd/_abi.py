@@ -130,9 +130,12 @@ _SIGS: dict[str, list] = {
                                             C.c_uint8],
     "focr_hip_focrq_writer_build": [_P, _P, _SZ, _P],
     "focr_hip_focrq_writer_write": [_P, C.c_char_p],
+    "focr_hip_ctx_scratch_bytes": [_P, _P],
     "focr_hip_prof_enable": [_P, _I32],
     "focr_hip_prof_reset": [_P],
     "focr_hip_prof_read": [_P, C.c_char_p, _SZ],
+    "focr_hip_mark": [_P],
+    "focr_hip_marks_read": [_P, _P, _SZ, _P],
 }
 
 _RESTYPE = {"focr_hip_last_error": C.c_char_p, "focr_hip_version": C.c_char_p,

@@ -63,39 +63,27 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-# Host-side sanitizers for the CPU-only checks of the host code (the .focrq
-# parser, the ABI's argument checks): every -fsanitize= applies to the host
-# pass only, the gfx950 code is built as usual. The result loads into a
-# process that preloads the clang ASan runtime (franken_ocr_amd/sanitize.py).
-SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
-            "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
-            "-Xarch_host", "-shared-libsan"]
-SAN_BUILD = PKG / "_build_san"
-SAN_OUT = SAN_BUILD / "libfocr_hip_san.so"
-
-
-def _compile(src: Path, sanitize: bool = False) -> Path:
-    obj = (SAN_BUILD if sanitize else BUILD) / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, *(SANITIZE if sanitize else []), "-x", "hip", "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path, extra: tuple) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON, *extra, "-x", "hip", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = False, sanitize: bool = False) -> Path:
-    """Compile every kernel/host source for gfx950 and link the shared library
-    (with sanitize: the host-sanitized copy in _build_san/ instead)."""
-    out_dir = SAN_BUILD if sanitize else BUILD
-    out_dir.mkdir(exist_ok=True)
-    out = SAN_OUT if sanitize else OUT
+def build(verbose: bool = False, extra: tuple = (), out: Path = OUT, build_dir: Path = BUILD) -> Path:
+    """Compile every kernel/host source for gfx950 and link the shared
+    library. `extra` flags go on every compile and the link (a variant build
+    into its own `build_dir` / `out`, e.g. the host-sanitized copy the CPU
+    sanitizer test makes)."""
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = min(8, len(srcs), os.cpu_count() or 1)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda src: _compile(src, sanitize), srcs))
+        objs = list(ex.map(lambda src: _compile(src, build_dir, tuple(extra)), srcs))
     tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", *(SANITIZE if sanitize else []), "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objs)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", *extra, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")

@@ -706,7 +706,9 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
     if (!out) return fail(FOCR_HIP_E_ARG, fmt("%s: null out", name));
     MoeScratch s;
     ScratchSource src{ctx};
+    std::unique_ptr<StaticScratchOrder> order;
     if (static_scratch) {
+        if (!ctx->static_scratch) ctx->static_scratch_err = static_scratch_init(ctx->device, &ctx->static_scratch);
         if (!ctx->static_scratch)
             return hip_fail(ctx->static_scratch_err != hipSuccess ? ctx->static_scratch_err : hipErrorInvalidSymbol,
                             "moe_decode_noalloc: static scratch address");
@@ -717,6 +719,10 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
                                               "buffer holds %zu",
                                               t, count.used, kStaticScratchBytes));
         src = ScratchSource{ctx, static_cast<char*>(ctx->static_scratch), kStaticScratchBytes, 0, false};
+        // every launch below is ordered after the device's previous call on
+        // the array; this call's completion is recorded when `order` ends
+        order = std::make_unique<StaticScratchOrder>(ctx->device, ctx->stream);
+        if (order->err() != hipSuccess) return hip_fail(order->err(), "moe_decode_noalloc: order after the previous call");
     }
     if ((st = moe_scratch(src, L, t, with_shared != 0, &s))) return st;
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
@@ -1632,9 +1638,8 @@ static void drain_prof(focr_hip_ctx* ctx) {
     for (auto& p : ctx->pending) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
-            auto& t = ctx->prof_totals[p.name];
-            t.first += 1;
-            t.second += ms;
+            auto& v = ctx->prof_samples[p.name];
+            if (v.size() < kProfMaxSamples) v.push_back(ms);
         }
         // not recycled: an event reused for a later dispatch has read back
         // elapsed times several times the kernel's (same step throughput)
@@ -1644,13 +1649,27 @@ static void drain_prof(focr_hip_ctx* ctx) {
     ctx->pending.clear();
 }
 
+static void drop_marks(focr_hip_ctx* ctx) {
+    for (hipEvent_t e : ctx->marks) hipEventDestroy(e);
+    ctx->marks.clear();
+}
+
 int32_t focr_hip_prof_reset(focr_hip_ctx* ctx) {
     if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
     std::lock_guard<std::mutex> lk(ctx->mu);
     hipSetDevice(ctx->device);
     drain_prof(ctx);
-    ctx->prof_totals.clear();
+    ctx->prof_samples.clear();
     return FOCR_HIP_OK;
+}
+
+// nearest rank: rank = ceil(q * n) clamped to [1, n], element rank - 1 of the
+// ascending samples (the reference's bench statistics, perf_harness.rs:276-282)
+static double nearest_rank(const std::vector<float>& sorted, double q) {
+    const size_t n = sorted.size();
+    size_t rank = static_cast<size_t>(std::ceil(q * static_cast<double>(n)));
+    rank = std::min(std::max<size_t>(rank, 1), n);
+    return sorted[rank - 1];
 }
 
 int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap) {
@@ -1660,15 +1679,54 @@ int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap) {
     drain_prof(ctx);
     std::string j = "{";
     bool first = true;
-    for (auto& kv : ctx->prof_totals) {
-        char buf[256];
-        snprintf(buf, sizeof(buf), "%s\"%s\":{\"count\":%ld,\"ms\":%.6f}", first ? "" : ",", kv.first.c_str(),
-                 kv.second.first, kv.second.second);
+    for (auto& kv : ctx->prof_samples) {
+        if (kv.second.empty()) continue;
+        std::vector<float> v = kv.second;
+        double total = 0.0;
+        for (float x : v) total += x;
+        std::sort(v.begin(), v.end());
+        char buf[384];
+        snprintf(buf, sizeof(buf),
+                 "%s\"%s\":{\"count\":%zu,\"ms\":%.6f,\"min_ms\":%.6f,\"p50_ms\":%.6f,\"p90_ms\":%.6f}",
+                 first ? "" : ",", kv.first.c_str(), v.size(), total, static_cast<double>(v.front()),
+                 nearest_rank(v, 0.5), nearest_rank(v, 0.9));
         j += buf;
         first = false;
     }
     j += "}";
     if (json && cap) snprintf(json, cap, "%s", j.c_str());
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_mark(focr_hip_ctx* ctx) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    FOCR_HIP_TRY(ctx->bind(), "mark: set device");
+    if (ctx->marks.size() >= kMaxMarks) return fail(FOCR_HIP_E_SHAPE, fmt("mark: more than %zu marks", kMaxMarks));
+    hipEvent_t e = nullptr;
+    FOCR_HIP_TRY(hipEventCreate(&e), "mark: event create");
+    hipError_t err = hipEventRecord(e, ctx->stream);
+    if (err != hipSuccess) {
+        hipEventDestroy(e);
+        FOCR_HIP_TRY(err, "mark: event record");
+    }
+    ctx->marks.push_back(e);
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_marks_read(focr_hip_ctx* ctx, float* ms, size_t cap, size_t* n_out) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    FOCR_HIP_TRY(ctx->bind(), "marks_read: set device");
+    hipError_t err = hipStreamSynchronize(ctx->stream);
+    const size_t n = ctx->marks.size() < 2 ? 0 : ctx->marks.size() - 1;
+    if (err == hipSuccess && n > cap) err = hipErrorInvalidValue;
+    for (size_t i = 0; i < n && err == hipSuccess; ++i) err = hipEventElapsedTime(&ms[i], ctx->marks[i], ctx->marks[i + 1]);
+    drop_marks(ctx);
+    if (err == hipErrorInvalidValue && n > cap)
+        return fail(FOCR_HIP_E_SHAPE, fmt("marks_read: %zu intervals, room for %zu", n, cap));
+    FOCR_HIP_TRY(err, "marks_read");
+    if (n_out) *n_out = n;
     return FOCR_HIP_OK;
 }
 

@@ -192,8 +192,19 @@ int32_t focr_hip_ctx_destroy(focr_hip_ctx* ctx) {
         hipEventDestroy(p.start);
         hipEventDestroy(p.stop);
     }
+    for (hipEvent_t e : ctx->marks) hipEventDestroy(e);
     hipStreamDestroy(ctx->stream);
     delete ctx;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_ctx_scratch_bytes(focr_hip_ctx* ctx, size_t* bytes) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    if (!bytes) return fail(FOCR_HIP_E_ARG, "focr_hip_ctx_scratch_bytes: null out");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    size_t total = 0;
+    for (auto& b : ctx->scratch) total += b.cap;
+    *bytes = total;
     return FOCR_HIP_OK;
 }
 

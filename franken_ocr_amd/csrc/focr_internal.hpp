@@ -58,9 +58,32 @@ enum ScratchSlot : int {
 // ---- static scratch of the allocation-free entry points ------------------
 // One array of this many bytes per GPU, held until the process ends.
 constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+// profiling: intervals kept per scope name, and step marks per context
+constexpr size_t kProfMaxSamples = 1 << 20;
+constexpr size_t kMaxMarks = 1 << 16;
 // With `device` current, the device address of that GPU's array (resolved
-// once per device; later calls return the cached address or error).
+// once per device and cached on success; a failure is returned and not
+// cached, so a later call resolves again).
 hipError_t static_scratch_init(int device, void** out);
+// Orders the calls that share one device's static array: construction makes
+// `stream` wait for the previous call's completion event (held under a
+// per-device lock until destruction), destruction records this call's.
+// Nothing is created or allocated. err() reports a failed wait.
+class StaticScratchOrder {
+   public:
+    StaticScratchOrder(int device, hipStream_t stream);
+    ~StaticScratchOrder();
+    StaticScratchOrder(const StaticScratchOrder&) = delete;
+    StaticScratchOrder& operator=(const StaticScratchOrder&) = delete;
+    hipError_t err() const { return err_; }
+
+   private:
+    int device_;
+    hipStream_t stream_;
+    hipEvent_t ev_ = nullptr;  // the device's completion event (null while capturing)
+    hipError_t err_ = hipSuccess;
+    bool locked_ = false, capturing_ = false;
+};
 
 struct ProfPending {
     std::string name;
@@ -83,10 +106,12 @@ struct focr_hip_ctx {
     // the error that kept it from resolving
     void* static_scratch = nullptr;
     hipError_t static_scratch_err = hipSuccess;
-    // profiling
+    // profiling: per scope name, every drained interval in ms
     bool prof = false;
     std::vector<focr::ProfPending> pending;
-    std::map<std::string, std::pair<long, double>> prof_totals;
+    std::map<std::string, std::vector<float>> prof_samples;
+    // step marks (focr_hip_mark): events recorded on the stream between steps
+    std::vector<hipEvent_t> marks;
 
     // Grow-only scratch. Returns nullptr (and sets the error) on failure.
     void* scratch_get(int slot, size_t bytes);

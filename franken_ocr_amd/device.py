@@ -58,6 +58,12 @@ class Context:
         _abi.call("focr_hip_ctx_stream", self.handle, C.byref(s))
         return int(s.value or 0)
 
+    def scratch_bytes(self) -> int:
+        """Bytes the context's grow-only scratch slots hold (a diagnostic)."""
+        n = C.c_size_t()
+        _abi.call("focr_hip_ctx_scratch_bytes", self.handle, C.byref(n))
+        return int(n.value)
+
     def info(self) -> dict:
         arch = C.create_string_buffer(64)
         cus = C.c_int32(0)
@@ -75,6 +81,17 @@ class Context:
         buf = C.create_string_buffer(1 << 16)
         _abi.call("focr_hip_prof_read", self.handle, buf, len(buf))
         return json.loads(buf.value.decode())
+
+    def mark(self) -> None:
+        """Record a step mark (an event) on the context's stream."""
+        _abi.call("focr_hip_mark", self.handle)
+
+    def marks_read(self, cap: int = 1 << 16) -> list[float]:
+        """Synchronise and return the ms between consecutive marks (and drop them)."""
+        out = np.zeros(cap, np.float32)
+        n = C.c_size_t()
+        _abi.call("focr_hip_marks_read", self.handle, out.ctypes.data_as(C.c_void_p), cap, C.byref(n))
+        return [float(v) for v in out[: n.value]]
 
     # -- allocation --
     def empty(self, shape, dtype) -> "DeviceArray":

@@ -228,12 +228,14 @@ class MoeLayer:
 
     def decode_noalloc(self, hidden: DeviceArray, out: DeviceArray, idx: DeviceArray | None = None,
                        gates: DeviceArray | None = None, norm_topk: bool = False, routed_scale: float = 1.0,
-                       with_shared: bool = False, check_route: bool = True) -> None:
+                       with_shared: bool = False, check_route: bool = True, ctx: Context | None = None) -> None:
         """`decode` with every intermediate in the library's static per-GPU
-        scratch: no device allocation (for graph capture and serving loops)."""
+        scratch: no device allocation (for graph capture and serving loops).
+        `ctx` issues it on another context's stream of the same device (the
+        library orders the calls that share the device's scratch)."""
         t = hidden.shape[0]
-        _abi.call("focr_hip_moe_decode_noalloc", self.ctx.handle, self._h, hidden.c_ptr, t, 1 if norm_topk else 0,
-                  float(routed_scale), 1 if with_shared else 0, out.c_ptr, _p(idx), _p(gates),
+        _abi.call("focr_hip_moe_decode_noalloc", (ctx or self.ctx).handle, self._h, hidden.c_ptr, t,
+                  1 if norm_topk else 0, float(routed_scale), 1 if with_shared else 0, out.c_ptr, _p(idx), _p(gates),
                   1 if check_route else 0)
 
     def prefill(self, x: DeviceArray, idx: DeviceArray, gates: DeviceArray, out: DeviceArray,

@@ -85,6 +85,10 @@ int32_t focr_hip_ctx_synchronize(focr_hip_ctx* ctx);
 int32_t focr_hip_device_synchronize(focr_hip_ctx* ctx);
 /* The context's hipStream_t, for callers that order their own work on it. */
 int32_t focr_hip_ctx_stream(focr_hip_ctx* ctx, void** stream);
+/* No counterpart in the reference (a diagnostic): the bytes the context's
+ * grow-only scratch slots hold now; an entry point that allocates nothing
+ * leaves it unchanged. */
+int32_t focr_hip_ctx_scratch_bytes(focr_hip_ctx* ctx, size_t* bytes);
 /* Device name / gcnArchName / CU count of the context's device. */
 int32_t focr_hip_ctx_device_info(focr_hip_ctx* ctx, char* arch, size_t arch_cap,
                                  int32_t* cu_count);
@@ -276,9 +280,14 @@ int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
  * E_SHAPE (at hidden 1280, inter 896, top-6 every t <= 64 fits, with a
  * shared expert up to 1792 wide). Nothing in the array must start at zero;
  * it keeps the last call's contents. Every call on one GPU shares its
- * array, so calls that overlap on one GPU (other contexts or streams) race.
- * check_route = 1 synchronises (not capturable); 0 leaves the device flag
- * unread. */
+ * array, so the calls on one GPU are ordered: each call's stream waits for
+ * the previous call's completion event (one event per GPU, created with the
+ * array's address at context creation) and records its own, so calls from
+ * several contexts or threads run one after another in the order they were
+ * issued. A call issued while its stream is being captured into a graph is
+ * not ordered that way: overlapping captured calls on one GPU race unless
+ * the graphs order them. check_route = 1 synchronises (not capturable); 0
+ * leaves the device flag unread. */
 int32_t focr_hip_moe_decode_noalloc(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
                                     const float* hidden, size_t t, int32_t norm_topk,
                                     float routed_scale, int32_t with_shared, float* out,
@@ -546,11 +555,22 @@ int32_t focr_hip_focrq_writer_write(const focr_hip_focrq_writer* w, const char* 
  * When enabled, every kernel launch carries HIP start/stop events in its
  * dispatch (hipExtLaunchKernelGGL), timing the kernel's own execution;
  * focr_hip_prof_read synchronises and returns, per kernel name, the launch
- * count and total milliseconds as a JSON object. The extra completion
- * signals slow a sequence of launches, so time throughput with it off. */
+ * count, total milliseconds and the minimum, median and 90th percentile of
+ * the launches (nearest rank, as the reference's bench statistics,
+ * benches/support/perf_harness.rs:186-282) as a JSON object. The extra
+ * completion signals slow a sequence of launches, so time throughput with it
+ * off. */
 int32_t focr_hip_prof_enable(focr_hip_ctx* ctx, int32_t on);
 int32_t focr_hip_prof_reset(focr_hip_ctx* ctx);
 int32_t focr_hip_prof_read(focr_hip_ctx* ctx, char* json, size_t cap);
+
+/* Step marks (no reference counterpart; the GPU form of the per-iteration
+ * wall-clock samples of perf_harness.rs:186-263): focr_hip_mark records an
+ * event on the context's stream; focr_hip_marks_read synchronises, writes the
+ * n - 1 intervals between consecutive marks (ms) into ms[0..cap) and forgets
+ * the marks. At most 65536 marks; E_SHAPE when cap is too small. */
+int32_t focr_hip_mark(focr_hip_ctx* ctx);
+int32_t focr_hip_marks_read(focr_hip_ctx* ctx, float* ms, size_t cap, size_t* n_out);
 
 #ifdef __cplusplus
 }

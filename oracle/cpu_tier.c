@@ -20,7 +20,7 @@ int cpu_detect_tier(void) {
     if (__builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw") &&
         __builtin_cpu_supports("avx512f"))
         return CPU_TIER_AVX512VNNI;
-#if defined(__GNUC__) && (__GNUC__ >= 11)
+#if defined(__clang__) || (defined(__GNUC__) && (__GNUC__ >= 11))
     if (__builtin_cpu_supports("avxvnni")) return CPU_TIER_AVXVNNI;
 #endif
     if (__builtin_cpu_supports("avx2")) return CPU_TIER_AVX2;
@@ -34,7 +34,7 @@ int cpu_tier_available(int tier) {
     switch (tier) {
     case CPU_TIER_SCALAR: return 1;
     case CPU_TIER_AVX2: return __builtin_cpu_supports("avx2") != 0;
-#if defined(__GNUC__) && (__GNUC__ >= 11)
+#if defined(__clang__) || (defined(__GNUC__) && (__GNUC__ >= 11))
     case CPU_TIER_AVXVNNI: return __builtin_cpu_supports("avxvnni") != 0;
 #endif
     case CPU_TIER_AVX512VNNI:
@@ -369,4 +369,169 @@ int cpu_moe_decode(int tier, const float* hidden, size_t t, size_t h, size_t int
     }
     free(partial);
     return 0;
+}
+
+/* ---- cfg1 batched: independent products, one task per instance ------------- */
+typedef struct {
+    int tier;
+    const int8_t *a, *b;
+    size_t m, k, n;
+    int32_t* out;
+} batched_job;
+
+static void batched_item(void* p, size_t i) {
+    batched_job* j = (batched_job*)p;
+    cpu_igemm_s8s8(j->tier, j->a + i * j->m * j->k, j->b + i * j->n * j->k, j->m, j->k, j->n,
+                   j->out + i * j->m * j->n);
+}
+
+void cpu_igemm_s8s8_batched(int tier, const int8_t* a, const int8_t* b, size_t batch, size_t m, size_t k, size_t n,
+                            int32_t* out) {
+    batched_job j = {tier, a, b, m, k, n, out};
+    pool_for(batch, batched_item, &j);
+}
+
+/* ---- nn::linear_int8_dynamic (nn.rs:151-173) on the tier -------------------- */
+typedef struct {
+    int tier;
+    const int8_t* xq;
+    const float* xs;
+    size_t m, k, n;
+    const int8_t* w;
+    const float* ws;
+    float* y;
+} linear_job;
+
+static void linear_block(void* p, size_t blk) {
+    linear_job* j = (linear_job*)p;
+    size_t base = blk * GEMV_BLOCK;
+    size_t cnt = j->n - base < GEMV_BLOCK ? j->n - base : GEMV_BLOCK;
+    int32_t* acc = (int32_t*)calloc(j->m * cnt, sizeof(int32_t));
+    cpu_igemm_s8s8(j->tier, j->xq, j->w + base * j->k, j->m, j->k, cnt, acc);
+    for (size_t r = 0; r < j->m; ++r)
+        for (size_t o = 0; o < cnt; ++o) {
+            float v = (float)acc[r * cnt + o] * j->xs[r];
+            j->y[r * j->n + base + o] = v * j->ws[base + o];
+        }
+    free(acc);
+}
+
+void cpu_linear_i8_dynamic(int tier, const float* x, size_t m, size_t k, const int8_t* w, const float* ws, size_t n,
+                           float* y) {
+    int8_t* xq = (int8_t*)malloc(m * k);
+    float* xs = (float*)malloc(m * sizeof(float));
+    for (size_t r = 0; r < m; ++r) xs[r] = oracle_quantize_row_dynamic(x + r * k, k, xq + r * k);
+    linear_job j = {tier, xq, xs, m, k, n, w, ws, y};
+    pool_for((n + GEMV_BLOCK - 1) / GEMV_BLOCK, linear_block, &j);
+    free(xq);
+    free(xs);
+}
+
+/* ---- decode_mlp_i8 with the shared expert (decoder.rs:2199-2268) -------------
+ * Per token: the top-k routed experts and the shared expert as concurrent
+ * serial tasks (decoder.rs:2231-2252); the routed outputs scaled by their
+ * gates and summed in slot order, the shared output added last. */
+typedef struct {
+    moe_job routed;
+    size_t shared_inter;
+    const int8_t *swg, *swu, *swd;
+    const float *ssg, *ssu, *ssd;
+} moe_shared_job;
+
+typedef struct {
+    moe_shared_job* job;
+    size_t top_k;
+} moe_shared_ctx;
+
+/* task j < top_k: routed slot j; task top_k: the shared expert */
+static void moe_shared_task(void* p, size_t j) {
+    moe_shared_ctx* c = (moe_shared_ctx*)p;
+    moe_shared_job* m = c->job;
+    if (j < c->top_k) {
+        moe_slot(&m->routed, j);
+        return;
+    }
+    expert_serial(m->routed.tier, m->routed.x, m->routed.h, m->shared_inter, m->swg, m->ssg, m->swu, m->ssu, m->swd,
+                  m->ssd, m->routed.partial + c->top_k * m->routed.h);
+}
+
+int cpu_moe_decode_shared(int tier, const float* hidden, size_t t, size_t h, size_t inter, size_t n_experts,
+                          size_t top_k, const float* router, const int8_t* wg, const float* sg, const int8_t* wu,
+                          const float* su, const int8_t* wd, const float* sd, int norm_topk, float routed_scale,
+                          const int8_t* swg, const float* ssg, const int8_t* swu, const float* ssu,
+                          const int8_t* swd, const float* ssd, size_t shared_inter, float* out, uint32_t* idx,
+                          float* gates) {
+    int st = oracle_route(hidden, t, h, router, n_experts, top_k, norm_topk, routed_scale, idx, gates, NULL);
+    if (st) return st;
+    float* partial = (float*)malloc((top_k + 1) * h * sizeof(float));
+    for (size_t tok = 0; tok < t; ++tok) {
+        moe_shared_job j = {{tier, hidden + tok * h, h, inter, idx + tok * top_k, gates + tok * top_k, wg, wu, wd,
+                             sg, su, sd, partial},
+                            shared_inter, swg, swu, swd, ssg, ssu, ssd};
+        moe_shared_ctx c = {&j, top_k};
+        pool_for(top_k + (swg ? 1 : 0), moe_shared_task, &c);
+        float* o = out + tok * h;
+        for (size_t col = 0; col < h; ++col) o[col] = 0.0f;
+        for (size_t s = 0; s < top_k; ++s)
+            for (size_t col = 0; col < h; ++col) o[col] += partial[s * h + col];
+        if (swg)
+            for (size_t col = 0; col < h; ++col) o[col] += partial[top_k * h + col];
+    }
+    free(partial);
+    return 0;
+}
+
+/* ---- one decoder layer's batched decode step (decoder.rs:2812-2933) ---------
+ * Per-stream RMSNorm; one M = B qkv GEMV over the pool; per stream RoPE at
+ * its position, ring write and R-SWA decode attention (single thread, streams
+ * one after another, rswa.rs:894-939); one M = B o_proj GEMV; per stream the
+ * residual, post-attention RMSNorm, decode_mlp_i8 (MoE + shared) and the
+ * second residual. x [b][h] is updated in place. */
+int cpu_decoder_layer_step(int tier, float* x, size_t b, const uint32_t* positions, float* const* ref_k,
+                           float* const* ref_v, size_t ref_cap, const uint32_t* prefill_len, float* const* ring_k,
+                           float* const* ring_v, uint32_t* ring_len, uint32_t* ring_pos, const float* input_ln,
+                           const float* post_ln, float eps, float theta, const int8_t* wqkv, const float* sqkv,
+                           const int8_t* wo, const float* so, const float* router, size_t n_experts, size_t top_k,
+                           size_t inter, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
+                           const int8_t* wd, const float* sd, const int8_t* swg, const float* ssg,
+                           const int8_t* swu, const float* ssu, const int8_t* swd, const float* ssd,
+                           size_t shared_inter) {
+    const size_t h = 1280, nh = 10, hd = 128, dim = nh * hd;
+    if (b == 0 || b > 32) return ORACLE_E_SHAPE;
+    float* normed = (float*)malloc(b * h * sizeof(float));
+    float* qkv = (float*)malloc(b * 3 * dim * sizeof(float));
+    float* ctx = (float*)malloc(b * dim * sizeof(float));
+    float* attn = (float*)malloc(b * h * sizeof(float));
+    float* mlp = (float*)malloc(h * sizeof(float));
+    uint32_t idx[64];
+    float gates[64];
+    int st = ORACLE_OK;
+    for (size_t s = 0; s < b; ++s) oracle_rms_norm(x + s * h, h, input_ln, eps, normed + s * h);
+    cpu_gemv_i8(tier, normed, b, wqkv, sqkv, 3 * dim, h, qkv);
+    for (size_t s = 0; s < b && st == ORACLE_OK; ++s) {
+        float* q = qkv + s * 3 * dim;
+        uint32_t slot;
+        st = oracle_rope(q, nh, hd, positions[s], theta);
+        if (st == ORACLE_OK) st = oracle_rope(q + dim, nh, hd, positions[s], theta);
+        if (st == ORACLE_OK)
+            st = oracle_ring_write(ring_k[s], ring_v[s], &ring_len[s], &ring_pos[s], q + dim, q + 2 * dim, &slot);
+        if (st == ORACLE_OK)
+            st = oracle_decode_attention(ref_k[s], ref_v[s], ref_cap, prefill_len[s], ring_k[s], ring_v[s],
+                                         ring_len[s], q, ctx + s * dim);
+    }
+    if (st == ORACLE_OK) cpu_gemv_i8(tier, ctx, b, wo, so, h, dim, attn);
+    for (size_t s = 0; s < b && st == ORACLE_OK; ++s) {
+        float* xs = x + s * h;
+        for (size_t c = 0; c < h; ++c) xs[c] = xs[c] + attn[s * h + c];
+        oracle_rms_norm(xs, h, post_ln, eps, normed + s * h);
+        st = cpu_moe_decode_shared(tier, normed + s * h, 1, h, inter, n_experts, top_k, router, wg, sg, wu, su, wd,
+                                   sd, 0, 1.0f, swg, ssg, swu, ssu, swd, ssd, shared_inter, mlp, idx, gates);
+        for (size_t c = 0; c < h && st == ORACLE_OK; ++c) xs[c] = xs[c] + mlp[c];
+    }
+    free(normed);
+    free(qkv);
+    free(ctx);
+    free(attn);
+    free(mlp);
+    return st;
 }

@@ -53,6 +53,59 @@ int cpu_moe_decode(int tier, const float* hidden, size_t t, size_t h, size_t int
                    const float* sd, int norm_topk, float routed_scale, float* out, uint32_t* idx,
                    float* gates);
 
+/* `batch` independent products (instance i: a + i*m*k, b + i*n*k, out + i*m*n,
+ * out += A.B^T), one task per instance over the pool. */
+void cpu_igemm_s8s8_batched(int tier, const int8_t* a, const int8_t* b, size_t batch, size_t m, size_t k,
+                            size_t n, int32_t* out);
+
+/* nn::linear_int8_dynamic (nn.rs:151-173): the dynamic activation rule per
+ * row, i32 products in 64-output-row blocks over the pool, ((f32)acc * a_s) *
+ * w_s. y [m][n]. */
+void cpu_linear_i8_dynamic(int tier, const float* x, size_t m, size_t k, const int8_t* w, const float* ws,
+                           size_t n, float* y);
+
+/* decode_mlp_i8 with the shared expert (swg NULL: none): the routed experts
+ * and the shared one as concurrent serial tasks per token. */
+int cpu_moe_decode_shared(int tier, const float* hidden, size_t t, size_t h, size_t inter, size_t n_experts,
+                          size_t top_k, const float* router, const int8_t* wg, const float* sg, const int8_t* wu,
+                          const float* su, const int8_t* wd, const float* sd, int norm_topk, float routed_scale,
+                          const int8_t* swg, const float* ssg, const int8_t* swu, const float* ssu,
+                          const int8_t* swd, const float* ssd, size_t shared_inter, float* out, uint32_t* idx,
+                          float* gates);
+
+/* One decoder layer of batched_decode_step_i8_streams (decoder.rs:2812-2933)
+ * for b streams (hidden 1280, 10 heads x 128): x [b][1280] in place; stream
+ * s's ring regions and cursors are advanced by its ring write. */
+int cpu_decoder_layer_step(int tier, float* x, size_t b, const uint32_t* positions, float* const* ref_k,
+                           float* const* ref_v, size_t ref_cap, const uint32_t* prefill_len, float* const* ring_k,
+                           float* const* ring_v, uint32_t* ring_len, uint32_t* ring_pos, const float* input_ln,
+                           const float* post_ln, float eps, float theta, const int8_t* wqkv, const float* sqkv,
+                           const int8_t* wo, const float* so, const float* router, size_t n_experts, size_t top_k,
+                           size_t inter, const int8_t* wg, const float* sg, const int8_t* wu, const float* su,
+                           const int8_t* wd, const float* sd, const int8_t* swg, const float* ssg,
+                           const int8_t* swu, const float* ssu, const int8_t* swd, const float* ssd,
+                           size_t shared_inter);
+
+/* ---- int4 (cpu_int4.c, built -O3 with LLVM for the x86-64 baseline ISA, as
+ * rustc's release profile builds the reference) ----------------------------
+ * The reference's two x86 int4 paths (int4.rs:454-460: no x86 MAC kernel):
+ * kind CPU_I4_PACKED = s4s8_packed_kernel_scalar (int4.rs:304-343),
+ * kind CPU_I4_UNPACK = igemm_s4s8 (int4.rs:245-278: the AVX2 nibble unpack of
+ * int4.rs:560-650 once per call, then igemm_s4s8_unpacked). out [m][n] is
+ * overwritten. */
+enum { CPU_I4_PACKED = 0, CPU_I4_UNPACK = 1 };
+void cpu_igemm_s4s8(int kind, const int8_t* a, const uint8_t* b_packed, const float* scales, size_t group,
+                    size_t m, size_t k, size_t n, float* out);
+/* moe_block over int4 experts with given routing (the structure of
+ * decoder.rs:2142-2181): each routed expert's members gathered in token
+ * order, its gate/up/down products as one m = M_e call each, SwiGLU and the
+ * ties-even act quantize per member, out[t] += w * y in ascending expert
+ * order; one thread. Same arguments as oracle_moe_prefill_i4. */
+int cpu_moe_prefill_i4(int kind, const float* x, size_t t, size_t h, size_t inter, size_t n_experts,
+                       size_t top_k, const uint32_t* idx, const float* gates, size_t group, const uint8_t* wg,
+                       const float* sg, const uint8_t* wu, const float* su, const uint8_t* wd, const float* sd,
+                       float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,16 @@ _SIGS = {
     "cpu_lm_head_i8": ([C.c_int, _P, _SZ, _P, _P, _SZ, _SZ, _P, _P], None),
     "cpu_moe_decode": ([C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_float,
                         _P, _P, _P], C.c_int),
+    "cpu_igemm_s8s8_batched": ([C.c_int, _P, _P, _SZ, _SZ, _SZ, _SZ, _P], None),
+    "cpu_linear_i8_dynamic": ([C.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _P], None),
+    "cpu_moe_decode_shared": ([C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, C.c_int,
+                               C.c_float, _P, _P, _P, _P, _P, _P, _SZ, _P, _P, _P], C.c_int),
+    "cpu_decoder_layer_step": ([C.c_int, _P, _SZ, _P, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P, C.c_float,
+                                C.c_float, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                _P, _P, _SZ], C.c_int),
+    "cpu_igemm_s4s8": ([C.c_int, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P], None),
+    "cpu_moe_prefill_i4": ([C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
+                           C.c_int),
 }
 
 _lib = None

@@ -1,12 +1,12 @@
 """Summaries of rocprofv3 output (the rocpd SQLite database it writes).
 
-    python -m franken_ocr_amd.rocprof_summary kernels DIR [--command "..."]
+    python rocprof_summary.py kernels DIR [--command "..."]
         per-kernel dispatch statistics from a --kernel-trace run (markdown)
-    python -m franken_ocr_amd.rocprof_summary timeline DIR [--command "..."]
+    python rocprof_summary.py timeline DIR [--command "..."]
         idle gaps between consecutive dispatches, by kernel pair (markdown)
-    python -m franken_ocr_amd.rocprof_summary counters DIR
+    python rocprof_summary.py counters DIR
         per-kernel mean of every collected counter from a --pmc run
-    python -m franken_ocr_amd.rocprof_summary traffic --fetch DIR --write DIR
+    python rocprof_summary.py traffic --fetch DIR --write DIR
         --copy-fetch DIR --copy-write DIR --copy-bytes N --kernel NAME --key KEY
         [--json FILE]
         HBM bytes per dispatch of NAME: FETCH_SIZE and WRITE_SIZE (KiB per
