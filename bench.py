@@ -83,7 +83,9 @@ def traffic_for(kernel: str, workload: str):
     return rec.get("bytes_per_dispatch")
 
 
-STAT_STEPS = 100  # the statistics passes run at least this many steps
+STAT_STEPS = 100  # the per-kernel statistics pass runs at least this many steps
+STAT_GROUPS = 100  # step statistics: this many samples ...
+STEPS_PER_MARK = 10  # ... each the mean of this many consecutive steps between two marks
 
 
 def timed(ctx, step, steps: int):
@@ -96,10 +98,12 @@ def timed(ctx, step, steps: int):
        time the kernel's own execution (they agree with rocprofv3's kernel
        trace); their completion signals slow the step as a whole, which is why
        throughput comes from pass 1. Per launch: mean, min, median, p90.
-    3. Step marks (an event recorded on the stream between steps) over
-       max(steps, STAT_STEPS) steps: the GPU-clock time of each step,
-       summarised as min / median / p90 / CoV (the reference's statistics,
-       perf_harness.rs:186-282, nearest-rank percentiles)."""
+    3. Step marks: an event recorded on the stream after every
+       STEPS_PER_MARK steps, STAT_GROUPS + 1 marks. Each sample is the
+       GPU-clock time between two marks over STEPS_PER_MARK (a mark per
+       step would add its own ~2 us to every sample), summarised as min /
+       median / p90 / CoV (the reference's statistics, perf_harness.rs:
+       186-282, nearest-rank percentiles)."""
     ctx.device_synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -116,11 +120,14 @@ def timed(ctx, step, steps: int):
     kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
     ctx.device_synchronize()
     ctx.mark()
-    for i in range(n_stat):
-        step(i)
+    for g in range(STAT_GROUPS):
+        for i in range(STEPS_PER_MARK):
+            step(g * STEPS_PER_MARK + i)
         ctx.mark()
-    step_ms = ctx.marks_read()
-    return el, prof, kernels, sample_stats([v * 1e-3 for v in step_ms], scale=1e6, unit="us")
+    group_ms = ctx.marks_read()
+    st = sample_stats([v * 1e-3 / STEPS_PER_MARK for v in group_ms], scale=1e6, unit="us")
+    st["steps_per_sample"] = STEPS_PER_MARK
+    return el, prof, kernels, st
 
 
 def nearest_rank(sorted_asc, q: float) -> float:

@@ -590,6 +590,7 @@ struct MoeScratch {
     float* shared_as;   // [t]
     float* ybuf;  // [pairs][hidden] weighted expert outputs (grouped down path only)
     void* sel;
+    void* xchg;   // the route's cross-block exchange (moe_route_xchg_bytes)
 };
 
 // Where an entry point's intermediates live: the context's grow-only slots
@@ -612,6 +613,14 @@ struct ScratchSource {
 
 int32_t moe_scratch(ScratchSource& src, const focr_hip_moe_layer* L, size_t t, bool with_shared, MoeScratch* s) {
     const size_t pairs = t * L->top_k;
+    // the route's exchange comes first: in the static array it is then always
+    // at offset 0 (zero from load time, and only the route writes there); a
+    // context slot is zeroed once, when it is allocated
+    const bool fresh = !src.base && !src.counting && src.ctx->scratch[kScrRouteX].cap == 0;
+    s->xchg = src.get(kScrRouteX, moe_route_xchg_bytes());
+    if (!s->xchg) return FOCR_HIP_E_OOM;
+    if (fresh && hipMemsetAsync(s->xchg, 0, moe_route_xchg_bytes(), src.ctx->stream) != hipSuccess)
+        return FOCR_HIP_E_OOM;
     const size_t sel_off = (pairs * 8 + 255) & ~static_cast<size_t>(255);
     char* route = static_cast<char*>(src.get(kScrRoute, sel_off + moe_sel_bytes()));
     s->xq = static_cast<int8_t*>(src.get(kScrXq, t * L->hidden));
@@ -662,7 +671,7 @@ int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     ProfScope ps(ctx, "moe_route");
     FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
-                                  probs, s.flag, sel, norm),
+                                  probs, s.flag, sel, s.xchg, norm),
                  "route launch");
     return FOCR_HIP_OK;
 }
@@ -682,6 +691,7 @@ int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const
     if ((st = launch_route(ctx, L, hidden, t, norm_topk, routed_scale, s, idx ? idx : s.idx, gates ? gates : s.gates,
                            probs, nullptr)))
         return st;
+    FOCR_HIP_TRY(launch_route_epoch_bump(ctx->stream, s.xchg), "route epoch launch");
     return check_route_flags(ctx, s.flag, t);
 }
 
@@ -736,7 +746,10 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
         const MoeSharedGateUp shgu{L->swg, L->swu, L->ssg, L->ssu, s.shared_act, (int)L->shared_inter};
         ProfScope ps(ctx, "moe_gate_up");
         e = launch_moe_gate_up(str, d, s.sel, s.xq, s.xs, L->wg, L->sg, L->wu, L->su, s.act, (int)L->inter, false,
-                               with_shared ? &shgu : nullptr);
+                               with_shared ? &shgu : nullptr, s.xchg);
+        // the gate/up launch advances the route's counter; without it the next
+        // call's route would take this call's records for its own
+        if (e != hipSuccess) launch_route_epoch_bump(str, s.xchg);
     }
     if (e == hipSuccess && with_shared) {
         {

@@ -42,6 +42,7 @@ enum ScratchSlot : int {
     kScrArg,    // argmax partial keys
     kScrLogits, // router logits / probs
     kScrRoute,  // routing indices / gates / permutation tables
+    kScrRouteX, // the route's cross-block exchange (zeroed once, never cleared)
     kScrAct,    // MoE SwiGLU activations [pairs][inter]
     kScrY,      // MoE weighted expert outputs [pairs][hidden]
     kScrShared, // shared-expert output [t][hidden]
@@ -322,9 +323,15 @@ struct MoeRouteNorm {
     float eps;
     float* h_out;
 };
+// The route's exchange buffer (bytes; zeroed once when allocated, then
+// never cleared: calls are told apart by its counter) and the route itself;
+// the gate/up launch given the same buffer advances the counter, and a route
+// launched without a gate/up after it is followed by launch_route_epoch_bump.
+size_t moe_route_xchg_bytes();
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel, const MoeRouteNorm* norm = nullptr);
+                            float* probs, int* flag, void* sel, void* xchg, const MoeRouteNorm* norm = nullptr);
+hipError_t launch_route_epoch_bump(hipStream_t s, void* xchg);
 // The shared expert's gate/up weights, folded into the routed gate/up launch
 // as extra blocks (every token a pair, act rows [t][inter]).
 struct MoeSharedGateUp {
@@ -335,7 +342,8 @@ struct MoeSharedGateUp {
 };
 hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
                               const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, bool shared, const MoeSharedGateUp* with_shared = nullptr);
+                              int inter, bool shared, const MoeSharedGateUp* with_shared = nullptr,
+                              void* route_xchg = nullptr);
 hipError_t launch_moe_down(hipStream_t s, const MoeDims& d, const void* sel, const float* act, const int8_t* wd,
                            const float* sd, float* ybuf, int inter, bool shared);
 // out[t] = slot-order sum of ybuf[t*top_k + j] (+ shared_y[t]); zero for a

@@ -57,23 +57,53 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
     return m ? __ffsll(static_cast<long long>(m)) - 1 : -1;
 }
 
-// ---- route: one block (16 waves) per token ---------------------------------
-constexpr int kRouteThreads = 1024;
+// ---- route: kRouteParts blocks per token, on one XCD -----------------------
+// Pulling the whole 327 KB router through one CU takes ~4.8 us (the per-CU
+// load path, not HBM), so each token's router rows are split over
+// kRouteParts blocks of kRouteThreads threads: part p computes the logits of
+// experts [p*EP, (p+1)*EP), EP = ceil(E / kRouteParts). The parts of a token
+// are placed on one XCD (workgroups go to the 8 XCDs round-robin, block b to
+// XCD b % 8), so they share that XCD's L2. Each part publishes its logits as
+// 8-byte words (f32 logit bits | the call's 32-bit tag << 32), one aligned
+// store each, so a word is either the old one or the new one; part 0 (the
+// leader) polls them with agent-scope loads (sc1: past the CU's L1, which
+// would otherwise serve a stale line on every poll after the first; a
+// workgroup-scope sc0 load did not see half of them) and gets the logit
+// with its tag. No atomic read-modify-writes, no fences. The wait is
+// bounded by the real-time clock: a part whose words have not all appeared
+// after kRouteWaitTicks is computed by the leader itself, so the result
+// never depends on the placement or on the other blocks being resident.
+// Either way each logit is the same f64 dot product in the same lane order
+// (lane l: float4 chunks l + 64 i, then the DPP tree), so the routing is
+// that of one block doing it all.
+//
+// Tags: a call's tag is the low 32 bits of 2 * counter + 1, counter = the
+// exchange buffer's header word, read by every block at its start and
+// advanced by the next kernel of the call (route_epoch_bump / the gate/up
+// kernel), so no word of an earlier call (or of the zeroed buffer) matches.
+// A graph that replays the call replays the bump too.
+//
+// Per-phase timestamps (s_memrealtime, one T = 8 step, from the first
+// block's start): blocks start over 0 - 1.4 us, the parts' dots end by
+// ~2.8 us; publishing before the token row's quantize and without a store
+// acknowledgement wait, and the softmax, rank and renorm in one wave with
+// cross-lane reads, keep the leader's tail short.
+constexpr int kRouteParts = 8;
+constexpr int kRouteThreads = 256;
 constexpr int kRouteWaves = kRouteThreads / 64;
-constexpr int kRouteEPW = 4;  // router rows per wave (16 waves x 4 = kMaxE)
-constexpr int kRouteNC = 5;   // float4 chunks per lane per batch: 64 x 5 x 4 = 1280 floats
+constexpr int kRouteRPW = 2;   // router rows per wave: kRouteWaves x 2 = 8 = E / kRouteParts at E = 64
+constexpr int kRouteNC = 5;    // float4 chunks per lane per batch: 64 x 5 x 4 = 1280 floats
+constexpr int kRouteEPP = kRouteWaves * kRouteRPW;  // experts per part (max)
+constexpr unsigned long long kRouteWaitTicks = 1000;  // s_memrealtime runs at 100 MHz: 10 us
+static_assert(kRouteEPP * kRouteParts >= kMaxE, "the parts cover every expert");
+static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
 
-// Wave w owns router rows e = 4w..4w+3 and lane l the float4 chunks
-// c = l + 64 i of a row. All of a batch's loads — the token row's chunks
-// first, then the four router rows' — are issued before any is used, so the
-// block has its whole 327 KB router request in flight at once (H = 1280 is
-// one batch). Every wave holds the whole token row, so each computes max|x|
-// for quantize_row_i8 itself; there is no barrier before the logits.
-// NORM: the decoder layer's residual + post-attention RMSNorm first
-// (decoder.rs:2596-2600): the token row is h = x + attn (h written to h_out
-// for the layer's final residual) and the routed row is rms_norm(h) * w, as
-// rms_norm_rows_kernel<1> computes it (f32 h, f64 sum of squares, f32
-// rstd); every wave holds the whole row, so each reduces it itself.
+struct RouteXchg {
+    unsigned long long counter;  // advanced once per call, after the route kernel
+    unsigned long long pad[15];
+    unsigned long long word[kMaxT][kRouteParts][kRouteEPP];  // logit bits | tag << 32
+};
+
 struct RouteNorm {
     const float* attn;  // [T][H]
     const float* w;     // [H]
@@ -81,50 +111,107 @@ struct RouteNorm {
     float* h_out;       // [T][H]
 };
 
+__device__ __forceinline__ unsigned long long realtime() { return __builtin_amdgcn_s_memrealtime(); }
+
+// The f64 logits of router rows r[0..kRouteRPW) (clamped in range by the
+// caller) against the routed row, in this wave: lane l owns float4 chunks
+// l + 64 i; every load of a batch is issued before its first use. Returns
+// the wave sums (every lane). amax (optional) gets max|row| over the wave.
 template <bool NORM>
-__global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void moe_route_kernel(
-    const float* __restrict__ x, const float* __restrict__ G, int H, int E, int K, int norm_topk,
-    float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
-    float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag,
-    MoeSel sel, const RouteNorm rn, int spread) {
-    __shared__ float s_logit[kMaxE];
-    __shared__ __align__(16) float s_p[kMaxE];
-    __shared__ int s_sel_e[kMaxK];
-    __shared__ float s_sel_w[kMaxK];
-    __shared__ int s_nvalid;
-    // Token t runs as block t * spread; the blocks between exit at once.
-    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8), so with
-    // spread 8 every token block lands on XCD 0 and the 327 KB router comes
-    // from HBM once into that XCD's L2, not once per XCD.
-    if (blockIdx.x % spread) return;
-    const int t = blockIdx.x / spread;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int H4 = H >> 2;
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H);
-    const float4* gr[kRouteEPW];
+__device__ __forceinline__ void route_dots(const float4* __restrict__ xr, const float4 (&nv)[kRouteNC],
+                                           const float* __restrict__ G, const int (&r)[kRouteRPW], int H4,
+                                           int lane, double (&out)[kRouteRPW], float* amax_out) {
+    const float4* gr[kRouteRPW];
 #pragma unroll
-    for (int k = 0; k < kRouteEPW; ++k) {
-        const int e = wave * kRouteEPW + k;
-        gr[k] = reinterpret_cast<const float4*>(G + static_cast<size_t>(e < E ? e : E - 1) * H);
-    }
-    // Loads are unconditional (address clamped into the row, a chunk past the
-    // row's end zeroed by a bit mask) so they issue as one batch of dwordx4
-    // loads, not as branches around each load.
+    for (int k = 0; k < kRouteRPW; ++k) gr[k] = reinterpret_cast<const float4*>(G + static_cast<size_t>(r[k]) * H4 * 4);
     auto masked = [](float4 v, unsigned m) {
         return make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
                            __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
     };
+    double acc[kRouteRPW];
+#pragma unroll
+    for (int k = 0; k < kRouteRPW; ++k) acc[k] = 0.0;
+    float amax = 0.0f;
+#pragma unroll 1
+    for (int c0 = lane; c0 < H4 + lane; c0 += 64 * kRouteNC) {
+        float4 xv[kRouteNC];
+        float4 gv[kRouteRPW][kRouteNC];
+        unsigned m[kRouteNC];
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const int c = c0 + 64 * i;
+            m[i] = c < H4 ? 0xFFFFFFFFu : 0u;
+            if constexpr (NORM) xv[i] = nv[i];
+            else xv[i] = xr[c < H4 ? c : H4 - 1];
+        }
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i)
+#pragma unroll
+            for (int k = 0; k < kRouteRPW; ++k) {
+                const int c = c0 + 64 * i;
+                gv[k][i] = gr[k][c < H4 ? c : H4 - 1];
+            }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first use
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const float4 xc = masked(xv[i], m[i]);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xc.x), fabsf(xc.y)), fmaxf(fabsf(xc.z), fabsf(xc.w))));
+            const double x0 = xc.x, x1 = xc.y, x2 = xc.z, x3 = xc.w;
+#pragma unroll
+            for (int k = 0; k < kRouteRPW; ++k) {
+                const float4 g = gv[k][i];
+                acc[k] = fma(x0, static_cast<double>(g.x), acc[k]);
+                acc[k] = fma(x1, static_cast<double>(g.y), acc[k]);
+                acc[k] = fma(x2, static_cast<double>(g.z), acc[k]);
+                acc[k] = fma(x3, static_cast<double>(g.w), acc[k]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRouteRPW; ++k) out[k] = wave_sum_d_full(acc[k]);
+    if (amax_out) *amax_out = wave_max_f_full(amax);
+}
 
-    // NORM: the residual row and the norm factor, from a per-wave copy of the
-    // whole row (NORM requires H <= 64 * 4 * kRouteNC: one batch below)
+// Grid: 8 * S blocks, S = ceil(T / 8) * kRouteParts. Block b sits on XCD
+// x = b % 8; its slot s = b / 8 is part s % kRouteParts of token
+// (s / kRouteParts) * 8 + x (blocks of tokens >= T exit at once). Part 0 of
+// a token is its leader: it gathers the logits and writes the token's
+// routing; part 1 (part 0 when kRouteParts == 1) quantizes the token row
+// after publishing; token 0's other parts zero the selection entries no
+// token owns.
+// NORM: the decoder layer's residual + post-attention RMSNorm first
+// (decoder.rs:2596-2600): the routed row is rms_norm(x + attn) * w, as
+// rms_norm_rows_kernel<1> computes it (f32 h, f64 sum of squares, f32
+// rstd); every wave holds the whole row and reduces it itself; the quantizer
+// part writes h = x + attn to h_out for the layer's final residual.
+template <bool NORM>
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+    const float* __restrict__ x, const float* __restrict__ G, int T, int H, int E, int K, int norm_topk,
+    float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
+    float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag, MoeSel sel,
+    const RouteNorm rn, RouteXchg* __restrict__ xch) {
+    __shared__ float s_logit[kMaxE];
+    __shared__ unsigned s_missing;  // leader: parts it computes itself (bit p)
+    const int xcd = blockIdx.x & 7;
+    const int slot = blockIdx.x >> 3;
+    const int part = slot % kRouteParts;
+    const int t = (slot / kRouteParts) * 8 + xcd;
+    if (t >= T) return;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int H4 = H >> 2;
+    const int EP = (E + kRouteParts - 1) / kRouteParts;
+    const unsigned tag = static_cast<unsigned>(
+        2ull * __hip_atomic_load(&xch->counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull);
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H);
+
+    // NORM: the routed row's chunks (one batch: NORM requires H <= 64 * 4 * kRouteNC)
     const float4* ar = NORM ? reinterpret_cast<const float4*>(rn.attn + static_cast<size_t>(t) * H) : nullptr;
-    const float4* wr = NORM ? reinterpret_cast<const float4*>(rn.w) : nullptr;
+    float4 nv[kRouteNC];
     float rstd = 1.0f;
-    float4 nv[kRouteNC];  // NORM: this lane's chunks of the normed row (the batch below is one pass)
     if constexpr (NORM) {
+        const float4* wr = reinterpret_cast<const float4*>(rn.w);
         float4 hv[kRouteNC], gw[kRouteNC];
-        // the norm weights load with the two rows (one round trip, not two)
 #pragma unroll
         for (int i = 0; i < kRouteNC; ++i) {
             const int c = lane + 64 * i;
@@ -151,165 +238,215 @@ __global__ __launch_bounds__(kRouteThreads) __attribute__((amdgpu_waves_per_eu(1
                                 (hv[i].w * rstd) * g.w);
         }
     }
-    // chunk c of the routed row: x itself, or (NORM) ((x + attn) * rstd) * w
-    auto row_chunk4 = [&](int c) {
-        const float4 a = xr[c];
-        if constexpr (!NORM) return a;
-        const float4 b = ar[c], g = wr[c];
-        return make_float4(((a.x + b.x) * rstd) * g.x, ((a.y + b.y) * rstd) * g.y, ((a.z + b.z) * rstd) * g.z,
-                           ((a.w + b.w) * rstd) * g.w);
-    };
 
-    // 1. logits as f64 dot products (rounded to f32 below) and max|x|
-    double acc[kRouteEPW];
-#pragma unroll
-    for (int k = 0; k < kRouteEPW; ++k) acc[k] = 0.0;
+    // 1. this part's logits: wave w owns rows e0 + kRouteRPW w + k
+    const bool quantizer = part == (kRouteParts > 1 ? 1 : 0);
+    const int e0 = part * EP;
     float amax = 0.0f;
-#pragma unroll 1
-    for (int c0 = lane; c0 < H4 + lane; c0 += 64 * kRouteNC) {
-        float4 xv[kRouteNC];
-        float4 gv[kRouteEPW][kRouteNC];
-        unsigned m[kRouteNC];
-#pragma unroll
-        for (int i = 0; i < kRouteNC; ++i) {
-            const int c = c0 + 64 * i;
-            m[i] = c < H4 ? 0xFFFFFFFFu : 0u;
-            if constexpr (NORM) xv[i] = nv[i];
-            else xv[i] = xr[c < H4 ? c : H4 - 1];
-        }
-        // chunk-major: the dot products below take chunk i of all four rows
-        // at once, so they can start as soon as the first chunks arrive
-#pragma unroll
-        for (int i = 0; i < kRouteNC; ++i)
-#pragma unroll
-            for (int k = 0; k < kRouteEPW; ++k) {
-                const int c = c0 + 64 * i;
-                gv[k][i] = gr[k][c < H4 ? c : H4 - 1];
-            }
-        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first use
-#pragma unroll
-        for (int i = 0; i < kRouteNC; ++i) {
-            const float4 xc = masked(xv[i], m[i]);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xc.x), fabsf(xc.y)), fmaxf(fabsf(xc.z), fabsf(xc.w))));
-            const double x0 = xc.x, x1 = xc.y, x2 = xc.z, x3 = xc.w;
-#pragma unroll
-            for (int k = 0; k < kRouteEPW; ++k) {
-                const float4 g = gv[k][i];
-                acc[k] = fma(x0, static_cast<double>(g.x), acc[k]);
-                acc[k] = fma(x1, static_cast<double>(g.y), acc[k]);
-                acc[k] = fma(x2, static_cast<double>(g.z), acc[k]);
-                acc[k] = fma(x3, static_cast<double>(g.w), acc[k]);
-            }
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < kRouteEPW; ++k) acc[k] = wave_sum_d_full(acc[k]);
-    if (lane < kRouteEPW) {
-        const int e = wave * kRouteEPW + lane;
-        const double a = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
-        if (e < E) s_logit[e] = static_cast<float>(a);
-    }
-
-    // 2. quantize_row_i8 of the token row (thread c owns chunk c; its wave
-    //    holds max|x| of the whole row)
-    amax = wave_max_f_full(amax);
-    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (threadIdx.x < H4) {
-        const float inv = 1.0f / a_scale;
-        const float4 xv = row_chunk4(threadIdx.x);
-        if constexpr (NORM) {
-            // h = x + attn for the residual, stored here rather than before
-            // the router loads: a store ahead of them makes their wait cover it
-            const float4 a = xr[threadIdx.x], b = ar[threadIdx.x];
-            reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[threadIdx.x] =
-                make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-        }
-        char4 q;
-        q.x = quant_i8(xv.x, inv, false);
-        q.y = quant_i8(xv.y, inv, false);
-        q.z = quant_i8(xv.z, inv, false);
-        q.w = quant_i8(xv.w, inv, false);
-        reinterpret_cast<char4*>(xq + static_cast<size_t>(t) * H)[threadIdx.x] = q;
-    }
-    if (threadIdx.x == 0) xs[t] = a_scale;
-    __syncthreads();
-
-    // 4. softmax in f64 over the f32 logits (wave 0, lane = expert): max,
-    //    exp, DPP-tree sum (the oracle's wave_tree_sum64 order), divide, round
-    //    to f32
-    if (wave == 0) {
-        const bool valid = lane < E;
-        const float lg = valid ? s_logit[lane] : -INFINITY;
-        const double mx = static_cast<double>(wave_max_f_full(lg));
-        double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
-        double sum = ex;
-        sum = wave_sum_d_full(sum);
-        const float p = static_cast<float>(ex / sum);
-        if (valid) {
-            s_p[lane] = p;
-            if (probs_out) probs_out[static_cast<size_t>(t) * E + lane] = p;
-        } else {
-            s_p[lane] = __int_as_float(0x7fc00000);  // NaN: never ranked
-        }
-        const unsigned long long fin = __ballot(valid && p == p);
-        if (lane == 0) s_nvalid = __popcll(fin);
-    }
-    __syncthreads();
-
-    // 5. greedy top-k == rank by (prob desc, index asc) among non-NaN probs:
-    //    thread (e, l) counts the experts 4l..4l+3 ahead of e, 16 lanes sum
     {
-        const int e = threadIdx.x >> 4;
-        const int l = threadIdx.x & 15;
-        const bool erow = e < E;
-        const float pe = s_p[e];
-        const float4 q = reinterpret_cast<const float4*>(s_p)[l];
-        const int j0 = 4 * l;
-        int ahead = 0;
-        ahead += (q.x > pe || (q.x == pe && j0 + 0 < e)) ? 1 : 0;
-        ahead += (q.y > pe || (q.y == pe && j0 + 1 < e)) ? 1 : 0;
-        ahead += (q.z > pe || (q.z == pe && j0 + 2 < e)) ? 1 : 0;
-        ahead += (q.w > pe || (q.w == pe && j0 + 3 < e)) ? 1 : 0;
-        ahead = reduce16_add(ahead);
-        const bool chosen = erow && pe == pe && ahead < K;
-        if (l == 0 && chosen) {
-            s_sel_e[ahead] = e;
-            s_sel_w[ahead] = pe;
+        int r[kRouteRPW];
+#pragma unroll
+        for (int k = 0; k < kRouteRPW; ++k) {
+            const int e = e0 + wave * kRouteRPW + k;
+            r[k] = e < E ? e : E - 1;
         }
-        if (sel.slot && l == 0 && erow)
-            sel.slot[e * kMaxT + t] = static_cast<uint8_t>(chosen && s_nvalid >= K ? ahead + 1 : 0);
+        double d[kRouteRPW];
+        route_dots<NORM>(xr, nv, G, r, H4, lane, d, quantizer && wave == 0 ? &amax : nullptr);
+        if (lane < kRouteRPW) {
+            const int el = wave * kRouteRPW + lane;
+            const double v = lane == 0 ? d[0] : d[1];
+            if (el < EP && e0 + el < E) s_logit[e0 + el] = static_cast<float>(v);
+        }
     }
     __syncthreads();
 
-    // 6. renormalise (sequential f32 sum in slot order), scale, publish
-    if (threadIdx.x < K) {
-        const int j = threadIdx.x;
-        const bool bad = s_nvalid < K;
-        float den = 0.0f;
-        for (int jj = 0; jj < K; ++jj) den += bad ? 0.0f : s_sel_w[jj];
-        den += 1e-20f;
-        const int ej = bad ? 0 : s_sel_e[j];
-        float w = bad ? 0.0f : s_sel_w[j];
-        if (norm_topk) w = w / den;
-        idx_out[t * K + j] = static_cast<uint32_t>(ej);
-        gates_out[t * K + j] = w * routed_scale;
-        if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
-        if (j == 0) flag[t] = bad ? 1 : 0;
+    if (part != 0) {
+        // 2. publish: one 8-byte word per logit (the logit's bits and the tag)
+        if (wave == 0 && lane < EP) {
+            const float lg = e0 + lane < E ? s_logit[e0 + lane] : 0.0f;
+            xch->word[t][part][lane] = static_cast<unsigned long long>(__float_as_uint(lg)) |
+                                       (static_cast<unsigned long long>(tag) << 32);
+        }
+        // 3. quantize_row_i8 of the token row (wave 0 of the quantizer part
+        //    holds the whole row's max|x|), after publishing
+        if (quantizer && wave == 0) {
+            const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / a_scale;
+#pragma unroll 1
+            for (int c = lane; c < H4; c += 64) {
+                float4 v;
+                if constexpr (NORM) {
+                    const float4 a = xr[c], b = ar[c], g = reinterpret_cast<const float4*>(rn.w)[c];
+                    const float4 h = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                    reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[c] = h;
+                    v = make_float4((h.x * rstd) * g.x, (h.y * rstd) * g.y, (h.z * rstd) * g.z, (h.w * rstd) * g.w);
+                } else {
+                    v = xr[c];
+                }
+                char4 q;
+                q.x = quant_i8(v.x, inv, false);
+                q.y = quant_i8(v.y, inv, false);
+                q.z = quant_i8(v.z, inv, false);
+                q.w = quant_i8(v.w, inv, false);
+                reinterpret_cast<char4*>(xq + static_cast<size_t>(t) * H)[c] = q;
+            }
+            if (lane == 0) xs[t] = a_scale;
+        }
+        // 4. token 0's non-leader parts zero the selection entries no token
+        //    owns (e >= E or t >= T), one 4-byte word (an expert row, tokens
+        //    t0..t0+3) at a time, byte by byte where a token owns part of it
+        if (sel.slot && t == 0) {
+            const int workers = kRouteParts - 1;
+#pragma unroll 1
+            for (int wi = (part - 1) * kRouteThreads + static_cast<int>(threadIdx.x); wi < kMaxE * kMaxT / 4;
+                 wi += workers * kRouteThreads) {
+                const int ei = wi / (kMaxT / 4), t0 = 4 * (wi % (kMaxT / 4));
+                uint8_t* w = sel.slot + 4 * wi;
+                if (ei >= E || t0 >= T) {
+                    *reinterpret_cast<uint32_t*>(w) = 0u;
+                } else {
+                    for (int ti = T; ti < t0 + 4; ++ti) w[ti - t0] = 0;
+                }
+            }
+        }
+        return;
     }
-    // block 0 zeroes the slot entries no token block owns (e >= E or t >= T):
-    // thread i owns bytes 4i..4i+3 (one expert row, tokens t0..t0+3) and
-    // writes them as one word unless a token block owns some of them
-    static_assert(kMaxE * kMaxT == 4 * kRouteThreads, "one slot word per thread");
-    if (sel.slot && t == 0) {
-        const int T = static_cast<int>(gridDim.x) / spread;
-        const int ei = threadIdx.x / (kMaxT / 4), t0 = 4 * (threadIdx.x % (kMaxT / 4));
-        uint8_t* w = sel.slot + 4 * threadIdx.x;
-        if (ei >= E || t0 >= T) {
-            *reinterpret_cast<uint32_t*>(w) = 0u;
-        } else {
-            for (int ti = T; ti < t0 + 4; ++ti) w[ti - t0] = 0;
+
+    // 5. leader: the other parts' logits (bounded wait); lane e >= EP polls
+    //    the word of expert e
+    const int nparts = (E + EP - 1) / EP;
+    if (wave == 0) {
+        const int pe = lane / EP, ie = lane % EP;
+        const bool watch = lane >= EP && lane < E;
+        bool ready = !watch;
+        float got = 0.0f;
+        const unsigned long long t_end = realtime() + kRouteWaitTicks;
+        while (true) {
+            if (!ready) {
+                const unsigned long long w =
+                    __hip_atomic_load(&xch->word[t][pe][ie], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (static_cast<unsigned>(w >> 32) == tag) {
+                    ready = true;
+                    got = __uint_as_float(static_cast<unsigned>(w));
+                }
+            }
+            if (__ballot(!ready) == 0ull || realtime() > t_end) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (watch && ready) s_logit[lane] = got;
+        // a part is computed here if any of its words is missing
+        unsigned long long miss_lanes = __ballot(watch && !ready);
+        unsigned miss = 0;
+        for (int pm = 1; pm < nparts; ++pm)
+            if ((miss_lanes >> (pm * EP)) & ((1ull << EP) - 1ull)) miss |= 1u << pm;
+        if (lane == 0) s_missing = miss;
+    }
+    if (!(kRouteParts > 1)) {
+        // one part: the leader is the quantizer (its wave 0 holds max|x|)
+        if (wave == 0) {
+            const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / a_scale;
+#pragma unroll 1
+            for (int c = lane; c < H4; c += 64) {
+                float4 v;
+                if constexpr (NORM) {
+                    const float4 a = xr[c], b = ar[c], g = reinterpret_cast<const float4*>(rn.w)[c];
+                    const float4 h = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                    reinterpret_cast<float4*>(rn.h_out + static_cast<size_t>(t) * H)[c] = h;
+                    v = make_float4((h.x * rstd) * g.x, (h.y * rstd) * g.y, (h.z * rstd) * g.z, (h.w * rstd) * g.w);
+                } else {
+                    v = xr[c];
+                }
+                char4 q;
+                q.x = quant_i8(v.x, inv, false);
+                q.y = quant_i8(v.y, inv, false);
+                q.z = quant_i8(v.z, inv, false);
+                q.w = quant_i8(v.w, inv, false);
+                reinterpret_cast<char4*>(xq + static_cast<size_t>(t) * H)[c] = q;
+            }
+            if (lane == 0) xs[t] = a_scale;
         }
     }
+    __syncthreads();
+    // a part that never published: its rows, computed here (same lanes, same order)
+    for (unsigned miss = s_missing; miss; miss &= miss - 1u) {
+        const int pm = __ffs(static_cast<int>(miss)) - 1;
+        int r[kRouteRPW];
+#pragma unroll
+        for (int k = 0; k < kRouteRPW; ++k) {
+            const int e = pm * EP + wave * kRouteRPW + k;
+            r[k] = e < E ? e : E - 1;
+        }
+        double d[kRouteRPW];
+        route_dots<NORM>(xr, nv, G, r, H4, lane, d, nullptr);
+        if (lane < kRouteRPW) {
+            const int el = wave * kRouteRPW + lane;
+            const double v = lane == 0 ? d[0] : d[1];
+            if (el < EP && pm * EP + el < E) s_logit[pm * EP + el] = static_cast<float>(v);
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+
+    // 6. softmax in f64 over the f32 logits (lane = expert): max, exp,
+    //    DPP-tree sum (the oracle's wave_tree_sum64 order), divide, round to
+    //    f32; a lane past E is NaN and never ranked
+    const bool valid = lane < E;
+    const float lg = valid ? s_logit[lane] : -INFINITY;
+    const double mx = static_cast<double>(wave_max_f_full(lg));
+    const double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
+    const double sum = wave_sum_d_full(ex);
+    const float pr = valid ? static_cast<float>(ex / sum) : __int_as_float(0x7fc00000);
+    if (valid && probs_out) probs_out[static_cast<size_t>(t) * E + lane] = pr;
+    const int nvalid = __popcll(__ballot(pr == pr));
+
+    // 7. greedy top-k (moe.rs:209-266): K times the largest remaining
+    //    probability, the lowest index among equal ones, NaN never; slot j is
+    //    the j-th pick. A probability is finite and >= +0 (ex >= 0, sum > 0),
+    //    so -inf marks a lane out of the running (NaN, past E, or picked).
+    //    Fewer than K finite probabilities: the token's routing failed
+    //    (flag), every output of it zero.
+    float pk = valid && pr == pr ? pr : -INFINITY;
+    int my_slot = -1;
+    int ej_mine = 0;
+    float wj_mine = 0.0f;
+    float den = 0.0f;
+    const bool bad = nvalid < K;
+    for (int j = 0; j < K; ++j) {
+        const float mv = wave_max_f_full(pk);
+        const unsigned long long mm = __ballot(pk == mv && mv != -INFINITY);
+        const int lj = mm ? __ffsll(static_cast<long long>(mm)) - 1 : 0;
+        const float wj = mm ? mv : 0.0f;
+        den += bad ? 0.0f : wj;  // sequential f32 sum in slot order
+        if (mm && lane == lj) {
+            pk = -INFINITY;
+            my_slot = j;
+        }
+        if (lane == j) {
+            ej_mine = lj;
+            wj_mine = wj;
+        }
+    }
+    const bool chosen = my_slot >= 0;
+
+    // 8. renormalise (the slot-order sum above + 1e-20), scale, publish
+    den += 1e-20f;
+    if (lane < K) {
+        const int ej = bad ? 0 : ej_mine;
+        float w = bad ? 0.0f : wj_mine;
+        if (norm_topk) w = w / den;
+        idx_out[t * K + lane] = static_cast<uint32_t>(ej);
+        gates_out[t * K + lane] = w * routed_scale;
+        if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
+        if (lane == 0) flag[t] = bad ? 1 : 0;
+    }
+    if (sel.slot && valid) sel.slot[lane * kMaxT + t] = static_cast<uint8_t>(chosen && !bad ? my_slot + 1 : 0);
+}
+
+// Advances the route exchange's counter once the route kernel of a call has
+// finished (stream order): the next call's records carry a new tag.
+__global__ void route_epoch_bump_kernel(RouteXchg* __restrict__ xch) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) xch->counter = xch->counter + 1ull;
 }
 
 // Expert of this block: lane e loads expert e's 64-byte slot row (four
@@ -447,6 +584,9 @@ struct SharedGU {
     const float *sg, *su;
     float* act;  // [T][I]
     int I, nslots;
+    // non-null: block (0, 0) advances the route exchange's counter (the
+    // call's route kernel has finished, by stream order)
+    unsigned long long* route_counter;
 };
 
 template <int LPR, int JC, bool ALLTOK>
@@ -461,6 +601,8 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(
     __shared__ float s_xs[64];  // one per lane of the staging wave
     __shared__ int s_np;
     constexpr int G = 256 / LPR;  // rows per block
+    if (sh.route_counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+        *sh.route_counter = *sh.route_counter + 1ull;
     const bool shb = static_cast<int>(blockIdx.y) < sh.nslots;  // block-uniform
     if (shb) {
         shared_T = T;
@@ -864,31 +1006,39 @@ bool dims_ok(const MoeDims& d) {
 
 size_t moe_sel_bytes() { return kMaxE * kMaxT + kMaxE * kMaxT * 4; }
 
+size_t moe_route_xchg_bytes() { return sizeof(RouteXchg); }
+
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel, const MoeRouteNorm* norm) {
-    if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048) return hipErrorInvalidValue;
-    // token blocks on as few XCDs as hold them (32 CUs each): one router fetch per XCD used
-    const int spread = d.t <= 32 ? 8 : 4;
-    const dim3 grid(static_cast<unsigned>(d.t * spread));
+                            float* probs, int* flag, void* sel, void* xchg, const MoeRouteNorm* norm) {
+    if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048 || !xchg) return hipErrorInvalidValue;
+    static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
+    // token t on XCD t % 8, its kRouteParts blocks at slots (t / 8) * kRouteParts + p
+    const dim3 grid(static_cast<unsigned>(8 * ((d.t + 7) / 8) * kRouteParts));
+    RouteXchg* x = static_cast<RouteXchg*>(xchg);
     if (norm) {
         // one batch of kRouteNC float4 per lane holds the whole row
         if (d.hidden > 64 * 4 * kRouteNC || !norm->attn || !norm->w || !norm->h_out) return hipErrorInvalidValue;
         const RouteNorm rn{norm->attn, norm->w, norm->eps, norm->h_out};
-        FOCR_LAUNCH(moe_route_kernel<true>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
-                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn,
-                    spread);
+        FOCR_LAUNCH(moe_route_kernel<true>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.t, d.hidden,
+                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn, x);
     } else {
-        FOCR_LAUNCH(moe_route_kernel<false>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.hidden,
+        FOCR_LAUNCH(moe_route_kernel<false>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.t, d.hidden,
                     d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel),
-                    RouteNorm{}, spread);
+                    RouteNorm{}, x);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_route_epoch_bump(hipStream_t s, void* xchg) {
+    if (!xchg) return hipErrorInvalidValue;
+    FOCR_LAUNCH(route_epoch_bump_kernel, dim3(1), dim3(64), 0, s, static_cast<RouteXchg*>(xchg));
     return hipGetLastError();
 }
 
 hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, const int8_t* xq, const float* xs,
                               const int8_t* wg, const float* sg, const int8_t* wu, const float* su, float* act,
-                              int inter, bool shared, const MoeSharedGateUp* with_shared) {
+                              int inter, bool shared, const MoeSharedGateUp* with_shared, void* route_xchg) {
     int lpr, jc;
     pick_lpr(d.hidden, &lpr, &jc);
     if (!dims_ok(d) || !sel || d.hidden % 16 != 0 || jc > 8) return hipErrorInvalidValue;
@@ -899,8 +1049,9 @@ hipError_t launch_moe_gate_up(hipStream_t s, const MoeDims& d, const void* sel, 
     if (with_shared && !shared) {
         const int per = gx * rows_per_block;
         sh = SharedGU{with_shared->wg, with_shared->wu, with_shared->sg, with_shared->su, with_shared->act,
-                      with_shared->inter, (with_shared->inter + per - 1) / per};
+                      with_shared->inter, (with_shared->inter + per - 1) / per, nullptr};
     }
+    sh.route_counter = route_xchg ? &static_cast<RouteXchg*>(route_xchg)->counter : nullptr;
     const dim3 grid(gx, max_active + sh.nslots);
     const int staged = d.t <= kAllTok ? d.t : kPairStage;
     const size_t lds = (static_cast<size_t>(staged) * d.hidden + 1023) & ~static_cast<size_t>(1023);
