@@ -131,6 +131,7 @@ _SIGS: dict[str, list] = {
     "focr_hip_focrq_writer_build": [_P, _P, _SZ, _P],
     "focr_hip_focrq_writer_write": [_P, C.c_char_p],
     "focr_hip_ctx_scratch_bytes": [_P, _P],
+    "focr_hip_ctx_set_route_wait": [_P, C.c_uint32],
     "focr_hip_prof_enable": [_P, _I32],
     "focr_hip_prof_reset": [_P],
     "focr_hip_prof_read": [_P, C.c_char_p, _SZ],

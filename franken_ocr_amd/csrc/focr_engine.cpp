@@ -671,7 +671,7 @@ int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float
     const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
     ProfScope ps(ctx, "moe_route");
     FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, hidden, L->router, norm_topk, routed_scale, s.xq, s.xs, idx, gates,
-                                  probs, s.flag, sel, s.xchg, norm),
+                                  probs, s.flag, sel, s.xchg, ctx->route_wait_ticks, norm),
                  "route launch");
     return FOCR_HIP_OK;
 }

@@ -198,6 +198,13 @@ int32_t focr_hip_ctx_destroy(focr_hip_ctx* ctx) {
     return FOCR_HIP_OK;
 }
 
+int32_t focr_hip_ctx_set_route_wait(focr_hip_ctx* ctx, uint32_t ticks) {
+    if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->route_wait_ticks = ticks;
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_ctx_scratch_bytes(focr_hip_ctx* ctx, size_t* bytes) {
     if (!ctx) return fail(FOCR_HIP_E_BAD_HANDLE, "null focr_hip_ctx");
     if (!bytes) return fail(FOCR_HIP_E_ARG, "focr_hip_ctx_scratch_bytes: null out");

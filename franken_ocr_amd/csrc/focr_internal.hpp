@@ -59,6 +59,7 @@ enum ScratchSlot : int {
 // ---- static scratch of the allocation-free entry points ------------------
 // One array of this many bytes per GPU, held until the process ends.
 constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+constexpr unsigned kRouteWaitTicksDefault = 1000;  // 10 us
 // profiling: intervals kept per scope name, and step marks per context
 constexpr size_t kProfMaxSamples = 1 << 20;
 constexpr size_t kMaxMarks = 1 << 16;
@@ -107,6 +108,8 @@ struct focr_hip_ctx {
     // the error that kept it from resolving
     void* static_scratch = nullptr;
     hipError_t static_scratch_err = hipSuccess;
+    // bound of the MoE route's cross-block wait (s_memrealtime ticks, 10 ns)
+    unsigned route_wait_ticks = focr::kRouteWaitTicksDefault;
     // profiling: per scope name, every drained interval in ms
     bool prof = false;
     std::vector<focr::ProfPending> pending;
@@ -330,7 +333,8 @@ struct MoeRouteNorm {
 size_t moe_route_xchg_bytes();
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel, void* xchg, const MoeRouteNorm* norm = nullptr);
+                            float* probs, int* flag, void* sel, void* xchg, unsigned wait_ticks,
+                            const MoeRouteNorm* norm = nullptr);
 hipError_t launch_route_epoch_bump(hipStream_t s, void* xchg);
 // The shared expert's gate/up weights, folded into the routed gate/up launch
 // as extra blocks (every token a pair, act rows [t][inter]).

@@ -282,6 +282,15 @@ __device__ __forceinline__ void fq_rows2_to_lds(const float4 (&v0)[NF], const fl
     s1 = a_scale1;
 }
 
+// The igemm form (simd::igemm_s8s8 on device buffers): y and the scales
+// unused, acc_out += the i32 sums (wrapping, as the reference's i32 adds);
+// grid row y advances W, xq and acc_out by sw, sx, so elements (a batch of
+// independent products in one launch).
+struct IgemmMode {
+    int accumulate;
+    size_t sw, sx, so;
+};
+
 // FQ: the <= 16 activation rows come as f32 (xf [M][K], K % 64 == 0,
 // K <= 1280) and every block quantizes them (quantize_row_i8, two rows per
 // wave in lockstep, while the first weight chunks are in flight) — the same
@@ -291,9 +300,15 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ ws, int N, int K,
     const int8_t* __restrict__ xq, const float* __restrict__ a_scales, int M,
     float* __restrict__ y, int32_t* __restrict__ acc_out, uint64_t* __restrict__ keys,
-    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words, const float* __restrict__ xf) {
+    int tiles_per_block, const uint32_t* __restrict__ ban_bits, int ban_words, const float* __restrict__ xf,
+    const IgemmMode im) {
     extern __shared__ int4 lds_dyn[];  // x [16][K/16 + 1] then per-wave [16][16] chunks
     __shared__ uint64_t lds_keys[kThreads / 64][16];
+    if (gridDim.y > 1) {  // the igemm form's batch: instance blockIdx.y
+        W += blockIdx.y * im.sw;
+        xq += blockIdx.y * im.sx;
+        acc_out += blockIdx.y * im.so;
+    }
     __shared__ float lds_as[16];
     const int C = K >> 4;
     const int xs = C + 1;  // x row stride in 16-byte chunks (one chunk of padding)
@@ -398,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
                 lds_xv[r * xs + (c < C ? c : C)] = v[j];
             }
         }
-        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M ? a_scales[threadIdx.x] : 0.0f;
+        if (threadIdx.x < 16) lds_as[threadIdx.x] = threadIdx.x < M && a_scales ? a_scales[threadIdx.x] : 0.0f;
     }
     __syncthreads();
     if (nq > 0) store(rg0);
@@ -426,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
         if (kc == nch - 1) {
             const int n = (tile0 + wave + (kThreads / 64) * (q / nch)) * 16 + col;
             const bool valid = n < N;
-            const float wscale = valid ? ws[n] : 0.0f;
+            const float wscale = valid && ws ? ws[n] : 0.0f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int i = 4 * g + v;
@@ -436,8 +451,12 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_kernel(
                     float yv = t0 * wscale;
                     if (BAN && ((ban_bits[static_cast<size_t>(i) * ban_words + (n >> 5)] >> (n & 31)) & 1u))
                         yv = -__builtin_inff();
-                    y[static_cast<size_t>(i) * N + n] = yv;
-                    if (acc_out) acc_out[static_cast<size_t>(i) * N + n] = av;
+                    if (y) y[static_cast<size_t>(i) * N + n] = yv;
+                    if (acc_out) {
+                        int32_t* o = acc_out + static_cast<size_t>(i) * N + n;
+                        *o = im.accumulate ? static_cast<int32_t>(static_cast<uint32_t>(*o) + static_cast<uint32_t>(av))
+                                           : av;
+                    }
                     if (keys) {
                         const uint64_t k = argmax_key(yv, static_cast<uint32_t>(n));
                         best[v] = k > best[v] ? k : best[v];
@@ -500,14 +519,6 @@ constexpr int kFqMaxK = 2048;  // f32-input form: a row's float4s held by one wa
 // rotates each (i, i + half) pair — lanes col and col ^ 1 hold the two halves
 // of the same rows — with the RoPE kernel's expressions, and writes q to its
 // row and k / v to the streams' ring slots instead of y.
-// The igemm form (simd::igemm_s8s8 on device buffers): y and the scales
-// unused, acc_out += the i32 sums (wrapping, as the reference's i32 adds);
-// grid row y advances W, xq and acc_out by sw, sx, so elements (a batch of
-// independent products in one launch).
-struct IgemmMode {
-    int accumulate;
-    size_t sw, sx, so;
-};
 // ADD (with FQ): the activation row is xf + xf2 (add_residual, decoder.rs:
 // 529-546, ahead of the post-attention norm); block 0 writes that sum to
 // h_out for the layer's final residual. resid (no ROPE): the epilogue returns
@@ -1063,7 +1074,7 @@ hipError_t launch_gemv_i8_f32_keys(hipStream_t s, const int8_t* w, const float* 
     const int grid = (tiles + tpb - 1) / tpb;
     if (nparts_out) *nparts_out = grid;
     FOCR_LAUNCH((gemv_i8_mfma_kernel<false, true>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k, nullptr,
-                nullptr, m, y, nullptr, arg_keys, tpb, nullptr, 0, x);
+                nullptr, m, y, nullptr, arg_keys, tpb, nullptr, 0, x, IgemmMode{});
     return hipGetLastError();
 }
 
@@ -1128,10 +1139,10 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
             if (ban_bits)
                 FOCR_LAUNCH((gemv_i8_mfma_kernel<true>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k, xq_r,
                             a_scales + r0, mr, y_r, acc_r, keys_r, tpb, ban_bits + static_cast<size_t>(r0) * ban_words,
-                            ban_words, nullptr);
+                            ban_words, nullptr, IgemmMode{});
             else
                 FOCR_LAUNCH((gemv_i8_mfma_kernel<false>), dim3(grid), dim3(kThreads), lds_mfma, s, w, ws, n, k,
-                            xq_r, a_scales + r0, mr, y_r, acc_r, keys_r, tpb, nullptr, 0, nullptr);
+                            xq_r, a_scales + r0, mr, y_r, acc_r, keys_r, tpb, nullptr, 0, nullptr, IgemmMode{});
         }
         return hipGetLastError();
     }
@@ -1209,6 +1220,29 @@ hipError_t launch_igemm_i8_mfma(hipStream_t s, const int8_t* a, const int8_t* b,
     const int cpw = ((k + 255) / 256 + 3) / 4;
     const dim3 grid(static_cast<unsigned>((n + 15) / 16), static_cast<unsigned>(batch));
     const IgemmMode im{1, static_cast<size_t>(n) * k, static_cast<size_t>(m) * k, static_cast<size_t>(m) * n};
+    // Many products (a batch of experts' projections): one 16-row tile per
+    // wave over the whole K, the four waves of a block sharing one staged
+    // copy of the instance's activation rows, the weight chunks pipelined two
+    // deep, about four blocks per CU. (The split-K form below suits a few
+    // products: each block stages the activations for a single 16-row tile,
+    // and its LDS admits three blocks per CU, so 64 instances' 3584 tiles took
+    // five rounds of blocks.)
+    const int tiles = (n + 15) / 16;
+    const size_t lds_tile = (16 * static_cast<size_t>(k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const int cus = 256;
+    if (k % 256 == 0 && static_cast<long>(batch) * tiles >= 4L * cus && lds_tile <= 65536) {
+        const long target_blocks = 4L * cus;
+        int tpb = static_cast<int>((static_cast<long>(batch) * tiles + target_blocks - 1) / target_blocks);
+        tpb = (tpb + 3) & ~3;  // whole rounds of the block's four waves
+        const dim3 tgrid(static_cast<unsigned>((tiles + tpb - 1) / tpb), static_cast<unsigned>(batch));
+        for (int r0 = 0; r0 < m; r0 += 16) {
+            const int mr = m - r0 < 16 ? m - r0 : 16;
+            FOCR_LAUNCH((gemv_i8_mfma_kernel<false>), tgrid, dim3(kThreads), lds_tile, s, b, nullptr, n, k,
+                        a + static_cast<size_t>(r0) * k, nullptr, mr, nullptr, out + static_cast<size_t>(r0) * n,
+                        nullptr, tpb, nullptr, 0, nullptr, im);
+        }
+        return hipGetLastError();
+    }
     for (int r0 = 0; r0 < m; r0 += 16) {
         const int mr = m - r0 < 16 ? m - r0 : 16;
         const int8_t* ar = a + static_cast<size_t>(r0) * k;

@@ -71,7 +71,8 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long m, int a) {
 // workgroup-scope sc0 load did not see half of them) and gets the logit
 // with its tag. No atomic read-modify-writes, no fences. The wait is
 // bounded by the real-time clock: a part whose words have not all appeared
-// after kRouteWaitTicks is computed by the leader itself, so the result
+// after wait_ticks (s_memrealtime runs at 100 MHz; 1000 = 10 us by default)
+// is computed by the leader itself, so the result
 // never depends on the placement or on the other blocks being resident.
 // Either way each logit is the same f64 dot product in the same lane order
 // (lane l: float4 chunks l + 64 i, then the DPP tree), so the routing is
@@ -94,7 +95,6 @@ constexpr int kRouteWaves = kRouteThreads / 64;
 constexpr int kRouteRPW = 2;   // router rows per wave: kRouteWaves x 2 = 8 = E / kRouteParts at E = 64
 constexpr int kRouteNC = 5;    // float4 chunks per lane per batch: 64 x 5 x 4 = 1280 floats
 constexpr int kRouteEPP = kRouteWaves * kRouteRPW;  // experts per part (max)
-constexpr unsigned long long kRouteWaitTicks = 1000;  // s_memrealtime runs at 100 MHz: 10 us
 static_assert(kRouteEPP * kRouteParts >= kMaxE, "the parts cover every expert");
 static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
 
@@ -116,11 +116,11 @@ __device__ __forceinline__ unsigned long long realtime() { return __builtin_amdg
 // The f64 logits of router rows r[0..kRouteRPW) (clamped in range by the
 // caller) against the routed row, in this wave: lane l owns float4 chunks
 // l + 64 i; every load of a batch is issued before its first use. Returns
-// the wave sums (every lane). amax (optional) gets max|row| over the wave.
+// the wave sums (every lane) and max|row| over the wave.
 template <bool NORM>
 __device__ __forceinline__ void route_dots(const float4* __restrict__ xr, const float4 (&nv)[kRouteNC],
                                            const float* __restrict__ G, const int (&r)[kRouteRPW], int H4,
-                                           int lane, double (&out)[kRouteRPW], float* amax_out) {
+                                           int lane, double (&out)[kRouteRPW], float& amax_out) {
     const float4* gr[kRouteRPW];
 #pragma unroll
     for (int k = 0; k < kRouteRPW; ++k) gr[k] = reinterpret_cast<const float4*>(G + static_cast<size_t>(r[k]) * H4 * 4);
@@ -169,7 +169,7 @@ __device__ __forceinline__ void route_dots(const float4* __restrict__ xr, const 
     }
 #pragma unroll
     for (int k = 0; k < kRouteRPW; ++k) out[k] = wave_sum_d_full(acc[k]);
-    if (amax_out) *amax_out = wave_max_f_full(amax);
+    amax_out = wave_max_f_full(amax);
 }
 
 // Grid: 8 * S blocks, S = ceil(T / 8) * kRouteParts. Block b sits on XCD
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     const float* __restrict__ x, const float* __restrict__ G, int T, int H, int E, int K, int norm_topk,
     float routed_scale, int8_t* __restrict__ xq, float* __restrict__ xs, uint32_t* __restrict__ idx_out,
     float* __restrict__ gates_out, float* __restrict__ probs_out, int* __restrict__ flag, MoeSel sel,
-    const RouteNorm rn, RouteXchg* __restrict__ xch) {
+    const RouteNorm rn, RouteXchg* __restrict__ xch, unsigned wait_ticks) {
     __shared__ float s_logit[kMaxE];
     __shared__ unsigned s_missing;  // leader: parts it computes itself (bit p)
     const int xcd = blockIdx.x & 7;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
             r[k] = e < E ? e : E - 1;
         }
         double d[kRouteRPW];
-        route_dots<NORM>(xr, nv, G, r, H4, lane, d, quantizer && wave == 0 ? &amax : nullptr);
+        route_dots<NORM>(xr, nv, G, r, H4, lane, d, amax);
         if (lane < kRouteRPW) {
             const int el = wave * kRouteRPW + lane;
             const double v = lane == 0 ? d[0] : d[1];
@@ -320,8 +320,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         const bool watch = lane >= EP && lane < E;
         bool ready = !watch;
         float got = 0.0f;
-        const unsigned long long t_end = realtime() + kRouteWaitTicks;
-        while (true) {
+        const unsigned long long t_end = realtime() + wait_ticks;
+        while (wait_ticks) {  // 0: no wait, every part computed below
             if (!ready) {
                 const unsigned long long w =
                     __hip_atomic_load(&xch->word[t][pe][ie], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -378,7 +378,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
             r[k] = e < E ? e : E - 1;
         }
         double d[kRouteRPW];
-        route_dots<NORM>(xr, nv, G, r, H4, lane, d, nullptr);
+        float amax_unused;
+        route_dots<NORM>(xr, nv, G, r, H4, lane, d, amax_unused);
         if (lane < kRouteRPW) {
             const int el = wave * kRouteRPW + lane;
             const double v = lane == 0 ? d[0] : d[1];
@@ -1010,7 +1011,8 @@ size_t moe_route_xchg_bytes() { return sizeof(RouteXchg); }
 
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
-                            float* probs, int* flag, void* sel, void* xchg, const MoeRouteNorm* norm) {
+                            float* probs, int* flag, void* sel, void* xchg, unsigned wait_ticks,
+                            const MoeRouteNorm* norm) {
     if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048 || !xchg) return hipErrorInvalidValue;
     static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
     // token t on XCD t % 8, its kRouteParts blocks at slots (t / 8) * kRouteParts + p
@@ -1021,11 +1023,12 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
         if (d.hidden > 64 * 4 * kRouteNC || !norm->attn || !norm->w || !norm->h_out) return hipErrorInvalidValue;
         const RouteNorm rn{norm->attn, norm->w, norm->eps, norm->h_out};
         FOCR_LAUNCH(moe_route_kernel<true>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.t, d.hidden,
-                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn, x);
+                    d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel), rn, x,
+                    wait_ticks);
     } else {
         FOCR_LAUNCH(moe_route_kernel<false>, grid, dim3(kRouteThreads), 0, s, hidden, router, d.t, d.hidden,
                     d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel),
-                    RouteNorm{}, x);
+                    RouteNorm{}, x, wait_ticks);
     }
     return hipGetLastError();
 }

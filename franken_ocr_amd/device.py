@@ -64,6 +64,11 @@ class Context:
         _abi.call("focr_hip_ctx_scratch_bytes", self.handle, C.byref(n))
         return int(n.value)
 
+    def set_route_wait(self, ticks: int) -> None:
+        """Bound of the MoE route's cross-block wait (10 ns ticks; a test hook:
+        0 makes every token's lead block compute all of its logits)."""
+        _abi.call("focr_hip_ctx_set_route_wait", self.handle, int(ticks))
+
     def info(self) -> dict:
         arch = C.create_string_buffer(64)
         cus = C.c_int32(0)

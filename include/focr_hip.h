@@ -89,6 +89,11 @@ int32_t focr_hip_ctx_stream(focr_hip_ctx* ctx, void** stream);
  * grow-only scratch slots hold now; an entry point that allocates nothing
  * leaves it unchanged. */
 int32_t focr_hip_ctx_scratch_bytes(focr_hip_ctx* ctx, size_t* bytes);
+/* No counterpart in the reference (a test hook): the bound, in 10 ns ticks
+ * (default 1000 = 10 us), of the MoE route's wait for the other blocks of a
+ * token; a part not seen within it is computed by the waiting block itself,
+ * with the same result. 0 takes that path for every part. */
+int32_t focr_hip_ctx_set_route_wait(focr_hip_ctx* ctx, uint32_t ticks);
 /* Device name / gcnArchName / CU count of the context's device. */
 int32_t focr_hip_ctx_device_info(focr_hip_ctx* ctx, char* arch, size_t arch_cap,
                                  int32_t* cu_count);

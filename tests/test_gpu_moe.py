@@ -232,3 +232,36 @@ def test_moe_shape_errors(ctx, gpu_layer):
 
     with pytest.raises(ContractViolation, match=r"t 65 outside"):
         gpu_layer.decode(ctx.empty((65, H), np.float32), ctx.empty((65, H), np.float32))
+
+
+@pytest.mark.parametrize("t", [1, 8, 40])
+def test_route_fallback_when_the_other_blocks_are_not_waited_for(layer_w, t):
+    # The route splits each token's router rows over several blocks that
+    # exchange logits through the L2, and a block that waited too long
+    # computes the missing logits itself. A wait bound of 0 forces that path
+    # for every part of every token: routing, probabilities and the layer
+    # output must be the same bits as with the exchange (and the oracle's).
+    from franken_ocr_amd.device import Context
+    from franken_ocr_amd.engine import MoeLayer
+
+    c = Context(0)
+    layer = MoeLayer(H, I, E, K, *layer_w, ctx=c)
+    x = synth.f32_normal(synth.seed_of(1300 + t), t * H).reshape(t, H)
+    dx = c.to_device(x)
+    res = []
+    for ticks in (1000, 0, 1000):
+        _say(f"route wait {ticks} ticks, t={t}")
+        c.set_route_wait(ticks)
+        di, dg, dp = c.empty((t, K), np.uint32), c.empty((t, K), np.float32), c.empty((t, E), np.float32)
+        layer.route(dx, di, dg, dp, norm_topk=True)
+        dout = c.empty((t, H), np.float32)
+        layer.decode(dx, dout, norm_topk=True)
+        res.append((di.numpy(), dg.numpy(), dp.numpy(), dout.numpy()))
+    for a, b in zip(res[0], res[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for a, b in zip(res[0], res[2]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    st, want_i, want_g, want_p = O.route(x, layer_w[0], E, K, norm_topk=True)
+    assert st == 0 and np.array_equal(res[1][0], want_i)
+    layer.free()
+    c.close()
