@@ -1136,6 +1136,195 @@ def cpu_decode_layer(args, inputs):
     return res
 
 
+# ---------------------------------------------------------------------------
+# one decoder layer over a chunked prefill (the MoE layer + shared expert)
+# ---------------------------------------------------------------------------
+
+def bench_prefill_layer(args, ctx):
+    """One MoE decoder layer of prefill_with_cache_i8_chunked (decoder.rs:
+    2461-2486) over a `tokens`-token sequence in chunks of `chunk`, each chunk
+    one focr_hip_decoder_layer_prefill call: RMSNorm, the fused qkv int8 GEMM,
+    RoPE, the chunk's K / V into the stream's reference block and its causal
+    attention, o_proj, residual + RMSNorm, route_default, the 64 routed
+    experts (top-6) and the 1792-wide shared expert on the matrix cores,
+    residual. Every step restores the layer input with one device copy (the
+    layer updates its rows in place), inside the timed region. Layer copies
+    rotate so weights come from HBM."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import DecoderLayer, MoeLayer, QInt8, RingCache, prefill_chunk_bounds
+
+    seq, chunk, D, SI = args.tokens, args.chunk, 1280, 1792
+    log(f"prefill_layer: seq={seq}, chunk={chunk}, {args.copies} layer copies")
+    base = make_moe_host(100)
+    sh = [synth.int8_uniform(synth.seed_of(800), SI * H), synth.f32_uniform(synth.seed_of(801), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(802), SI * H), synth.f32_uniform(synth.seed_of(803), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(804), H * SI), synth.f32_uniform(synth.seed_of(805), H, 1e-3, 2e-2)]
+    wqkv = synth.int8_uniform(synth.seed_of(806), 3 * D * H)
+    sqkv = synth.f32_uniform(synth.seed_of(807), 3 * D, 1e-3, 2e-2)
+    wo = synth.int8_uniform(synth.seed_of(808), H * D)
+    so = synth.f32_uniform(synth.seed_of(809), H, 1e-3, 2e-2)
+    ln1 = synth.f32_uniform(synth.seed_of(810), H, 0.5, 1.5)
+    ln2 = synth.f32_uniform(synth.seed_of(811), H, 0.5, 1.5)
+    layers, keep = [], []
+    routers = []
+    for c in range(args.copies):
+        router = synth.f32_normal(synth.seed_of(1000 + c), E * H, 0.0, 0.02).reshape(E, H)
+        routers.append(router)
+        moe = MoeLayer(H, I, E, K, router, *base[1:], ctx=ctx)
+        moe.set_shared(SI, *sh)
+        qkv, o = QInt8(wqkv, sqkv, 3 * D, H, ctx), QInt8(wo, so, H, D, ctx)
+        keep += [moe, qkv, o]
+        layers.append(DecoderLayer(H, ln1, ln2, qkv, o, moe=moe, ctx=ctx))
+    caches = [RingCache(1, seq, ctx=ctx) for _ in layers]
+    x_host = synth.f32_normal(synth.seed_of(830), seq * H).reshape(seq, H)
+    x0 = ctx.to_device(x_host)
+    x = ctx.empty((seq, H), np.float32)
+    idx = ctx.empty((seq, K), np.uint32)
+    bounds = prefill_chunk_bounds(seq, chunk)
+    views = [(c0, x.view_rows(c0, c1), idx.view_rows(c0, c1)) for c0, c1 in bounds]
+    n = len(layers)
+
+    def step(i):
+        j = i % n
+        x.copy_from_device(x0)
+        for c0, xc, ic in views:
+            layers[j].prefill(caches[j], 0, xc, c0, ic, check_route=False)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    # layer copy 0 once more for the CPU leg's comparison
+    step(0)
+    gpu_out = x.numpy()
+    counts = np.bincount(idx.numpy().ravel(), minlength=E)
+    # algorithmic work per step: int8 products (2 ops per multiply-add) and
+    # the attention's f32 flops
+    ops = {"linear_i8": 2.0 * seq * (3 * D * H + H * D),
+           "i8_gate_up": 2.0 * seq * K * 2 * I * H, "i8_down": 2.0 * seq * K * H * I,
+           "i8_shared": 2.0 * seq * 3 * SI * H}
+    flops = {"attn_prefill": attn_flops(seq), "moe_route": 2.0 * seq * E * H}
+    peak = {k: MFMA_INT8_PEAK_TOPS for k in ops}
+    peak.update({k: MFMA_F32_PEAK_TFLOPS for k in flops})
+    work = {**ops, **flops}
+    n_stat = max(args.steps, STAT_STEPS)  # steps of timed()'s per-kernel pass
+    per_step = {k: (prof[k]["ms"] / n_stat if k in prof else float("nan")) for k in work}
+    ideal_ms = sum(work[k] / (peak[k] * 1e12) * 1e3 for k in work)
+    int8_ops = sum(ops.values())
+    util = {
+        "int8_ops_per_step": int8_ops, "f32_flops_per_step": sum(flops.values()),
+        "ideal_ms_at_peak": round(ideal_ms, 5),
+        # the fraction of the step a machine at MI355X's dense peaks would need
+        # for the same products (int8 at 5.0 POP/s, f32 at 157.3 TFLOP/s)
+        "frac_of_step": round(ideal_ms / ms, 4),
+        "int8_tops_over_step": round(int8_ops / (ms * 1e-3) / 1e12, 2),
+        "per_kernel": {k: {"ms_per_step": round(per_step[k], 5),
+                           "achieved": round(work[k] / (per_step[k] * 1e-3) / 1e12, 2),
+                           "unit": "TOP/s" if k in ops else "TFLOP/s",
+                           "frac": round(work[k] / (per_step[k] * 1e-3) / 1e12 / peak[k], 4)}
+                       for k in work if per_step[k] == per_step[k]},
+    }
+    top = max((k for k in ops if k in prof), key=lambda k: per_step[k])
+    launches = max(prof[top]["count"] // n_stat, 1)
+    t_us = kernel_us(prof, top)
+    ach = work[top] / launches / (t_us * 1e-6) / 1e12
+    log(f"per-kernel avg us {kernels}")
+    return {
+        "metric": f"chunked-prefill decoder layer tokens/s (one MoE layer, {seq} tokens in chunks of {chunk}) + "
+                  f"MFMA utilisation, 1 GPU",
+        "value": round(seq * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "prefill_layer", "seq": seq, "chunk": chunk, "chunks": len(bounds), "hidden": H,
+                   "heads": 10, "head_dim": 128, "experts": E, "top_k": K, "inter": I, "shared_inter": SI,
+                   "layer_copies_rotated": n, "experts_hit": int((counts > 0).sum()),
+                   "tokens_per_expert_max": int(counts.max())},
+        "roofline": {"bound": "mfma", "kernel": top, "achieved": round(ach, 2), "peak": MFMA_INT8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(ach / MFMA_INT8_PEAK_TOPS, 4),
+                     "traffic": traffic_for(top, f"prefill_layer_{seq}_c{chunk}"),
+                     "algorithmic_ops_per_launch": work[top] / launches, "avg_launch_us": round(t_us, 3),
+                     **launch_stats(prof, top)},
+        "mfma_utilisation": util,
+        "kernel_avg_us": kernels,
+        "step_us": sstats,
+        "_cpu_inputs": dict(x=x_host, gpu_out=gpu_out, chunk=chunk, base=base, sh=sh, wqkv=wqkv, sqkv=sqkv, wo=wo,
+                            so=so, ln1=ln1, ln2=ln2, router=routers[0], SI=SI),
+    }
+
+
+def cpu_prefill_layer(args, inputs):
+    """The same layer over the same sequence on the host: linear_int8_dynamic
+    (nn.rs:151-173) on the best int8 tier over all threads for qkv, o_proj,
+    every expert's gate / up / down and the shared expert's, moe_block_i8's
+    gather / scatter (decoder.rs:2142-2181) in numpy, RMSNorm / RoPE /
+    route_default from the oracle's C, and the chunk's causal attention by
+    the f32 restatement of decoder.rs:1282-1340 on one thread."""
+    from oracle import pyoracle as O
+
+    d = inputs
+    L, P = O.lib(), O.p
+    tier = L.cpu_detect_tier()
+    x0, chunk, SI = d["x"], d["chunk"], d["SI"]
+    seq, Dm = x0.shape[0], 1280
+    _, wg, sg, wu, su, wd, sd = d["base"]
+    swg, ssg, swu, ssu, swd, ssd = d["sh"]
+    router = d["router"]
+
+    def lin(a, w, ws, n):
+        a = np.ascontiguousarray(a, np.float32)
+        y = np.empty((a.shape[0], n), np.float32)
+        L.cpu_linear_i8_dynamic(tier, P(a), a.shape[0], a.shape[1], P(w), P(ws), n, P(y))
+        return y
+
+    def silu_mul(g, u):
+        with np.errstate(over="ignore"):  # exp(-g) overflows to inf for g < -88: silu -> -0
+            return (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+
+    def layer():
+        x = np.array(x0, np.float32)
+        kall = np.zeros((seq, Dm), np.float32)
+        vall = np.zeros((seq, Dm), np.float32)
+        for c0 in range(0, seq, chunk):
+            c1 = min(seq, c0 + chunk)
+            xc = x[c0:c1]
+            qkv = lin(O.rms_norm(xc, d["ln1"]), d["wqkv"], d["sqkv"], 3 * Dm)
+            q = np.stack([O.rope(qkv[r, :Dm], c0 + r) for r in range(c1 - c0)])
+            kall[c0:c1] = np.stack([O.rope(qkv[r, Dm:2 * Dm], c0 + r) for r in range(c1 - c0)])
+            vall[c0:c1] = qkv[:, 2 * Dm:]
+            cx = np.zeros((c1 - c0, Dm), np.float32)
+            L.oracle_chunk_prefill_attention_f32(P(q), c1 - c0, P(kall), P(vall), c1, 10, 128, c0, P(cx))
+            h = (xc + lin(cx, d["wo"], d["so"], H)).astype(np.float32)
+            n2 = O.rms_norm(h, d["ln2"])
+            st, idx, gates, _ = O.route(n2, router, E, K, norm_topk=False, routed_scale=1.0)
+            assert st == 0
+            mlp = np.zeros_like(h)
+            for e in np.unique(idx):
+                rows, slots = np.nonzero(idx == e)
+                sub = n2[rows]
+                a = silu_mul(lin(sub, wg[e * I * H:(e + 1) * I * H], sg[e * I:(e + 1) * I], I),
+                             lin(sub, wu[e * I * H:(e + 1) * I * H], su[e * I:(e + 1) * I], I))
+                y = lin(a, wd[e * H * I:(e + 1) * H * I], sd[e * H:(e + 1) * H], H)
+                np.add.at(mlp, rows, gates[rows, slots][:, None] * y)
+            a = silu_mul(lin(n2, swg, ssg, SI), lin(n2, swu, ssu, SI))
+            mlp += lin(a, swd, ssd, H)
+            x[c0:c1] = h + mlp
+        return x
+
+    out = [None]
+
+    def call():
+        out[0] = layer()
+
+    res = cpu_stats(call, seq, "tokens/s", args.cpu_seconds, min_iters=2)
+    got, want = d["gpu_out"], out[0]
+    rr = (np.abs(got.astype(np.float64) - want) /
+          np.maximum(np.abs(want), np.abs(want).max(axis=1, keepdims=True) * 1e-2)).max(axis=1)
+    res.update({"cores": int(L.cpu_threads()), "kind": "port", "tier": L.cpu_tier_feature(tier).decode(),
+                "gpu_rows_within_1e-3": round(float((rr <= 1e-3).mean()), 4),
+                "sample": f"whole layer passes over {seq} tokens in chunks of {chunk} (int8 products over all "
+                          f"threads, the attention on one); gpu_rows_within_1e-3 compares the GPU's output rows"})
+    return res
+
+
 def bench_decode_step(args, ctx):
     """One decode token for B streams through the whole decoder: 12 layers
     (decoder.rs:2542-2627 per layer; layer 0 the 6848-wide dense MLP, layers
@@ -1271,6 +1460,7 @@ WORKLOADS = {
     "decode_layer": (bench_decode_layer, cpu_decode_layer),
     "decode_step": (bench_decode_step, None),
     "prefill_attn": (bench_prefill_attn, cpu_prefill_attn),
+    "prefill_layer": (bench_prefill_layer, cpu_prefill_layer),
 }
 
 
@@ -1290,6 +1480,7 @@ EXTRAS = [
     ("prefill_attn_1024", "prefill_attn", 1024, 1, 20, 3),
     ("linear_i8_m8192", "linear_i8", 8192, 3, 20, 3),
     ("decode_layer_b8", "decode_layer", 8, 6, 50, 5),
+    ("prefill_layer_1024", "prefill_layer", 1024, 2, 10, 2),
 ]
 _EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us", "step_us")
 
@@ -1360,7 +1551,8 @@ def main() -> int:
                 "igemm_batched": (1, 1),
                 "copy": (1, 1),
                 "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
-                "decode_layer": (8, 6), "decode_step": (8, 1), "prefill_attn": (1024, 1)}
+                "decode_layer": (8, 6), "decode_step": (8, 1), "prefill_attn": (1024, 1),
+                "prefill_layer": (1024, 2)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

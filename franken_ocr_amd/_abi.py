@@ -95,6 +95,7 @@ _SIGS: dict[str, list] = {
     "focr_hip_rms_norm": [_P, _P, _SZ, _SZ, _P, _F32, _P],
     "focr_hip_decoder_layer_create": [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _F32, _P],
     "focr_hip_decoder_layer_free": [_P],
+    "focr_hip_decoder_layer_prefill": [_P, _P, _P, _SZ, _P, _SZ, _SZ, _P, _I32],
     "focr_hip_decoder_layer_step": [_P, _P, _P, _P, _P, _P, _I32],
     "focr_hip_rswa_create": [_P, _SZ, _SZ, _P],
     "focr_hip_rswa_free": [_P],

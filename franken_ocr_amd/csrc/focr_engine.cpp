@@ -616,10 +616,11 @@ int32_t moe_scratch(ScratchSource& src, const focr_hip_moe_layer* L, size_t t, b
     // the route's exchange comes first: in the static array it is then always
     // at offset 0 (zero from load time, and only the route writes there); a
     // context slot is zeroed once, when it is allocated
-    const bool fresh = !src.base && !src.counting && src.ctx->scratch[kScrRouteX].cap == 0;
-    s->xchg = src.get(kScrRouteX, moe_route_xchg_bytes());
+    const size_t xb = moe_route_xchg_bytes(kMoeMaxT);  // one size for every decode call
+    const bool fresh = !src.base && !src.counting && src.ctx->scratch[kScrRouteX].cap < xb;
+    s->xchg = src.get(kScrRouteX, xb);
     if (!s->xchg) return FOCR_HIP_E_OOM;
-    if (fresh && hipMemsetAsync(s->xchg, 0, moe_route_xchg_bytes(), src.ctx->stream) != hipSuccess)
+    if (fresh && hipMemsetAsync(s->xchg, 0, src.ctx->scratch[kScrRouteX].cap, src.ctx->stream) != hipSuccess)
         return FOCR_HIP_E_OOM;
     const size_t sel_off = (pairs * 8 + 255) & ~static_cast<size_t>(255);
     char* route = static_cast<char*>(src.get(kScrRoute, sel_off + moe_sel_bytes()));
@@ -976,9 +977,8 @@ int32_t ensure_tiled(focr_hip_ctx* ctx, int8_t** dst, const int8_t* src, size_t 
 
 extern "C" {
 
-int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
                                    const float* bias, float* y) {
-    ENGINE_CTX(ctx);
     if (!w) return fail(FOCR_HIP_E_BAD_HANDLE, "linear_int8_dynamic: null weight handle");
     if (!x || !y) return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: null device pointer");
     if (m < 1 || m > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, fmt("linear_int8_dynamic: m %zu outside 1..=1048576", m));
@@ -1030,10 +1030,15 @@ int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
     return FOCR_HIP_OK;
 }
 
-int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
+int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+                                   const float* bias, float* y) {
+    ENGINE_CTX(ctx);
+    return linear_i8_dynamic_impl(ctx, w, x, m, bias, y);
+}
+
+static int32_t moe_prefill_i8_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
                                 const uint32_t* idx, const float* gates, int32_t with_shared, float* out,
                                 int32_t check_idx) {
-    ENGINE_CTX(ctx);
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "moe_prefill_i8: null moe layer");
     if (!x || !idx || !gates || !out) return fail(FOCR_HIP_E_ARG, "moe_prefill_i8: null pointer");
     if (t < 1 || t > 16384) return fail(FOCR_HIP_E_SHAPE, fmt("moe_prefill_i8: t %zu outside 1..=16384", t));
@@ -1099,6 +1104,13 @@ int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, 
                         fmt("moe_prefill_i8: expert index out of range (n_experts %zu)", L->n_experts));
     }
     return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_moe_prefill_i8(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
+                                const uint32_t* idx, const float* gates, int32_t with_shared, float* out,
+                                int32_t check_idx) {
+    ENGINE_CTX(ctx);
+    return moe_prefill_i8_impl(ctx, L, x, t, idx, gates, with_shared, out, check_idx);
 }
 
 // ---- R-SWA --------------------------------------------------------------------
@@ -1567,9 +1579,8 @@ int32_t focr_hip_prefill_attention(focr_hip_ctx* ctx, const float* q, const floa
     return attn_run(ctx, name, gm, q, k, v, out, seq, 0, seq, num_heads);
 }
 
-int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
+static int32_t rswa_prefill_chunk_impl(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
                                     const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out) {
-    ENGINE_CTX(ctx);
     const char* name = "rswa_prefill_chunk";
     if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
     if (stream >= c->n_streams)
@@ -1598,6 +1609,141 @@ int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t 
     c->prefill_len[stream] = static_cast<int64_t>(c0 + cs);
     c->ring_len[stream] = 0;
     c->ring_pos[stream] = 0;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
+                                    const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out) {
+    ENGINE_CTX(ctx);
+    return rswa_prefill_chunk_impl(ctx, c, stream, q_chunk, k_chunk, v_chunk, cs, c0, out);
+}
+
+// ---- one decoder layer over a prefill chunk (decoder.rs:2428-2520) ---------------
+
+// route_default (moe.rs:273-280: norm_topk_prob false, scaling 1.0) of a
+// prefill chunk's t rows: idx / gates [t][top_k], flag [t] (1: fewer than
+// top_k finite scores). The split route kernel without the decode kernels'
+// selection matrices; its exchange buffer grows to t tokens (zeroed when it
+// grows) and a one-thread launch advances the buffer's counter after it.
+static int32_t prefill_route_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
+                                  uint32_t* idx, float* gates, int* flag) {
+    const size_t xb = moe_route_xchg_bytes(t);
+    const bool grow = ctx->scratch[kScrRouteX].cap < xb;
+    void* xchg = ctx->scratch_get(kScrRouteX, xb);
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
+    if (!xchg || !xq || !xs) return FOCR_HIP_E_OOM;
+    if (grow) FOCR_HIP_TRY(hipMemsetAsync(xchg, 0, ctx->scratch[kScrRouteX].cap, ctx->stream), "route exchange zero");
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    {
+        ProfScope ps(ctx, "moe_route");
+        FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, x, L->router, 0, 1.0f, xq, xs, idx, gates, nullptr, flag,
+                                      nullptr, xchg, ctx->route_wait_ticks),
+                     "prefill route launch");
+    }
+    FOCR_HIP_TRY(launch_route_epoch_bump(ctx->stream, xchg), "route epoch launch");
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+                                       size_t stream, float* x, size_t cs, size_t c0, uint32_t* route_idx,
+                                       int32_t check_route) {
+    ENGINE_CTX(ctx);
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_prefill: null layer");
+    if (!cache) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_prefill: null rswa cache");
+    if (!x) return fail(FOCR_HIP_E_ARG, "decoder_layer_prefill: null x");
+    if (L->n_heads != 10 || L->head_dim != 128)
+        return fail(FOCR_HIP_E_SHAPE, "decoder_layer_prefill: the R-SWA cache holds 10 heads x 128");
+    if (cs < 1 || cs > static_cast<size_t>(kLayerPrefillMaxRows))
+        return fail(FOCR_HIP_E_SHAPE,
+                    fmt("decoder_layer_prefill: chunk of %zu rows outside 1..=%d", cs, kLayerPrefillMaxRows));
+    if (stream >= cache->n_streams)
+        return fail(FOCR_HIP_E_SHAPE, fmt("rswa: stream %zu >= num_streams %zu", stream, cache->n_streams));
+    // the chunk order rswa_prefill_chunk requires, checked before any launch
+    if (c0 != 0 && cache->prefill_len[stream] != static_cast<int64_t>(c0))
+        return fail(FOCR_HIP_E_STATE, fmt("rswa_prefill_chunk: chunk starts at %zu but the stream holds %lld prefill "
+                                          "tokens",
+                                          c0, static_cast<long long>(cache->prefill_len[stream])));
+    if (c0 + cs > cache->ref_capacity)
+        return fail(FOCR_HIP_E_STATE,
+                    fmt("rswa: prefill seq %zu exceeds ref_capacity %zu", c0 + cs, cache->ref_capacity));
+    const size_t H = L->hidden, D = L->n_heads * L->head_dim;
+    const size_t I = L->gate ? L->gate->n : 0, K = L->moe ? L->moe->top_k : 0;
+    // one scratch slot carved into the chunk's intermediates
+    const size_t fl = cs * (H + 3 * D + 3 * D + D + H + H + H) + (L->gate ? 2 * cs * I : 0) + cs * K * 2 + cs;
+    char* base = static_cast<char*>(ctx->scratch_get(kScrLayer, fl * 4 + 20 * 256));
+    if (!base) return FOCR_HIP_E_OOM;
+    auto take = [&](size_t bytes) {
+        char* r = base;
+        base += (bytes + 255) & ~static_cast<size_t>(255);
+        return r;
+    };
+    float* nrm = reinterpret_cast<float*>(take(cs * H * 4));
+    float* qkv = reinterpret_cast<float*>(take(cs * 3 * D * 4));
+    float* q = reinterpret_cast<float*>(take(cs * D * 4));
+    float* k = reinterpret_cast<float*>(take(cs * D * 4));
+    float* v = reinterpret_cast<float*>(take(cs * D * 4));
+    float* cx = reinterpret_cast<float*>(take(cs * D * 4));
+    float* attn = reinterpret_cast<float*>(take(cs * H * 4));
+    float* h = reinterpret_cast<float*>(take(cs * H * 4));
+    float* mlp = reinterpret_cast<float*>(take(cs * H * 4));
+    hipStream_t s = ctx->stream;
+    int32_t st;
+    // 1. input RMSNorm; 2. q / k / v = linear_int8_dynamic (one fused [3 D, H]
+    //    weight: the same quantized rows times each projection's rows); 3.
+    //    RoPE at the chunk's positions c0 ..; 4. K / V into the stream's
+    //    reference block and the chunk's causal attention over [0, c0 + cs)
+    {
+        ProfScope ps(ctx, "layer_prefill_norm");
+        FOCR_HIP_TRY(launch_rms_norm(s, x, L->input_ln, (int)cs, (int)H, L->eps, nrm), "rms_norm launch");
+    }
+    if ((st = linear_i8_dynamic_impl(ctx, L->qkv, nrm, cs, nullptr, qkv))) return st;
+    {
+        ProfScope ps(ctx, "layer_prefill_rope");
+        FOCR_HIP_TRY(launch_rope_rows(s, qkv, (int)cs, (int)c0, L->inv_freq, (int)L->n_heads, (int)L->head_dim, q, k,
+                                      v),
+                     "rope launch");
+    }
+    if ((st = rswa_prefill_chunk_impl(ctx, cache, stream, q, k, v, cs, c0, cx))) return st;
+    // 5. o_proj; 6. residual + post-attention RMSNorm
+    if ((st = linear_i8_dynamic_impl(ctx, L->o_proj, cx, cs, nullptr, attn))) return st;
+    {
+        ProfScope ps(ctx, "layer_prefill_residual_norm");
+        FOCR_HIP_TRY(launch_residual_rms_norm(s, x, attn, L->post_ln, (int)cs, (int)H, L->eps, h, nrm),
+                     "residual rms_norm launch");
+    }
+    // 7. prefill_mlp_i8 (decoder.rs:2184-2195): moe_block_i8 (route_default,
+    //    the routed experts and the shared one) or the dense expert_mlp_i8
+    if (L->moe) {
+        uint32_t* idx = reinterpret_cast<uint32_t*>(take(cs * K * 4));
+        float* gates = reinterpret_cast<float*>(take(cs * K * 4));
+        int* flag = reinterpret_cast<int*>(take(cs * 4));
+        if ((st = prefill_route_impl(ctx, L->moe, nrm, cs, idx, gates, flag))) return st;
+        if (check_route) {
+            std::vector<int> flags(cs);
+            FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), flag, cs * sizeof(int), hipMemcpyDeviceToHost, s), "D2H route flag");
+            FOCR_HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+            for (size_t i = 0; i < cs; ++i)
+                if (flags[i]) return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", i));
+        }
+        if (route_idx)
+            FOCR_HIP_TRY(hipMemcpyAsync(route_idx, idx, cs * K * 4, hipMemcpyDeviceToDevice, s), "route idx copy");
+        if ((st = moe_prefill_i8_impl(ctx, L->moe, nrm, cs, idx, gates, L->moe->swg ? 1 : 0, mlp, 0))) return st;
+    } else {
+        float* g = reinterpret_cast<float*>(take(cs * I * 4));
+        float* u = reinterpret_cast<float*>(take(cs * I * 4));
+        if ((st = linear_i8_dynamic_impl(ctx, L->gate, nrm, cs, nullptr, g)) ||
+            (st = linear_i8_dynamic_impl(ctx, L->up, nrm, cs, nullptr, u)))
+            return st;
+        {
+            ProfScope ps(ctx, "layer_prefill_silu");
+            FOCR_HIP_TRY(launch_silu_mul(s, g, u, g, cs * I), "silu launch");
+        }
+        if ((st = linear_i8_dynamic_impl(ctx, L->down, g, cs, nullptr, mlp))) return st;
+    }
+    // 8. the second residual
+    ProfScope ps(ctx, "layer_prefill_residual");
+    FOCR_HIP_TRY(launch_add_rows(s, h, mlp, x, cs * H), "residual launch");
     return FOCR_HIP_OK;
 }
 

@@ -326,11 +326,13 @@ struct MoeRouteNorm {
     float eps;
     float* h_out;
 };
-// The route's exchange buffer (bytes; zeroed once when allocated, then
-// never cleared: calls are told apart by its counter) and the route itself;
+// The route's exchange buffer for t tokens (bytes; zeroed once when
+// allocated, then never cleared: calls are told apart by its counter) and
+// the route itself (t <= 64 with the selection matrices sel, up to 16384
+// without them: a prefill chunk's idx / gates);
 // the gate/up launch given the same buffer advances the counter, and a route
 // launched without a gate/up after it is followed by launch_route_epoch_bump.
-size_t moe_route_xchg_bytes();
+size_t moe_route_xchg_bytes(size_t t);
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, void* sel, void* xchg, unsigned wait_ticks,
@@ -363,6 +365,7 @@ hipError_t launch_moe_combine(hipStream_t s, const MoeDims& d, const float* ybuf
 constexpr int kMoeGroupedDownT = 40;
 // Tokens per MoE decode call (the route kernel's selection matrices hold 64).
 constexpr int kMoeMaxT = 64;
+constexpr int kLayerPrefillMaxRows = 4096;  // rows of one decoder_layer_prefill chunk
 // down + slot-order combine in one launch, reading the routing from idx /
 // gates / flag ([t][top_k]) and the act rows of every pair (t*top_k + j).
 hipError_t launch_moe_down_combine(hipStream_t s, const MoeDims& d, const uint32_t* idx, const float* gates,
@@ -439,6 +442,9 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
                              int streams, int n_heads, int head_dim, float* q, float* k, float* v,
                              const RopeRing* ring);
+// Prefill rows at positions c0 + r: fused qkv [rows][3 D] -> q, k (RoPE) and v, each [rows][D].
+hipError_t launch_rope_rows(hipStream_t s, const float* qkv, int rows, int c0, const float* inv_freq, int n_heads,
+                            int head_dim, float* q, float* k, float* v);
 hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n);
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n);
 // k_int4.hip

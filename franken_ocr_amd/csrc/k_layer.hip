@@ -239,6 +239,35 @@ __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __res
     }
 }
 
+// Chunked prefill (decoder.rs:2470-2482): fused qkv rows [rows][3 D] of
+// the positions c0 .. c0 + rows split into q, k (RoPE at the row's position,
+// RopeTable::build + apply_rope, decoder.rs:170-268: the same expressions as
+// rope_split_kernel) and v, each [rows][D] token-major. One block per row.
+__global__ __launch_bounds__(kThreads) void rope_rows_kernel(const float* __restrict__ qkv, int c0,
+                                                             const float* __restrict__ inv_freq, int n_heads,
+                                                             int head_dim, float* __restrict__ q,
+                                                             float* __restrict__ k, float* __restrict__ v) {
+    const int r = blockIdx.x;
+    const int D = n_heads * head_dim;
+    const int half = head_dim >> 1;
+    const float* row = qkv + static_cast<size_t>(r) * 3 * D;
+    const float p = static_cast<float>(c0 + r);
+    for (int t = threadIdx.x; t < n_heads * half; t += kThreads) {
+        const int hd = t / half, i = t - hd * half;
+        const float angle = p * inv_freq[i];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        const int j0 = hd * head_dim + i, j1 = j0 + half;
+        const float qa = row[j0], qb = row[j1];
+        const float ka = row[D + j0], kb = row[D + j1];
+        q[static_cast<size_t>(r) * D + j0] = qa * cs - qb * sn;
+        q[static_cast<size_t>(r) * D + j1] = qb * cs + qa * sn;
+        k[static_cast<size_t>(r) * D + j0] = ka * cs - kb * sn;
+        k[static_cast<size_t>(r) * D + j1] = kb * cs + ka * sn;
+    }
+    for (int j = threadIdx.x; j < D; j += kThreads) v[static_cast<size_t>(r) * D + j] = row[2 * D + j];
+}
+
 // act = silu(g) * u (decoder.rs:1746-1752), the dense MLP's SwiGLU.
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                             float* __restrict__ act, size_t n) {
@@ -285,6 +314,15 @@ hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePosition
     }
     FOCR_LAUNCH(rope_split_kernel, dim3(streams), dim3(kThreads), 0, s, qkv, pos, inv_freq, n_heads, head_dim, q, k,
                 v, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows(hipStream_t s, const float* qkv, int rows, int c0, const float* inv_freq, int n_heads,
+                            int head_dim, float* q, float* k, float* v) {
+    if (rows < 1 || c0 < 0 || n_heads < 1 || head_dim < 2 || head_dim % 2 || !qkv || !inv_freq || !q || !k || !v)
+        return hipErrorInvalidValue;
+    FOCR_LAUNCH(rope_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, qkv, c0, inv_freq,
+                n_heads, head_dim, q, k, v);
     return hipGetLastError();
 }
 

@@ -98,11 +98,16 @@ constexpr int kRouteEPP = kRouteWaves * kRouteRPW;  // experts per part (max)
 static_assert(kRouteEPP * kRouteParts >= kMaxE, "the parts cover every expert");
 static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
 
+// The exchange buffer: this header, then the words [T][kRouteParts][kRouteEPP]
+// (logit bits | tag << 32) of a call over T tokens.
 struct RouteXchg {
     unsigned long long counter;  // advanced once per call, after the route kernel
     unsigned long long pad[15];
-    unsigned long long word[kMaxT][kRouteParts][kRouteEPP];  // logit bits | tag << 32
 };
+__device__ __forceinline__ unsigned long long* route_word(RouteXchg* x, int t, int part, int i) {
+    return reinterpret_cast<unsigned long long*>(x + 1) + (static_cast<size_t>(t) * kRouteParts + part) * kRouteEPP + i;
+}
+constexpr int kRouteMaxT = 16384;  // tokens of one route call without the selection matrices (prefill)
 
 struct RouteNorm {
     const float* attn;  // [T][H]
@@ -264,8 +269,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         // 2. publish: one 8-byte word per logit (the logit's bits and the tag)
         if (wave == 0 && lane < EP) {
             const float lg = e0 + lane < E ? s_logit[e0 + lane] : 0.0f;
-            xch->word[t][part][lane] = static_cast<unsigned long long>(__float_as_uint(lg)) |
-                                       (static_cast<unsigned long long>(tag) << 32);
+            *route_word(xch, t, part, lane) = static_cast<unsigned long long>(__float_as_uint(lg)) |
+                                              (static_cast<unsigned long long>(tag) << 32);
         }
         // 3. quantize_row_i8 of the token row (wave 0 of the quantizer part
         //    holds the whole row's max|x|), after publishing
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         while (wait_ticks) {  // 0: no wait, every part computed below
             if (!ready) {
                 const unsigned long long w =
-                    __hip_atomic_load(&xch->word[t][pe][ie], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_load(route_word(xch, t, pe, ie), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (static_cast<unsigned>(w >> 32) == tag) {
                     ready = true;
                     got = __uint_as_float(static_cast<unsigned>(w));
@@ -1007,13 +1012,20 @@ bool dims_ok(const MoeDims& d) {
 
 size_t moe_sel_bytes() { return kMaxE * kMaxT + kMaxE * kMaxT * 4; }
 
-size_t moe_route_xchg_bytes() { return sizeof(RouteXchg); }
+size_t moe_route_xchg_bytes(size_t t) {
+    return sizeof(RouteXchg) + t * kRouteParts * kRouteEPP * sizeof(unsigned long long);
+}
 
 hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
                             int norm_topk, float routed_scale, int8_t* xq, float* xs, uint32_t* idx, float* gates,
                             float* probs, int* flag, void* sel, void* xchg, unsigned wait_ticks,
                             const MoeRouteNorm* norm) {
-    if (!dims_ok(d) || d.hidden % 4 != 0 || d.hidden > 2048 || !xchg) return hipErrorInvalidValue;
+    // with the selection matrices (the decode kernels' input) t <= kMaxT; a
+    // prefill chunk's routing alone, t <= kRouteMaxT
+    const int t_max = sel ? kMaxT : kRouteMaxT;
+    if (d.t < 1 || d.t > t_max || d.n_experts < 1 || d.n_experts > kMaxE || d.top_k < 1 || d.top_k > kMaxK ||
+        d.top_k > d.n_experts || d.hidden % 4 != 0 || d.hidden > 2048 || !xchg)
+        return hipErrorInvalidValue;
     static_assert(kRouteRPW == 2, "route_dots results are taken as d[0] / d[1]");
     // token t on XCD t % 8, its kRouteParts blocks at slots (t / 8) * kRouteParts + p
     const dim3 grid(static_cast<unsigned>(8 * ((d.t + 7) / 8) * kRouteParts));

@@ -431,6 +431,17 @@ class DecoderLayer:
         _abi.call("focr_hip_decoder_layer_step", self.ctx.handle, self._h, cache._h, pos.ctypes.data_as(C.c_void_p),
                   x.c_ptr, _p(route_idx), 1 if check_route else 0)
 
+    def prefill(self, cache: "RingCache", stream: int, x: DeviceArray, c0: int, route_idx: DeviceArray | None = None,
+                check_route: bool = True) -> None:
+        """One chunk of prefill_with_cache_i8_chunked (decoder.rs:2461-2486) for
+        this layer: x [cs, hidden] (device; the rows of positions c0 .. c0 + cs
+        - 1 of stream `stream`) updated in place; the chunk's K / V land in the
+        stream's reference block. route_idx [cs, top_k] (optional) receives a
+        MoE layer's expert ids."""
+        cs = x.shape[0]
+        _abi.call("focr_hip_decoder_layer_prefill", self.ctx.handle, self._h, cache._h, int(stream), x.c_ptr, cs,
+                  int(c0), _p(route_idx), 1 if check_route else 0)
+
     def free(self) -> None:
         if self._h:
             _abi.lib().focr_hip_decoder_layer_free(self._h)

@@ -461,6 +461,25 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* layer);
 int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
                                     focr_hip_rswa* cache, const uint32_t* positions, float* x,
                                     uint32_t* route_idx, int32_t check_route);
+/* One decoder layer over a prefill chunk of one stream: the per-layer body of
+ * prefill_with_cache_i8_chunked (decoder.rs:2428-2520; :2461-2486 for one
+ * layer). x [cs, hidden] f32 device holds the chunk's rows (positions c0 ..
+ * c0 + cs - 1) and is updated in place: RMSNorm -> q / k / v through
+ * linear_int8_dynamic (the dynamic activation rule) -> RoPE at the rows'
+ * positions -> K / V into the stream's reference block at [c0, c0 + cs) and
+ * the chunk's causal attention over [0, c0 + cs) (focr_hip_rswa_prefill_chunk,
+ * which sets the stream's prefill length to c0 + cs, ring empty) -> o_proj ->
+ * residual -> RMSNorm -> prefill_mlp_i8 (moe_block_i8: route_default
+ * (norm_topk false, scale 1.0) of the chunk's rows, the routed int8 experts
+ * and the shared expert on the matrix cores; or the dense expert_mlp_i8) ->
+ * residual. Chunks of one stream come in order (c0 = 0, then the previous
+ * chunk's end), as rswa_prefill_chunk requires; cs <= 4096. route_idx
+ * (device, nullable) receives a MoE layer's expert ids [cs, top_k]; with
+ * check_route = 1 a MoE layer synchronises and returns E_ROUTE for a row with
+ * no finite router score (the reference's route error). */
+int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
+                                       focr_hip_rswa* cache, size_t stream, float* x, size_t cs,
+                                       size_t c0, uint32_t* route_idx, int32_t check_route);
 
 /* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
  * The reader restates weights.rs:443-620 (format detection by magic, the

@@ -391,6 +391,53 @@ def decoder_layer_step(x, positions, rings, lw, eps=1e-6, theta=10000.0):
     return out
 
 
+def decoder_layer_prefill(x, c0, k_prev, v_prev, lw, eps=1e-6, theta=10000.0):
+    """One layer of prefill_with_cache_i8_chunked (decoder.rs:2461-2486) for
+    the chunk rows x [cs, H] at positions c0 .. c0 + cs - 1, given the
+    earlier chunks' RoPE'd K / V k_prev, v_prev [c0, D] (token-major):
+    RMSNorm -> q / k / v = linear_int8_dynamic -> RoPE -> chunk_prefill_attention
+    over [0, c0 + cs) -> o_proj -> residual -> RMSNorm -> prefill_mlp_i8 ->
+    residual. lw as decoder_layer_step's, with moe (router, wg, sg, wu, su,
+    wd, sd, n_experts, top_k, inter, shared) or dense (wg, sg, wu, su, wd, sd,
+    inter). Returns (out [cs, H], k [cs, D], v [cs, D], idx [cs, top_k] or None)."""
+    x = _c(x, np.float32)
+    cs, H = x.shape
+    D = 10 * 128
+    normed = rms_norm(x, lw["input_ln"], eps)
+    st, qkv, _, _ = linear_i8_dynamic(normed, lw["qkv"][0], lw["qkv"][1], 3 * D)
+    assert st == 0
+    q = np.stack([rope(qkv[r, :D], c0 + r, theta=theta) for r in range(cs)])
+    k = np.stack([rope(qkv[r, D:2 * D], c0 + r, theta=theta) for r in range(cs)])
+    v = np.ascontiguousarray(qkv[:, 2 * D:])
+    kp = np.concatenate([np.asarray(k_prev, np.float32).reshape(c0, D), k])
+    vp = np.concatenate([np.asarray(v_prev, np.float32).reshape(c0, D), v])
+    st, ctx = chunk_prefill_attention(q, kp, vp, 10, 128, c0)
+    assert st == 0
+    st, attn, _, _ = linear_i8_dynamic(ctx, lw["o"][0], lw["o"][1], H)
+    assert st == 0
+    h = (x + attn).astype(np.float32)
+    normed2 = rms_norm(h, lw["post_ln"], eps)
+    idx = None
+    if "moe" in lw:
+        m = lw["moe"]
+        # route_default (moe.rs:273-280): norm_topk_prob false, scaling 1.0
+        st, idx, gates, _ = route(normed2, m["router"], m["n_experts"], m["top_k"], norm_topk=False, routed_scale=1.0)
+        assert st == 0
+        st, mlp = moe_prefill_i8(normed2, idx, gates, m["wg"], m["sg"], m["wu"], m["su"], m["wd"], m["sd"],
+                                 m["n_experts"], m["inter"], shared=m.get("shared"))
+    else:
+        d = lw["dense"]
+        # expert_mlp_i8 (decoder.rs:2120-2135) is moe_block_i8's body for one
+        # expert taking every row at weight 1.0 (w * y with w = 1 is exact)
+        one_i = np.zeros((cs, 1), np.uint32)
+        one_g = np.ones((cs, 1), np.float32)
+        st, mlp = moe_prefill_i8(normed2, one_i, one_g, d["wg"], d["sg"], d["wu"], d["su"], d["wd"], d["sd"], 1,
+                                 d["inter"])
+    assert st == 0
+    out = (h + mlp.reshape(cs, H)).astype(np.float32)
+    return out, k, v, idx
+
+
 class Ring:
     """One stream's RingCache regions in host memory (head-major f32)."""
 
