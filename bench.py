@@ -1326,15 +1326,16 @@ def cpu_prefill_layer(args, inputs):
 
 
 def bench_decode_step(args, ctx):
-    """One decode token for B streams through the whole decoder: 12 layers
-    (decoder.rs:2542-2627 per layer; layer 0 the 6848-wide dense MLP, layers
-    1-11 MoE with the 1792-wide shared expert), the final RMSNorm and the
-    129280-row LM head + argmax (decoder.rs:2275-2296; sampler.rs:168-186).
+    """One decode token for B streams through the whole decoder in one call
+    (focr_hip_decoder_step): 12 layers (decoder.rs:2542-2627 per layer; layer
+    0 the 6848-wide dense MLP, layers 1-11 MoE with the 1792-wide shared
+    expert), the final RMSNorm and the 129280-row LM head + argmax
+    (decoder.rs:2275-2296; sampler.rs:168-186).
     Each stream has a 1024-token reference block; every layer has its own
     weights and cache. The step's input row stands in for the token-embedding
     lookup (the embedding table is outside this path)."""
     from franken_ocr_amd import synth
-    from franken_ocr_amd.engine import DecoderLayer, MoeLayer, QInt8, RingCache, lm_head_i8, rms_norm
+    from franken_ocr_amd.engine import Decoder, DecoderLayer, MoeLayer, QInt8, RingCache
 
     B, G, D, SI, ID, V, NL = args.tokens, 1024, 1280, 1792, 6848, 129280, 12
     log(f"decode_step: {B} streams, {NL} layers, ref {G} tokens")
@@ -1369,24 +1370,21 @@ def bench_decode_step(args, ctx):
         caches.append(cache)
     lm = QInt8(synth.int8_uniform(synth.seed_of(850), V * H), synth.f32_uniform(synth.seed_of(851), V, 1e-3, 2e-2), V,
                H, ctx)
-    final_ln = ctx.to_device(ln[2])
+    dec = Decoder(layers, ln[2], lm, ctx=ctx)
     x0 = ctx.to_device(synth.f32_normal(synth.seed_of(830), B * H).reshape(B, H))
-    x, xn = ctx.empty((B, H), np.float32), ctx.empty((B, H), np.float32)
+    x = ctx.empty((B, H), np.float32)
     tok = ctx.empty((B,), np.uint32)
     pos = np.full(B, G, np.uint32)
-    idx = [ctx.empty((B, K), np.uint32) for _ in range(NL)]
+    ridx = ctx.empty((NL, B, K), np.uint32)
 
     def step(i):
         x.copy_from_device(x0)  # stands in for the embedding lookup of the previous token
-        for l in range(NL):
-            layers[l].step(caches[l], pos + i, x, idx[l], check_route=False)
-        rms_norm(x, xn, final_ln)
-        lm_head_i8(lm, xn, tok)
+        dec.step(caches, pos + i, x, tok, route_idx=ridx)  # one call: 12 layers, final norm, LM head, argmax
 
     for i in range(args.warmup):
         step(i)
     ctx.device_synchronize()
-    U = [len(np.unique(idx[l].numpy())) for l in range(1, NL)]
+    U = [len(np.unique(ridx.numpy()[l])) for l in range(1, NL)]
     el, prof, kernels, sstats = timed(ctx, step, args.steps)
     ms = el / args.steps * 1e3
     keys = G + min(128, args.warmup + args.steps)  # the rings' fill during the timed pass

@@ -266,9 +266,8 @@ int32_t focr_hip_gemv_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float
     return FOCR_HIP_OK;
 }
 
-int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m, float* logits,
+static int32_t lm_head_i8_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m, float* logits,
                             uint32_t* argmax) {
-    ENGINE_CTX(ctx);
     int32_t st = gemv_checks("lm_head_i8", w, m);
     if (st) return st;
     if (!x || !argmax) return fail(FOCR_HIP_E_ARG, "lm_head_i8: null device pointer");
@@ -301,6 +300,12 @@ int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const fl
     ProfScope ps(ctx, "argmax_reduce");
     FOCR_HIP_TRY(launch_argmax_reduce(ctx->stream, keys, (int)m, np, argmax), "argmax launch");
     return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_lm_head_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m, float* logits,
+                            uint32_t* argmax) {
+    ENGINE_CTX(ctx);
+    return lm_head_i8_impl(ctx, w, x, m, logits, argmax);
 }
 
 }  // extern "C"
@@ -363,12 +368,11 @@ int32_t sampler_check(focr_hip_ctx* ctx, const SamplerArgs& a, size_t m) {
 
 extern "C" {
 
-int32_t focr_hip_lm_head_sample_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+static int32_t lm_head_sample_i8_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
                                    uint32_t* history, size_t history_cap, uint32_t* history_len, size_t ngram_size,
                                    size_t window, const uint32_t* whitelist, size_t n_whitelist, float temperature,
                                    uint32_t eos_token_id, int32_t append, float* logits, uint32_t* tokens,
                                    uint8_t* is_eos, int32_t check) {
-    ENGINE_CTX(ctx);
     int32_t st = gemv_checks("lm_head_sample_i8", w, m);
     if (st) return st;
     if (!x || !tokens) return fail(FOCR_HIP_E_ARG, "lm_head_sample_i8: null device pointer");
@@ -399,6 +403,16 @@ int32_t focr_hip_lm_head_sample_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
                      "sample_finish launch");
     }
     return check ? sampler_check(ctx, a, m) : FOCR_HIP_OK;
+}
+
+int32_t focr_hip_lm_head_sample_i8(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
+                                   uint32_t* history, size_t history_cap, uint32_t* history_len, size_t ngram_size,
+                                   size_t window, const uint32_t* whitelist, size_t n_whitelist, float temperature,
+                                   uint32_t eos_token_id, int32_t append, float* logits, uint32_t* tokens,
+                                   uint8_t* is_eos, int32_t check) {
+    ENGINE_CTX(ctx);
+    return lm_head_sample_i8_impl(ctx, w, x, m, history, history_cap, history_len, ngram_size, window, whitelist,
+                                  n_whitelist, temperature, eos_token_id, append, logits, tokens, is_eos, check);
 }
 
 int32_t focr_hip_sample_rows(focr_hip_ctx* ctx, const float* logits, size_t m, size_t n, uint32_t* history,
@@ -1376,9 +1390,8 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* L) {
     return FOCR_HIP_OK;
 }
 
-int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+static int32_t decoder_layer_step_impl(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
                                     const uint32_t* positions, float* x, uint32_t* route_idx, int32_t check_route) {
-    ENGINE_CTX(ctx);
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null layer");
     if (!cache) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_step: null rswa cache");
     if (!positions || !x) return fail(FOCR_HIP_E_ARG, "decoder_layer_step: null positions or x");
@@ -1510,6 +1523,12 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
                  "dense down launch");
     FOCR_HIP_TRY(launch_add_rows(s, h, attn, x, B * H), "residual launch");
     return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+                                    const uint32_t* positions, float* x, uint32_t* route_idx, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    return decoder_layer_step_impl(ctx, L, cache, positions, x, route_idx, check_route);
 }
 
 // ---- prefill attention (decoder.rs:568-640, :1282-1340) ------------------------
@@ -1745,6 +1764,127 @@ int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder
     ProfScope ps(ctx, "layer_prefill_residual");
     FOCR_HIP_TRY(launch_add_rows(s, h, mlp, x, cs * H), "residual launch");
     return FOCR_HIP_OK;
+}
+
+// ---- the whole batched decode step (decoder.rs:2812-2965) ------------------------
+
+int32_t focr_hip_decoder_create(focr_hip_ctx* ctx, size_t n_layers, const focr_hip_decoder_layer* const* layers,
+                                const float* final_norm, float rms_eps, const focr_hip_qint8* lm_head,
+                                focr_hip_decoder** out) {
+    ENGINE_CTX(ctx);
+    if (!out) return fail(FOCR_HIP_E_ARG, "decoder_create: null out");
+    *out = nullptr;
+    if (!layers || !final_norm) return fail(FOCR_HIP_E_ARG, "decoder_create: null layers or final_norm");
+    if (!lm_head) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_create: null lm_head");
+    if (n_layers < 1 || n_layers > 256)
+        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_create: %zu layers outside 1..=256", n_layers));
+    const size_t H = layers[0] ? layers[0]->hidden : 0;
+    size_t top_k = 0;
+    for (size_t l = 0; l < n_layers; ++l) {
+        const focr_hip_decoder_layer* L = layers[l];
+        if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("decoder_create: null layer %zu", l));
+        if (L->hidden != H)
+            return fail(FOCR_HIP_E_SHAPE, fmt("decoder_create: layer %zu hidden %zu != %zu", l, L->hidden, H));
+        if (L->moe) {
+            if (top_k && L->moe->top_k != top_k)
+                return fail(FOCR_HIP_E_SHAPE, fmt("decoder_create: layer %zu top_k %zu != %zu", l, L->moe->top_k,
+                                                  top_k));
+            top_k = L->moe->top_k;
+        }
+    }
+    if (lm_head->k != H)
+        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_create: lm_head [%zu, %zu] does not take hidden %zu", lm_head->n,
+                                          lm_head->k, H));
+    auto* d = new focr_hip_decoder();
+    d->ctx = ctx;
+    d->hidden = H;
+    d->top_k = top_k;
+    d->eps = rms_eps;
+    d->layers.assign(layers, layers + n_layers);
+    d->lm_head = lm_head;
+    hipError_t e = hipMalloc(&d->final_norm, H * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(d->final_norm, final_norm, H * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(d->final_norm);
+        delete d;
+        return hip_fail(e, "decoder_create upload");
+    }
+    *out = d;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_free(focr_hip_decoder* d) {
+    if (!d) return FOCR_HIP_OK;
+    hipSetDevice(d->ctx->device);
+    hipStreamSynchronize(d->ctx->stream);
+    hipFree(d->final_norm);
+    delete d;
+    return FOCR_HIP_OK;
+}
+
+// every layer's decode step, then the final RMSNorm of each row into the
+// returned buffer (the LM head's input)
+static int32_t decoder_layers_impl(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr_hip_rswa* const* caches,
+                                   const uint32_t* positions, float* x, uint32_t* route_idx, int32_t check_route,
+                                   float** normed, size_t* n_streams) {
+    if (!d) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_step: null decoder");
+    if (!caches || !positions || !x) return fail(FOCR_HIP_E_ARG, "decoder_step: null caches, positions or x");
+    const size_t NL = d->layers.size();
+    for (size_t l = 0; l < NL; ++l)
+        if (!caches[l]) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("decoder_step: null rswa cache for layer %zu", l));
+    const size_t B = caches[0]->n_streams;
+    for (size_t l = 1; l < NL; ++l)
+        if (caches[l]->n_streams != B)
+            return fail(FOCR_HIP_E_SHAPE, fmt("decoder_step: layer %zu cache holds %zu streams, layer 0's %zu", l,
+                                              caches[l]->n_streams, B));
+    for (size_t l = 0; l < NL; ++l) {
+        const focr_hip_decoder_layer* L = d->layers[l];
+        uint32_t* ri = (route_idx && L->moe) ? route_idx + l * B * d->top_k : nullptr;
+        int32_t st = decoder_layer_step_impl(ctx, L, caches[l], positions, x, ri, check_route);
+        if (st) return st;
+    }
+    float* xn = static_cast<float*>(ctx->scratch_get(kScrDec, B * d->hidden * sizeof(float)));
+    if (!xn) return FOCR_HIP_E_OOM;
+    {
+        ProfScope ps(ctx, "rms_norm");
+        FOCR_HIP_TRY(launch_rms_norm(ctx->stream, x, d->final_norm, (int)B, (int)d->hidden, d->eps, xn),
+                     "final rms_norm launch");
+    }
+    *normed = xn;
+    *n_streams = B;
+    return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_step(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr_hip_rswa* const* caches,
+                              const uint32_t* positions, float* x, float* logits, uint32_t* tokens,
+                              uint32_t* route_idx, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    if (!tokens) return fail(FOCR_HIP_E_ARG, "decoder_step: null tokens");
+    float* xn = nullptr;
+    size_t B = 0;
+    int32_t st = decoder_layers_impl(ctx, d, caches, positions, x, route_idx, check_route, &xn, &B);
+    if (st) return st;
+    return lm_head_i8_impl(ctx, d->lm_head, xn, B, logits, tokens);
+}
+
+int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr_hip_rswa* const* caches,
+                                     const uint32_t* positions, float* x, uint32_t* history, size_t history_cap,
+                                     uint32_t* history_len, size_t ngram_size, size_t window,
+                                     const uint32_t* whitelist, size_t n_whitelist, float temperature,
+                                     uint32_t eos_token_id, int32_t append, float* logits, uint32_t* tokens,
+                                     uint8_t* is_eos, uint32_t* route_idx, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    if (!tokens) return fail(FOCR_HIP_E_ARG, "decoder_step_sample: null tokens");
+    if (temperature > 0.0f)  // refused before any layer runs (the sampler refuses it too)
+        return fail(FOCR_HIP_E_NOT_IMPLEMENTED, "native_engine::sampler::decode_step_premasked — temperature>0 "
+                                                "sampling is outside the greedy fp32 spine");
+    float* xn = nullptr;
+    size_t B = 0;
+    int32_t st = decoder_layers_impl(ctx, d, caches, positions, x, route_idx, check_route, &xn, &B);
+    if (st) return st;
+    return lm_head_sample_i8_impl(ctx, d->lm_head, xn, B, history, history_cap, history_len, ngram_size, window,
+                                  whitelist, n_whitelist, temperature, eos_token_id, append, logits, tokens, is_eos,
+                                  check_route);
 }
 
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,

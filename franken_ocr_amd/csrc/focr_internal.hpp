@@ -53,6 +53,7 @@ enum ScratchSlot : int {
     kScrBan,    // sampler ban bitmaps
     kScrLayer,  // decoder layer step intermediates
     kScrAttn,   // prefill attention key-range partials
+    kScrDec,    // decode step: the final-normed rows
     kScrCount
 };
 
@@ -178,6 +179,17 @@ struct focr_hip_decoder_layer {
     // for the one GEMV launch that computes both; owned
     int8_t* gate_up_w = nullptr;
     float* gate_up_s = nullptr;
+};
+
+// decoder.rs DecoderWeightCacheI8 for the decode spine: the layers (borrowed),
+// the final RMSNorm weight (owned device copy) and the LM head (borrowed).
+struct focr_hip_decoder {
+    focr_hip_ctx* ctx = nullptr;
+    size_t hidden = 0, top_k = 0;
+    float eps = 1e-6f;
+    std::vector<const focr_hip_decoder_layer*> layers;
+    float* final_norm = nullptr;  // [hidden]
+    const focr_hip_qint8* lm_head = nullptr;
 };
 
 struct focr_hip_moe_layer_i4 {

@@ -452,3 +452,65 @@ class DecoderLayer:
             self.free()
         except Exception:
             pass
+
+
+class Decoder:
+    """The decode spine of DecoderWeightCacheI8 as one device call per token:
+    the layers in order (borrowed and kept alive here), the final RMSNorm
+    weight (host f32 [hidden]) and the int8 LM head."""
+
+    def __init__(self, layers: list[DecoderLayer], final_norm, lm_head: QInt8, eps: float = 1e-6,
+                 ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self._keep = (list(layers), lm_head)
+        self.n_layers = len(layers)
+        self._h = C.c_void_p()
+        handles = (C.c_void_p * len(layers))(*[layer._h.value for layer in layers])
+        fn = np.ascontiguousarray(final_norm, dtype=np.float32)
+        _abi.call("focr_hip_decoder_create", self.ctx.handle, len(layers), C.cast(handles, C.c_void_p),
+                  fn.ctypes.data_as(C.c_void_p), float(eps), lm_head.handle, C.byref(self._h))
+
+    def _caches(self, caches):
+        if len(caches) != self.n_layers:
+            raise ValueError(f"{len(caches)} caches for {self.n_layers} layers")
+        return (C.c_void_p * len(caches))(*[c._h.value for c in caches])
+
+    def step(self, caches: list["RingCache"], positions, x: DeviceArray, tokens: DeviceArray,
+             logits: DeviceArray | None = None, route_idx: DeviceArray | None = None,
+             check_route: bool = False) -> None:
+        """batched_decode_step_i8 + batched_lm_head_i8 + argmax_row for every
+        stream (decoder.rs:2812-2965, sampler.rs:168-186): x [n_streams, hidden]
+        (device) holds the token embeddings and receives the last layer's
+        hidden rows; tokens [n_streams] the argmax ids; logits (optional)
+        [n_streams, vocab]; route_idx (optional) [n_layers, n_streams, top_k]."""
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        cs = self._caches(caches)
+        _abi.call("focr_hip_decoder_step", self.ctx.handle, self._h, C.cast(cs, C.c_void_p),
+                  pos.ctypes.data_as(C.c_void_p), x.c_ptr, _p(logits), tokens.c_ptr, _p(route_idx),
+                  1 if check_route else 0)
+
+    def step_sample(self, caches: list["RingCache"], positions, x: DeviceArray, tokens: DeviceArray,
+                    history: DeviceArray | None = None, history_len: DeviceArray | None = None,
+                    ngram_size: int = DEFAULT_NO_REPEAT_NGRAM_SIZE, window: int = NGRAM_WINDOW_SINGLE,
+                    whitelist: DeviceArray | None = None, temperature: float = 0.0, eos: int = DEFAULT_EOS_TOKEN_ID,
+                    append: bool = False, logits: DeviceArray | None = None, is_eos: DeviceArray | None = None,
+                    route_idx: DeviceArray | None = None, check_route: bool = False) -> None:
+        """The same step with the no-repeat-ngram greedy sampler in the
+        LM-head epilogue (sampler.rs:426-460, :491-545) instead of the argmax."""
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        cs = self._caches(caches)
+        _abi.call("focr_hip_decoder_step_sample", self.ctx.handle, self._h, C.cast(cs, C.c_void_p),
+                  pos.ctypes.data_as(C.c_void_p), x.c_ptr,
+                  *_sampler_args(history, history_len, ngram_size, window, whitelist, temperature, eos, append),
+                  _p(logits), tokens.c_ptr, _p(is_eos), _p(route_idx), 1 if check_route else 0)
+
+    def free(self) -> None:
+        if self._h:
+            _abi.lib().focr_hip_decoder_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass

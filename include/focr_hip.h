@@ -62,6 +62,7 @@ typedef struct focr_hip_qint8 focr_hip_qint8;
 typedef struct focr_hip_moe_layer focr_hip_moe_layer;
 typedef struct focr_hip_moe_layer_i4 focr_hip_moe_layer_i4;
 typedef struct focr_hip_decoder_layer focr_hip_decoder_layer;
+typedef struct focr_hip_decoder focr_hip_decoder;
 typedef struct focr_hip_rswa focr_hip_rswa;
 typedef struct focr_hip_focrq focr_hip_focrq;
 typedef struct focr_hip_focrq_writer focr_hip_focrq_writer;
@@ -480,6 +481,43 @@ int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_la
 int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
                                        focr_hip_rswa* cache, size_t stream, float* x, size_t cs,
                                        size_t c0, uint32_t* route_idx, int32_t check_route);
+
+/* ---- the whole batched decode step ----------------------------------------
+ * The decode spine of DecoderWeightCacheI8: n_layers layer handles in order
+ * (borrowed: they must outlive the decoder), the final RMSNorm weight (host
+ * [hidden], copied) and the int8 LM head [vocab, hidden] (borrowed). Every
+ * layer has the same hidden size, the MoE layers one top_k. */
+int32_t focr_hip_decoder_create(focr_hip_ctx* ctx, size_t n_layers,
+                                const focr_hip_decoder_layer* const* layers, const float* final_norm,
+                                float rms_eps, const focr_hip_qint8* lm_head, focr_hip_decoder** out);
+int32_t focr_hip_decoder_free(focr_hip_decoder* dec);
+/* One decode token for every stream, in one call: decoder.rs:2812-2933
+ * batched_decode_step_i8 (stream_ids = 0 .. n_streams) through every layer
+ * (each as focr_hip_decoder_layer_step), then :2943-2965 batched_lm_head_i8
+ * (the final RMSNorm per row, the LM head) and sampler.rs:168-186 argmax_row.
+ * caches: n_layers R-SWA caches (layer l's, all with the same n_streams);
+ * positions [n_streams] host; x [n_streams, hidden] device: the token
+ * embeddings in, the last layer's hidden rows out (what
+ * batched_decode_step_i8 returns, before the final norm); logits
+ * [n_streams, vocab] device (nullable); tokens [n_streams] u32 device: the
+ * argmax per row; route_idx (device, nullable) [n_layers][n_streams][top_k]
+ * receives each MoE layer's expert ids (a dense layer's slice untouched).
+ * check_route as focr_hip_decoder_layer_step. */
+int32_t focr_hip_decoder_step(focr_hip_ctx* ctx, const focr_hip_decoder* dec, focr_hip_rswa* const* caches,
+                              const uint32_t* positions, float* x, float* logits, uint32_t* tokens,
+                              uint32_t* route_idx, int32_t check_route);
+/* The same step with the greedy no-repeat-ngram sampler in the LM-head
+ * epilogue instead of the plain argmax: the layers as focr_hip_decoder_step,
+ * then the final RMSNorm and focr_hip_lm_head_sample_i8 with these sampler
+ * arguments (sampler.rs:426-460 decode_step_premasked per stream,
+ * :491-545 batched_decode_step). */
+int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* dec,
+                                     focr_hip_rswa* const* caches, const uint32_t* positions, float* x,
+                                     uint32_t* history, size_t history_cap, uint32_t* history_len,
+                                     size_t ngram_size, size_t window, const uint32_t* whitelist,
+                                     size_t n_whitelist, float temperature, uint32_t eos_token_id,
+                                     int32_t append, float* logits, uint32_t* tokens, uint8_t* is_eos,
+                                     uint32_t* route_idx, int32_t check_route);
 
 /* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
  * The reader restates weights.rs:443-620 (format detection by magic, the
