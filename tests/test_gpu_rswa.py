@@ -181,3 +181,38 @@ def test_rswa_state_errors(ctx):
     with pytest.raises(StateError, match="exceeds ref_capacity"):
         big = ctx.to_device(np.zeros(NH * 17 * D, np.float32))
         cache.record_prefill(0, big, big, 17)
+
+
+def test_rswa_attention_across_cache_shapes(ctx):
+    """Caches of different stream counts and capacities share the context's
+    split-K partials buffer: attended in turn and twice around, including 70
+    streams (two launches of at most 64), each stream within 1e-4 of the
+    oracle and the same answer each time."""
+    from franken_ocr_amd.engine import RingCache
+
+    shapes = [(3, 200), (70, 64), (8, 1024)]
+    setups = []
+    for n, (b, cap) in enumerate(shapes):
+        rng = np.random.default_rng(40 + n)
+        cache = RingCache(b, cap, ctx)
+        rings = [O.Ring(cap) for _ in range(b)]
+        _fill(cache, rings, ctx, b, cap - 5 * n, 900 + 100 * n)
+        _random_rings(cache, rings, ctx, b, rng, 950 + 100 * n)
+        q = synth.f32_normal(synth.seed_of(990 + n), b * NH * D).reshape(b, NH * D)
+        setups.append((cache, rings, q, ctx.to_device(q), ctx.empty((b, NH * D), np.float32)))
+    first = {}
+    for rnd in range(2):
+        for n, (cache, rings, q, dq, dout) in enumerate(setups):
+            _say(f"round {rnd}: {shapes[n][0]} streams, capacity {shapes[n][1]}")
+            cache.decode_attention(dq, dout)
+            got = dout.numpy()
+            if rnd == 0:
+                for s in range(len(rings)):
+                    st, want = rings[s].attend(q[s])
+                    assert st == 0
+                    assert_rel(got[s], want.astype(np.float64), 1e-4)
+                first[n] = got
+            else:
+                assert np.array_equal(got, first[n]), shapes[n]
+    for cache, *_ in setups:
+        cache.free()
