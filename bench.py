@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Default workload (BASELINE.json's metric, config 3 at T = 8): one step is one
+Default workload (the headline metric: config 3 at T = 8): one step is one
 decode MoE layer over T = 8 tokens — router (f32 [64,1280]), top-6 with
 renormalised gates, 64 int8 experts (gate/up [896,1280], down [1280,896],
 per-row f32 scales), SwiGLU, slot-order combine. Inputs are resident in HBM
@@ -707,7 +707,7 @@ def make_i4_layer(seed: int, group: int = 32):
 
 
 def h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, steps, gu_name, dn_name, per_expert_bytes):
-    """SURVEY H5's views of the prefill MoE's int8 MFMA utilisation (ops /
+    """Three views of the prefill MoE's int8 MFMA utilisation (ops /
     time / 5.0 POPS): cold (rotating layer copies, the measured step), warm
     (one layer, MALL-resident) and the compute-bound bucket (every expert at
     M_e >= 195, where ops/byte ~ 3.2 M_e: token t routes to hot[(t + j) % 8],
@@ -738,6 +738,29 @@ def h5_views(ctx, layers, dx, di, dg, dout, idx, T, prof, ms, steps, gu_name, dn
                    "weight_bytes_per_step": 8 * per_expert_bytes},
     }
     return views, ms_w, kernels_w, kernels_b
+
+
+def i4_mfma_ceiling(counts, achieved_tops: float) -> dict:
+    """The fraction of the int8 MFMA peak the int4 grouped GEMM can reach.
+    int4.rs:304-343 scales each 32-wide K group's i32 partial separately:
+    acc += s[n, g] * (f32)acc_g, two VALU instructions (convert, FMA) per
+    output element and group. One v_mfma_i32_32x32x32_i8 is one group of a
+    32 x 32 tile: 32 cycles of the SIMD's matrix core, while its 16 elements
+    per lane cost 32 VALU instructions of 4 cycles each (wave64 on 16 lanes;
+    packed FP32 is not used), so the formulation is VALU-bound at 32 / 128 =
+    0.25 of the MFMA peak. The row tiles (64 rows of one expert, computed as
+    one or two 32-row MFMA tiles) cost their padded rows: ceiling = 0.25 x
+    rows routed / rows computed."""
+    computed = 0
+    for c in counts:
+        for t in range((int(c) + 63) // 64):
+            nr = min(64, int(c) - 64 * t)
+            computed += 32 if nr <= 32 else 64
+    useful = int(counts.sum())
+    ceil = 0.25 * useful / max(computed, 1)
+    frac = achieved_tops / MFMA_INT8_PEAK_TOPS
+    return {"frac": round(ceil, 4), "valu_bound_frac": 0.25, "valu_per_mfma_floor": 32, "rows_routed": useful,
+            "rows_computed": computed, "achieved_of_ceiling": round(frac / ceil, 4)}
 
 
 def bench_prefill_i4(args, ctx):
@@ -782,12 +805,13 @@ def bench_prefill_i4(args, ctx):
         "roofline": {"bound": "mfma", "kernel": "i4_gate_up", "achieved": round(gu_tops, 2),
                      "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(gu_tops / MFMA_INT8_PEAK_TOPS, 4),
                      "traffic": traffic_for("i4_gate_up", f"moe_prefill_i4_m{T}"),
-                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3), **launch_stats(prof, "i4_gate_up")},
+                     "algorithmic_ops_per_launch": gu_ops, "avg_launch_us": round(gu_us, 3), **launch_stats(prof, "i4_gate_up"),
+                     "mfma_ceiling": i4_mfma_ceiling(counts, gu_tops)},
         "layer_mfma": {"achieved_tops": round(layer_tops, 2), "frac": round(layer_tops / MFMA_INT8_PEAK_TOPS, 4),
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
                        "warm_ms_per_step": round(ms_w, 5)},
-        # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
+        # int8 MFMA utilisation three ways (ops / time / 5.0 POPS): cold, warm, the compute-bound bucket
         "mfma_utilisation": views,
         "kernel_avg_us": kernels,
         "step_us": sstats,
@@ -995,7 +1019,7 @@ def bench_prefill_i8(args, ctx):
                        "ops_per_step": gu_ops + dn_ops, "weight_bytes_per_step": wbytes,
                        "hbm_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
                        "warm_ms_per_step": round(ms_w, 5)},
-        # SURVEY H5's three views of int8 MFMA utilisation (ops / time / 5.0 POPS)
+        # int8 MFMA utilisation three ways (ops / time / 5.0 POPS): cold, warm, the compute-bound bucket
         "mfma_utilisation": views,
         "kernel_avg_us": kernels,
         "step_us": sstats,
@@ -1464,7 +1488,7 @@ WORKLOADS = {
 
 # Secondary configurations measured after the headline in the default run and
 # reported under "extra" (key, workload, tokens, copies, steps, warmup): the
-# other SURVEY configs and the prefill paths, each timed the same way as its
+# other configs and the prefill paths, each timed the same way as its
 # own --workload run, with fewer steps.
 EXTRAS = [
     ("cfg1_igemm_m16", "igemm", 16, 64, 200, 20),

@@ -359,7 +359,7 @@ __device__ __forceinline__ void s4_tile(const int8_t* __restrict__ A, int K, int
                     const float xs = s_rs[m];
                     const float g = ((t ? acc1[v] : acc0[v]) * kOut) * xs;
                     const float u = (xu[m * 64 + wcol * 32 + (l & 31)] * kOut) * xs;
-                    ep.out[static_cast<size_t>(r0 + m) * N + n] = silu_f(g) * u;
+                    ep.out[static_cast<size_t>(r0 + m) * N + n] = silu_fast(g) * u;
                 }
             }
         }

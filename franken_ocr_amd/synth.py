@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configs (numpy, vectorised).
+"""Seeded synthetic inputs for the benchmark configs (numpy, vectorised).
 
 A counter-based generator: value ``i`` of the stream for tensor seed ``s``
 is splitmix64's i-th output, ``mix(s + (i + 1) * 0x9E3779B97F4A7C15)``, so a

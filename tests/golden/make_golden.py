@@ -2,7 +2,7 @@
 
     python tests/golden/make_golden.py
 
-Writes small seeded instances of every BASELINE config (inputs + the
+Writes small seeded instances of every benchmark config (inputs + the
 oracle's outputs) as compressed .npz, the 24 self-test i32 vectors of
 dispatch.rs:352-429, and the reference's in-code known answers as JSON.
 The reference (Rust) cannot run here; its known answers are copied as data

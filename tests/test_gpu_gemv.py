@@ -1,7 +1,7 @@
 """GPU parity for the decode GEMV and the LM head + argmax on uploaded int8
 weights (decoder.rs:1607-1640, :2703-2747, :2275-2296; sampler.rs:168-186).
 The f32 logits are expected bit-exact (same IEEE ops in the same order);
-BASELINE's floor is rel 1e-4. Argmax ids are bit-exact."""
+The configs' floor is rel 1e-4. Argmax ids are bit-exact."""
 
 from __future__ import annotations
 

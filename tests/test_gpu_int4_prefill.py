@@ -2,7 +2,7 @@
 structure of decoder.rs:2142-2181 over int4 experts on the gfx950 matrix
 cores — against the CPU oracle (oracle_moe_prefill_i4), through the C ABI.
 
-Tolerance: layer output within rel 1e-3 (BASELINE cfg4's f32 bar; relative
+Tolerance: layer output within rel 1e-3 (config 4's f32 bar; relative
 to each element, floored at 1% of its row's largest magnitude). The int4 GEMMs themselves are bit-exact (the drop-in entry runs the
 same MFMA kernel and is compared exactly in test_gpu_tier.py); the slack is
 for SiLU's expf, whose last-ulp differences from the host libm can move a

@@ -1,6 +1,6 @@
 """GPU parity for the MoE decode layer (moe.rs:181-266 route;
 decoder.rs:2199-2268 decode_mlp_i8 per token): routing indices bit-exact,
-gates within rel 1e-6, layer output within rel 1e-3 (BASELINE cfg3) — the
+gates within rel 1e-6, layer output within rel 1e-3 (config 3's tolerance) — the
 only f32 differences come from expf in SiLU (~1 ulp) propagating through
 the act re-quantization."""
 

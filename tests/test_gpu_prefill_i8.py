@@ -5,7 +5,7 @@ accumulation): nn::linear_int8_dynamic (nn.rs:151-173) and moe_block_i8
 The linear's outputs are bit-exact: the activation bytes follow the same
 rule (true division, ties to even), the i32 sums are exact, and the dequant
 is the same two rounded multiplies (+ bias). The MoE block is compared within
-rel 1e-3 (the layer-output tolerance of the BASELINE MoE config): SiLU goes
+rel 1e-3 (the MoE configs' layer-output tolerance): SiLU goes
 through expf, which may differ from glibc's by an ulp and flip an act code
 in the re-quantization, everything else is the same arithmetic."""
 

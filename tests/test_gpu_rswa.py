@@ -1,5 +1,5 @@
 """GPU parity for R-SWA: ring write regimes bit-exact (slots, cursors, the
-written rows), decode attention within rel 1e-4 (BASELINE cfg5) of the CPU
+written rows), decode attention within rel 1e-4 (config 5's tolerance) of the CPU
 online-softmax path (rswa.rs:894-939), B = 8 streams, G = 1024 reference
 rows, ring at random fill level and wrap offset."""
 

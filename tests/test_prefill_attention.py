@@ -1,7 +1,7 @@
 """Prefill attention (decoder.rs:568-640) and chunked prefill attention
 (decoder.rs:1282-1340) on the f32 matrix cores, against the CPU oracle.
 
-Tolerance: rel 1e-4 (BASELINE's attention bound) against the oracle, which
+Tolerance: rel 1e-4 (the attention tolerance) against the oracle, which
 evaluates the attention math in float64 and rounds once: the reference's
 attention runs in ft-kernel-cpu (un-vendored, f32, unknown summation order),
 and any f32 evaluation is about 1e-4 from the exact result at 1024 keys, so
