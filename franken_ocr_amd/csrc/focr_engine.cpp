@@ -672,8 +672,9 @@ int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* h
 // The route kernel writes flag[t] = 1 for a token with fewer than top_k
 // finite router scores (moe.rs:261-265). Reading it synchronises.
 int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
-    int flags[kMoeMaxT] = {};  // t <= kMoeMaxT (moe_checks)
-    FOCR_HIP_TRY(hipMemcpyAsync(flags, dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "D2H route flag");
+    std::vector<int> flags(t);
+    FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+                 "D2H route flag");
     FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (size_t i = 0; i < t; ++i)
         if (flags[i]) return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", i));
@@ -695,9 +696,49 @@ int32_t launch_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float
 
 extern "C" {
 
+// route (moe.rs:181-266) of t rows (up to kRouteRowsMax) without the decode
+// kernels' selection matrices: idx / gates [t][top_k], probs [t][E]
+// (nullable), flag [t] (1: fewer than top_k finite scores). The split route
+// kernel; its exchange buffer grows to t tokens (zeroed when it grows) and a
+// one-thread launch advances the buffer's counter after it.
+constexpr size_t kRouteRowsMax = 16384;
+static int32_t route_rows_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
+                               int32_t norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs,
+                               int* flag) {
+    const size_t xb = moe_route_xchg_bytes(t);
+    const bool grow = ctx->scratch[kScrRouteX].cap < xb;
+    void* xchg = ctx->scratch_get(kScrRouteX, xb);
+    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
+    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
+    if (!xchg || !xq || !xs) return FOCR_HIP_E_OOM;
+    if (grow) FOCR_HIP_TRY(hipMemsetAsync(xchg, 0, ctx->scratch[kScrRouteX].cap, ctx->stream), "route exchange zero");
+    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+    {
+        ProfScope ps(ctx, "moe_route");
+        FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, x, L->router, norm_topk, routed_scale, xq, xs, idx, gates, probs,
+                                      flag, nullptr, xchg, ctx->route_wait_ticks),
+                     "route launch");
+    }
+    FOCR_HIP_TRY(launch_route_epoch_bump(ctx->stream, xchg), "route epoch launch");
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
                            int32_t norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs) {
     ENGINE_CTX(ctx);
+    if (t > static_cast<size_t>(kMoeMaxT)) {
+        // prefill-sized calls (moe.rs:181-243 routes every row of a chunk)
+        if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "moe_route: null moe layer");
+        if (!hidden) return fail(FOCR_HIP_E_ARG, "moe_route: null hidden");
+        if (t > kRouteRowsMax)
+            return fail(FOCR_HIP_E_SHAPE, fmt("moe_route: t %zu outside 1..=%zu for one call", t, kRouteRowsMax));
+        if (!idx || !gates) return fail(FOCR_HIP_E_ARG, "moe_route: idx and gates are required above 64 rows");
+        int* flag = static_cast<int*>(ctx->scratch_get(kScrFlag, t * sizeof(int)));
+        if (!flag) return FOCR_HIP_E_OOM;
+        int32_t st = route_rows_impl(ctx, L, hidden, t, norm_topk, routed_scale, idx, gates, probs, flag);
+        if (st) return st;
+        return check_route_flags(ctx, flag, t);
+    }
     int32_t st = moe_checks("moe_route", L, hidden, t, 0);
     if (st) return st;
     MoeScratch s;
@@ -1640,28 +1681,10 @@ int32_t focr_hip_rswa_prefill_chunk(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t 
 // ---- one decoder layer over a prefill chunk (decoder.rs:2428-2520) ---------------
 
 // route_default (moe.rs:273-280: norm_topk_prob false, scaling 1.0) of a
-// prefill chunk's t rows: idx / gates [t][top_k], flag [t] (1: fewer than
-// top_k finite scores). The split route kernel without the decode kernels'
-// selection matrices; its exchange buffer grows to t tokens (zeroed when it
-// grows) and a one-thread launch advances the buffer's counter after it.
+// prefill chunk's t rows
 static int32_t prefill_route_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
                                   uint32_t* idx, float* gates, int* flag) {
-    const size_t xb = moe_route_xchg_bytes(t);
-    const bool grow = ctx->scratch[kScrRouteX].cap < xb;
-    void* xchg = ctx->scratch_get(kScrRouteX, xb);
-    int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, t * L->hidden));
-    float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, t * sizeof(float)));
-    if (!xchg || !xq || !xs) return FOCR_HIP_E_OOM;
-    if (grow) FOCR_HIP_TRY(hipMemsetAsync(xchg, 0, ctx->scratch[kScrRouteX].cap, ctx->stream), "route exchange zero");
-    const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
-    {
-        ProfScope ps(ctx, "moe_route");
-        FOCR_HIP_TRY(launch_moe_route(ctx->stream, d, x, L->router, 0, 1.0f, xq, xs, idx, gates, nullptr, flag,
-                                      nullptr, xchg, ctx->route_wait_ticks),
-                     "prefill route launch");
-    }
-    FOCR_HIP_TRY(launch_route_epoch_bump(ctx->stream, xchg), "route epoch launch");
-    return FOCR_HIP_OK;
+    return route_rows_impl(ctx, L, x, t, 0, 1.0f, idx, gates, nullptr, flag);
 }
 
 int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,

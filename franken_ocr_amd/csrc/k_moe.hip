@@ -1,13 +1,13 @@
 // k_moe.hip — the MoE decode layer (decoder.rs:2199-2268 decode_mlp_i8 over
 // T tokens) as four stream-ordered kernels:
 //
-//   route    one block per token: router logits as f64 dot products rounded
-//            to f32, quantize_row_i8 of the token row, f64 softmax rounded to
-//            f32, greedy top-k (= rank by (prob desc, index asc), NaN
-//            skipped; moe.rs:209-266), optional renorm and scale
-//            (moe.rs:226-236). Writes idx/gates [t][k] and the selection
-//            matrices slot[e][t] / gate[e][t]; no atomics, nothing carried
-//            between calls.
+//   route    eight blocks per token on one XCD (below): router logits as f64
+//            dot products rounded to f32, quantize_row_i8 of the token row,
+//            f64 softmax rounded to f32, greedy top-k (= rank by (prob desc,
+//            index asc), NaN skipped; moe.rs:209-266), optional renorm and
+//            scale (moe.rs:226-236). Writes idx/gates [t][k] and the
+//            selection matrices slot[e][t] / gate[e][t]; no atomics; the only
+//            state between calls is the logit exchange's tag counter.
 //   gate_up  grid (active-expert slot a, row block): one ballot over the
 //            experts' slot rows gives the active set and the a-th expert;
 //            issues the expert's gate and up row loads, stages the token rows

@@ -301,9 +301,11 @@ int32_t focr_hip_moe_decode_noalloc(focr_hip_ctx* ctx, const focr_hip_moe_layer*
 /* Size in bytes of the per-GPU static scratch of the allocation-free entry
  * points. */
 size_t focr_hip_static_scratch_bytes(void);
-/* moe.rs:181-266 route alone: idx/gates [t, top_k] device pointers; probs
- * (nullable) receives the f32 softmax [t, E]. Synchronises to report
- * E_ROUTE. */
+/* moe.rs:181-266 route alone for t rows, 1 <= t <= 16384 (a decode step or
+ * every row of a prefill chunk, moe.rs:181-243): idx/gates [t, top_k]
+ * device pointers (required above 64 rows); probs (nullable) receives the
+ * f32 softmax [t, E]. Synchronises to report E_ROUTE for the first row with
+ * no finite router score. */
 int32_t focr_hip_moe_route(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
                            const float* hidden, size_t t, int32_t norm_topk, float routed_scale,
                            uint32_t* idx, float* gates, float* probs);

@@ -52,7 +52,7 @@ def gpu_layer(ctx, layer_w):
     return MoeLayer(H, I, E, K, *layer_w, ctx=ctx)
 
 
-@pytest.mark.parametrize("t", [1, 8, 32, 64])
+@pytest.mark.parametrize("t", [1, 8, 32, 64, 65, 300, 1024])
 @pytest.mark.parametrize("norm_topk", [True, False])
 def test_route_bit_exact(ctx, gpu_layer, layer_w, t, norm_topk):
     _say(f"route t={t} norm={norm_topk}")
@@ -218,12 +218,16 @@ def test_moe_shared_expert_grouped_path(ctx, layer_w):
     assert_rel(dout.numpy(), out.astype(np.float64), 1e-3)
 
 
-def test_route_nan_reports_error(ctx, gpu_layer):
+@pytest.mark.parametrize("t", [2, 200])
+def test_route_nan_reports_error(ctx, gpu_layer, t):
+    """A row without a finite router score is reported (moe.rs:261-265),
+    also past 64 rows (the prefill-sized route), naming the first such row."""
     from franken_ocr_amd._abi import RouteError
 
-    x = np.full((2, H), np.nan, np.float32)
-    didx, dg = ctx.empty((2, K), np.uint32), ctx.empty((2, K), np.float32)
-    with pytest.raises(RouteError, match="no finite router score"):
+    x = synth.f32_normal(synth.seed_of(290), t * H).reshape(t, H)
+    x[t - 1] = np.nan
+    didx, dg = ctx.empty((t, K), np.uint32), ctx.empty((t, K), np.float32)
+    with pytest.raises(RouteError, match=f"no finite router score for token {t - 1}"):
         gpu_layer.route(ctx.to_device(x), didx, dg)
 
 
