@@ -489,7 +489,9 @@ void free_moe(focr_hip_moe_layer* L) {
         hipFree(L->ssu);
         hipFree(L->ssd);
     }
-    for (int8_t* p : {L->wg_mfma, L->wu_mfma, L->wd_mfma, L->swg_mfma, L->swu_mfma, L->swd_mfma}) hipFree(p);
+    for (int8_t* p : {L->wg_mfma, L->wu_mfma, L->wd_mfma, L->swg_mfma, L->swu_mfma, L->swd_mfma, L->swgu_cat})
+        hipFree(p);
+    hipFree(L->ssgu_cat);
 }
 
 }  // namespace
@@ -563,10 +565,12 @@ int32_t focr_hip_moe_layer_set_shared(focr_hip_moe_layer* L, size_t shared_inter
         hipFree(L->ssu);
         hipFree(L->ssd);
     }
-    for (int8_t** p : {&L->swg_mfma, &L->swu_mfma, &L->swd_mfma}) {  // rebuilt by the next prefill
+    for (int8_t** p : {&L->swg_mfma, &L->swu_mfma, &L->swd_mfma, &L->swgu_cat}) {  // rebuilt by the next prefill
         hipFree(*p);
         *p = nullptr;
     }
+    hipFree(L->ssgu_cat);
+    L->ssgu_cat = nullptr;
     L->shared_inter = shared_inter;
     L->swg = tmp.swg;
     L->ssg = tmp.ssg;
@@ -1040,6 +1044,23 @@ static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w
     if (!i8_mfma_supported(static_cast<int>(w->k)))
         return fail(FOCR_HIP_E_SHAPE,
                     fmt("linear_int8_dynamic: k %zu is not a multiple of 64 (the matrix-core K stage)", w->k));
+    // up to 256 rows without a bias, where it is the faster: the split-K GEMV
+    // in 16-row groups on the upload layout (a prefill chunk's o_proj gets 10
+    // blocks of the tiled GEMM at this size, (n / 16) x (m / 16) here)
+    if (!bias && gemv_rows_preferred((int)w->n, (int)w->k, (int)m, false)) {
+        int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
+        float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
+        if (!xq || !xs) return FOCR_HIP_E_OOM;
+        {
+            ProfScope ps(ctx, "quantize_rows_dyn");
+            FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
+                         "quantize launch");
+        }
+        ProfScope ps(ctx, "linear_i8");
+        FOCR_HIP_TRY(launch_gemv_i8_rows(ctx->stream, w->w, w->scales, (int)w->n, (int)w->k, xq, xs, (int)m, y),
+                     "linear_i8 launch");
+        return FOCR_HIP_OK;
+    }
     // 256 rows and up: 256 x 128 LDS-staged tiles on the tiled operands;
     // fewer: 64-row tiles on the fragment-order weight copy
     const bool big = i8_gemm256_supported((int)m, (int)w->n, (int)w->k);
@@ -1117,6 +1138,26 @@ static int32_t moe_prefill_i8_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* 
             (st = ensure_tiled(ctx, &L->swu_mfma, L->swu, 1, S, H, "moe_prefill_i8")) ||
             (st = ensure_tiled(ctx, &L->swd_mfma, L->swd, 1, H, S, "moe_prefill_i8")))
             return st;
+        // chunks of up to 256 rows: the shared expert's products on the split-K
+        // GEMV, whose SwiGLU form reads the gate rows then the up rows
+        if (!L->swgu_cat && gemv_rows_preferred((int)S, (int)H, (int)t, true)) {
+            int8_t* w = nullptr;
+            float* sc = nullptr;
+            hipError_t e = hipMalloc(&w, 2 * S * H);
+            if (e == hipSuccess) e = hipMalloc(&sc, 2 * S * sizeof(float));
+            if (e == hipSuccess) e = hipMemcpyAsync(w, L->swg, S * H, hipMemcpyDeviceToDevice, ctx->stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(w + S * H, L->swu, S * H, hipMemcpyDeviceToDevice, ctx->stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(sc, L->ssg, S * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(sc + S, L->ssu, S * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+            if (e != hipSuccess) {
+                hipFree(w);
+                hipFree(sc);
+                return hip_fail(e, "moe_prefill_i8: shared gate/up copy");
+            }
+            L->swgu_cat = w;
+            L->ssgu_cat = sc;
+        }
     }
     auto take = [](char*& p, size_t bytes) {
         char* r = p;

@@ -155,6 +155,11 @@ struct focr_hip_moe_layer {
     // first prefill call; always owned
     mutable int8_t *wg_mfma = nullptr, *wu_mfma = nullptr, *wd_mfma = nullptr;
     mutable int8_t *swg_mfma = nullptr, *swu_mfma = nullptr, *swd_mfma = nullptr;
+    // the shared expert's gate rows then up rows ([2 shared_inter][hidden])
+    // and their scales, for the SwiGLU product of prefill chunks; built on
+    // the first prefill call; always owned
+    mutable int8_t* swgu_cat = nullptr;
+    mutable float* ssgu_cat = nullptr;
 };
 
 // One decoder layer for decode steps (decoder.rs:1971-1982 CachedLayerI8):
@@ -307,6 +312,19 @@ hipError_t launch_gemv_i8_banned(hipStream_t s, const int8_t* w, const float* ws
 // to h_out, in one launch; the quantize kernel; y = dequant(W . xq) + resid.
 // Each returns hipErrorNotSupported where its shape is outside the one-launch
 // form (the caller then runs the separate kernels).
+// prefill-sized int8 products (1 <= m <= kRowsMaxM prequantized rows) on the
+// split-K GEMV in 16-row groups: y = ((f32)acc * xs) * ws [m][n]; the SwiGLU
+// form takes the gate rows then the up rows ([2n][k], scales [2n]) and
+// writes act = silu(g) * u [m][n]
+constexpr int kRowsMaxM = 256;
+bool gemv_rows_supported(int n, int k, int m);
+// whether that path is the faster one for the shape (its L2 re-reads grow with
+// the block count)
+bool gemv_rows_preferred(int n, int k, int m, bool swiglu);
+hipError_t launch_gemv_i8_rows(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
+                               const float* xs, int m, float* y);
+hipError_t launch_swiglu_i8_rows(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
+                                 const int8_t* xq, const float* xs, int m, float* act);
 hipError_t launch_swiglu_i8_f32_add(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
                                     const float* x, const float* x2, float* h_out, const float* norm_w, float eps,
                                     int m, float* act, int cu_count);

@@ -289,6 +289,10 @@ __device__ __forceinline__ void fq_rows2_to_lds(const float4 (&v0)[NF], const fl
 struct IgemmMode {
     int accumulate;
     size_t sw, sx, so;
+    // row groups (the split-K kernel, rows > 0): blockIdx.y takes activation
+    // rows [16 y, 16 y + 16) of `rows`; y and a_scales advance by sy / sa
+    size_t sy, sa;
+    int rows;
 };
 
 // FQ: the <= 16 activation rows come as f32 (xf [M][K], K % 64 == 0,
@@ -549,6 +553,9 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_mfma_splitk_kernel(
         W += blockIdx.y * im.sw;
         xq += blockIdx.y * im.sx;
         acc_out += blockIdx.y * im.so;
+        if (y) y += blockIdx.y * im.sy;
+        if (a_scales) a_scales += blockIdx.y * im.sa;
+        if (im.rows > 0) M = min(16, im.rows - 16 * static_cast<int>(blockIdx.y));  // block-uniform
     }
     __shared__ v4i_m red[kThreads / 64][64];
     __shared__ v4i_m red_u[SWIGLU ? kThreads / 64 : 1][64];  // SWIGLU: the up tile's partials
@@ -1001,6 +1008,65 @@ hipError_t launch_gemv_i8_resid(hipStream_t s, const int8_t* w, const float* ws,
                         k, xq_r, a_scales + r0, mr, y_r, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, IgemmMode{}, ra);
     }
     return hipGetLastError();
+}
+
+// Prefill-sized products on the split-K kernel: m <= kRowsMaxM prequantized
+// rows xq [m][k] with scales xs [m], in groups of 16 on grid.y (each block
+// stages its group's rows and takes 16 output columns, the four waves on
+// interleaved 256-byte K chunks); the weight rows come from L2 for every
+// group after the first. y = ((f32)acc * xs) * ws, the linear's epilogue
+// (SWIGLU: w_gu holds the gate rows then the up rows, act = silu(g) * u).
+bool gemv_rows_supported(int n, int k, int m) {
+    if (m < 1 || m > kRowsMaxM || n < 1 || k < 64 || k % 64 != 0 || k > 256 * 4 * kSplitKMaxChunks) return false;
+    const size_t lds = (static_cast<size_t>(16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) * sizeof(int4);
+    const size_t lds_static = (kThreads / 64) * 64 * sizeof(int4) * 2 + 16 * sizeof(float);
+    return lds + lds_static <= max_lds_per_block();
+}
+
+// Every block re-reads its 16 activation rows and its 16 (SwiGLU: 32) weight
+// rows through L2, so past about 2048 blocks of that traffic the tiled GEMMs
+// are faster despite their few blocks (measured at m = 256, k = 1280: n =
+// 1280 9.7 us here against 15.7; n = 3840 21.4 against 15.7).
+bool gemv_rows_preferred(int n, int k, int m, bool swiglu) {
+    if (!gemv_rows_supported(n, k, m)) return false;
+    const long blocks = static_cast<long>((n + 15) / 16) * ((m + 15) / 16) * (swiglu ? 2 : 1);
+    return blocks <= 2048;
+}
+
+template <bool SWIGLU>
+static hipError_t launch_rows(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
+                              const float* xs, int m, float* y) {
+    if (!gemv_rows_supported(n, k, m)) return hipErrorInvalidValue;
+    const size_t lds = (static_cast<size_t>(m < 16 ? m : 16) * (k / 16 + 1) + (kThreads / 64) * kMfmaTileBytes / 16) *
+                       sizeof(int4);
+    const dim3 grid((n + 15) / 16, (m + 15) / 16);
+    IgemmMode im{};
+    im.sx = static_cast<size_t>(16) * k;
+    im.sy = static_cast<size_t>(16) * n;
+    im.sa = 16;
+    im.rows = m;
+    const int mr = m < 16 ? m : 16;
+    const int cpw = ((k + 255) / 256 + 3) / 4;
+    if (cpw <= 2)
+        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<2, false, false, kFqMaxK / 256, false, SWIGLU>), grid, dim3(kThreads),
+                    lds, s, w, ws, n, k, xq, xs, mr, y, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
+    else if (cpw <= 4)
+        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<4, false, false, kFqMaxK / 256, false, SWIGLU>), grid, dim3(kThreads),
+                    lds, s, w, ws, n, k, xq, xs, mr, y, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
+    else
+        FOCR_LAUNCH((gemv_i8_mfma_splitk_kernel<8, false, false, kFqMaxK / 256, false, SWIGLU>), grid, dim3(kThreads),
+                    lds, s, w, ws, n, k, xq, xs, mr, y, nullptr, nullptr, nullptr, 0.0f, RopeEpi{}, im, RowAdd{});
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_i8_rows(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
+                               const float* xs, int m, float* y) {
+    return launch_rows<false>(s, w, ws, n, k, xq, xs, m, y);
+}
+
+hipError_t launch_swiglu_i8_rows(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
+                                 const int8_t* xq, const float* xs, int m, float* act) {
+    return launch_rows<true>(s, w_gu, ws_gu, n, k, xq, xs, m, act);
 }
 
 hipError_t launch_permute_rows_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k, int D, int head_dim,

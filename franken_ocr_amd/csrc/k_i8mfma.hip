@@ -377,15 +377,23 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     if (with_shared) {
         const int SI = static_cast<int>(L->shared_inter);
         ProfScope ps(ctx, "i8_shared");
-        if ((e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg_mfma, L->ssg, L->swu_mfma, L->ssu, SI, w.shared_act)) !=
-            hipSuccess)
-            return e;
+        // up to 256 rows, where it is the faster: the split-K GEMV in 16-row
+        // groups (the tiled GEMMs launch 20-56 blocks at this size); the same
+        // products and epilogue expressions
+        const bool rows_gu = L->swgu_cat && gemv_rows_preferred(SI, H, t, true);
+        const bool rows_d = gemv_rows_preferred(H, SI, t, false);
+        if (rows_gu)
+            e = launch_swiglu_i8_rows(s, L->swgu_cat, L->ssgu_cat, SI, H, w.xq, w.xs, t, w.shared_act);
+        else
+            e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg_mfma, L->ssg, L->swu_mfma, L->ssu, SI, w.shared_act);
+        if (e != hipSuccess) return e;
         if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
             hipSuccess)
             return e;
-        if ((e = launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd_mfma, L->ssd, H, nullptr, w.shared_y)) !=
-            hipSuccess)
-            return e;
+        e = rows_d ? launch_gemv_i8_rows(s, L->swd, L->ssd, H, SI, w.shared_aq, w.shared_as, t, w.shared_y)
+                   : launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd_mfma, L->ssd, H, nullptr,
+                                      w.shared_y);
+        if (e != hipSuccess) return e;
     }
     {
         ProfScope ps(ctx, "i8_combine");

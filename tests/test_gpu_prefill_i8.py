@@ -37,7 +37,8 @@ def assert_rel(got, want, rtol):
                                         (100, 1280, 3840, True), (513, 896, 1280, False), (7, 6848, 64, True),
                                         (130, 1792, 300, False), (256, 1280, 256, True), (700, 960, 1000, True),
                                         (300, 6848, 96, False), (512, 1280, 6848, True), (257, 192, 33, True),
-                                        (256, 8256, 40, True)])
+                                        (256, 8256, 40, True), (256, 1280, 1280, False), (17, 1280, 3840, False),
+                                        (200, 6848, 1280, False), (256, 1792, 1280, False)])
 def test_linear_i8_dynamic_bit_exact(ctx, m, k, n, bias):
     from franken_ocr_amd.engine import QInt8, linear_i8_dynamic
 
