@@ -675,13 +675,15 @@ int32_t moe_checks(const char* name, const focr_hip_moe_layer* L, const float* h
 
 // The route kernel writes flag[t] = 1 for a token with fewer than top_k
 // finite router scores (moe.rs:261-265). Reading it synchronises.
-int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t) {
+// token_base: the first row's index in the caller's call (chunked calls).
+int32_t check_route_flags(focr_hip_ctx* ctx, const int* dflag, size_t t, size_t token_base = 0) {
     std::vector<int> flags(t);
     FOCR_HIP_TRY(hipMemcpyAsync(flags.data(), dflag, t * sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
                  "D2H route flag");
     FOCR_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (size_t i = 0; i < t; ++i)
-        if (flags[i]) return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", i));
+        if (flags[i])
+            return fail(FOCR_HIP_E_ROUTE, fmt("moe::route: no finite router score for token %zu", token_base + i));
     return FOCR_HIP_OK;
 }
 
@@ -769,7 +771,7 @@ namespace {
 int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
                         int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
                         float* gates, int32_t check_route, const float* resid, bool static_scratch = false,
-                        const MoeRouteNorm* norm = nullptr) {
+                        const MoeRouteNorm* norm = nullptr, size_t token_base = 0) {
     const char* name = static_scratch ? "moe_decode_noalloc" : "moe_decode";
     int32_t st = moe_checks(name, L, hidden, t, with_shared);
     if (st) return st;
@@ -842,7 +844,7 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
                                     resid, out, (int)L->inter);
     }
     if (e != hipSuccess) return hip_fail(e, "moe_decode launch");
-    if (check_route) return check_route_flags(ctx, s.flag, t);
+    if (check_route) return check_route_flags(ctx, s.flag, t, token_base);
     return FOCR_HIP_OK;
 }
 
@@ -850,12 +852,38 @@ int32_t moe_decode_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const fl
 
 extern "C" {
 
+// Calls of more than kMoeMaxT rows run as consecutive chunks of kMoeMaxT
+// (every token's routing and expert outputs are independent of the others',
+// so the rows are the ones a single call would give).
+constexpr size_t kMoeDecodeMaxT = 16384;
+static int32_t moe_decode_chunked(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
+                                  int32_t norm_topk, float routed_scale, int32_t with_shared, float* out,
+                                  uint32_t* idx, float* gates, int32_t check_route, bool static_scratch) {
+    if (t <= static_cast<size_t>(kMoeMaxT))
+        return moe_decode_impl(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
+                               nullptr, static_scratch);
+    const char* name = static_scratch ? "moe_decode_noalloc" : "moe_decode";
+    if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("%s: null moe layer", name));
+    if (!hidden || !out) return fail(FOCR_HIP_E_ARG, fmt("%s: null hidden or out", name));
+    if (t > kMoeDecodeMaxT)
+        return fail(FOCR_HIP_E_SHAPE, fmt("%s: t %zu outside 1..=%zu for one call", name, t, kMoeDecodeMaxT));
+    const size_t H = L->hidden, K = L->top_k;
+    for (size_t t0 = 0; t0 < t; t0 += kMoeMaxT) {
+        const size_t n = std::min<size_t>(kMoeMaxT, t - t0);
+        int32_t st = moe_decode_impl(ctx, L, hidden + t0 * H, n, norm_topk, routed_scale, with_shared, out + t0 * H,
+                                     idx ? idx + t0 * K : nullptr, gates ? gates + t0 * K : nullptr, check_route,
+                                     nullptr, static_scratch, nullptr, t0);
+        if (st) return st;
+    }
+    return FOCR_HIP_OK;
+}
+
 int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
                             int32_t norm_topk, float routed_scale, int32_t with_shared, float* out, uint32_t* idx,
                             float* gates, int32_t check_route) {
     ENGINE_CTX(ctx);
-    return moe_decode_impl(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
-                           nullptr);
+    return moe_decode_chunked(ctx, L, hidden, t, norm_topk, routed_scale, with_shared, out, idx, gates, check_route,
+                              false);
 }
 
 int32_t focr_hip_moe_decode_noalloc(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* hidden, size_t t,
@@ -1481,8 +1509,32 @@ static int32_t decoder_layer_step_impl(focr_hip_ctx* ctx, const focr_hip_decoder
     if (L->n_heads != 10 || L->head_dim != 128)
         return fail(FOCR_HIP_E_SHAPE, "decoder_layer_step: the R-SWA cache holds 10 heads x 128");
     const size_t max_b = L->gate ? std::min<size_t>(32, 57344 / L->gate->n) : 32;
-    if (B < 1 || B > max_b)
-        return fail(FOCR_HIP_E_SHAPE, fmt("decoder_layer_step: %zu streams outside 1..=%zu", B, max_b));
+    if (B < 1) return fail(FOCR_HIP_E_SHAPE, "decoder_layer_step: no streams");
+    if (B > max_b) {
+        // more streams than one pass takes: groups of max_b streams, each
+        // through a view of the cache that holds just its streams' regions
+        // and cursors (every stream's step is independent of the others')
+        for (size_t s0 = 0; s0 < B; s0 += max_b) {
+            const size_t n = std::min(max_b, B - s0);
+            focr_hip_rswa view;
+            view.ctx = cache->ctx;
+            view.n_streams = n;
+            view.ref_capacity = cache->ref_capacity;
+            view.base = cache->ref_k(s0);
+            view.prefill_len.assign(cache->prefill_len.begin() + s0, cache->prefill_len.begin() + s0 + n);
+            view.ring_len.assign(cache->ring_len.begin() + s0, cache->ring_len.begin() + s0 + n);
+            view.ring_pos.assign(cache->ring_pos.begin() + s0, cache->ring_pos.begin() + s0 + n);
+            const size_t K = L->moe ? L->moe->top_k : 0;
+            int32_t st = decoder_layer_step_impl(ctx, L, &view, positions + s0, x + s0 * H,
+                                                 route_idx ? route_idx + s0 * K : nullptr, check_route);
+            // the cursors the group's launches were made with (the step's
+            // launches are issued; the ring slots advance with them)
+            std::copy(view.ring_len.begin(), view.ring_len.end(), cache->ring_len.begin() + s0);
+            std::copy(view.ring_pos.begin(), view.ring_pos.end(), cache->ring_pos.begin() + s0);
+            if (st) return st;
+        }
+        return FOCR_HIP_OK;
+    }
     const size_t I = L->gate ? L->gate->n : 0;
     // one scratch slot carved into the step's intermediates
     const size_t fl = B * (3 * D + D + D + H + H + H) + (L->gate ? 3 * B * I : 0);
@@ -1928,7 +1980,14 @@ int32_t focr_hip_decoder_step(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr
     size_t B = 0;
     int32_t st = decoder_layers_impl(ctx, d, caches, positions, x, route_idx, check_route, &xn, &B);
     if (st) return st;
-    return lm_head_i8_impl(ctx, d->lm_head, xn, B, logits, tokens);
+    // the LM head takes up to 32 rows per pass
+    const size_t H = d->hidden, V = d->lm_head->n;
+    for (size_t r0 = 0; r0 < B; r0 += 32) {
+        const size_t m = std::min<size_t>(32, B - r0);
+        if ((st = lm_head_i8_impl(ctx, d->lm_head, xn + r0 * H, m, logits ? logits + r0 * V : nullptr, tokens + r0)))
+            return st;
+    }
+    return FOCR_HIP_OK;
 }
 
 int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr_hip_rswa* const* caches,
@@ -1946,9 +2005,18 @@ int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* 
     size_t B = 0;
     int32_t st = decoder_layers_impl(ctx, d, caches, positions, x, route_idx, check_route, &xn, &B);
     if (st) return st;
-    return lm_head_sample_i8_impl(ctx, d->lm_head, xn, B, history, history_cap, history_len, ngram_size, window,
-                                  whitelist, n_whitelist, temperature, eos_token_id, append, logits, tokens, is_eos,
-                                  check_route);
+    // the sampling LM head takes up to 32 rows per pass
+    const size_t H = d->hidden, V = d->lm_head->n;
+    for (size_t r0 = 0; r0 < B; r0 += 32) {
+        const size_t m = std::min<size_t>(32, B - r0);
+        if ((st = lm_head_sample_i8_impl(ctx, d->lm_head, xn + r0 * H, m, history ? history + r0 * history_cap : nullptr,
+                                         history_cap, history_len ? history_len + r0 : nullptr, ngram_size, window,
+                                         whitelist, n_whitelist, temperature, eos_token_id, append,
+                                         logits ? logits + r0 * V : nullptr, tokens + r0,
+                                         is_eos ? is_eos + r0 : nullptr, check_route)))
+            return st;
+    }
+    return FOCR_HIP_OK;
 }
 
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,

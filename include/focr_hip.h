@@ -268,7 +268,8 @@ int32_t focr_hip_moe_layer_free(focr_hip_moe_layer* layer);
  * and softmax in f64, rounded to f32), per (token, slot) the int8 SwiGLU
  * expert (decoder.rs:1744-1755), y *= gate, combine in slot order, plus the
  * shared expert when with_shared. hidden/out [t, hidden] f32; idx/gates
- * [t, top_k] (both nullable). Device pointers. t <= 64. Returns E_ROUTE when
+ * [t, top_k] (both nullable). Device pointers. t <= 16384 (more than 64 rows run
+ * as consecutive chunks of 64: the same rows). Returns E_ROUTE when
  * a token has no finite router score (moe.rs:261-265) — detected on the
  * device and reported by a synchronising check only when check_route = 1. */
 int32_t focr_hip_moe_decode(focr_hip_ctx* ctx, const focr_hip_moe_layer* layer,
@@ -460,7 +461,8 @@ int32_t focr_hip_decoder_layer_free(focr_hip_decoder_layer* layer);
  * host (each stream's absolute position, SPEC-095); route_idx (device,
  * nullable) receives a MoE layer's expert ids [n_streams, top_k]. With
  * check_route = 1 a MoE layer synchronises and returns E_ROUTE for a row with
- * no finite router score. n_streams <= 32 (<= 8 for the 6848-wide dense MLP). */
+ * no finite router score. Any number of streams: more than 32 (8 with the
+ * 6848-wide dense MLP) run in groups of that many, each the same as alone. */
 int32_t focr_hip_decoder_layer_step(focr_hip_ctx* ctx, const focr_hip_decoder_layer* layer,
                                     focr_hip_rswa* cache, const uint32_t* positions, float* x,
                                     uint32_t* route_idx, int32_t check_route);

@@ -101,7 +101,7 @@ def _caches(ctx, B, seed):
     return out, rings
 
 
-@pytest.mark.parametrize("B", [1, 5])
+@pytest.mark.parametrize("B", [1, 5, 40])
 def test_decoder_step_equals_the_calls_one_by_one(ctx, model, B):
     from franken_ocr_amd.engine import lm_head_i8, rms_norm
 
@@ -115,18 +115,20 @@ def test_decoder_step_equals_the_calls_one_by_one(ctx, model, B):
     xn = ctx.empty((B, H), np.float32)
     pos = np.array([G + 2 * s for s in range(B)], np.uint32)
     for step in range(2):
-        ta, tb = ctx.empty((B,), np.uint32), ctx.empty((B,), np.uint32)
+        ta, tb = ctx.empty((B, 1), np.uint32), ctx.empty((B,), np.uint32)
         la, lb = ctx.empty((B, V), np.float32), ctx.empty((B, V), np.float32)
         ia = [ctx.empty((B, K), np.uint32) for _ in range(3)]
         ib = ctx.empty((3, B, K), np.uint32)
         for li, layer in enumerate(layers):
             layer.step(ca[li], pos + step, xa, ia[li] if li else None, check_route=False)
         rms_norm(xa, xn, final_dev)
-        lm_head_i8(lm, xn, ta, la)
+        for r0 in range(0, B, 32):  # the LM head takes up to 32 rows per call
+            r1 = min(B, r0 + 32)
+            lm_head_i8(lm, xn.view_rows(r0, r1), ta.view_rows(r0, r1), la.view_rows(r0, r1))
         dec.step(cb, pos + step, xb, tb, lb, ib)
         assert np.array_equal(xa.numpy(), xb.numpy()), step
         assert np.array_equal(la.numpy(), lb.numpy()), step
-        assert np.array_equal(ta.numpy(), tb.numpy()), step
+        assert np.array_equal(ta.numpy().ravel(), tb.numpy()), step
         for li in (1, 2):
             assert np.array_equal(ia[li].numpy(), ib.numpy()[li]), (step, li)
         for li in range(3):

@@ -120,6 +120,36 @@ def test_decoder_layer_steps_match_oracle(ctx, kind, B):
         want = got  # continue from the device's state (both rings hold the same steps)
 
 
+@pytest.mark.parametrize("kind,B", [("moe", 40), ("dense", 12)])
+def test_decoder_layer_more_streams_than_one_pass(ctx, kind, B):
+    """More streams than one pass takes (32; 8 with the 6848-wide dense MLP)
+    run in groups through views of the cache: each stream equals the same
+    stream stepped alone, bit for bit, over two steps, and the cursors
+    advance for every stream."""
+    from franken_ocr_amd.engine import RingCache
+
+    _say(f"{kind} layer, {B} streams, 2 steps (groups)")
+    lw = _weights(14000 if kind == "moe" else 14500, None if kind == "moe" else 6848)
+    layer = _gpu_layer(ctx, lw)
+    cache, _, kv = _prefill(ctx, B, 14600)
+    x = synth.f32_normal(synth.seed_of(14700), B * H).reshape(B, H)
+    pos = np.array([G + (5 * s) % 17 for s in range(B)], np.uint32)
+    dx = ctx.to_device(x)
+    for step in range(2):
+        layer.step(cache, pos + step, dx, check_route=False)
+    assert [cache.state(s) for s in range(B)] == [(G, 2, 2)] * B
+    got = dx.numpy()
+    for s in sorted({0, 7, 8, 31, 32, B - 1} & set(range(B))):
+        one = RingCache(1, G, ctx=ctx)
+        one.record_prefill(0, ctx.to_device(kv[s][0]), ctx.to_device(kv[s][1]), G)
+        d1 = ctx.to_device(np.ascontiguousarray(x[s:s + 1]))
+        for step in range(2):
+            layer.step(one, pos[s:s + 1] + step, d1, check_route=False)
+        assert np.array_equal(d1.numpy()[0], got[s]), f"stream {s}"
+        one.free()
+    cache.free()
+
+
 def test_decoder_layer_batched_equals_per_stream(ctx):
     from franken_ocr_amd.engine import RingCache
 

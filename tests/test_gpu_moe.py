@@ -234,8 +234,34 @@ def test_route_nan_reports_error(ctx, gpu_layer, t):
 def test_moe_shape_errors(ctx, gpu_layer):
     from franken_ocr_amd._abi import ContractViolation
 
-    with pytest.raises(ContractViolation, match=r"t 65 outside"):
-        gpu_layer.decode(ctx.empty((65, H), np.float32), ctx.empty((65, H), np.float32))
+    with pytest.raises(ContractViolation, match=r"t 16385 outside 1..=16384"):
+        gpu_layer.decode(ctx.empty((16385, H), np.float32), ctx.empty((16385, H), np.float32))
+
+
+def test_moe_decode_past_64_rows_runs_in_chunks(ctx, gpu_layer, layer_w):
+    """A call of more than 64 rows runs as chunks of 64: its rows are the
+    bits of the same rows decoded in separate calls, and match the oracle; a
+    row without a finite score is reported by its index in the whole call."""
+    from franken_ocr_amd._abi import RouteError
+
+    t = 150
+    _say(f"moe_decode t={t} (chunks of 64)")
+    x = synth.f32_normal(synth.seed_of(380), t * H).reshape(t, H)
+    dout, didx, dg = ctx.empty((t, H), np.float32), ctx.empty((t, K), np.uint32), ctx.empty((t, K), np.float32)
+    gpu_layer.decode(ctx.to_device(x), dout, didx, dg, norm_topk=True)
+    got, gi = dout.numpy(), didx.numpy()
+    for r0, r1 in ((0, 50), (50, 64), (64, 150)):
+        o = ctx.empty((r1 - r0, H), np.float32)
+        gpu_layer.decode(ctx.to_device(np.ascontiguousarray(x[r0:r1])), o, norm_topk=True)
+        assert np.array_equal(o.numpy(), got[r0:r1]), (r0, r1)
+    st, out, idx, gates = O.moe_decode(x, *layer_w, E, K, I, norm_topk=True)
+    assert st == 0
+    assert np.array_equal(gi, idx)
+    np.testing.assert_allclose(dg.numpy(), gates, rtol=1e-6, atol=0)
+    assert_rel(got, out.astype(np.float64), 1e-3)
+    x[70] = np.nan
+    with pytest.raises(RouteError, match="no finite router score for token 70"):
+        gpu_layer.decode(ctx.to_device(x), dout)
 
 
 @pytest.mark.parametrize("t", [1, 8, 40])
