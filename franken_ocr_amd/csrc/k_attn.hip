@@ -252,19 +252,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // Fold the key ranges: out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,
 // M = max_s m_s (a range with no key of the row has m = -inf, l = 0, O = 0).
 // Thread = one dim of one (row, head).
+// Up to kMergeBatch splits, every split's (max, denominator) and output
+// value are requested at once (clamped duplicates past nsplit, never used),
+// then folded in split order; a loop that loaded one split at a time waited
+// on each in turn. More splits take that loop. Both fold the same values in
+// the same order.
+constexpr int kMergeBatch = 16;
+
 __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
     const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s)
-        M = fmaxf(M, a.part_ml[((static_cast<size_t>(s) * a.heads + h) * a.cs + row) * 2]);
     float den = 0.0f, acc = 0.0f;
-    for (int s = 0; s < a.nsplit; ++s) {
-        const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
-        const float ms = a.part_ml[pidx * 2];
-        if (ms == -INFINITY) continue;
-        const float w = expf(ms - M);
-        den += w * a.part_ml[pidx * 2 + 1];
-        acc += w * a.part_o[pidx * kD + d];
+    if (a.nsplit <= kMergeBatch) {
+        float ms[kMergeBatch], ls[kMergeBatch], os[kMergeBatch];
+#pragma unroll
+        for (int s = 0; s < kMergeBatch; ++s) {
+            const int sc = s < a.nsplit ? s : a.nsplit - 1;
+            const size_t pidx = (static_cast<size_t>(sc) * a.heads + h) * a.cs + row;
+            ms[s] = a.part_ml[pidx * 2];
+            ls[s] = a.part_ml[pidx * 2 + 1];
+            os[s] = a.part_o[pidx * kD + d];
+        }
+        // every use unconditional (a guarded use lets the compiler sink the
+        // load under the guard, one wait per split again): the duplicates
+        // past nsplit repeat the last split's max, and an unused split adds
+        // a selected +0 (the sums never hold -0, so x + 0 == x), also where
+        // a split with no keys left its values unwritten
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kMergeBatch; ++s) M = fmaxf(M, ms[s]);
+#pragma unroll
+        for (int s = 0; s < kMergeBatch; ++s) {
+            const bool use = s < a.nsplit && ms[s] != -INFINITY;
+            const float w = expf((use ? ms[s] : M) - M);
+            const float dl = w * ls[s], da = w * os[s];
+            den += use ? dl : 0.0f;
+            acc += use ? da : 0.0f;
+        }
+    } else {
+        float M = -INFINITY;
+        for (int s = 0; s < a.nsplit; ++s)
+            M = fmaxf(M, a.part_ml[((static_cast<size_t>(s) * a.heads + h) * a.cs + row) * 2]);
+        for (int s = 0; s < a.nsplit; ++s) {
+            const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
+            const float ms = a.part_ml[pidx * 2];
+            if (ms == -INFINITY) continue;
+            const float w = expf(ms - M);
+            den += w * a.part_ml[pidx * 2 + 1];
+            acc += w * a.part_o[pidx * kD + d];
+        }
     }
     a.out[static_cast<size_t>(row) * a.ldo + static_cast<size_t>(h) * a.ho + d] = acc / den;
 }
