@@ -110,6 +110,7 @@ def timed(ctx, step, steps: int):
         step(i)
     ctx.device_synchronize()
     el = time.perf_counter() - t0
+    log(f"timed pass: {steps} steps in {el * 1e3:.3f} ms")
     n_stat = max(steps, STAT_STEPS)
     ctx.prof_reset()
     ctx.prof_enable(True)
@@ -119,15 +120,24 @@ def timed(ctx, step, steps: int):
     ctx.prof_enable(False)
     kernels = {k: round(v["ms"] / max(v["count"], 1) * 1e3, 3) for k, v in prof.items()}
     ctx.device_synchronize()
+    log(f"per-kernel pass: {n_stat} steps")
     ctx.mark()
     for g in range(STAT_GROUPS):
         for i in range(STEPS_PER_MARK):
             step(g * STEPS_PER_MARK + i)
         ctx.mark()
     group_ms = ctx.marks_read()
+    log(f"step-statistics pass: {STAT_GROUPS} x {STEPS_PER_MARK} steps")
     st = sample_stats([v * 1e-3 / STEPS_PER_MARK for v in group_ms], scale=1e6, unit="us")
     st["steps_per_sample"] = STEPS_PER_MARK
     return el, prof, kernels, st
+
+
+def set_stat_sizes(stat_steps: int, stat_groups: int) -> None:
+    """Sizes of timed()'s statistics passes (small for counter runs, where
+    every dispatch is slow)."""
+    global STAT_STEPS, STAT_GROUPS
+    STAT_STEPS, STAT_GROUPS = max(1, stat_steps), max(1, stat_groups)
 
 
 def nearest_rank(sorted_asc, q: float) -> float:
@@ -1558,6 +1568,10 @@ def main() -> int:
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0,
                     help="CPU baseline sample of each secondary configuration")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stat-steps", type=int, default=STAT_STEPS,
+                    help="steps of the per-kernel statistics pass (at least --steps)")
+    ap.add_argument("--stat-groups", type=int, default=STAT_GROUPS,
+                    help="samples of the step statistics (each the mean of 10 steps); small values for counter runs")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations the default (moe_decode) run reports under 'extra'")
     ap.add_argument("--library-ref", action="store_true",
@@ -1565,6 +1579,7 @@ def main() -> int:
     ap.add_argument("--no-views", action="store_true",
                     help="prefill MoE workloads: skip the warm and bucket re-runs (profile the cold step alone)")
     args = ap.parse_args()
+    set_stat_sizes(args.stat_steps, args.stat_groups)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU code); run with --gpus 1",
               file=sys.stderr)
