@@ -1513,6 +1513,9 @@ EXTRAS = [
     ("linear_i8_m8192", "linear_i8", 8192, 3, 20, 3),
     ("decode_layer_b8", "decode_layer", 8, 6, 50, 5),
     ("prefill_layer_1024", "prefill_layer", 1024, 2, 10, 2),
+    # the same 1024 tokens as one chunk: HBM holds the whole prompt's rows, and
+    # the routed experts are read once instead of once per 256-row chunk
+    ("prefill_layer_1024_c1024", "prefill_layer", 1024, 2, 10, 2, {"chunk": 1024}),
 ]
 _EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us", "step_us")
 
@@ -1524,11 +1527,13 @@ def run_extras(ctx, base_args) -> dict:
     import gc
 
     out = {}
-    for key, wl, tokens, copies, steps, warmup in EXTRAS:
+    for key, wl, tokens, copies, steps, warmup, *over in EXTRAS:
         if wl not in WORKLOADS:
             continue
         a = argparse.Namespace(**vars(base_args))
         a.workload, a.tokens, a.copies, a.steps, a.warmup = wl, tokens, copies, steps, warmup
+        for k, v in (over[0] if over else {}).items():
+            setattr(a, k, v)
         a.cpu_seconds = base_args.extra_cpu_seconds
         log(f"extra {key}")
         run, cpu = WORKLOADS[wl]

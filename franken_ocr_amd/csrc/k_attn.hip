@@ -8,8 +8,9 @@
 // f32 attention to rounding.
 //
 // Block = 4 waves on one head and 64 query rows (16 per wave); the block
-// walks its key range in tiles of 64 keys, staged in LDS and shared by the
-// waves. Per wave and 16-key subtile, S^T = K . Q^T (A = 16 keys x 4 dims from
+// walks its key range in tiles of 32 keys, staged in LDS and shared by the
+// waves (34 KB, so three blocks share a CU). Per wave and 16-key subtile,
+// S^T = K . Q^T (A = 16 keys x 4 dims from
 // LDS, B = 4 dims x 16 query rows from registers), so the accumulator lands
 // with lane (g = lane / 16, j = lane % 16) holding S[row j][keys 4g .. 4g + 3]
 // — exactly the B operand P^T[key][row j] the P.V product needs (keys taken in
@@ -18,10 +19,17 @@
 // 8 * (4g + r') + m, so each lane ends holding 32 consecutive dims of its row.
 // Dims of the score dot are taken in the order 32g + s (s = 0..31).
 //
+// The scores are kept in base-2 units: the kernel's scale is
+// log2(e) / sqrt(128), so exp(s / sqrt(128) - max) is exp2 of the scaled
+// score minus its max (the hardware v_exp_f32, about 1 ulp; the argument's
+// extra rounding is ~|x| * 2^-24, far inside the attention's 1e-4).
+//
 // Long prefixes are split into key ranges over more blocks (split-K); each
 // writes its running max, denominator and unnormalised output, and a merge
 // kernel folds them (log-sum-exp). A row whose keys all lie in other ranges
-// contributes max -inf and nothing else.
+// contributes max -inf and nothing else. The ranges hold equal numbers of
+// tiles, sized so the blocks that have keys fill the GPU about once (the
+// causal chunk's row tiles need different numbers of tiles).
 #include "focr_internal.hpp"
 #include "k_common.hpp"
 
@@ -29,8 +37,10 @@ namespace focr {
 namespace {
 
 constexpr int kD = 128;          // head_dim
-constexpr int kKT = 64;          // keys per LDS tile
+constexpr int kKT = 32;          // keys per LDS tile
 constexpr int kLdsRow = kD + 4;  // padded LDS row (floats)
+constexpr int kBlocksPerCu = 3;  // the kernel's residency (LDS 34 KB, waves_per_eu 3)
+constexpr float kLog2e = 1.4426950408889634f;
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
@@ -39,10 +49,10 @@ struct AttnArgs {
     const float* v;
     float* out;      // single range: normalised context, out + i * ldo + h * ho
     float* part_o;   // split: [split][head][row][kD] unnormalised
-    float* part_ml;  // split: [split][head][row][2] (max, denominator)
+    float* part_ml;  // split: [split][head][row][2] (base-2 max, denominator)
     int ldq, hq, ldk, hk, ldv, hv, ldo, ho;
     int cs, c0, c1, heads, split_len, nsplit;
-    float scale;
+    float scale;     // log2(e) / sqrt(head_dim)
 };
 
 // Combine lane l's value with lanes l ^ 16, l ^ 32, l ^ 48 (the four 16-lane
@@ -75,7 +85,11 @@ __device__ __forceinline__ float wave16_sum(float v) {
     return c + b;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_prefill_kernel(const AttnArgs a) {
+constexpr int kSub = kKT / 16;             // 16-key MFMA subtiles per tile
+constexpr int kPieces = kKT * kD / 4 / 256;  // float4 of one matrix per thread and tile
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerCu))) void attn_prefill_kernel(
+    const AttnArgs a) {
     extern __shared__ float4 lds_kv4[];  // K tile then V tile, [kKT][kLdsRow] floats each
     float* lk = reinterpret_cast<float*>(lds_kv4);
     float* lv = lk + kKT * kLdsRow;
@@ -112,7 +126,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     for (int m = 0; m < 8; ++m) oacc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // tile loads: 64 keys x 128 floats = 2048 float4 per matrix, 8 per thread
+    // tile loads: 32 keys x 128 floats = 1024 float4 per matrix, 4 per thread
     const int c4 = threadIdx.x & 31;  // float4 column
     const int r8 = threadIdx.x >> 5;  // 8 rows per pass
     const float* kh = a.k + static_cast<size_t>(h) * a.hk + 4 * c4;
@@ -120,9 +134,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     // The tile after the current one is loaded into registers while the
     // current one is consumed from LDS (key rows clamped into the prefix; a
     // load past the range end is never used).
-    v4f pk[8], pv[8];
+    v4f pk[kPieces], pv[kPieces];
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
+    for (int p = 0; p < kPieces; ++p) {
         int key = ks + r8 + 8 * p;
         key = key < a.c1 ? key : a.c1 - 1;
         pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
@@ -131,25 +145,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     for (int kb = ks; kb < ke; kb += kKT) {
         __syncthreads();  // the previous tile's readers are done
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
+        for (int p = 0; p < kPieces; ++p) {
             *reinterpret_cast<v4f*>(lk + (r8 + 8 * p) * kLdsRow + 4 * c4) = pk[p];
             *reinterpret_cast<v4f*>(lv + (r8 + 8 * p) * kLdsRow + 4 * c4) = pv[p];
         }
         __syncthreads();
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
+        for (int p = 0; p < kPieces; ++p) {
             int key = kb + kKT + r8 + 8 * p;
             key = key < a.c1 ? key : a.c1 - 1;
             pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
             pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
         }
 
-        // S^T for the 4 subtiles of 16 keys; each score dot runs as two
+        // S^T for the subtiles of 16 keys; each score dot runs as two
         // 16-step MFMA chains (64 dims each) added at the end, halving the
         // f32 accumulation chain of the 128-term dot
-        v4f sacc[4];
+        v4f sacc[kSub];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
+        for (int n = 0; n < kSub; ++n) {
             v4f sc[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c) sc[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -165,10 +179,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             sacc[n] = sc[0] + sc[1];
         }
         // scale, causal / range mask, online softmax (row j over 4 lanes)
-        float pr[4][4];
+        float pr[kSub][4];
         float tmax = -INFINITY;
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < kSub; ++n)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = kb + 16 * n + 4 * g + r;
@@ -179,13 +193,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             }
         tmax = wave16_max(tmax);
         const float m_new = fmaxf(m_run, tmax);
-        const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
         float tsum = 0.0f;
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < kSub; ++n)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = pr[n][r] == -INFINITY ? 0.0f : expf(pr[n][r] - m_new);
+                const float p = pr[n][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pr[n][r] - m_new);
                 pr[n][r] = p;
                 tsum += p;
             }
@@ -194,12 +208,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         m_run = m_new;
         // this tile's V^T . P^T in fresh accumulators (step (n, r) is key
         // kb + 16n + 4g + r), folded into the running output once per tile:
-        // 64-term sums then a per-tile sum, not one long f32 chain
+        // 32-term sums then a per-tile sum, not one long f32 chain
         v4f otile[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) otile[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < kSub; ++n)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float* vr = lv + (16 * n + 4 * g + r) * kLdsRow + 8 * j;
@@ -249,8 +263,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     if (g == 0) *reinterpret_cast<float2*>(a.part_ml + pidx * 2) = make_float2(m_run, l_run);
 }
 
-// Fold the key ranges: out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,
-// M = max_s m_s (a range with no key of the row has m = -inf, l = 0, O = 0).
+// Fold the key ranges: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
+// M = max_s m_s, the maxima in base-2 units (a range with no key of the row
+// has m = -inf, l = 0, O = 0).
 // Thread = one dim of one (row, head).
 // Up to kMergeBatch splits, every split's (max, denominator) and output
 // value are requested at once (clamped duplicates past nsplit, never used),
@@ -283,7 +298,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
             const bool use = s < a.nsplit && ms[s] != -INFINITY;
-            const float w = expf((use ? ms[s] : M) - M);
+            const float w = __builtin_amdgcn_exp2f((use ? ms[s] : M) - M);
             const float dl = w * ls[s], da = w * os[s];
             den += use ? dl : 0.0f;
             acc += use ? da : 0.0f;
@@ -296,7 +311,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
             const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
             const float ms = a.part_ml[pidx * 2];
             if (ms == -INFINITY) continue;
-            const float w = expf(ms - M);
+            const float w = __builtin_amdgcn_exp2f(ms - M);
             den += w * a.part_ml[pidx * 2 + 1];
             acc += w * a.part_o[pidx * kD + d];
         }
@@ -339,14 +354,25 @@ size_t attn_partials_bytes(int cs, int heads, int nsplit) {
 }
 
 int attn_pick_splits(int cs, int c1, int heads, int cu_count, int* split_len) {
+    // Row tile i (64 rows) needs the tiles of keys [0, min(c1, c0 + 64 (i + 1))):
+    // ranges of B tiles give sum over i of ceil(n_i / B) blocks with keys per
+    // head, and B is the smallest that keeps those within one residency of
+    // the GPU (blocks past a row tile's keys exit at once).
+    const int c0 = c1 - cs;
     const int qtiles = (cs + 63) / 64;
-    const int want = (2 * cu_count + qtiles * heads - 1) / (qtiles * heads);  // about two blocks per CU
-    int nsplit = want < 1 ? 1 : want;
-    int len = (c1 + nsplit - 1) / nsplit;
-    len = ((len + kKT - 1) / kKT) * kKT;  // whole tiles per range
-    nsplit = (c1 + len - 1) / len;
+    const long long slots = static_cast<long long>(kBlocksPerCu) * (cu_count > 0 ? cu_count : 1);
+    int per = 1;  // tiles per range
+    for (;; ++per) {
+        long long blocks = 0;
+        for (int i = 0; i < qtiles; ++i) {
+            const int n = (min(c1, c0 + 64 * (i + 1)) + kKT - 1) / kKT;
+            blocks += (n + per - 1) / per;
+        }
+        if (blocks * heads <= slots || static_cast<long long>(per) * kKT >= c1) break;
+    }
+    const int len = per * kKT;
     *split_len = len;
-    return nsplit;
+    return (c1 + len - 1) / len;
 }
 
 hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q, const float* k, const float* v,
@@ -356,7 +382,7 @@ hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q
         split_len % kKT != 0 || static_cast<long long>(nsplit) * split_len < c1)
         return hipErrorInvalidValue;
     AttnArgs a{q, k, v, out, nullptr, nullptr, gm.ldq, gm.hq, gm.ldk, gm.hk, gm.ldv, gm.hv, gm.ldo, gm.ho,
-               cs, c0, c1, heads, split_len, nsplit, 1.0f / sqrtf(static_cast<float>(head_dim))};
+               cs, c0, c1, heads, split_len, nsplit, kLog2e / sqrtf(static_cast<float>(head_dim))};
     if (nsplit > 1) {
         a.part_o = part;
         a.part_ml = part + static_cast<size_t>(nsplit) * heads * cs * kD;
