@@ -704,13 +704,26 @@ extern "C" {
 
 // route (moe.rs:181-266) of t rows (up to kRouteRowsMax) without the decode
 // kernels' selection matrices: idx / gates [t][top_k], probs [t][E]
-// (nullable), flag [t] (1: fewer than top_k finite scores). The split route
+// (nullable), flag [t] (1: fewer than top_k finite scores). Rows up to 1280
+// wide take the many-row route (a logits kernel that reads the router once
+// per 8 tokens, then the rank kernel; the logits in the logits slot): the
+// split route's arithmetic, bit for bit. Wider rows take the split route
 // kernel; its exchange buffer grows to t tokens (zeroed when it grows) and a
 // one-thread launch advances the buffer's counter after it.
 constexpr size_t kRouteRowsMax = 16384;
 static int32_t route_rows_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
                                int32_t norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs,
                                int* flag) {
+    if (moe_route_rows_supported(static_cast<int>(L->hidden))) {
+        float* lg = static_cast<float*>(ctx->scratch_get(kScrLogits, t * L->n_experts * sizeof(float)));
+        if (!lg) return FOCR_HIP_E_OOM;
+        const MoeDims d{(int)t, (int)L->hidden, (int)L->inter, (int)L->n_experts, (int)L->top_k};
+        ProfScope ps(ctx, "moe_route");
+        FOCR_HIP_TRY(launch_moe_route_rows(ctx->stream, d, x, L->router, norm_topk, routed_scale, idx, gates, probs,
+                                           flag, lg),
+                     "route launch");
+        return FOCR_HIP_OK;
+    }
     const size_t xb = moe_route_xchg_bytes(t);
     const bool grow = ctx->scratch[kScrRouteX].cap < xb;
     void* xchg = ctx->scratch_get(kScrRouteX, xb);

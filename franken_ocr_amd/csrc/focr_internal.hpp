@@ -368,6 +368,13 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
                             float* probs, int* flag, void* sel, void* xchg, unsigned wait_ticks,
                             const MoeRouteNorm* norm = nullptr);
 hipError_t launch_route_epoch_bump(hipStream_t s, void* xchg);
+// The many-row route (a prefill chunk, t <= 16384, hidden <= 1280): the split
+// route's logits computed eight tokens per router read into logits [t][E],
+// then its softmax / top-k per token; no exchange buffer, no quantized rows.
+bool moe_route_rows_supported(int hidden);
+hipError_t launch_moe_route_rows(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
+                                 int norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs,
+                                 int* flag, float* logits);
 // The shared expert's gate/up weights, folded into the routed gate/up launch
 // as extra blocks (every token a pair, act rows [t][inter]).
 struct MoeSharedGateUp {

@@ -177,6 +177,70 @@ __device__ __forceinline__ void route_dots(const float4* __restrict__ xr, const 
     amax_out = wave_max_f_full(amax);
 }
 
+// Steps 6-8 of the route for token t in one wave (lane = expert, lg = its
+// logit for lane < E): the f64 softmax, the greedy top-k and the renormalised
+// gates, the outputs and the selection entries. The split route's leader and
+// the many-row route's rank kernel both end here, so their routing is the
+// same arithmetic.
+__device__ __forceinline__ void route_rank(float lg_in, int lane, int t, int E, int K, int norm_topk,
+                                           float routed_scale, uint32_t* __restrict__ idx_out,
+                                           float* __restrict__ gates_out, float* __restrict__ probs_out,
+                                           int* __restrict__ flag, const MoeSel& sel) {
+    // 6. softmax in f64 over the f32 logits (lane = expert): max, exp,
+    //    DPP-tree sum (the oracle's wave_tree_sum64 order), divide, round to
+    //    f32; a lane past E is NaN and never ranked
+    const bool valid = lane < E;
+    const float lg = valid ? lg_in : -INFINITY;
+    const double mx = static_cast<double>(wave_max_f_full(lg));
+    const double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
+    const double sum = wave_sum_d_full(ex);
+    const float pr = valid ? static_cast<float>(ex / sum) : __int_as_float(0x7fc00000);
+    if (valid && probs_out) probs_out[static_cast<size_t>(t) * E + lane] = pr;
+    const int nvalid = __popcll(__ballot(pr == pr));
+
+    // 7. greedy top-k (moe.rs:209-266): K times the largest remaining
+    //    probability, the lowest index among equal ones, NaN never; slot j is
+    //    the j-th pick. A probability is finite and >= +0 (ex >= 0, sum > 0),
+    //    so -inf marks a lane out of the running (NaN, past E, or picked).
+    //    Fewer than K finite probabilities: the token's routing failed
+    //    (flag), every output of it zero.
+    float pk = valid && pr == pr ? pr : -INFINITY;
+    int my_slot = -1;
+    int ej_mine = 0;
+    float wj_mine = 0.0f;
+    float den = 0.0f;
+    const bool bad = nvalid < K;
+    for (int j = 0; j < K; ++j) {
+        const float mv = wave_max_f_full(pk);
+        const unsigned long long mm = __ballot(pk == mv && mv != -INFINITY);
+        const int lj = mm ? __ffsll(static_cast<long long>(mm)) - 1 : 0;
+        const float wj = mm ? mv : 0.0f;
+        den += bad ? 0.0f : wj;  // sequential f32 sum in slot order
+        if (mm && lane == lj) {
+            pk = -INFINITY;
+            my_slot = j;
+        }
+        if (lane == j) {
+            ej_mine = lj;
+            wj_mine = wj;
+        }
+    }
+    const bool chosen = my_slot >= 0;
+
+    // 8. renormalise (the slot-order sum above + 1e-20), scale, publish
+    den += 1e-20f;
+    if (lane < K) {
+        const int ej = bad ? 0 : ej_mine;
+        float w = bad ? 0.0f : wj_mine;
+        if (norm_topk) w = w / den;
+        idx_out[t * K + lane] = static_cast<uint32_t>(ej);
+        gates_out[t * K + lane] = w * routed_scale;
+        if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
+        if (lane == 0) flag[t] = bad ? 1 : 0;
+    }
+    if (sel.slot && valid) sel.slot[lane * kMaxT + t] = static_cast<uint8_t>(chosen && !bad ? my_slot + 1 : 0);
+}
+
 // Grid: 8 * S blocks, S = ceil(T / 8) * kRouteParts. Block b sits on XCD
 // x = b % 8; its slot s = b / 8 is part s % kRouteParts of token
 // (s / kRouteParts) * 8 + x (blocks of tokens >= T exit at once). Part 0 of
@@ -393,66 +457,110 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         __syncthreads();
     }
     if (wave != 0) return;
-
-    // 6. softmax in f64 over the f32 logits (lane = expert): max, exp,
-    //    DPP-tree sum (the oracle's wave_tree_sum64 order), divide, round to
-    //    f32; a lane past E is NaN and never ranked
-    const bool valid = lane < E;
-    const float lg = valid ? s_logit[lane] : -INFINITY;
-    const double mx = static_cast<double>(wave_max_f_full(lg));
-    const double ex = valid ? exp(static_cast<double>(lg) - mx) : 0.0;
-    const double sum = wave_sum_d_full(ex);
-    const float pr = valid ? static_cast<float>(ex / sum) : __int_as_float(0x7fc00000);
-    if (valid && probs_out) probs_out[static_cast<size_t>(t) * E + lane] = pr;
-    const int nvalid = __popcll(__ballot(pr == pr));
-
-    // 7. greedy top-k (moe.rs:209-266): K times the largest remaining
-    //    probability, the lowest index among equal ones, NaN never; slot j is
-    //    the j-th pick. A probability is finite and >= +0 (ex >= 0, sum > 0),
-    //    so -inf marks a lane out of the running (NaN, past E, or picked).
-    //    Fewer than K finite probabilities: the token's routing failed
-    //    (flag), every output of it zero.
-    float pk = valid && pr == pr ? pr : -INFINITY;
-    int my_slot = -1;
-    int ej_mine = 0;
-    float wj_mine = 0.0f;
-    float den = 0.0f;
-    const bool bad = nvalid < K;
-    for (int j = 0; j < K; ++j) {
-        const float mv = wave_max_f_full(pk);
-        const unsigned long long mm = __ballot(pk == mv && mv != -INFINITY);
-        const int lj = mm ? __ffsll(static_cast<long long>(mm)) - 1 : 0;
-        const float wj = mm ? mv : 0.0f;
-        den += bad ? 0.0f : wj;  // sequential f32 sum in slot order
-        if (mm && lane == lj) {
-            pk = -INFINITY;
-            my_slot = j;
-        }
-        if (lane == j) {
-            ej_mine = lj;
-            wj_mine = wj;
-        }
-    }
-    const bool chosen = my_slot >= 0;
-
-    // 8. renormalise (the slot-order sum above + 1e-20), scale, publish
-    den += 1e-20f;
-    if (lane < K) {
-        const int ej = bad ? 0 : ej_mine;
-        float w = bad ? 0.0f : wj_mine;
-        if (norm_topk) w = w / den;
-        idx_out[t * K + lane] = static_cast<uint32_t>(ej);
-        gates_out[t * K + lane] = w * routed_scale;
-        if (sel.slot && !bad) sel.gate[ej * kMaxT + t] = w * routed_scale;
-        if (lane == 0) flag[t] = bad ? 1 : 0;
-    }
-    if (sel.slot && valid) sel.slot[lane * kMaxT + t] = static_cast<uint8_t>(chosen && !bad ? my_slot + 1 : 0);
+    route_rank(s_logit[lane < kMaxE ? lane : 0], lane, t, E, K, norm_topk, routed_scale, idx_out, gates_out,
+               probs_out, flag, sel);
 }
 
 // Advances the route exchange's counter once the route kernel of a call has
 // finished (stream order): the next call's records carry a new tag.
 __global__ void route_epoch_bump_kernel(RouteXchg* __restrict__ xch) {
     if (threadIdx.x == 0 && blockIdx.x == 0) xch->counter = xch->counter + 1ull;
+}
+
+// ---- route of many rows (a prefill chunk): logits, then the rank ------------
+// The split route reads the router once per token (327 KB each, through the
+// token's XCD L2), which is what a 256-1024-row chunk pays for. Here a block
+// holds two router rows per wave in registers (eight experts) and runs them
+// against kRowsTB token rows staged in LDS (all their loads in flight at
+// once): the router is read once per kRowsTB tokens (4 up to 512 rows, where
+// the blocks are few, else 8). Each logit is route_dots' f64 dot in the same
+// lane order (lane l: float4 chunks l + 64 i, x, y, z, w in turn) and the
+// same DPP tree, so the logits are the split route's bit for bit;
+// route_rank_kernel then runs the split route's own softmax / top-k
+// (route_rank) on them, one wave per token. The f64 FMAs, converts and DPP
+// trees bound it (about 10 us of VALU at 1024 rows). Rows up to 1280
+// wide (one batch of kRouteNC float4 per lane); no exchange buffer, no
+// quantized rows.
+template <int kRowsTB>
+__global__ __launch_bounds__(256) void route_logits_kernel(const float* __restrict__ x, const float* __restrict__ G,
+                                                           int T, int H, int E, float* __restrict__ logits) {
+    // the block's kRowsTB token rows, staged at once (every load in flight
+    // together), then read per token from LDS
+    __shared__ float4 s_x[kRowsTB][64 * kRouteNC];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int H4 = H >> 2;
+    const int t0 = static_cast<int>(blockIdx.x) * kRowsTB;
+    const int e0 = static_cast<int>(blockIdx.y) * kRouteEPP + wave * kRouteRPW;
+    float4 gv[kRouteRPW][kRouteNC];
+    unsigned m[kRouteNC];
+#pragma unroll
+    for (int i = 0; i < kRouteNC; ++i) {
+        const int c = lane + 64 * i;
+        m[i] = c < H4 ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+        for (int k = 0; k < kRouteRPW; ++k) {
+            const int e = e0 + k < E ? e0 + k : E - 1;
+            gv[k][i] = reinterpret_cast<const float4*>(G + static_cast<size_t>(e) * H)[c < H4 ? c : H4 - 1];
+        }
+    }
+    constexpr int kPer = kRowsTB * 64 * kRouteNC / 256;  // float4 per thread
+    float4 st[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int q = static_cast<int>(threadIdx.x) + 256 * j;
+        const int u = q / (64 * kRouteNC), c = q % (64 * kRouteNC);
+        const int t = t0 + u < T ? t0 + u : T - 1;
+        st[j] = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * H)[c < H4 ? c : H4 - 1];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int q = static_cast<int>(threadIdx.x) + 256 * j;
+        s_x[q / (64 * kRouteNC)][q % (64 * kRouteNC)] = st[j];
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int u = 0; u < kRowsTB; ++u) {
+        const int t = t0 + u;
+        double acc[kRouteRPW];
+#pragma unroll
+        for (int k = 0; k < kRouteRPW; ++k) acc[k] = 0.0;
+#pragma unroll
+        for (int i = 0; i < kRouteNC; ++i) {
+            const float4 xv = s_x[u][lane + 64 * i];
+            const float4 xc = make_float4(__uint_as_float(__float_as_uint(xv.x) & m[i]),
+                                          __uint_as_float(__float_as_uint(xv.y) & m[i]),
+                                          __uint_as_float(__float_as_uint(xv.z) & m[i]),
+                                          __uint_as_float(__float_as_uint(xv.w) & m[i]));
+            const double x0 = xc.x, x1 = xc.y, x2 = xc.z, x3 = xc.w;
+#pragma unroll
+            for (int k = 0; k < kRouteRPW; ++k) {
+                const float4 g = gv[k][i];
+                acc[k] = fma(x0, static_cast<double>(g.x), acc[k]);
+                acc[k] = fma(x1, static_cast<double>(g.y), acc[k]);
+                acc[k] = fma(x2, static_cast<double>(g.z), acc[k]);
+                acc[k] = fma(x3, static_cast<double>(g.w), acc[k]);
+            }
+        }
+        double d[kRouteRPW];
+#pragma unroll
+        for (int k = 0; k < kRouteRPW; ++k) d[k] = wave_sum_d_full(acc[k]);
+        if (t < T && lane < kRouteRPW && e0 + lane < E)
+            logits[static_cast<size_t>(t) * E + e0 + lane] = static_cast<float>(lane == 0 ? d[0] : d[1]);
+    }
+}
+
+// One wave per token: its E logits (lane = expert) through route_rank.
+__global__ __launch_bounds__(256) void route_rank_kernel(const float* __restrict__ logits, int T, int E, int K,
+                                                         int norm_topk, float routed_scale,
+                                                         uint32_t* __restrict__ idx_out,
+                                                         float* __restrict__ gates_out,
+                                                         float* __restrict__ probs_out, int* __restrict__ flag) {
+    const int t = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float lg = logits[static_cast<size_t>(t) * E + (lane < E ? lane : 0)];
+    route_rank(lg, lane, t, E, K, norm_topk, routed_scale, idx_out, gates_out, probs_out, flag, MoeSel{});
 }
 
 // Expert of this block: lane e loads expert e's 64-byte slot row (four
@@ -1042,6 +1150,28 @@ hipError_t launch_moe_route(hipStream_t s, const MoeDims& d, const float* hidden
                     d.n_experts, d.top_k, norm_topk, routed_scale, xq, xs, idx, gates, probs, flag, sel_of(sel),
                     RouteNorm{}, x, wait_ticks);
     }
+    return hipGetLastError();
+}
+
+bool moe_route_rows_supported(int hidden) { return hidden % 4 == 0 && hidden > 0 && hidden <= 64 * 4 * kRouteNC; }
+
+hipError_t launch_moe_route_rows(hipStream_t s, const MoeDims& d, const float* hidden, const float* router,
+                                 int norm_topk, float routed_scale, uint32_t* idx, float* gates, float* probs,
+                                 int* flag, float* logits) {
+    if (d.t < 1 || d.t > kRouteMaxT || d.n_experts < 1 || d.n_experts > kMaxE || d.top_k < 1 ||
+        d.top_k > kMaxK || d.top_k > d.n_experts || !moe_route_rows_supported(d.hidden) || !logits)
+        return hipErrorInvalidValue;
+    const unsigned parts = static_cast<unsigned>((d.n_experts + kRouteEPP - 1) / kRouteEPP);
+    if (d.t <= 512)
+        FOCR_LAUNCH(route_logits_kernel<4>, dim3(static_cast<unsigned>((d.t + 3) / 4), parts), dim3(256), 0, s,
+                    hidden, router, d.t, d.hidden, d.n_experts, logits);
+    else
+        FOCR_LAUNCH(route_logits_kernel<8>, dim3(static_cast<unsigned>((d.t + 7) / 8), parts), dim3(256), 0, s,
+                    hidden, router, d.t, d.hidden, d.n_experts, logits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    FOCR_LAUNCH(route_rank_kernel, dim3(static_cast<unsigned>((d.t + 3) / 4)), dim3(256), 0, s, logits, d.t,
+                d.n_experts, d.top_k, norm_topk, routed_scale, idx, gates, probs, flag);
     return hipGetLastError();
 }
 

@@ -67,6 +67,37 @@ def test_route_bit_exact(ctx, gpu_layer, layer_w, t, norm_topk):
     np.testing.assert_allclose(dp.numpy(), probs, rtol=1e-6, atol=1e-12)
 
 
+@pytest.mark.parametrize("tied", [False, True])
+def test_route_many_rows_equals_the_split_route(ctx, layer_w, tied):
+    """Above 64 rows the route runs as a logits kernel (the router read once
+    per 8 tokens) and a rank kernel; at most 64 it is the split route. The
+    same f64 dots in the same lane order and the same softmax / top-k: a
+    200-row call gives the bits of the 64-row call on its first 64 rows
+    (indices, gates, probabilities), also with tied router rows."""
+    from franken_ocr_amd.engine import MoeLayer
+
+    router = layer_w[0].copy()
+    if tied:
+        router[[2, 11, 19, 33, 47, 52, 60], :] = np.abs(synth.f32_normal(synth.seed_of(711), H, 0.0, 0.02)) * 5.0
+    L = MoeLayer(H, I, E, K, router, *layer_w[1:], ctx=ctx)
+    t = 200
+    x = synth.f32_normal(synth.seed_of(712), t * H).reshape(t, H)
+    if tied:
+        x = np.abs(x)
+    outs = []
+    for n in (64, t):
+        didx, dg, dp = ctx.empty((n, K), np.uint32), ctx.empty((n, K), np.float32), ctx.empty((n, E), np.float32)
+        L.route(ctx.to_device(np.ascontiguousarray(x[:n])), didx, dg, dp, norm_topk=True)
+        outs.append((didx.numpy(), dg.numpy(), dp.numpy()))
+    (i64, g64, p64), (ia, ga, pa) = outs
+    assert np.array_equal(ia[:64], i64)
+    assert np.array_equal(ga[:64].view(np.uint32), g64.view(np.uint32))
+    assert np.array_equal(pa[:64].view(np.uint32), p64.view(np.uint32))
+    st, idx, w, probs = O.route(x, router, E, K, norm_topk=True)
+    assert st == 0 and np.array_equal(ia, idx)
+    np.testing.assert_allclose(ga, w, rtol=1e-6, atol=0)
+
+
 def test_route_ties_at_the_cutoff_pick_lower_indices(ctx):
     """Seven identical router rows that dominate every token: their logits and
     probabilities are bit-identical, so the greedy top-6 (moe.rs:215-240: rank
