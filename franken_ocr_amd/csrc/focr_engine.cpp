@@ -1745,8 +1745,11 @@ int32_t focr_hip_prefill_attention(focr_hip_ctx* ctx, const float* q, const floa
     return attn_run(ctx, name, gm, q, k, v, out, seq, 0, seq, num_heads);
 }
 
+// kv_in_place: the chunk's K / V rows are in the reference block already
+// (the prefill layer's RoPE writes them there); k_chunk / v_chunk unused.
 static int32_t rswa_prefill_chunk_impl(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
-                                    const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out) {
+                                    const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out,
+                                    bool kv_in_place = false) {
     const char* name = "rswa_prefill_chunk";
     if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
     if (stream >= c->n_streams)
@@ -1757,12 +1760,14 @@ static int32_t rswa_prefill_chunk_impl(focr_hip_ctx* ctx, focr_hip_rswa* c, size
                                           c0, static_cast<long long>(c->prefill_len[stream])));
     if (c0 + cs > c->ref_capacity)
         return fail(FOCR_HIP_E_STATE, fmt("rswa: prefill seq %zu exceeds ref_capacity %zu", c0 + cs, c->ref_capacity));
-    int32_t st = attn_checks(name, q_chunk, k_chunk, v_chunk, out, cs, c0 + cs, kNumHeads, kHeadDim);
+    int32_t st = attn_checks(name, q_chunk, kv_in_place ? q_chunk : k_chunk, kv_in_place ? q_chunk : v_chunk, out,
+                             cs, c0 + cs, kNumHeads, kHeadDim);
     if (st) return st;
     if (cs) {
-        FOCR_HIP_TRY(launch_attn_scatter_kv(ctx->stream, k_chunk, v_chunk, (int)cs, kNumHeads, c->ref_k(stream),
-                                            c->ref_v(stream), (int)c->ref_capacity, (int)c0),
-                     "rswa_prefill_chunk scatter");
+        if (!kv_in_place)
+            FOCR_HIP_TRY(launch_attn_scatter_kv(ctx->stream, k_chunk, v_chunk, (int)cs, kNumHeads, c->ref_k(stream),
+                                                c->ref_v(stream), (int)c->ref_capacity, (int)c0),
+                         "rswa_prefill_chunk scatter");
         const int dim = kNumHeads * kHeadDim;
         const int hs = static_cast<int>(c->ref_capacity) * kHeadDim;
         const AttnGeom gm{dim, kHeadDim, kHeadDim, hs, kHeadDim, hs, dim, kHeadDim};
@@ -1818,7 +1823,7 @@ int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder
     const size_t H = L->hidden, D = L->n_heads * L->head_dim;
     const size_t I = L->gate ? L->gate->n : 0, K = L->moe ? L->moe->top_k : 0;
     // one scratch slot carved into the chunk's intermediates
-    const size_t fl = cs * (H + 3 * D + 3 * D + D + H + H + H) + (L->gate ? 2 * cs * I : 0) + cs * K * 2 + cs;
+    const size_t fl = cs * (H + 3 * D + D + D + H + H + H) + (L->gate ? 2 * cs * I : 0) + cs * K * 2 + cs;
     char* base = static_cast<char*>(ctx->scratch_get(kScrLayer, fl * 4 + 20 * 256));
     if (!base) return FOCR_HIP_E_OOM;
     auto take = [&](size_t bytes) {
@@ -1829,8 +1834,6 @@ int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder
     float* nrm = reinterpret_cast<float*>(take(cs * H * 4));
     float* qkv = reinterpret_cast<float*>(take(cs * 3 * D * 4));
     float* q = reinterpret_cast<float*>(take(cs * D * 4));
-    float* k = reinterpret_cast<float*>(take(cs * D * 4));
-    float* v = reinterpret_cast<float*>(take(cs * D * 4));
     float* cx = reinterpret_cast<float*>(take(cs * D * 4));
     float* attn = reinterpret_cast<float*>(take(cs * H * 4));
     float* h = reinterpret_cast<float*>(take(cs * H * 4));
@@ -1848,11 +1851,14 @@ int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder
     if ((st = linear_i8_dynamic_impl(ctx, L->qkv, nrm, cs, nullptr, qkv))) return st;
     {
         ProfScope ps(ctx, "layer_prefill_rope");
-        FOCR_HIP_TRY(launch_rope_rows(s, qkv, (int)cs, (int)c0, L->inv_freq, (int)L->n_heads, (int)L->head_dim, q, k,
-                                      v),
+        // k and v straight into the stream's head-major reference block at c0
+        const size_t hs = cache->ref_capacity * L->head_dim;
+        FOCR_HIP_TRY(launch_rope_rows(s, qkv, (int)cs, (int)c0, L->inv_freq, (int)L->n_heads, (int)L->head_dim, q,
+                                      cache->ref_k(stream) + c0 * L->head_dim, cache->ref_v(stream) + c0 * L->head_dim,
+                                      L->head_dim, hs),
                      "rope launch");
     }
-    if ((st = rswa_prefill_chunk_impl(ctx, cache, stream, q, k, v, cs, c0, cx))) return st;
+    if ((st = rswa_prefill_chunk_impl(ctx, cache, stream, q, nullptr, nullptr, cs, c0, cx, true))) return st;
     // 5. o_proj; 6. residual + post-attention RMSNorm
     if ((st = linear_i8_dynamic_impl(ctx, L->o_proj, cx, cs, nullptr, attn))) return st;
     {

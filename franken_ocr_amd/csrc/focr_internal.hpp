@@ -479,9 +479,14 @@ hipError_t launch_qkv_rope_f32(hipStream_t s, const int8_t* w_perm, const float*
 hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePositions& pos, const float* inv_freq,
                              int streams, int n_heads, int head_dim, float* q, float* k, float* v,
                              const RopeRing* ring);
-// Prefill rows at positions c0 + r: fused qkv [rows][3 D] -> q, k (RoPE) and v, each [rows][D].
+// Prefill rows at positions c0 + r: fused qkv [rows][3 D] -> q [rows][D]
+// (RoPE), k (RoPE) and v with element (r, head h, dim d) at
+// k / v + r * kv_row_stride + h * kv_head_stride + d (token-major: D,
+// head_dim; a head-major reference block at c0: head_dim, capacity *
+// head_dim). head_dim a multiple of 8, strides multiples of 4.
 hipError_t launch_rope_rows(hipStream_t s, const float* qkv, int rows, int c0, const float* inv_freq, int n_heads,
-                            int head_dim, float* q, float* k, float* v);
+                            int head_dim, float* q, float* k, float* v, size_t kv_row_stride,
+                            size_t kv_head_stride);
 hipError_t launch_add_rows(hipStream_t s, const float* a, const float* b, float* out, size_t n);
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, float* act, size_t n);
 // k_int4.hip

@@ -242,30 +242,63 @@ __global__ __launch_bounds__(kThreads) void rope_split_kernel(const float* __res
 // Chunked prefill (decoder.rs:2470-2482): fused qkv rows [rows][3 D] of
 // the positions c0 .. c0 + rows split into q, k (RoPE at the row's position,
 // RopeTable::build + apply_rope, decoder.rs:170-268: the same expressions as
-// rope_split_kernel) and v, each [rows][D] token-major. One block per row.
+// rope_split_kernel) and v. q is token-major [rows][D]; k and v element
+// (row r, head h, dim d) go to kv.k / kv.v + r * row_stride + h * head_stride
+// + d: token-major, or the stream's head-major reference block at c0 (the
+// attention's K / V, so no separate copy). One block per row: the row's
+// head_dim / 2 sin / cos pairs once (the angle p * inv_freq[i] is the same
+// for every head and for q and k), then the rotations four pairs per thread.
+struct RopeKv {
+    float* k;
+    float* v;
+    size_t row_stride, head_stride;
+};
+constexpr int kRopeMaxHalf = 256;
+
 __global__ __launch_bounds__(kThreads) void rope_rows_kernel(const float* __restrict__ qkv, int c0,
                                                              const float* __restrict__ inv_freq, int n_heads,
-                                                             int head_dim, float* __restrict__ q,
-                                                             float* __restrict__ k, float* __restrict__ v) {
+                                                             int head_dim, float* __restrict__ q, const RopeKv kv) {
+    __shared__ float s_sn[kRopeMaxHalf], s_cs[kRopeMaxHalf];
     const int r = blockIdx.x;
     const int D = n_heads * head_dim;
     const int half = head_dim >> 1;
     const float* row = qkv + static_cast<size_t>(r) * 3 * D;
     const float p = static_cast<float>(c0 + r);
-    for (int t = threadIdx.x; t < n_heads * half; t += kThreads) {
-        const int hd = t / half, i = t - hd * half;
+    for (int i = threadIdx.x; i < half; i += kThreads) {
         const float angle = p * inv_freq[i];
         float sn, cs;
         sincosf(angle, &sn, &cs);
-        const int j0 = hd * head_dim + i, j1 = j0 + half;
-        const float qa = row[j0], qb = row[j1];
-        const float ka = row[D + j0], kb = row[D + j1];
-        q[static_cast<size_t>(r) * D + j0] = qa * cs - qb * sn;
-        q[static_cast<size_t>(r) * D + j1] = qb * cs + qa * sn;
-        k[static_cast<size_t>(r) * D + j0] = ka * cs - kb * sn;
-        k[static_cast<size_t>(r) * D + j1] = kb * cs + ka * sn;
+        s_sn[i] = sn;
+        s_cs[i] = cs;
     }
-    for (int j = threadIdx.x; j < D; j += kThreads) v[static_cast<size_t>(r) * D + j] = row[2 * D + j];
+    __syncthreads();
+    float* qr = q + static_cast<size_t>(r) * D;
+    float* kr = kv.k + static_cast<size_t>(r) * kv.row_stride;
+    float* vr = kv.v + static_cast<size_t>(r) * kv.row_stride;
+    const int q4 = half >> 2;  // groups of four pairs per head
+    for (int t = threadIdx.x; t < n_heads * q4; t += kThreads) {
+        const int hd = t / q4, i = 4 * (t - hd * q4);
+        const int j0 = hd * head_dim + i, j1 = j0 + half;
+        const float4 qa = *reinterpret_cast<const float4*>(row + j0), qb = *reinterpret_cast<const float4*>(row + j1);
+        const float4 ka = *reinterpret_cast<const float4*>(row + D + j0);
+        const float4 kb = *reinterpret_cast<const float4*>(row + D + j1);
+        const float4 sn = *reinterpret_cast<const float4*>(s_sn + i), cs = *reinterpret_cast<const float4*>(s_cs + i);
+        const size_t o0 = hd * kv.head_stride + i, o1 = o0 + half;
+        *reinterpret_cast<float4*>(qr + j0) = make_float4(qa.x * cs.x - qb.x * sn.x, qa.y * cs.y - qb.y * sn.y,
+                                                          qa.z * cs.z - qb.z * sn.z, qa.w * cs.w - qb.w * sn.w);
+        *reinterpret_cast<float4*>(qr + j1) = make_float4(qb.x * cs.x + qa.x * sn.x, qb.y * cs.y + qa.y * sn.y,
+                                                          qb.z * cs.z + qa.z * sn.z, qb.w * cs.w + qa.w * sn.w);
+        *reinterpret_cast<float4*>(kr + o0) = make_float4(ka.x * cs.x - kb.x * sn.x, ka.y * cs.y - kb.y * sn.y,
+                                                          ka.z * cs.z - kb.z * sn.z, ka.w * cs.w - kb.w * sn.w);
+        *reinterpret_cast<float4*>(kr + o1) = make_float4(kb.x * cs.x + ka.x * sn.x, kb.y * cs.y + ka.y * sn.y,
+                                                          kb.z * cs.z + ka.z * sn.z, kb.w * cs.w + ka.w * sn.w);
+    }
+    const int d4 = head_dim >> 2;
+    for (int f = threadIdx.x; f < n_heads * d4; f += kThreads) {
+        const int hd = f / d4, d = 4 * (f - hd * d4);
+        *reinterpret_cast<float4*>(vr + hd * kv.head_stride + d) =
+            *reinterpret_cast<const float4*>(row + 2 * D + hd * head_dim + d);
+    }
 }
 
 // act = silu(g) * u (decoder.rs:1746-1752), the dense MLP's SwiGLU.
@@ -318,11 +351,15 @@ hipError_t launch_rope_split(hipStream_t s, const float* qkv, const RopePosition
 }
 
 hipError_t launch_rope_rows(hipStream_t s, const float* qkv, int rows, int c0, const float* inv_freq, int n_heads,
-                            int head_dim, float* q, float* k, float* v) {
-    if (rows < 1 || c0 < 0 || n_heads < 1 || head_dim < 2 || head_dim % 2 || !qkv || !inv_freq || !q || !k || !v)
+                            int head_dim, float* q, float* k, float* v, size_t kv_row_stride,
+                            size_t kv_head_stride) {
+    // float4 rotations: head_dim a multiple of 8 (four pairs per thread), the
+    // row and head strides multiples of 4 floats (16-byte aligned stores)
+    if (rows < 1 || c0 < 0 || n_heads < 1 || head_dim < 8 || head_dim % 8 || head_dim / 2 > kRopeMaxHalf || !qkv ||
+        !inv_freq || !q || !k || !v || kv_row_stride % 4 || kv_head_stride % 4)
         return hipErrorInvalidValue;
     FOCR_LAUNCH(rope_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, qkv, c0, inv_freq,
-                n_heads, head_dim, q, k, v);
+                n_heads, head_dim, q, RopeKv{k, v, kv_row_stride, kv_head_stride});
     return hipGetLastError();
 }
 
