@@ -1444,6 +1444,90 @@ def bench_decode_step(args, ctx):
     }
 
 
+def bench_prefill(args, ctx):
+    """The whole prefill of one stream in one call (focr_hip_decoder_prefill:
+    prefill_with_cache_i8_chunked, decoder.rs:2428-2520): a `tokens`-token
+    sequence in chunks of `chunk` (0: the monolithic schedule) through 12
+    layers (layer 0 the 6848-wide dense MLP, layers 1-11 MoE with the
+    1792-wide shared expert, every layer its own weights and cache), then the
+    final RMSNorm + LM head + argmax of the last row (the first generated
+    token). Every step restores the input embeddings with one device copy,
+    inside the timed region."""
+    from franken_ocr_amd import synth
+    from franken_ocr_amd.engine import Decoder, DecoderLayer, MoeLayer, QInt8, RingCache, prefill_chunk_bounds
+
+    seq, chunk, D, SI, ID, V, NL = args.tokens, args.chunk, 1280, 1792, 6848, 129280, 12
+    log(f"prefill: seq={seq}, chunk={chunk or 'monolithic'}, {NL} layers")
+    base = make_moe_host(100)
+    sh = [synth.int8_uniform(synth.seed_of(800), SI * H), synth.f32_uniform(synth.seed_of(801), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(802), SI * H), synth.f32_uniform(synth.seed_of(803), SI, 1e-3, 2e-2),
+          synth.int8_uniform(synth.seed_of(804), H * SI), synth.f32_uniform(synth.seed_of(805), H, 1e-3, 2e-2)]
+    wqkv = synth.int8_uniform(synth.seed_of(806), 3 * D * H)
+    sqkv = synth.f32_uniform(synth.seed_of(807), 3 * D, 1e-3, 2e-2)
+    wo = synth.int8_uniform(synth.seed_of(808), H * D)
+    so = synth.f32_uniform(synth.seed_of(809), H, 1e-3, 2e-2)
+    ln = [synth.f32_uniform(synth.seed_of(810 + i), H, 0.5, 1.5) for i in range(3)]
+    dense = [synth.int8_uniform(synth.seed_of(840), ID * H), synth.f32_uniform(synth.seed_of(841), ID, 1e-3, 2e-2),
+             synth.int8_uniform(synth.seed_of(842), ID * H), synth.f32_uniform(synth.seed_of(843), ID, 1e-3, 2e-2),
+             synth.int8_uniform(synth.seed_of(844), H * ID), synth.f32_uniform(synth.seed_of(845), H, 1e-3, 2e-2)]
+    layers, caches = [], []
+    for l in range(NL):
+        qkv, o = QInt8(wqkv, sqkv, 3 * D, H, ctx), QInt8(wo, so, H, D, ctx)
+        if l == 0:
+            mlp = dict(dense=(QInt8(dense[0], dense[1], ID, H, ctx), QInt8(dense[2], dense[3], ID, H, ctx),
+                              QInt8(dense[4], dense[5], H, ID, ctx)))
+        else:
+            router = synth.f32_normal(synth.seed_of(1000 + l), E * H, 0.0, 0.02).reshape(E, H)
+            moe = MoeLayer(H, I, E, K, router, *base[1:], ctx=ctx)
+            moe.set_shared(SI, *sh)
+            mlp = dict(moe=moe)
+        layers.append(DecoderLayer(H, ln[0], ln[1], qkv, o, ctx=ctx, **mlp))
+        caches.append(RingCache(1, seq, ctx=ctx))
+    lm = QInt8(synth.int8_uniform(synth.seed_of(850), V * H), synth.f32_uniform(synth.seed_of(851), V, 1e-3, 2e-2), V,
+               H, ctx)
+    dec = Decoder(layers, ln[2], lm, ctx=ctx)
+    x0 = ctx.to_device(synth.f32_normal(synth.seed_of(830), seq * H).reshape(seq, H))
+    x = ctx.empty((seq, H), np.float32)
+    tok = ctx.empty((1,), np.uint32)
+
+    def step(i):
+        x.copy_from_device(x0)  # the input embeddings (the lookup is outside this path)
+        dec.prefill(caches, 0, x, seq, chunk=chunk, token=tok)  # one call: every chunk through 12 layers + LM head
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.device_synchronize()
+    el, prof, kernels, sstats = timed(ctx, step, args.steps)
+    ms = el / args.steps * 1e3
+    nb = len(prefill_chunk_bounds(seq, chunk or seq))
+    # algorithmic work per step: int8 products (2 ops per multiply-add) and
+    # the attention's f32 flops
+    int8_ops = 2.0 * seq * (NL * (3 * D * H + H * D) + (NL - 1) * (K * 3 * I * H + 3 * SI * H) + 3 * ID * H) + \
+        2.0 * V * H
+    f32_flops = NL * attn_flops(seq) + (NL - 1) * 2.0 * seq * E * H
+    ideal_ms = (int8_ops / (MFMA_INT8_PEAK_TOPS * 1e12) + f32_flops / (MFMA_F32_PEAK_TFLOPS * 1e12)) * 1e3
+    weights = NL * (3 * D * H + H * D) + (NL - 1) * (E * 3 * I * H + 3 * SI * H) + 3 * ID * H + V * H
+    log(f"per-kernel avg us {kernels}")
+    return {
+        "metric": f"whole prefill tokens/s (12 layers, {seq} tokens, "
+                  f"{'one chunk' if not chunk or chunk >= seq else f'chunks of {chunk}'}, + first token), 1 GPU",
+        "value": round(seq * args.steps / el, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "dtype": "int8",
+        "config": {"workload": "prefill", "seq": seq, "chunk": chunk, "chunks": nb, "layers": NL, "hidden": H,
+                   "experts": E, "top_k": K, "inter": I, "shared_inter": SI, "dense_inter": ID, "vocab": V},
+        "roofline": {"bound": "mfma", "kernel": "the whole prefill", "achieved": round(int8_ops / (ms * 1e-3) / 1e12, 2),
+                     "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(int8_ops / (ms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 4), "traffic": None,
+                     "avg_step_us": round(ms * 1e3, 3)},
+        "mfma_utilisation": {"int8_ops_per_step": int8_ops, "f32_flops_per_step": f32_flops,
+                             "ideal_ms_at_peak": round(ideal_ms, 5), "frac_of_step": round(ideal_ms / ms, 4),
+                             "weight_bytes_per_chunk": int(weights),
+                             "weight_gbs_over_step": round(weights * nb / (ms * 1e-3) / 1e9, 1)},
+        "kernel_avg_us": kernels,
+        "step_us": sstats,
+        "_cpu_inputs": None,
+    }
+
+
 # ---------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size (the reference
 # point for the FETCH_SIZE / WRITE_SIZE counters)
@@ -1493,6 +1577,7 @@ WORKLOADS = {
     "decode_step": (bench_decode_step, None),
     "prefill_attn": (bench_prefill_attn, cpu_prefill_attn),
     "prefill_layer": (bench_prefill_layer, cpu_prefill_layer),
+    "prefill": (bench_prefill, None),
 }
 
 
@@ -1516,6 +1601,9 @@ EXTRAS = [
     # the same 1024 tokens as one chunk: HBM holds the whole prompt's rows, and
     # the routed experts are read once instead of once per 256-row chunk
     ("prefill_layer_1024_c1024", "prefill_layer", 1024, 2, 10, 2, {"chunk": 1024}),
+    # the whole prefill of a 1024-token prompt, 12 layers + the first token, in one call
+    ("prefill_1024", "prefill", 1024, 1, 10, 2),
+    ("prefill_1024_c1024", "prefill", 1024, 1, 10, 2, {"chunk": 1024}),
 ]
 _EXTRA_KEYS = ("layer_roofline", "mfma_utilisation", "layer_mfma", "kernel_avg_us", "step_us")
 
@@ -1594,7 +1682,7 @@ def main() -> int:
                 "copy": (1, 1),
                 "moe_prefill_i4": (512, 3), "moe_prefill_i8": (512, 2), "linear_i8": (2048, 3),
                 "decode_layer": (8, 6), "decode_step": (8, 1), "prefill_attn": (1024, 1),
-                "prefill_layer": (1024, 2)}
+                "prefill_layer": (1024, 2), "prefill": (1024, 1)}
     dt, dc = defaults[args.workload]
     args.tokens = args.tokens or dt
     args.copies = args.copies or dc

@@ -102,6 +102,7 @@ _SIGS: dict[str, list] = {
     "focr_hip_decoder_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I32],
     "focr_hip_decoder_step_sample": [_P, _P, _P, _P, _P, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _F32, C.c_uint32, _I32,
                                      _P, _P, _P, _P, _I32],
+    "focr_hip_decoder_prefill": [_P, _P, _P, _SZ, _P, _SZ, _SZ, _P, _P, _P, _I32],
     "focr_hip_rswa_create": [_P, _SZ, _SZ, _P],
     "focr_hip_rswa_free": [_P],
     "focr_hip_rswa_record_prefill": [_P, _P, _SZ, _P, _P, _SZ],

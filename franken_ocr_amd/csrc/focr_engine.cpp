@@ -1798,10 +1798,9 @@ static int32_t prefill_route_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L
     return route_rows_impl(ctx, L, x, t, 0, 1.0f, idx, gates, nullptr, flag);
 }
 
-int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
-                                       size_t stream, float* x, size_t cs, size_t c0, uint32_t* route_idx,
-                                       int32_t check_route) {
-    ENGINE_CTX(ctx);
+static int32_t decoder_layer_prefill_impl(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+                                          size_t stream, float* x, size_t cs, size_t c0, uint32_t* route_idx,
+                                          int32_t check_route) {
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_prefill: null layer");
     if (!cache) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_layer_prefill: null rswa cache");
     if (!x) return fail(FOCR_HIP_E_ARG, "decoder_layer_prefill: null x");
@@ -1899,6 +1898,13 @@ int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder
     ProfScope ps(ctx, "layer_prefill_residual");
     FOCR_HIP_TRY(launch_add_rows(s, h, mlp, x, cs * H), "residual launch");
     return FOCR_HIP_OK;
+}
+
+int32_t focr_hip_decoder_layer_prefill(focr_hip_ctx* ctx, const focr_hip_decoder_layer* L, focr_hip_rswa* cache,
+                                       size_t stream, float* x, size_t cs, size_t c0, uint32_t* route_idx,
+                                       int32_t check_route) {
+    ENGINE_CTX(ctx);
+    return decoder_layer_prefill_impl(ctx, L, cache, stream, x, cs, c0, route_idx, check_route);
 }
 
 // ---- the whole batched decode step (decoder.rs:2812-2965) ------------------------
@@ -2036,6 +2042,53 @@ int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* 
             return st;
     }
     return FOCR_HIP_OK;
+}
+
+// ---- the whole prefill of one stream (decoder.rs:2428-2520) ---------------------
+
+int32_t focr_hip_decoder_prefill(focr_hip_ctx* ctx, const focr_hip_decoder* d, focr_hip_rswa* const* caches,
+                                 size_t stream, float* x, size_t seq, size_t chunk, float* logits, uint32_t* token,
+                                 uint32_t* route_idx, int32_t check_route) {
+    ENGINE_CTX(ctx);
+    if (!d) return fail(FOCR_HIP_E_BAD_HANDLE, "decoder_prefill: null decoder");
+    if (!caches || !x) return fail(FOCR_HIP_E_ARG, "decoder_prefill: null caches or x");
+    if (seq < 1) return fail(FOCR_HIP_E_SHAPE, "decoder_prefill: empty sequence");
+    const size_t NL = d->layers.size();
+    for (size_t l = 0; l < NL; ++l) {
+        if (!caches[l]) return fail(FOCR_HIP_E_BAD_HANDLE, fmt("decoder_prefill: null rswa cache for layer %zu", l));
+        if (stream >= caches[l]->n_streams)
+            return fail(FOCR_HIP_E_SHAPE, fmt("rswa: stream %zu >= num_streams %zu", stream, caches[l]->n_streams));
+        if (seq > caches[l]->ref_capacity)
+            return fail(FOCR_HIP_E_STATE,
+                        fmt("rswa: prefill seq %zu exceeds ref_capacity %zu", seq, caches[l]->ref_capacity));
+    }
+    // prefill_chunk_bounds(seq, chunk) with every layer per chunk, the chunk
+    // loop outermost as in the reference; chunk 0: the monolithic schedule.
+    // A chunk is at most the layer step's row limit.
+    const size_t step = std::min<size_t>(chunk ? chunk : seq, static_cast<size_t>(kLayerPrefillMaxRows));
+    const size_t H = d->hidden;
+    int32_t st;
+    for (size_t c0 = 0; c0 < seq; c0 += step) {
+        const size_t cs = std::min(step, seq - c0);
+        for (size_t l = 0; l < NL; ++l) {
+            const focr_hip_decoder_layer* L = d->layers[l];
+            uint32_t* ri = (route_idx && L->moe) ? route_idx + (l * seq + c0) * d->top_k : nullptr;
+            if ((st = decoder_layer_prefill_impl(ctx, L, caches[l], stream, x + c0 * H, cs, c0, ri, check_route)))
+                return st;
+        }
+    }
+    if (!logits && !token) return FOCR_HIP_OK;
+    // the first generated token: model.norm of the last position, the LM
+    // head and argmax_row (decoder.rs:2943-2965, sampler.rs:168-186)
+    float* xn = static_cast<float*>(ctx->scratch_get(kScrDec, H * sizeof(float) + 256));
+    if (!xn) return FOCR_HIP_E_OOM;
+    uint32_t* tok = token ? token : reinterpret_cast<uint32_t*>(xn + H);
+    {
+        ProfScope ps(ctx, "rms_norm");
+        FOCR_HIP_TRY(launch_rms_norm(ctx->stream, x + (seq - 1) * H, d->final_norm, 1, (int)H, d->eps, xn),
+                     "final rms_norm launch");
+    }
+    return lm_head_i8_impl(ctx, d->lm_head, xn, 1, logits, tok);
 }
 
 int32_t focr_hip_rswa_get_state(const focr_hip_rswa* c, size_t stream, uint32_t* prefill_len, uint32_t* ring_len,

@@ -504,6 +504,19 @@ class Decoder:
                   *_sampler_args(history, history_len, ngram_size, window, whitelist, temperature, eos, append),
                   _p(logits), tokens.c_ptr, _p(is_eos), _p(route_idx), 1 if check_route else 0)
 
+    def prefill(self, caches: list["RingCache"], stream: int, x: DeviceArray, seq: int, chunk: int | None = None,
+                token: DeviceArray | None = None, logits: DeviceArray | None = None,
+                route_idx: DeviceArray | None = None, check_route: bool = False) -> None:
+        """prefill_with_cache_i8_chunked (decoder.rs:2428-2520) of one stream:
+        x [seq, hidden] (device) holds the input embeddings and receives the
+        last layer's hidden rows; every layer's chunk K / V go to caches[l]'s
+        stream; chunk None is the monolithic schedule. token / logits
+        (optional): the first generated token from the last position (final
+        norm, LM head, argmax); route_idx (optional) [n_layers, seq, top_k]."""
+        cs = self._caches(caches)
+        _abi.call("focr_hip_decoder_prefill", self.ctx.handle, self._h, C.cast(cs, C.c_void_p), int(stream), x.c_ptr,
+                  int(seq), int(chunk or 0), _p(logits), _p(token), _p(route_idx), 1 if check_route else 0)
+
     def free(self) -> None:
         if self._h:
             _abi.lib().focr_hip_decoder_free(self._h)

@@ -522,6 +522,23 @@ int32_t focr_hip_decoder_step_sample(focr_hip_ctx* ctx, const focr_hip_decoder* 
                                      size_t n_whitelist, float temperature, uint32_t eos_token_id,
                                      int32_t append, float* logits, uint32_t* tokens, uint8_t* is_eos,
                                      uint32_t* route_idx, int32_t check_route);
+/* The whole prefill of one stream in one call: decoder.rs:2428-2520
+ * prefill_with_cache_i8_chunked over the decoder's layers. For each chunk
+ * [c0, c1) of prefill_chunk_bounds(seq, chunk), in order, every layer as
+ * focr_hip_decoder_layer_prefill (layer l's chunk K / V into caches[l],
+ * stream `stream`, starting over at c0 = 0); chunk 0 is the monolithic
+ * schedule (the reference's chunk = None); a chunk is at most 4096 rows.
+ * x [seq, hidden] device: the input embeddings in, the last layer's hidden
+ * rows out (the model.norm-ready hidden the reference returns). With logits
+ * [vocab] and / or token [1] (device, nullable) it also takes the first
+ * generated token: the final RMSNorm of row seq - 1, the LM head and
+ * argmax_row. route_idx (device, nullable) [n_layers][seq][top_k] receives
+ * each MoE layer's expert ids (a dense layer's slice untouched); check_route
+ * as focr_hip_decoder_layer_prefill (a chunk's row index in the message).
+ * seq <= every cache's ref_capacity. */
+int32_t focr_hip_decoder_prefill(focr_hip_ctx* ctx, const focr_hip_decoder* dec, focr_hip_rswa* const* caches,
+                                 size_t stream, float* x, size_t seq, size_t chunk, float* logits,
+                                 uint32_t* token, uint32_t* route_idx, int32_t check_route);
 
 /* ---- weight container: .focrq / safetensors (weights.rs, quant/focrq.rs) --
  * The reader restates weights.rs:443-620 (format detection by magic, the

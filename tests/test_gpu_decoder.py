@@ -235,3 +235,74 @@ def test_decoder_step_argument_errors(ctx, model):
     for c in caches + [other]:
         c.free()
     dec.free()
+
+
+def _ref_block(ctx, cache, seq):
+    import ctypes as C
+
+    reg = cache.regions(0)
+    out = []
+    for key in ("ref_k", "ref_v"):
+        full = np.empty((10, seq, 128), np.float32)  # ref_capacity == seq
+        _abi.call("focr_hip_d2h", ctx.handle, full.ctypes.data_as(C.c_void_p), C.c_void_p(reg[key]), full.nbytes)
+        out.append(full)
+    return out
+
+
+@pytest.mark.parametrize("chunk", [64, None])
+def test_decoder_prefill_equals_the_layer_calls(ctx, model, chunk):
+    """focr_hip_decoder_prefill (prefill_with_cache_i8_chunked, decoder.rs:
+    2428-2520) is the per-layer prefill issued chunk by chunk, every layer per
+    chunk, then the final norm + LM head + argmax of the last row: the same
+    bits (hidden rows, every layer's reference block, expert ids, logits,
+    token). chunk None: the monolithic schedule, one chunk of all rows."""
+    from franken_ocr_amd.engine import RingCache, lm_head_i8, prefill_chunk_bounds, rms_norm
+
+    seq = 150
+    _say(f"prefill of {seq} rows, chunk {chunk}: one call vs the layer calls")
+    layers, lm, dec = _device(ctx, model)
+    final_dev = ctx.to_device(model[1])
+    x0 = synth.f32_normal(synth.seed_of(23000), seq * H).reshape(seq, H)
+    ca = [RingCache(1, seq, ctx=ctx) for _ in range(3)]
+    cb = [RingCache(1, seq, ctx=ctx) for _ in range(3)]
+    xa, xb = ctx.to_device(x0), ctx.to_device(x0)
+    moe = ["moe" in lw for lw in model[0]]
+    ia = ctx.empty((3 * seq, K), np.uint32)
+    ib = np.zeros((3, seq, K), np.uint32)
+    ta, tb = ctx.empty((1,), np.uint32), ctx.empty((1, 1), np.uint32)
+    la, lb = ctx.empty((1, V), np.float32), ctx.empty((1, V), np.float32)
+    dec.prefill(ca, 0, xa, seq, chunk=chunk, token=ta, logits=la, route_idx=ia)
+    for c0, c1 in prefill_chunk_bounds(seq, chunk or seq):
+        for li, layer in enumerate(layers):
+            ri = ctx.empty((c1 - c0, K), np.uint32) if moe[li] else None
+            layer.prefill(cb[li], 0, xb.view_rows(c0, c1), c0, ri)
+            if ri is not None:
+                ib[li, c0:c1] = ri.numpy()
+    xn = ctx.empty((1, H), np.float32)
+    rms_norm(xb.view_rows(seq - 1, seq), xn, final_dev)
+    lm_head_i8(lm, xn, tb, lb)
+    assert np.array_equal(xa.numpy(), xb.numpy())
+    assert np.array_equal(ta.numpy().ravel(), tb.numpy().ravel())
+    assert np.array_equal(la.numpy(), lb.numpy())
+    got_idx = ia.numpy().reshape(3, seq, K)
+    for li in range(3):
+        assert ca[li].state(0) == (seq, 0, 0)
+        for a, b in zip(_ref_block(ctx, ca[li], seq), _ref_block(ctx, cb[li], seq)):
+            assert np.array_equal(a, b), f"layer {li} reference block"
+        if moe[li]:
+            assert np.array_equal(got_idx[li], ib[li])
+    assert np.isfinite(xa.numpy()).all()
+
+
+def test_decoder_prefill_argument_errors(ctx, model):
+    from franken_ocr_amd.engine import RingCache
+
+    layers, lm, dec = _device(ctx, model)
+    x = ctx.empty((40, H), np.float32)
+    small = [RingCache(1, 32, ctx=ctx) for _ in range(3)]
+    with pytest.raises(_abi.FocrHipError, match="exceeds ref_capacity"):
+        dec.prefill(small, 0, x, 40)
+    with pytest.raises(_abi.FocrHipError, match="stream 1 >= num_streams 1"):
+        dec.prefill(small, 1, x, 16)
+    with pytest.raises(ValueError, match="2 caches for 3 layers"):
+        dec.prefill(small[:2], 0, x, 16)
