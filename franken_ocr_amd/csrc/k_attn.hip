@@ -131,32 +131,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
     const int r8 = threadIdx.x >> 5;  // 8 rows per pass
     const float* kh = a.k + static_cast<size_t>(h) * a.hk + 4 * c4;
     const float* vh = a.v + static_cast<size_t>(h) * a.hv + 4 * c4;
-    // The tile after the current one is loaded into registers while the
-    // current one is consumed from LDS (key rows clamped into the prefix; a
-    // load past the range end is never used).
+    // Tile loads of keys kb .. kb + kKT - 1 (rows clamped into the prefix; a
+    // row past the range end is never used) and their LDS stores.
     v4f pk[kPieces], pv[kPieces];
+    auto load_tile = [&](int kb) {
 #pragma unroll
-    for (int p = 0; p < kPieces; ++p) {
-        int key = ks + r8 + 8 * p;
-        key = key < a.c1 ? key : a.c1 - 1;
-        pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
-        pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
-    }
-    for (int kb = ks; kb < ke; kb += kKT) {
-        __syncthreads();  // the previous tile's readers are done
+        for (int p = 0; p < kPieces; ++p) {
+            int key = kb + r8 + 8 * p;
+            key = key < a.c1 ? key : a.c1 - 1;
+            pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
+            pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
+        }
+    };
+    auto store_tile = [&]() {
 #pragma unroll
         for (int p = 0; p < kPieces; ++p) {
             *reinterpret_cast<v4f*>(lk + (r8 + 8 * p) * kLdsRow + 4 * c4) = pk[p];
             *reinterpret_cast<v4f*>(lv + (r8 + 8 * p) * kLdsRow + 4 * c4) = pv[p];
         }
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < kPieces; ++p) {
-            int key = kb + kKT + r8 + 8 * p;
-            key = key < a.c1 ? key : a.c1 - 1;
-            pk[p] = *reinterpret_cast<const v4f*>(kh + static_cast<size_t>(key) * a.ldk);
-            pv[p] = *reinterpret_cast<const v4f*>(vh + static_cast<size_t>(key) * a.ldv);
-        }
+    };
+    if (ks < ke) {
+        load_tile(ks);
+        store_tile();
+    }
+    // every load so far (the Q fragment too) complete on every path into
+    // the loop, so the loop's first MFMAs wait for none of the tile loads
+    // issued inside it (vmcnt(0): the counter drains in issue order)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    // Each iteration issues the next tile's loads first, consumes the
+    // current tile from LDS while they are in flight, then (after every wave
+    // has read it) stores the next tile over it. The loads are consumed in
+    // the iteration that issues them: a load carried into the next iteration
+    // was folded with the one before the loop into a single load at the top
+    // of the loop, which waited out a full memory round trip on every tile.
+    for (int kb = ks; kb < ke; kb += kKT) {
+        const bool more = kb + kKT < ke;
+        if (more) load_tile(kb + kKT);
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the tile's MFMAs
 
         // S^T for the subtiles of 16 keys; each score dot runs as two
         // 16-step MFMA chains (64 dims each) added at the end, halving the
@@ -206,12 +218,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
         tsum = wave16_sum(tsum);
         l_run = l_run * corr + tsum;
         m_run = m_new;
-        // this tile's V^T . P^T in fresh accumulators (step (n, r) is key
-        // kb + 16n + 4g + r), folded into the running output once per tile:
-        // 32-term sums then a per-tile sum, not one long f32 chain
-        v4f otile[8];
+        // the running output rescaled to the new max, then this tile's
+        // V^T . P^T accumulated into it (step (n, r) is key kb + 16n + 4g + r)
 #pragma unroll
-        for (int m = 0; m < 8; ++m) otile[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int m = 0; m < 8; ++m) oacc[m] = oacc[m] * corr;
 #pragma unroll
         for (int n = 0; n < kSub; ++n)
 #pragma unroll
@@ -220,17 +230,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
                 const v4f v0 = *reinterpret_cast<const v4f*>(vr);
                 const v4f v1 = *reinterpret_cast<const v4f*>(vr + 4);
                 const float b = pr[n][r];
-                otile[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.x, b, otile[0], 0, 0, 0);
-                otile[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.y, b, otile[1], 0, 0, 0);
-                otile[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.z, b, otile[2], 0, 0, 0);
-                otile[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.w, b, otile[3], 0, 0, 0);
-                otile[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.x, b, otile[4], 0, 0, 0);
-                otile[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.y, b, otile[5], 0, 0, 0);
-                otile[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.z, b, otile[6], 0, 0, 0);
-                otile[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.w, b, otile[7], 0, 0, 0);
+                oacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.x, b, oacc[0], 0, 0, 0);
+                oacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.y, b, oacc[1], 0, 0, 0);
+                oacc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.z, b, oacc[2], 0, 0, 0);
+                oacc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.w, b, oacc[3], 0, 0, 0);
+                oacc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.x, b, oacc[4], 0, 0, 0);
+                oacc[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.y, b, oacc[5], 0, 0, 0);
+                oacc[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.z, b, oacc[6], 0, 0, 0);
+                oacc[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.w, b, oacc[7], 0, 0, 0);
             }
-#pragma unroll
-        for (int m = 0; m < 8; ++m) oacc[m] = oacc[m] * corr + otile[m];
+        if (more) {  // block-uniform
+            __syncthreads();  // every wave is done with this tile
+            store_tile();
+            __syncthreads();
+        }
     }
     if (wrow >= a.cs) return;
     // lane (g, j) holds O[row j][32g + 8r' + m] in oacc[m][r']
