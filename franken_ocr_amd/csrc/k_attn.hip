@@ -106,6 +106,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
     const int kmax = min(a.c1, a.c0 + row0 + 64);
     const int ks = split * a.split_len;
     const int ke = min(ks + a.split_len, kmax);
+    // a range past the row tile's last key: nothing to do or write (the
+    // merge skips it by the same bound); block-uniform
+    if (ks >= ke) return;
 
     // Q fragment: qf[s] = q[row j][32g + s], s = 0..31
     float qf[32];
@@ -171,25 +174,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before the tile's MFMAs
 
         // S^T for the subtiles of 16 keys; each score dot runs as two
-        // 16-step MFMA chains (64 dims each) added at the end, halving the
-        // f32 accumulation chain of the 128-term dot
+        // 16-step MFMA chains (dims 32g + 16h + [0, 16), h = 0, 1) added at
+        // the end, halving the f32 accumulation chain of the 128-term dot.
+        // The 2 * kSub chains advance together: each step reads their four
+        // dims of K (one 16-byte LDS read per chain) and issues one MFMA per
+        // chain and dim, so a chain's dependent MFMAs interleave with the
+        // other chains' (each chain's own order is unchanged: u, then dim).
+        v4f sc[kSub][2];
+#pragma unroll
+        for (int n = 0; n < kSub; ++n) sc[n][0] = sc[n][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u2 = 0; u2 < 4; ++u2) {
+            v4f kf[kSub][2];
+#pragma unroll
+            for (int n = 0; n < kSub; ++n)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+                    kf[n][hh] = *reinterpret_cast<const v4f*>(lk + (16 * n + j) * kLdsRow + 32 * g + 16 * hh + 4 * u2);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int n = 0; n < kSub; ++n)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        sc[n][hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[n][hh][c], qf[16 * hh + 4 * u2 + c],
+                                                                         sc[n][hh], 0, 0, 0);
+        }
         v4f sacc[kSub];
 #pragma unroll
-        for (int n = 0; n < kSub; ++n) {
-            v4f sc[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) sc[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const v4f kf = *reinterpret_cast<const v4f*>(lk + (16 * n + j) * kLdsRow + 32 * g + 4 * u);
-                v4f& acc = sc[u >> 2];
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[4 * u], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[4 * u + 1], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[4 * u + 2], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[4 * u + 3], acc, 0, 0, 0);
-            }
-            sacc[n] = sc[0] + sc[1];
-        }
+        for (int n = 0; n < kSub; ++n) sacc[n] = sc[n][0] + sc[n][1];
         // scale, causal / range mask, online softmax (row j over 4 lanes)
         float pr[kSub][4];
         float tmax = -INFINITY;
@@ -280,8 +293,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kBlocksPerC
 // M = max_s m_s, the maxima in base-2 units (a range with no key of the row
 // has m = -inf, l = 0, O = 0).
 // Thread = one dim of one (row, head).
-// Up to kMergeBatch splits, every split's (max, denominator) and output
-// value are requested at once (clamped duplicates past nsplit, never used),
+// Only the ranges below the row tile's last key were written (ns of them).
+// Up to kMergeBatch ranges, every range's (max, denominator) and output
+// value are requested at once (clamped duplicates past ns, never used),
 // then folded in split order; a loop that loaded one split at a time waited
 // on each in turn. More splits take that loop. Both fold the same values in
 // the same order.
@@ -289,12 +303,16 @@ constexpr int kMergeBatch = 16;
 
 __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
     const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    // the row's 64-row tile has keys [0, kmax): the ranges from kmax on had
+    // no block write them
+    const int kmax = min(a.c1, a.c0 + (row / 64 + 1) * 64);
+    const int ns = min(a.nsplit, (kmax + a.split_len - 1) / a.split_len);
     float den = 0.0f, acc = 0.0f;
-    if (a.nsplit <= kMergeBatch) {
+    if (ns <= kMergeBatch) {
         float ms[kMergeBatch], ls[kMergeBatch], os[kMergeBatch];
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
-            const int sc = s < a.nsplit ? s : a.nsplit - 1;
+            const int sc = s < ns ? s : ns - 1;
             const size_t pidx = (static_cast<size_t>(sc) * a.heads + h) * a.cs + row;
             ms[s] = a.part_ml[pidx * 2];
             ls[s] = a.part_ml[pidx * 2 + 1];
@@ -302,15 +320,14 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
         }
         // every use unconditional (a guarded use lets the compiler sink the
         // load under the guard, one wait per split again): the duplicates
-        // past nsplit repeat the last split's max, and an unused split adds
-        // a selected +0 (the sums never hold -0, so x + 0 == x), also where
-        // a split with no keys left its values unwritten
+        // past ns repeat the last written range's max, and an unused range
+        // adds a selected +0 (the sums never hold -0, so x + 0 == x)
         float M = -INFINITY;
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) M = fmaxf(M, ms[s]);
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
-            const bool use = s < a.nsplit && ms[s] != -INFINITY;
+            const bool use = s < ns && ms[s] != -INFINITY;
             const float w = __builtin_amdgcn_exp2f((use ? ms[s] : M) - M);
             const float dl = w * ls[s], da = w * os[s];
             den += use ? dl : 0.0f;
@@ -318,9 +335,9 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
         }
     } else {
         float M = -INFINITY;
-        for (int s = 0; s < a.nsplit; ++s)
+        for (int s = 0; s < ns; ++s)
             M = fmaxf(M, a.part_ml[((static_cast<size_t>(s) * a.heads + h) * a.cs + row) * 2]);
-        for (int s = 0; s < a.nsplit; ++s) {
+        for (int s = 0; s < ns; ++s) {
             const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
             const float ms = a.part_ml[pidx * 2];
             if (ms == -INFINITY) continue;
