@@ -98,6 +98,33 @@ def test_route_many_rows_equals_the_split_route(ctx, layer_w, tied):
     np.testing.assert_allclose(ga, w, rtol=1e-6, atol=0)
 
 
+@pytest.mark.parametrize("e,k,h", [(37, 5, 1280), (9, 2, 640), (64, 8, 1024)])
+def test_route_many_rows_other_shapes(ctx, e, k, h):
+    """The many-row route at expert counts that leave a part of the last
+    eight-expert block empty, other top-k and narrower rows: the bits of the
+    split route on the first 64 rows, the oracle's indices on all 100."""
+    from franken_ocr_amd.engine import MoeLayer
+
+    inter = 64
+    w = make_layer(720 + e, h=h, inter=inter, e=e)
+    L = MoeLayer(h, inter, e, k, *w, ctx=ctx)
+    t = 100
+    x = synth.f32_normal(synth.seed_of(721 + e), t * h).reshape(t, h)
+    outs = []
+    for n in (64, t):
+        didx, dg, dp = ctx.empty((n, k), np.uint32), ctx.empty((n, k), np.float32), ctx.empty((n, e), np.float32)
+        L.route(ctx.to_device(np.ascontiguousarray(x[:n])), didx, dg, dp, norm_topk=True)
+        outs.append((didx.numpy(), dg.numpy(), dp.numpy()))
+    (i64, g64, p64), (ia, ga, pa) = outs
+    assert np.array_equal(ia[:64], i64)
+    assert np.array_equal(ga[:64].view(np.uint32), g64.view(np.uint32))
+    assert np.array_equal(pa[:64].view(np.uint32), p64.view(np.uint32))
+    st, idx, gw, probs = O.route(x, w[0], e, k, norm_topk=True)
+    assert st == 0 and np.array_equal(ia, idx)
+    np.testing.assert_allclose(ga, gw, rtol=1e-6, atol=0)
+    np.testing.assert_allclose(pa, probs, rtol=1e-6, atol=1e-12)
+
+
 def test_route_ties_at_the_cutoff_pick_lower_indices(ctx):
     """Seven identical router rows that dominate every token: their logits and
     probabilities are bit-identical, so the greedy top-6 (moe.rs:215-240: rank
