@@ -23,16 +23,22 @@
 // column l % 32, bytes 16 (l / 32) + [0, 16) of the 32-wide K step; C element
 // v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.
 //
-// Activations: 512-byte K chunks of the tile's 64 rows (32 KB) are staged in
+// Activations: 256-byte K chunks of the tile's 64 rows (16 KB) are staged in
 // LDS through registers (two buffers; the next chunk's loads are in flight
-// while the current one's 8 stages run, and land in the other buffer at the
+// while the current one's 4 stages run, and land in the other buffer at the
 // end), the 16-byte piece p of row r at slot p ^ (r & 15): the 16 rows a
 // quarter-wave's fragment read touches then start on 16 different banks.
+// With 32 KB of LDS and at most 168 registers a block, three blocks share a
+// CU: measured against 512-byte chunks with four fragment stages in flight
+// (two blocks a CU), the prefill layer's grouped gate/up at 256 / 1024 rows
+// went 33.2 -> 31.5 / 54.4 -> 51.4 us and the down 41.8 -> 35.3 us at 1024
+// rows; the depth of the fragment ring alone (two or four stages) moved
+// nothing, so the two-stage ring pays for the third block's registers.
 // (Direct global -> LDS loads would save the registers, but the compiler
 // cannot tell the buffer they fill from the one being read and drains every
 // load before each LDS read.)
 // Weights go global -> VGPR, each lane loading exactly the 16-byte fragments
-// its MFMAs take, four 64-byte K stages ahead, from a fragment-ordered copy
+// its MFMAs take, two 64-byte K stages ahead, from a fragment-ordered copy
 // (launch_retile_i8) made once per handle: a wave's fragment load is then
 // 1 KB contiguous. Read in the upload layout ([E][N][K], output-channel-major,
 // what decode uses), each load touched 32 rows — 32 cache lines — and the
@@ -50,9 +56,12 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int BM = kMoePlanTileRows;  // 64 rows per block tile
 constexpr int KB = 64;                // K bytes per stage (two MFMA K steps)
-constexpr int KC = 512;               // K bytes per staged activation chunk
+constexpr int KC = 256;               // K bytes per staged activation chunk
+constexpr int PPR = KC / 16;          // 16-byte pieces per staged row (a multiple of 16: the swizzle)
 constexpr int SPC = KC / KB;          // stages per chunk
 constexpr int kXcds = 8;
+constexpr int kRing = 2;              // K stages of weight fragments in flight
+static_assert(PPR % 16 == 0, "the LDS swizzle permutes pieces within groups of 16");
 
 enum I8Epi { kI8Linear = 0, kI8Swiglu = 1, kI8Down = 2 };
 
@@ -132,16 +141,16 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
             for (int s = 0; s < 2; ++s)
                 f[2 * j + s] = *reinterpret_cast<const v4i*>(bp[j] + static_cast<size_t>(2 * ss + s) * 1024);
     };
-    // a ring of four stages of fragments, stage st in f[st % 4], loaded four
-    // stages ahead (SPC = 8 stages per chunk keeps the ring index a constant)
-    v4i f[4][4];
+    // a ring of kRing stages of fragments, stage st in f[st % kRing], loaded
+    // kRing stages ahead (SPC a multiple of kRing keeps the ring index a constant)
+    v4i f[kRing][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) load_b(q, f[q]);
+    for (int q = 0; q < kRing; ++q) load_b(q, f[q]);
     __syncthreads();  // the row tables
 
-    // Chunk c of the activations: 64 rows x 32 pieces of 16 bytes; thread tid
-    // loads pieces tid + 256 i (row q / 32, piece q % 32: 32 threads read a
-    // row's 512 contiguous bytes) into registers, and stores piece p of row r
+    // Chunk c of the activations: 64 rows x PPR pieces of 16 bytes; thread tid
+    // loads pieces tid + 256 i (row q / PPR, piece q % PPR: PPR threads read a
+    // row's KC contiguous bytes) into registers, and stores piece p of row r
     // at LDS slot p ^ (r & 15). Pieces past K are clamped into the row (never
     // read).
     const int nchunks = (K + KC - 1) / KC;
@@ -150,7 +159,7 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
 #pragma unroll
         for (int i = 0; i < APT; ++i) {
             const int q = tid + 256 * i;
-            const int r = q >> 5, p = q & 31;
+            const int r = q / PPR, p = q % PPR;
             int kb = c * KC + 16 * p;
             kb = kb < K ? kb : 0;
             v[i] = *reinterpret_cast<const v4i*>(a.A + static_cast<size_t>(s_arow[r]) * K + kb);
@@ -160,7 +169,7 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
 #pragma unroll
         for (int i = 0; i < APT; ++i) {
             const int q = tid + 256 * i;
-            const int r = q >> 5, p = q & 31;
+            const int r = q / PPR, p = q % PPR;
             *reinterpret_cast<v4i*>(base + r * KC + 16 * (p ^ (r & 15))) = v[i];
         }
     };
@@ -173,7 +182,7 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
         const v4i z = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const int c16 = 4 * ls + 2 * s + h;  // 16-byte chunk of the 512-byte row
+            const int c16 = 4 * ls + 2 * s + h;  // 16-byte piece of the staged row
             const v4i a0 = *reinterpret_cast<const v4i*>(buf + c32 * KC + 16 * (c16 ^ (c32 & 15)));
             const v4i a1 = *reinterpret_cast<const v4i*>(buf + (32 + c32) * KC + 16 * (c16 ^ ((32 + c32) & 15)));
             const v4i b0 = live ? f[s] : z;
@@ -185,7 +194,7 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
         }
     };
 
-    static_assert(SPC % 4 == 0, "the fragment ring must divide a chunk's stages");
+    static_assert(SPC % kRing == 0, "the fragment ring must divide a chunk's stages");
     // Chunk c: its SPC stages from LDS, the next chunk's loads in flight
     // meanwhile, stored to the other buffer at the end (the last chunk
     // reloads itself: every iteration is the same straight-line code, which
@@ -203,9 +212,9 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
 #pragma unroll
         for (int ls = 0; ls < SPC; ++ls) {
             const int st = c * SPC + ls;
-            compute(buf, ls, f[ls % 4], st < S);
+            compute(buf, ls, f[ls % kRing], st < S);
             __builtin_amdgcn_sched_barrier(0);  // keep each stage's refill after its MFMAs
-            load_b(st + 4, f[ls % 4]);
+            load_b(st + kRing, f[ls % kRing]);
             __builtin_amdgcn_sched_barrier(0);
         }
         store_chunk(next, av);
@@ -254,7 +263,7 @@ __device__ __forceinline__ void i8_tile(const I8Args& a, int e, int r0, int nr, 
 
 // Dense: grid (row tile, column block) over the M rows of one matrix.
 template <int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i8_gemm_kernel(I8Args a, int M) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_gemm_kernel(I8Args a, int M) {
     const int r0 = blockIdx.x * BM;
     i8_tile<EPI>(a, 0, r0, min(BM, M - r0), blockIdx.y);
 }
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
 // (block b runs unit (b % 8) * per + b / 8), so an expert's row tiles that
 // share a weight slab run together on one XCD and its L2 serves the repeats.
 template <int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i8_grouped_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_grouped_kernel(
     I8Args a, const int* __restrict__ n_tiles, const int* __restrict__ tile_e, const int* __restrict__ tile_r0,
     const int* __restrict__ tile_nr, const int* __restrict__ exp_nt, const int* __restrict__ exp_t0) {
     constexpr int BNB = bcols<EPI>();
