@@ -489,9 +489,8 @@ void free_moe(focr_hip_moe_layer* L) {
         hipFree(L->ssu);
         hipFree(L->ssd);
     }
-    for (int8_t* p : {L->wg_mfma, L->wu_mfma, L->wd_mfma, L->swg_mfma, L->swu_mfma, L->swd_mfma, L->swgu_cat})
+    for (int8_t* p : {L->wg_mfma, L->wu_mfma, L->wd_mfma, L->swg_mfma, L->swu_mfma, L->swd_mfma})
         hipFree(p);
-    hipFree(L->ssgu_cat);
 }
 
 }  // namespace
@@ -565,12 +564,10 @@ int32_t focr_hip_moe_layer_set_shared(focr_hip_moe_layer* L, size_t shared_inter
         hipFree(L->ssu);
         hipFree(L->ssd);
     }
-    for (int8_t** p : {&L->swg_mfma, &L->swu_mfma, &L->swd_mfma, &L->swgu_cat}) {  // rebuilt by the next prefill
+    for (int8_t** p : {&L->swg_mfma, &L->swu_mfma, &L->swd_mfma}) {  // rebuilt by the next prefill
         hipFree(*p);
         *p = nullptr;
     }
-    hipFree(L->ssgu_cat);
-    L->ssgu_cat = nullptr;
     L->shared_inter = shared_inter;
     L->swg = tmp.swg;
     L->ssg = tmp.ssg;
@@ -1179,26 +1176,6 @@ static int32_t moe_prefill_i8_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* 
             (st = ensure_tiled(ctx, &L->swu_mfma, L->swu, 1, S, H, "moe_prefill_i8")) ||
             (st = ensure_tiled(ctx, &L->swd_mfma, L->swd, 1, H, S, "moe_prefill_i8")))
             return st;
-        // chunks of up to 256 rows: the shared expert's products on the split-K
-        // GEMV, whose SwiGLU form reads the gate rows then the up rows
-        if (!L->swgu_cat && gemv_rows_preferred((int)S, (int)H, (int)t, true)) {
-            int8_t* w = nullptr;
-            float* sc = nullptr;
-            hipError_t e = hipMalloc(&w, 2 * S * H);
-            if (e == hipSuccess) e = hipMalloc(&sc, 2 * S * sizeof(float));
-            if (e == hipSuccess) e = hipMemcpyAsync(w, L->swg, S * H, hipMemcpyDeviceToDevice, ctx->stream);
-            if (e == hipSuccess) e = hipMemcpyAsync(w + S * H, L->swu, S * H, hipMemcpyDeviceToDevice, ctx->stream);
-            if (e == hipSuccess) e = hipMemcpyAsync(sc, L->ssg, S * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(sc + S, L->ssu, S * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
-            if (e != hipSuccess) {
-                hipFree(w);
-                hipFree(sc);
-                return hip_fail(e, "moe_prefill_i8: shared gate/up copy");
-            }
-            L->swgu_cat = w;
-            L->ssgu_cat = sc;
-        }
     }
     auto take = [](char*& p, size_t bytes) {
         char* r = p;

@@ -155,11 +155,6 @@ struct focr_hip_moe_layer {
     // first prefill call; always owned
     mutable int8_t *wg_mfma = nullptr, *wu_mfma = nullptr, *wd_mfma = nullptr;
     mutable int8_t *swg_mfma = nullptr, *swu_mfma = nullptr, *swd_mfma = nullptr;
-    // the shared expert's gate rows then up rows ([2 shared_inter][hidden])
-    // and their scales, for the SwiGLU product of prefill chunks; built on
-    // the first prefill call; always owned
-    mutable int8_t* swgu_cat = nullptr;
-    mutable float* ssgu_cat = nullptr;
 };
 
 // One decoder layer for decode steps (decoder.rs:1971-1982 CachedLayerI8):

@@ -273,16 +273,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 // block, tile by tile, and cut into 8 contiguous parts, part x for XCD x
 // (block b runs unit (b % 8) * per + b / 8), so an expert's row tiles that
 // share a weight slab run together on one XCD and its L2 serves the repeats.
+// The first sh_blocks blocks (a multiple of 8; 0 for none) run a second,
+// dense product in the same launch: `sh` over all sh_rows rows (the shared
+// expert's gate/up, which reads the same quantized rows), its units (row
+// tile, column block) ordered column block by column block and cut into 8
+// contiguous parts the same way. Its blocks take the slots the routed units
+// leave free, so its own launch and the idle CUs of its small grid go.
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_grouped_kernel(
     I8Args a, const int* __restrict__ n_tiles, const int* __restrict__ tile_e, const int* __restrict__ tile_r0,
-    const int* __restrict__ tile_nr, const int* __restrict__ exp_nt, const int* __restrict__ exp_t0) {
+    const int* __restrict__ tile_nr, const int* __restrict__ exp_nt, const int* __restrict__ exp_t0, I8Args sh,
+    int sh_rows, int sh_blocks) {
     constexpr int BNB = bcols<EPI>();
+    int b = static_cast<int>(blockIdx.x);
+    if (b < sh_blocks) {
+        const int ncb_s = (sh.N + BNB - 1) / BNB;
+        const int nt_s = (sh_rows + BM - 1) / BM;
+        const int units_s = nt_s * ncb_s;
+        const int per_s = sh_blocks / kXcds;
+        const int ks = b / kXcds;
+        const int gs = (b % kXcds) * per_s + ks;
+        if (gs >= units_s) return;
+        const int cb = gs / nt_s, r0 = (gs - cb * nt_s) * BM;
+        i8_tile<EPI>(sh, 0, r0, min(BM, sh_rows - r0), cb);
+        return;
+    }
+    b -= sh_blocks;
     const int ncb = (a.N + BNB - 1) / BNB;
     const int units = *n_tiles * ncb;
     const int per = (units + kXcds - 1) / kXcds;
-    const int k = static_cast<int>(blockIdx.x) / kXcds;
-    const int g = (static_cast<int>(blockIdx.x) % kXcds) * per + k;
+    const int k = b / kXcds;
+    const int g = (b % kXcds) * per + k;
     if (k >= per || g >= units) return;
     const int e = tile_e[g / ncb];
     const int t0 = exp_t0[e], nt = exp_nt[e];
@@ -360,19 +381,31 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
             hipSuccess)
             return e;
     }
-    auto grouped = [&](auto epi, const I8Args& a) {
+    // sh_rows > 0: the dense product `sh` over that many rows rides in the
+    // same launch (its blocks first, a multiple of 8 of them)
+    auto grouped = [&](auto epi, const I8Args& a, const I8Args& sh, int sh_rows) {
         constexpr int EPI = decltype(epi)::value;
         const int ncb = (a.N + bcols<EPI>() - 1) / bcols<EPI>();
         const int max_units = p.max_tiles * ncb;
-        const dim3 grid(static_cast<unsigned>(kXcds * ((max_units + kXcds - 1) / kXcds)));
+        int sh_blocks = 0;
+        if (sh_rows > 0) {
+            const int units_s = ((sh_rows + BM - 1) / BM) * ((sh.N + bcols<EPI>() - 1) / bcols<EPI>());
+            sh_blocks = kXcds * ((units_s + kXcds - 1) / kXcds);
+        }
+        const dim3 grid(static_cast<unsigned>(sh_blocks + kXcds * ((max_units + kXcds - 1) / kXcds)));
         FOCR_LAUNCH(i8_grouped_kernel<EPI>, grid, dim3(256), 0, s, a, p.n_tiles, p.tile_e, p.tile_r0, p.tile_nr,
-                    p.exp_nt, p.exp_t0);
+                    p.exp_nt, p.exp_t0, sh, sh_rows, sh_blocks);
         return hipGetLastError();
     };
+    const int SI = with_shared ? static_cast<int>(L->shared_inter) : 0;
     {
         ProfScope ps(ctx, "i8_gate_up");
         const I8Args a{w.xq, w.xs, p.perm, top_k, L->wg_mfma, L->sg, L->wu_mfma, L->su, nullptr, nullptr, w.act, H, I};
-        if ((e = grouped(std::integral_constant<int, kI8Swiglu>(), a)) != hipSuccess) return e;
+        // the shared expert's gate/up (every token row, SwiGLU) as extra units
+        const I8Args sh{w.xq, w.xs, nullptr, 1, L->swg_mfma, L->ssg, L->swu_mfma, L->ssu, nullptr, nullptr,
+                        w.shared_act, H, SI};
+        if ((e = grouped(std::integral_constant<int, kI8Swiglu>(), a, sh, with_shared ? t : 0)) != hipSuccess)
+            return e;
     }
     {
         ProfScope ps(ctx, "i8_quantize_act");
@@ -381,21 +414,16 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     {
         ProfScope ps(ctx, "i8_down");
         const I8Args a{w.aq, w.as, p.perm, top_k, L->wd_mfma, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
-        if ((e = grouped(std::integral_constant<int, kI8Down>(), a)) != hipSuccess) return e;
+        if ((e = grouped(std::integral_constant<int, kI8Down>(), a, a, 0)) != hipSuccess) return e;
     }
     if (with_shared) {
-        const int SI = static_cast<int>(L->shared_inter);
         ProfScope ps(ctx, "i8_shared");
-        // up to 256 rows, where it is the faster: the split-K GEMV in 16-row
-        // groups (the tiled GEMMs launch 20-56 blocks at this size); the same
-        // products and epilogue expressions
-        const bool rows_gu = L->swgu_cat && gemv_rows_preferred(SI, H, t, true);
+        // the gate/up ran with the routed units; the down product up to 256
+        // rows, where it is the faster, on the split-K GEMV in 16-row groups
+        // (the tiled GEMM launches 20 blocks at this size; its K of 1792 would
+        // make its blocks twice as long as the routed down units, so it does
+        // not ride in their launch); the same products and epilogue expressions
         const bool rows_d = gemv_rows_preferred(H, SI, t, false);
-        if (rows_gu)
-            e = launch_swiglu_i8_rows(s, L->swgu_cat, L->ssgu_cat, SI, H, w.xq, w.xs, t, w.shared_act);
-        else
-            e = launch_swiglu_i8(s, w.xq, w.xs, t, H, L->swg_mfma, L->ssg, L->swu_mfma, L->ssu, SI, w.shared_act);
-        if (e != hipSuccess) return e;
         if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
             hipSuccess)
             return e;

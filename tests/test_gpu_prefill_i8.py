@@ -131,12 +131,15 @@ def test_moe_prefill_i8_matches_oracle(ctx, gpu_layer, layer_w, t):
     assert np.array_equal(dout.numpy(), again.numpy())
 
 
-def test_moe_prefill_i8_hot_expert_and_shared(ctx, layer_w):
-    """Every token routed to the same six experts (130 rows each: three
-    64-row tiles per expert, the last one ragged) plus the shared expert."""
+@pytest.mark.parametrize("t", [130, 300])
+def test_moe_prefill_i8_hot_expert_and_shared(ctx, layer_w, t):
+    """Every token routed to the same six experts (t rows each: 64-row tiles
+    per expert, the last one ragged) plus the shared expert, whose gate/up
+    runs as extra units of the routed launch (3 and 5 row tiles)."""
     from franken_ocr_amd.engine import MoeLayer
 
-    t, si = 130, 1792
+    si = 1792
+    _say(f"moe prefill i8 shared t={t}")
     x = synth.f32_normal(synth.seed_of(9500), t * H).reshape(t, H)
     idx = np.tile(np.array([[40, 3, 17, 63, 0, 9]], np.uint32), (t, 1))
     gates = synth.f32_uniform(synth.seed_of(9501), t * K, 0.05, 1.0).reshape(t, K)
