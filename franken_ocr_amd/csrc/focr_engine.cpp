@@ -1150,9 +1150,11 @@ int32_t focr_hip_linear_i8_dynamic(focr_hip_ctx* ctx, const focr_hip_qint8* w, c
     return linear_i8_dynamic_impl(ctx, w, x, m, bias, y);
 }
 
+// resid non-null: out = resid + the block's output (the decoder layer's
+// residual, added in the combine)
 static int32_t moe_prefill_i8_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* L, const float* x, size_t t,
                                 const uint32_t* idx, const float* gates, int32_t with_shared, float* out,
-                                int32_t check_idx) {
+                                int32_t check_idx, const float* resid = nullptr) {
     if (!L) return fail(FOCR_HIP_E_BAD_HANDLE, "moe_prefill_i8: null moe layer");
     if (!x || !idx || !gates || !out) return fail(FOCR_HIP_E_ARG, "moe_prefill_i8: null pointer");
     if (t < 1 || t > 16384) return fail(FOCR_HIP_E_SHAPE, fmt("moe_prefill_i8: t %zu outside 1..=16384", t));
@@ -1207,7 +1209,7 @@ static int32_t moe_prefill_i8_impl(focr_hip_ctx* ctx, const focr_hip_moe_layer* 
         w.shared_y = reinterpret_cast<float*>(c);
     }
     FOCR_HIP_TRY(launch_moe_prefill_i8(ctx->stream, L, x, static_cast<int>(t), static_cast<int>(K), idx, gates,
-                                       with_shared, out, w, ctx),
+                                       with_shared, out, w, ctx, resid),
                  "moe_prefill_i8 launch");
     if (check_idx) {
         int err = 0;
@@ -1858,7 +1860,8 @@ static int32_t decoder_layer_prefill_impl(focr_hip_ctx* ctx, const focr_hip_deco
         }
         if (route_idx)
             FOCR_HIP_TRY(hipMemcpyAsync(route_idx, idx, cs * K * 4, hipMemcpyDeviceToDevice, s), "route idx copy");
-        if ((st = moe_prefill_i8_impl(ctx, L->moe, nrm, cs, idx, gates, L->moe->swg ? 1 : 0, mlp, 0))) return st;
+        // 8. the second residual, x = h + mlp, in the MoE block's combine
+        return moe_prefill_i8_impl(ctx, L->moe, nrm, cs, idx, gates, L->moe->swg ? 1 : 0, x, 0, h);
     } else {
         float* g = reinterpret_cast<float*>(take(cs * I * 4));
         float* u = reinterpret_cast<float*>(take(cs * I * 4));

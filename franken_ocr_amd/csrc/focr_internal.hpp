@@ -531,9 +531,10 @@ MoePlan moe_plan_view(int* plan, int tk, int n_experts);
 hipError_t launch_moe_prefill_plan(hipStream_t s, const float* x, int t, int H, int rule, int8_t* xq, float* xs,
                                    const uint32_t* idx, int top_k, int E, const MoePlan& p, int* err);
 // out[t] = the token's pair rows of ybuf [t*top_k][H] summed in ascending
-// expert order (slot order among equal experts), + shared_y[t] if non-null.
+// expert order (slot order among equal experts), + shared_y[t] if non-null;
+// resid non-null: out[t] = resid[t] + that (the layer's residual add).
 hipError_t launch_moe_prefill_combine(hipStream_t s, const float* ybuf, const uint32_t* idx, int t, int H,
-                                      int top_k, const float* shared_y, float* out);
+                                      int top_k, const float* shared_y, float* out, const float* resid = nullptr);
 // The int4 layer keeps its experts in the MFMA-tiled layout: b [E][n][k/2]
 // packed and sc [E][n][k/group] are copied into b_tiled / s_tiled (same sizes,
 // each allocation followed by s4_tile_pad_bytes() of readable padding).
@@ -586,10 +587,11 @@ struct MoeI8Scratch {
     float* shared_y;    // [t][hidden]
 };
 // moe_block_i8 over the routing idx/gates [t][top_k] (+ the shared expert),
-// on the layer's fragment-ordered copies (moe_prefill_i8_prepare).
+// on the layer's fragment-ordered copies (moe_prefill_i8_prepare); resid
+// non-null: out = resid + the block's output (added in the combine).
 hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, int with_shared, float* out,
-                                 MoeI8Scratch& w, focr_hip_ctx* ctx);
+                                 MoeI8Scratch& w, focr_hip_ctx* ctx, const float* resid = nullptr);
 
 // k_sampler.hip — greedy decode sampler (sampler.rs): per-row ban bitmaps
 // of the sliding-window no-repeat-ngram processor, then token / EOS / history

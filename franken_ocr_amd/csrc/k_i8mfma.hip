@@ -370,7 +370,7 @@ hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, in
 
 hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, int with_shared, float* out,
-                                 MoeI8Scratch& w, focr_hip_ctx* ctx) {
+                                 MoeI8Scratch& w, focr_hip_ctx* ctx, const float* resid) {
     const int H = static_cast<int>(L->hidden), I = static_cast<int>(L->inter), E = static_cast<int>(L->n_experts);
     const int TK = t * top_k;
     const MoePlan p = moe_plan_view(w.plan, TK, E);
@@ -434,7 +434,8 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     }
     {
         ProfScope ps(ctx, "i8_combine");
-        if ((e = launch_moe_prefill_combine(s, w.ybuf, idx, t, H, top_k, with_shared ? w.shared_y : nullptr, out)) !=
+        if ((e = launch_moe_prefill_combine(s, w.ybuf, idx, t, H, top_k, with_shared ? w.shared_y : nullptr, out,
+                                            resid)) !=
             hipSuccess)
             return e;
     }

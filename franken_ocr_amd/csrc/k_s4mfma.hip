@@ -652,11 +652,13 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
 // ---- combine: out[t] = sum of the token's pair rows in ascending expert order --
 // The token's slots sorted by (expert, slot): slot j's rank counts the slots
 // ahead of it, the first K threads publish order[rank] = j. shared_y (the
-// shared expert's output, nullable) is added last (decoder.rs:2176-2179).
+// shared expert's output, nullable) is added last (decoder.rs:2176-2179);
+// resid (nullable) is the decoder layer's residual, add_residual(h, mlp)
+// (decoder.rs:2494, :2531), so the layer's separate add launch goes.
 __global__ __launch_bounds__(256) void i4_combine_kernel(const float* __restrict__ ybuf,
                                                          const uint32_t* __restrict__ idx, int H, int K,
                                                          const float* __restrict__ shared_y,
-                                                         float* __restrict__ out) {
+                                                         float* __restrict__ out, const float* __restrict__ resid) {
     __shared__ int s_order[kMaxK];
     const int t = blockIdx.y;
     const int c = blockIdx.x * 256 + threadIdx.x;
@@ -681,6 +683,7 @@ __global__ __launch_bounds__(256) void i4_combine_kernel(const float* __restrict
     for (int j = 0; j < kMaxK; ++j)
         if (j < K) o = o + v[j];
     if (shared_y) o = o + shared_y[static_cast<size_t>(t) * H + c];
+    if (resid) o = resid[static_cast<size_t>(t) * H + c] + o;
     out[static_cast<size_t>(t) * H + c] = o;
 }
 
@@ -772,8 +775,9 @@ hipError_t launch_moe_prefill_plan(hipStream_t s, const float* x, int t, int H, 
 }
 
 hipError_t launch_moe_prefill_combine(hipStream_t s, const float* ybuf, const uint32_t* idx, int t, int H,
-                                      int top_k, const float* shared_y, float* out) {
-    FOCR_LAUNCH(i4_combine_kernel, dim3((H + 255) / 256, t), dim3(256), 0, s, ybuf, idx, H, top_k, shared_y, out);
+                                      int top_k, const float* shared_y, float* out, const float* resid) {
+    FOCR_LAUNCH(i4_combine_kernel, dim3((H + 255) / 256, t), dim3(256), 0, s, ybuf, idx, H, top_k, shared_y, out,
+                resid);
     return hipGetLastError();
 }
 
