@@ -10,7 +10,9 @@
 //     with the SwiGLU epilogue (expert_mlp_i8, decoder.rs:2120-2135),
 //     re-quantization of the act rows by the dynamic rule, a grouped down GEMM
 //     whose epilogue multiplies by the pair's gate, the combine in ascending
-//     expert order, and the shared expert (all rows, dense) added last.
+//     expert order, and the shared expert (all rows, dense) added last; its
+//     gate/up and down products run as extra units of the two grouped
+//     launches.
 //
 // Integer sums are exact, so every i32 accumulator equals the CPU's; the f32
 // outputs follow the reference's formulas (SiLU through expf).
@@ -411,26 +413,25 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
         ProfScope ps(ctx, "i8_quantize_act");
         if ((e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, kQuantDynamic)) != hipSuccess) return e;
     }
-    {
-        ProfScope ps(ctx, "i8_down");
-        const I8Args a{w.aq, w.as, p.perm, top_k, L->wd_mfma, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
-        if ((e = grouped(std::integral_constant<int, kI8Down>(), a, a, 0)) != hipSuccess) return e;
-    }
     if (with_shared) {
         ProfScope ps(ctx, "i8_shared");
-        // the gate/up ran with the routed units; the down product up to 256
-        // rows, where it is the faster, on the split-K GEMV in 16-row groups
-        // (the tiled GEMM launches 20 blocks at this size; its K of 1792 would
-        // make its blocks twice as long as the routed down units, so it does
-        // not ride in their launch); the same products and epilogue expressions
-        const bool rows_d = gemv_rows_preferred(H, SI, t, false);
         if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
             hipSuccess)
             return e;
-        e = rows_d ? launch_gemv_i8_rows(s, L->swd, L->ssd, H, SI, w.shared_aq, w.shared_as, t, w.shared_y)
-                   : launch_linear_i8(s, w.shared_aq, w.shared_as, t, SI, L->swd_mfma, L->ssd, H, nullptr,
-                                      w.shared_y);
-        if (e != hipSuccess) return e;
+    }
+    {
+        ProfScope ps(ctx, "i8_down");
+        // the shared expert's down product (K = shared_inter, all t rows, gate
+        // 1: y = 1 * y, the dense product's value) as extra units: measured
+        // against its own launch (the split-K GEMV at 256 rows, the tiled GEMM
+        // above), the prefill layer went 0.653 -> 0.629 ms at chunks of 256
+        // and 0.310 -> 0.291 ms at one 1024-row chunk, although its units run
+        // twice the K of the routed ones
+        const I8Args a{w.aq, w.as, p.perm, top_k, L->wd_mfma, L->sd, nullptr, nullptr, nullptr, gates, w.ybuf, I, H};
+        const I8Args sh{w.shared_aq, w.shared_as, nullptr, 1, L->swd_mfma, L->ssd, nullptr, nullptr, nullptr,
+                        nullptr, w.shared_y, SI, H};
+        if ((e = grouped(std::integral_constant<int, kI8Down>(), a, sh, with_shared ? t : 0)) != hipSuccess)
+            return e;
     }
     {
         ProfScope ps(ctx, "i8_combine");
