@@ -273,6 +273,14 @@ hipError_t launch_igemm_i8_batched(hipStream_t s, const int8_t* a, const int8_t*
 constexpr int kQuantRuleDynamic = 2;
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int8_t* xq,
                                 float* a_scales, int rule);
+// two row sets [m][K] (each row as launch_quantize_rows does it) in one launch
+struct QuantRows {
+    const float* x;
+    int8_t* xq;
+    float* scales;
+    int m, K;
+};
+hipError_t launch_quantize_rows2(hipStream_t s, const QuantRows& r1, const QuantRows& r2, int rule);
 // y[m,n] = ((f32)acc * a_scales[m]) * ws[n]; acc (nullable) gets raw i32;
 // arg_keys (nullable) gets per-block argmax keys [m][nparts].
 hipError_t launch_gemv_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k,

@@ -46,6 +46,19 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_vec_kernel(const float
                                          a_scales + row, rule, red);
 }
 
+// Two row sets in one launch (blocks [0, r1.m) the first, the rest the
+// second), each row exactly as quantize_rows_vec_kernel does it: the MoE
+// block's routed and shared act rows, whose widths differ.
+template <int NC>
+__global__ __launch_bounds__(kThreads) void quantize_rows2_vec_kernel(QuantRows r1, QuantRows r2, int rule) {
+    __shared__ float red[kThreads / 64];
+    const bool first = static_cast<int>(blockIdx.x) < r1.m;  // block-uniform
+    const QuantRows r = first ? r1 : r2;
+    const int row = first ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - r1.m;
+    block_quantize_row_vec<kThreads, NC>(r.x + static_cast<size_t>(row) * r.K, r.K,
+                                         r.xq + static_cast<size_t>(row) * r.K, r.scales + row, rule, red);
+}
+
 // JB = row chunks (16 B) a lane holds in flight per batch; R = weight rows a
 // 16-lane group computes per activation chunk it reads from LDS (LDS bytes
 // per weight byte = M / R: at M = 8 the one-row form is LDS-bound). A tile
@@ -918,6 +931,23 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, int
         FOCR_LAUNCH(quantize_rows_vec_kernel<8>, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales, rule);
     else
         FOCR_LAUNCH(quantize_rows_kernel, dim3(m), dim3(kThreads), 0, s, x, k, xq, a_scales, rule);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows2(hipStream_t s, const QuantRows& r1, const QuantRows& r2, int rule) {
+    auto vec_ok = [](const QuantRows& r) {
+        return r.K > 0 && r.K % 4 == 0 && r.K <= 2 * 4 * kThreads && reinterpret_cast<uintptr_t>(r.x) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(r.xq) % 4 == 0;
+    };
+    if (r1.m <= 0 || r2.m <= 0 || !vec_ok(r1) || !vec_ok(r2)) {  // one launch per set
+        hipError_t e = launch_quantize_rows(s, r1.x, r1.m, r1.K, r1.xq, r1.scales, rule);
+        return e != hipSuccess ? e : launch_quantize_rows(s, r2.x, r2.m, r2.K, r2.xq, r2.scales, rule);
+    }
+    const int kmax = r1.K > r2.K ? r1.K : r2.K;
+    if (kmax <= 1 * 4 * kThreads)
+        FOCR_LAUNCH(quantize_rows2_vec_kernel<1>, dim3(r1.m + r2.m), dim3(kThreads), 0, s, r1, r2, rule);
+    else
+        FOCR_LAUNCH(quantize_rows2_vec_kernel<2>, dim3(r1.m + r2.m), dim3(kThreads), 0, s, r1, r2, rule);
     return hipGetLastError();
 }
 

@@ -411,13 +411,14 @@ hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, con
     }
     {
         ProfScope ps(ctx, "i8_quantize_act");
-        if ((e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, kQuantDynamic)) != hipSuccess) return e;
-    }
-    if (with_shared) {
-        ProfScope ps(ctx, "i8_shared");
-        if ((e = launch_quantize_rows(s, w.shared_act, t, SI, w.shared_aq, w.shared_as, kQuantDynamic)) !=
-            hipSuccess)
-            return e;
+        // the routed act rows and (with the shared expert) its act rows in one launch
+        const QuantRows routed{w.act, w.aq, w.as, TK, I};
+        if (with_shared)
+            e = launch_quantize_rows2(s, routed, QuantRows{w.shared_act, w.shared_aq, w.shared_as, t, SI},
+                                      kQuantDynamic);
+        else
+            e = launch_quantize_rows(s, w.act, TK, I, w.aq, w.as, kQuantDynamic);
+        if (e != hipSuccess) return e;
     }
     {
         ProfScope ps(ctx, "i8_down");
