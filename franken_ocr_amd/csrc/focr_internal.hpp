@@ -326,8 +326,6 @@ bool gemv_rows_supported(int n, int k, int m);
 bool gemv_rows_preferred(int n, int k, int m, bool swiglu);
 hipError_t launch_gemv_i8_rows(hipStream_t s, const int8_t* w, const float* ws, int n, int k, const int8_t* xq,
                                const float* xs, int m, float* y);
-hipError_t launch_swiglu_i8_rows(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
-                                 const int8_t* xq, const float* xs, int m, float* act);
 hipError_t launch_swiglu_i8_f32_add(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
                                     const float* x, const float* x2, float* h_out, const float* norm_w, float eps,
                                     int m, float* act, int cu_count);
@@ -566,10 +564,6 @@ hipError_t launch_retile_i8(hipStream_t s, const int8_t* src, int n_mats, int n,
 // on rows already quantized by the dynamic rule; w in fragment order.
 hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* w,
                             const float* ws, int n, const float* bias, float* y);
-// act[m][n] = silu(((f32)acc_g * xs[m]) * sg[n]) * (((f32)acc_u * xs[m]) * su[n]);
-// wg, wu in fragment order.
-hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
-                            const float* sg, const int8_t* wu, const float* su, int n, float* act);
 // k_i8gemm.hip — the same product for large row counts: 256 x 128 block
 // tiles, both operands in a tiled order (the activations written so by the
 // quantizer, the weights retiled once). Needs m >= 256 and k a multiple of 64.

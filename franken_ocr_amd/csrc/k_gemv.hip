@@ -1094,11 +1094,6 @@ hipError_t launch_gemv_i8_rows(hipStream_t s, const int8_t* w, const float* ws, 
     return launch_rows<false>(s, w, ws, n, k, xq, xs, m, y);
 }
 
-hipError_t launch_swiglu_i8_rows(hipStream_t s, const int8_t* w_gu, const float* ws_gu, int n, int k,
-                                 const int8_t* xq, const float* xs, int m, float* act) {
-    return launch_rows<true>(s, w_gu, ws_gu, n, k, xq, xs, m, act);
-}
-
 hipError_t launch_permute_rows_i8(hipStream_t s, const int8_t* w, const float* ws, int n, int k, int D, int head_dim,
                                   int8_t* w_out, float* ws_out) {
     if (n != 3 * D || head_dim % 2 || D % head_dim) return hipErrorInvalidValue;

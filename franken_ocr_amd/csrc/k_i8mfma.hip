@@ -361,15 +361,6 @@ hipError_t launch_linear_i8(hipStream_t s, const int8_t* xq, const float* xs, in
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu_i8(hipStream_t s, const int8_t* xq, const float* xs, int m, int k, const int8_t* wg,
-                            const float* sg, const int8_t* wu, const float* su, int n, float* act) {
-    if (!i8_mfma_supported(k) || m <= 0 || n <= 0) return hipErrorInvalidValue;
-    I8Args a{xq, xs, nullptr, 1, wg, sg, wu, su, nullptr, nullptr, act, k, n};
-    const dim3 grid((m + BM - 1) / BM, (n + bcols<kI8Swiglu>() - 1) / bcols<kI8Swiglu>());
-    FOCR_LAUNCH(i8_gemm_kernel<kI8Swiglu>, grid, dim3(256), 0, s, a, m);
-    return hipGetLastError();
-}
-
 hipError_t launch_moe_prefill_i8(hipStream_t s, const focr_hip_moe_layer* L, const float* x, int t, int top_k,
                                  const uint32_t* idx, const float* gates, int with_shared, float* out,
                                  MoeI8Scratch& w, focr_hip_ctx* ctx, const float* resid) {
