@@ -1074,8 +1074,16 @@ int32_t ensure_tiled(focr_hip_ctx* ctx, int8_t** dst, const int8_t* src, size_t 
 
 extern "C" {
 
+// norm_w (nullable): x is first RMS-normalised with that weight and eps, in
+// the quantize launch; only on the 256 x 128 tiled path (the caller checks
+// linear_i8_norm_fusable)
+static bool linear_i8_norm_fusable(const focr_hip_qint8* w, size_t m) {
+    return w && !gemv_rows_preferred((int)w->n, (int)w->k, (int)m, false) &&
+           i8_gemm256_supported((int)m, (int)w->n, (int)w->k) && w->k <= 4096;
+}
+
 static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
-                                   const float* bias, float* y) {
+                                   const float* bias, float* y, const float* norm_w = nullptr, float eps = 0.0f) {
     if (!w) return fail(FOCR_HIP_E_BAD_HANDLE, "linear_int8_dynamic: null weight handle");
     if (!x || !y) return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: null device pointer");
     if (m < 1 || m > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, fmt("linear_int8_dynamic: m %zu outside 1..=1048576", m));
@@ -1085,6 +1093,8 @@ static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w
     // up to 256 rows without a bias, where it is the faster: the split-K GEMV
     // in 16-row groups on the upload layout (a prefill chunk's o_proj gets 10
     // blocks of the tiled GEMM at this size, (n / 16) x (m / 16) here)
+    if (norm_w && !linear_i8_norm_fusable(w, m))
+        return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: the fused norm needs the tiled path");
     if (!bias && gemv_rows_preferred((int)w->n, (int)w->k, (int)m, false)) {
         int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
         float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
@@ -1125,7 +1135,11 @@ static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w
     if (!xq || !xs) return FOCR_HIP_E_OOM;
     {
         ProfScope ps(ctx, "quantize_rows_dyn");
-        if (big)
+        if (big && norm_w)
+            FOCR_HIP_TRY(launch_rms_norm_quantize_rows_tiled(ctx->stream, x, norm_w, eps, (int)m, (int)w->k, xq, xs,
+                                                             kQuantRuleDynamic),
+                         "norm + quantize launch");
+        else if (big)
             FOCR_HIP_TRY(launch_quantize_rows_tiled(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
                          "quantize launch");
         else
@@ -1822,11 +1836,16 @@ static int32_t decoder_layer_prefill_impl(focr_hip_ctx* ctx, const focr_hip_deco
     //    weight: the same quantized rows times each projection's rows); 3.
     //    RoPE at the chunk's positions c0 ..; 4. K / V into the stream's
     //    reference block and the chunk's causal attention over [0, c0 + cs)
-    {
-        ProfScope ps(ctx, "layer_prefill_norm");
-        FOCR_HIP_TRY(launch_rms_norm(s, x, L->input_ln, (int)cs, (int)H, L->eps, nrm), "rms_norm launch");
+    // the input norm inside qkv's quantize launch where qkv takes the tiled GEMM
+    if (linear_i8_norm_fusable(L->qkv, cs)) {
+        if ((st = linear_i8_dynamic_impl(ctx, L->qkv, x, cs, nullptr, qkv, L->input_ln, L->eps))) return st;
+    } else {
+        {
+            ProfScope ps(ctx, "layer_prefill_norm");
+            FOCR_HIP_TRY(launch_rms_norm(s, x, L->input_ln, (int)cs, (int)H, L->eps, nrm), "rms_norm launch");
+        }
+        if ((st = linear_i8_dynamic_impl(ctx, L->qkv, nrm, cs, nullptr, qkv))) return st;
     }
-    if ((st = linear_i8_dynamic_impl(ctx, L->qkv, nrm, cs, nullptr, qkv))) return st;
     {
         ProfScope ps(ctx, "layer_prefill_rope");
         // k and v straight into the stream's head-major reference block at c0

@@ -572,6 +572,9 @@ size_t i8_gemm256_a_bytes(int m, int k);  // tiled activation buffer
 size_t i8_gemm256_b_bytes(int n, int k);  // tiled weight buffer
 hipError_t launch_i8_gemm256_retile_b(hipStream_t s, const int8_t* w, int n, int k, int8_t* wt);
 hipError_t launch_quantize_rows_tiled(hipStream_t s, const float* x, int m, int k, int8_t* xt, float* xs, int rule);
+// the same after the decoder's RMSNorm of each row (weight nw, k <= 4096)
+hipError_t launch_rms_norm_quantize_rows_tiled(hipStream_t s, const float* x, const float* nw, float eps, int m,
+                                              int k, int8_t* xt, float* xs, int rule);
 hipError_t launch_i8_gemm256(hipStream_t s, const int8_t* xt, const float* xs, int m, int k, const int8_t* wt,
                              const float* ws, int n, const float* bias, float* y);
 struct MoeI8Scratch {

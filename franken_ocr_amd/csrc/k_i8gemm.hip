@@ -291,11 +291,15 @@ __global__ __launch_bounds__(256) void retile_tiled_kernel(const int8_t* __restr
 // stores each as one 4-byte word of its 16-byte piece. Rows of the last tile
 // past M are left unwritten (their products are never stored). F4L > 0: the
 // lane's F4L float4s stay in registers between the amax and the quantize
-// pass (x read once); F4L = 0: any K, x read twice.
-template <int F4L>
+// pass (x read once); F4L = 0: any K, x read twice. NORM (F4L > 0): the row
+// is first RMS-normalised as the decoder's rms_norm does it (the sum of
+// squares in f64, rstd = 1 / sqrt(ss / K + eps) rounded to f32, y = (x *
+// rstd) * w), so the f32 normed rows never go to memory and their launch goes.
+template <int F4L, bool NORM = false>
 __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* __restrict__ x, int M, int K,
                                                                   int8_t* __restrict__ xt, float* __restrict__ xs,
-                                                                  int rule) {
+                                                                  int rule, const float* __restrict__ nw, float eps) {
+    static_assert(!NORM || F4L > 0, "the normed row is held in registers");
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
     if (row >= M) return;  // whole wave
     const v4f* xr = reinterpret_cast<const v4f*>(x + static_cast<size_t>(row) * K);
@@ -316,6 +320,23 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
         v4f v[F4L];
 #pragma unroll
         for (int j = 0; j < F4L; ++j) v[j] = l + 64 * j < nf ? xr[l + 64 * j] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (NORM) {
+            const v4f* w4 = reinterpret_cast<const v4f*>(nw);
+            v4f g[F4L];
+#pragma unroll
+            for (int j = 0; j < F4L; ++j) g[j] = l + 64 * j < nf ? w4[l + 64 * j] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < F4L; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss = fma(static_cast<double>(v[j][e]), static_cast<double>(v[j][e]), ss);
+            ss = wave_sum_d_full(ss);
+            const float rstd = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(K) + static_cast<double>(eps)));
+#pragma unroll
+            for (int j = 0; j < F4L; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[j][e] = (v[j][e] * rstd) * g[j][e];
+        }
 #pragma unroll
         for (int j = 0; j < F4L; ++j) amax = absmax(amax, v[j]);
         amax = wave_max_f_full(amax);
@@ -356,20 +377,42 @@ hipError_t launch_i8_gemm256_retile_b(hipStream_t s, const int8_t* w, int n, int
     return hipGetLastError();
 }
 
+hipError_t launch_rms_norm_quantize_rows_tiled(hipStream_t s, const float* x, const float* nw, float eps, int m,
+                                              int k, int8_t* xt, float* xs, int rule) {
+    if (m <= 0 || k < BK || k % BK || !nw || reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(nw) % 16)
+        return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>((m + 3) / 4));
+    const int f4l = (k / 4 + 63) / 64;  // float4s per lane
+    if (f4l <= 4)
+        FOCR_LAUNCH((quantize_rows_tiled_kernel<4, true>), grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nw, eps);
+    else if (f4l <= 8)
+        FOCR_LAUNCH((quantize_rows_tiled_kernel<8, true>), grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nw, eps);
+    else if (f4l <= 16)
+        FOCR_LAUNCH((quantize_rows_tiled_kernel<16, true>), grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nw, eps);
+    else
+        return hipErrorInvalidValue;  // rows wider than 4096: the separate norm
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_rows_tiled(hipStream_t s, const float* x, int m, int k, int8_t* xt, float* xs, int rule) {
     if (m <= 0 || k < BK || k % BK) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>((m + 3) / 4));
     const int f4l = (k / 4 + 63) / 64;  // float4s per lane
     if (f4l <= 4)
-        FOCR_LAUNCH(quantize_rows_tiled_kernel<4>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule);
+        FOCR_LAUNCH(quantize_rows_tiled_kernel<4>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nullptr,
+                    0.0f);
     else if (f4l <= 8)
-        FOCR_LAUNCH(quantize_rows_tiled_kernel<8>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule);
+        FOCR_LAUNCH(quantize_rows_tiled_kernel<8>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nullptr,
+                    0.0f);
     else if (f4l <= 16)
-        FOCR_LAUNCH(quantize_rows_tiled_kernel<16>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule);
+        FOCR_LAUNCH(quantize_rows_tiled_kernel<16>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nullptr,
+                    0.0f);
     else if (f4l <= 28)
-        FOCR_LAUNCH(quantize_rows_tiled_kernel<28>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule);
+        FOCR_LAUNCH(quantize_rows_tiled_kernel<28>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nullptr,
+                    0.0f);
     else
-        FOCR_LAUNCH(quantize_rows_tiled_kernel<0>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule);
+        FOCR_LAUNCH(quantize_rows_tiled_kernel<0>, grid, dim3(256), 0, s, x, m, k, xt, xs, rule, nullptr,
+                    0.0f);
     return hipGetLastError();
 }
 
