@@ -1082,10 +1082,23 @@ static bool linear_i8_norm_fusable(const focr_hip_qint8* w, size_t m) {
            i8_gemm256_supported((int)m, (int)w->n, (int)w->k) && w->k <= 4096;
 }
 
+// The activation layout linear_int8_dynamic quantizes x into (row-major, or
+// the 256 x 128 GEMM's tiled order) and its bytes, in the kScrXq slot.
+static bool linear_i8_act_tiled(const focr_hip_qint8* w, size_t m, const float* bias) {
+    if (!bias && gemv_rows_preferred((int)w->n, (int)w->k, (int)m, false)) return false;
+    return i8_gemm256_supported((int)m, (int)w->n, (int)w->k);
+}
+static size_t linear_i8_act_bytes(const focr_hip_qint8* w, size_t m, const float* bias) {
+    return linear_i8_act_tiled(w, m, bias) ? i8_gemm256_a_bytes((int)m, (int)w->k) : m * w->k;
+}
+
+// prequant: the rows are already quantized by the dynamic rule in the
+// kScrXq / kScrXs slots, in linear_i8_act_tiled's layout (x unused)
 static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w, const float* x, size_t m,
-                                   const float* bias, float* y, const float* norm_w = nullptr, float eps = 0.0f) {
+                                   const float* bias, float* y, const float* norm_w = nullptr, float eps = 0.0f,
+                                   bool prequant = false) {
     if (!w) return fail(FOCR_HIP_E_BAD_HANDLE, "linear_int8_dynamic: null weight handle");
-    if (!x || !y) return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: null device pointer");
+    if ((!x && !prequant) || !y) return fail(FOCR_HIP_E_ARG, "linear_int8_dynamic: null device pointer");
     if (m < 1 || m > (1u << 20)) return fail(FOCR_HIP_E_SHAPE, fmt("linear_int8_dynamic: m %zu outside 1..=1048576", m));
     if (!i8_mfma_supported(static_cast<int>(w->k)))
         return fail(FOCR_HIP_E_SHAPE,
@@ -1099,7 +1112,7 @@ static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w
         int8_t* xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, m * w->k));
         float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
         if (!xq || !xs) return FOCR_HIP_E_OOM;
-        {
+        if (!prequant) {
             ProfScope ps(ctx, "quantize_rows_dyn");
             FOCR_HIP_TRY(launch_quantize_rows(ctx->stream, x, (int)m, (int)w->k, xq, xs, kQuantRuleDynamic),
                          "quantize launch");
@@ -1133,7 +1146,7 @@ static int32_t linear_i8_dynamic_impl(focr_hip_ctx* ctx, const focr_hip_qint8* w
         ctx->scratch_get(kScrXq, big ? i8_gemm256_a_bytes((int)m, (int)w->k) : m * w->k));
     float* xs = static_cast<float*>(ctx->scratch_get(kScrXs, m * sizeof(float)));
     if (!xq || !xs) return FOCR_HIP_E_OOM;
-    {
+    if (!prequant) {
         ProfScope ps(ctx, "quantize_rows_dyn");
         if (big && norm_w)
             FOCR_HIP_TRY(launch_rms_norm_quantize_rows_tiled(ctx->stream, x, norm_w, eps, (int)m, (int)w->k, xq, xs,
@@ -1680,7 +1693,8 @@ namespace {
 // The shared body: causal attention of cs queries (positions c0 ..) over a
 // c1-key prefix, geometry as AttnGeom, on the context's stream.
 int32_t attn_run(focr_hip_ctx* ctx, const char* name, const AttnGeom& gm, const float* q, const float* k,
-                 const float* v, float* out, size_t cs, size_t c0, size_t c1, size_t heads) {
+                 const float* v, float* out, size_t cs, size_t c0, size_t c1, size_t heads,
+                 AttnQuantOut* qo = nullptr) {
     int split_len = 0;
     const int nsplit = attn_pick_splits((int)cs, (int)c1, (int)heads, ctx->cu_count, &split_len);
     float* part = nullptr;
@@ -1690,7 +1704,7 @@ int32_t attn_run(focr_hip_ctx* ctx, const char* name, const AttnGeom& gm, const 
     }
     ProfScope ps(ctx, "attn_prefill");
     FOCR_HIP_TRY(launch_attn_prefill(ctx->stream, gm, q, k, v, out, (int)cs, (int)c0, (int)c1, (int)heads, kHeadDim,
-                                     nsplit, split_len, part),
+                                     nsplit, split_len, part, qo),
                  name);
     return FOCR_HIP_OK;
 }
@@ -1742,7 +1756,7 @@ int32_t focr_hip_prefill_attention(focr_hip_ctx* ctx, const float* q, const floa
 // (the prefill layer's RoPE writes them there); k_chunk / v_chunk unused.
 static int32_t rswa_prefill_chunk_impl(focr_hip_ctx* ctx, focr_hip_rswa* c, size_t stream, const float* q_chunk,
                                     const float* k_chunk, const float* v_chunk, size_t cs, size_t c0, float* out,
-                                    bool kv_in_place = false) {
+                                    bool kv_in_place = false, AttnQuantOut* qo = nullptr) {
     const char* name = "rswa_prefill_chunk";
     if (!c) return fail(FOCR_HIP_E_BAD_HANDLE, "null rswa cache");
     if (stream >= c->n_streams)
@@ -1765,7 +1779,7 @@ static int32_t rswa_prefill_chunk_impl(focr_hip_ctx* ctx, focr_hip_rswa* c, size
         const int hs = static_cast<int>(c->ref_capacity) * kHeadDim;
         const AttnGeom gm{dim, kHeadDim, kHeadDim, hs, kHeadDim, hs, dim, kHeadDim};
         if ((st = attn_run(ctx, name, gm, q_chunk, c->ref_k(stream), c->ref_v(stream), out, cs, c0, c0 + cs,
-                           kNumHeads)))
+                           kNumHeads, qo)))
             return st;
     }
     // the reference seeds the ring once from the whole prefix (record_prefill,
@@ -1855,9 +1869,18 @@ static int32_t decoder_layer_prefill_impl(focr_hip_ctx* ctx, const focr_hip_deco
                                       L->head_dim, hs),
                      "rope launch");
     }
-    if ((st = rswa_prefill_chunk_impl(ctx, cache, stream, q, nullptr, nullptr, cs, c0, cx, true))) return st;
+    // the split merge writes the context rows quantized for o_proj, in the
+    // layout and scratch o_proj's linear_int8_dynamic reads
+    AttnQuantOut qo{};
+    qo.tiled = linear_i8_act_tiled(L->o_proj, cs, nullptr);
+    qo.xq = static_cast<int8_t*>(ctx->scratch_get(kScrXq, linear_i8_act_bytes(L->o_proj, cs, nullptr)));
+    qo.xs = static_cast<float*>(ctx->scratch_get(kScrXs, cs * sizeof(float)));
+    if (!qo.xq || !qo.xs) return FOCR_HIP_E_OOM;
+    if ((st = rswa_prefill_chunk_impl(ctx, cache, stream, q, nullptr, nullptr, cs, c0, cx, true, &qo))) return st;
     // 5. o_proj; 6. residual + post-attention RMSNorm
-    if ((st = linear_i8_dynamic_impl(ctx, L->o_proj, cx, cs, nullptr, attn))) return st;
+    if ((st = linear_i8_dynamic_impl(ctx, L->o_proj, qo.done ? nullptr : cx, cs, nullptr, attn, nullptr, 0.0f,
+                                     qo.done)))
+        return st;
     {
         ProfScope ps(ctx, "layer_prefill_residual_norm");
         FOCR_HIP_TRY(launch_residual_rms_norm(s, x, attn, L->post_ln, (int)cs, (int)H, L->eps, h, nrm),

@@ -419,10 +419,20 @@ struct AttnGeom {
 // blocks per CU, in whole 64-key tiles.
 int attn_pick_splits(int cs, int c1, int heads, int cu_count, int* split_len);
 size_t attn_partials_bytes(int cs, int heads, int nsplit);
+// qo (nullable): where the split merge may write the context rows quantized
+// for the next int8 product instead of out (the dynamic rule, row-major or in
+// the 256 x 128 GEMM's tiled order); done tells whether it did (a single key
+// range writes out in f32, the caller quantizes).
+struct AttnQuantOut {
+    int8_t* xq;
+    float* xs;
+    bool tiled;
+    bool done;
+};
 // part: attn_partials_bytes() of scratch when nsplit > 1 (unused otherwise).
 hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q, const float* k, const float* v,
                                float* out, int cs, int c0, int c1, int heads, int head_dim, int nsplit,
-                               int split_len, float* part);
+                               int split_len, float* part, AttnQuantOut* qo = nullptr);
 // Token-major chunk rows [cs][heads*128] of K and V into head-major
 // reference blocks [heads][cap][128] at rows c0 .. c0 + cs - 1.
 hipError_t launch_attn_scatter_kv(hipStream_t s, const float* k_chunk, const float* v_chunk, int cs, int heads,

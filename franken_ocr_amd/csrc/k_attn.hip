@@ -349,6 +349,104 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
     a.out[static_cast<size_t>(row) * a.ldo + static_cast<size_t>(h) * a.ho + d] = acc / den;
 }
 
+// The same merge with the next product's activation quantization fused in
+// (o_proj's linear_int8_dynamic: the dynamic rule over the whole output row):
+// one block per row over every head, thread t folding the float4 groups
+// t + 256 i of the row's heads * 128 values exactly as attn_merge_kernel
+// folds each value (the same splits, order and expressions), then the row's
+// amax, a_scale = amax / 127 (1 for a zero row) and the codes as the row
+// quantizers form them, written row-major (TILED false) or in the 256 x 128
+// GEMM's tiled order, four codes to a word. The f32 context rows are never
+// stored and the quantize launch goes.
+constexpr int kMqGroups = 2;  // float4 groups per thread: rows up to 2048 values
+
+template <bool TILED>
+__global__ __launch_bounds__(256) void attn_merge_quant_kernel(const AttnArgs a, int8_t* __restrict__ xq,
+                                                               float* __restrict__ xs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int D = a.heads * kD, D4 = D >> 2;
+    const int kmax = min(a.c1, a.c0 + (row / 64 + 1) * 64);
+    const int ns = min(a.nsplit, (kmax + a.split_len - 1) / a.split_len);
+    float4 val[kMqGroups];
+    float amax = 0.0f;
+#pragma unroll
+    for (int gi = 0; gi < kMqGroups; ++gi) {
+        const int g4 = tid + 256 * gi;
+        float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (g4 < D4) {
+            const int h = (4 * g4) / kD, d = (4 * g4) % kD;
+            float den = 0.0f;
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (ns <= kMergeBatch) {
+                float ms[kMergeBatch], ls[kMergeBatch];
+                float4 os[kMergeBatch];
+#pragma unroll
+                for (int s = 0; s < kMergeBatch; ++s) {
+                    const int sc = s < ns ? s : ns - 1;
+                    const size_t pidx = (static_cast<size_t>(sc) * a.heads + h) * a.cs + row;
+                    ms[s] = a.part_ml[pidx * 2];
+                    ls[s] = a.part_ml[pidx * 2 + 1];
+                    os[s] = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d);
+                }
+                float M = -INFINITY;
+#pragma unroll
+                for (int s = 0; s < kMergeBatch; ++s) M = fmaxf(M, ms[s]);
+#pragma unroll
+                for (int s = 0; s < kMergeBatch; ++s) {
+                    const bool use = s < ns && ms[s] != -INFINITY;
+                    const float w = __builtin_amdgcn_exp2f((use ? ms[s] : M) - M);
+                    const float dl = w * ls[s];
+                    den += use ? dl : 0.0f;
+                    acc.x += use ? w * os[s].x : 0.0f;
+                    acc.y += use ? w * os[s].y : 0.0f;
+                    acc.z += use ? w * os[s].z : 0.0f;
+                    acc.w += use ? w * os[s].w : 0.0f;
+                }
+            } else {
+                float M = -INFINITY;
+                for (int s = 0; s < ns; ++s)
+                    M = fmaxf(M, a.part_ml[((static_cast<size_t>(s) * a.heads + h) * a.cs + row) * 2]);
+                for (int s = 0; s < ns; ++s) {
+                    const size_t pidx = (static_cast<size_t>(s) * a.heads + h) * a.cs + row;
+                    const float ms = a.part_ml[pidx * 2];
+                    if (ms == -INFINITY) continue;
+                    const float w = __builtin_amdgcn_exp2f(ms - M);
+                    den += w * a.part_ml[pidx * 2 + 1];
+                    const float4 o = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d);
+                    acc.x += w * o.x;
+                    acc.y += w * o.y;
+                    acc.z += w * o.z;
+                    acc.w += w * o.w;
+                }
+            }
+            r = make_float4(acc.x / den, acc.y / den, acc.z / den, acc.w / den);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r.x), fabsf(r.y)), fmaxf(fabsf(r.z), fabsf(r.w))));
+        }
+        val[gi] = r;
+    }
+    amax = wave_max_f_full(amax);
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float a_scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / a_scale;
+    const int nst = D / kI8TiledStage;
+#pragma unroll
+    for (int gi = 0; gi < kMqGroups; ++gi) {
+        const int g4 = tid + 256 * gi;
+        if (g4 >= D4) continue;
+        const float4 r = val[gi];
+        const uint32_t word = static_cast<uint32_t>(static_cast<uint8_t>(quant_rule(r.x, a_scale, inv, kQuantDynamic))) |
+                              static_cast<uint32_t>(static_cast<uint8_t>(quant_rule(r.y, a_scale, inv, kQuantDynamic))) << 8 |
+                              static_cast<uint32_t>(static_cast<uint8_t>(quant_rule(r.z, a_scale, inv, kQuantDynamic))) << 16 |
+                              static_cast<uint32_t>(static_cast<uint8_t>(quant_rule(r.w, a_scale, inv, kQuantDynamic))) << 24;
+        const size_t off = TILED ? i8_tiled_act_off(row, g4 >> 2, nst) + 4 * (g4 & 3) : static_cast<size_t>(row) * D + 4 * g4;
+        *reinterpret_cast<uint32_t*>(xq + off) = word;
+    }
+    if (tid == 0) xs[row] = a_scale;
+}
+
 // Chunk rows [cs][heads*128] (token-major) into a cache's head-major
 // reference block: ref[h][c0 + i][:] = chunk[i][h*128 ..]. Thread = one
 // float4 of one (row, head), K and V together.
@@ -407,7 +505,7 @@ int attn_pick_splits(int cs, int c1, int heads, int cu_count, int* split_len) {
 
 hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q, const float* k, const float* v,
                                float* out, int cs, int c0, int c1, int heads, int head_dim, int nsplit,
-                               int split_len, float* part) {
+                               int split_len, float* part, AttnQuantOut* qo) {
     if (head_dim != kD || cs < 1 || c1 < 1 || c0 < 0 || c0 + cs != c1 || heads < 1 || nsplit < 1 ||
         split_len % kKT != 0 || static_cast<long long>(nsplit) * split_len < c1)
         return hipErrorInvalidValue;
@@ -420,7 +518,17 @@ hipError_t launch_attn_prefill(hipStream_t s, const AttnGeom& gm, const float* q
     const dim3 grid((cs + 63) / 64, heads, nsplit);
     FOCR_LAUNCH(attn_prefill_kernel, grid, dim3(256), 2 * kKT * kLdsRow * sizeof(float), s, a);
     hipError_t e = hipGetLastError();
+    if (qo) qo->done = false;
     if (e != hipSuccess || nsplit == 1) return e;
+    const int D = heads * kD;
+    if (qo && D % kI8TiledStage == 0 && D <= 4 * 256 * kMqGroups) {
+        if (qo->tiled)
+            FOCR_LAUNCH(attn_merge_quant_kernel<true>, dim3(cs), dim3(256), 0, s, a, qo->xq, qo->xs);
+        else
+            FOCR_LAUNCH(attn_merge_quant_kernel<false>, dim3(cs), dim3(256), 0, s, a, qo->xq, qo->xs);
+        qo->done = true;
+        return hipGetLastError();
+    }
     FOCR_LAUNCH(attn_merge_kernel, dim3(cs, heads), dim3(kD), 0, s, a);
     return hipGetLastError();
 }

@@ -316,4 +316,17 @@ __device__ __forceinline__ float silu_fast(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// The activation order of the 256 x 128 int8 GEMM (k_i8gemm.hip): rows in
+// tiles of 256, each tile stored stage by stage (64 K bytes), each stage as
+// 256 rows of 64 bytes with the 16-byte piece p of row r at slot
+// p ^ ((r / 4) & 3) (its LDS image). Byte offset of K piece p of row r, nst
+// = K / 64 stages. Written by the quantizers that feed that GEMM.
+constexpr int kI8TiledRows = 256;
+constexpr int kI8TiledStage = 64;
+__device__ __forceinline__ int i8_tiled_swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ size_t i8_tiled_act_off(int r, int p, int nst) {
+    const int t = r / kI8TiledRows, rr = r % kI8TiledRows, st = p >> 2, sl = (p & 3) ^ i8_tiled_swz(rr);
+    return ((static_cast<size_t>(t) * nst + st) * kI8TiledRows + rr) * kI8TiledStage + 16 * sl;
+}
+
 }  // namespace focr

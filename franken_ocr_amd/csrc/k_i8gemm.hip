@@ -3,7 +3,7 @@
 // v_mfma_i32_32x32x32_i8, y = ((f32)acc * a_s[row]) * w_s[col] (+ bias), the
 // decoder's dequant order (decoder.rs:1636). A is the quantized activation
 // rows [M][K], B the weights ([N][K], output-channel-major), both in the
-// tiled order of tiled_off() (each 64-byte K stage of a row tile one
+// tiled order of i8_tiled_act_off() (each 64-byte K stage of a row tile one
 // contiguous run, already laid out as its LDS image): the quantizer writes
 // A that way and the weights are retiled once per handle.
 //
@@ -60,6 +60,8 @@ constexpr int RPI = 64 / SR;  // staged rows per 1 KB load instruction
 // line get distinct keys, so 16 consecutive rows read at one K piece touch 16
 // distinct 16-byte bank groups
 __device__ __forceinline__ int swz(int r) { return (r / (16 / SR)) & (SR - 1); }
+// the activation order is the shared one of k_common.hpp (i8_tiled_act_off)
+static_assert(TM == kI8TiledRows && BK == kI8TiledStage && SR == 4, "tiled activation order");
 
 // s_waitcnt vmcnt(n) only (expcnt / lgkmcnt left alone), n < 64: the low 4
 // bits of the count in bits 3:0, the high 2 in bits 15:14
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(WPE, WPE))
         bbr[j] = has_bias ? a.bias[col] : 0.0f;
     }
 
-    // Both operands come in the tiled order (tiled_off below): each stage of
+    // Both operands come in the tiled order (see i8_tiled_act_off): each stage of
     // a row tile is one contiguous run in the exact LDS image, so load
     // instruction i of the wave copies 1 KB (q = wave + NW i) of it.
     const size_t a_stage = static_cast<size_t>(TM) * BK, b_stage = static_cast<size_t>(TN) * BK;
@@ -260,12 +262,8 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(WPE, WPE))
 // The tiled operand order: rows in tiles of T (256 for the activations, 128
 // for the weights), each tile stored stage by stage (64 K bytes), each stage
 // as T rows of 64 bytes with the 16-byte piece p of row r at slot
-// p ^ swz(r) (the LDS image). Byte offset of K piece p (16 bytes) of row r:
-template <int T>
-__device__ __forceinline__ size_t tiled_off(int r, int p, int nst) {
-    const int t = r / T, rr = r % T, st = p / SR, sl = (p % SR) ^ swz(rr);
-    return ((static_cast<size_t>(t) * nst + st) * T + rr) * BK + 16 * sl;
-}
+// p ^ swz(r) (the LDS image); for the activations i8_tiled_act_off
+// (k_common.hpp) gives the byte offset of K piece p of row r.
 
 // weights [N][K] -> tiled order (tile height TN), rows past N zero; one
 // thread per output 16-byte unit
@@ -313,7 +311,7 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             word |= static_cast<uint32_t>(static_cast<uint8_t>(quant_rule(v[e], a_scale, inv, rule))) << (8 * e);
-        *reinterpret_cast<uint32_t*>(xt + tiled_off<TM>(row, f >> 2, nst) + 4 * (f & 3)) = word;
+        *reinterpret_cast<uint32_t*>(xt + i8_tiled_act_off(row, f >> 2, nst) + 4 * (f & 3)) = word;
     };
     float amax = 0.0f;
     if constexpr (F4L > 0) {

@@ -153,6 +153,38 @@ def test_layer_prefill_matches_oracle(ctx, host, oracle_out, kind, chunk):
     layer.free()
 
 
+@pytest.mark.parametrize("n", [24, 448])
+def test_layer_prefill_one_chunk_matches_oracle(ctx, host, n):
+    """One chunk of the MoE layer. At 448 rows qkv and o_proj take the 256 x
+    128 tiled GEMM, so the input norm runs inside qkv's quantize launch and
+    the attention's split merge writes o_proj's rows quantized in the tiled
+    order (the 300-row cases above take the row-major forms); 24 rows make a
+    single key range, whose f32 context o_proj quantizes itself."""
+    from franken_ocr_amd.engine import RingCache
+
+    lw, moe, dense, _ = host
+    x = synth.f32_normal(synth.seed_of(1541 + n), n * H).reshape(n, H)
+    lwk = dict(lw)
+    lwk["moe"] = moe
+    z = np.zeros((0, D), np.float32)
+    _say(f"oracle moe layer over one {n}-row chunk")
+    want, want_k, want_v, want_idx = O.decoder_layer_prefill(x, 0, z, z, lwk)
+    layer, keep = _device_layer(ctx, lw, moe)
+    cache = RingCache(1, n, ctx=ctx)
+    dx = ctx.to_device(x)
+    didx = ctx.empty((n, K), np.uint32)
+    _say(f"moe one chunk of {n} rows")
+    layer.prefill(cache, 0, dx, 0, didx)
+    assert_rows_close(dx.numpy(), want, didx.numpy(), want_idx)
+    reg = cache.regions(0)
+    for key, w in (("ref_k", want_k), ("ref_v", want_v)):
+        full = np.empty((10, n, 128), np.float32)  # ref_capacity == n
+        _abi.call("focr_hip_d2h", ctx.handle, full.ctypes.data_as(C.c_void_p), C.c_void_p(reg[key]), full.nbytes)
+        assert _rel(full, _head_major(w, n)) <= 1e-4, key
+    cache.free()
+    layer.free()
+
+
 def test_layer_prefill_chunks_must_come_in_order(ctx, host):
     from franken_ocr_amd.engine import RingCache
 
