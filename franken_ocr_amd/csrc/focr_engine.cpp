@@ -1851,7 +1851,9 @@ static int32_t decoder_layer_prefill_impl(focr_hip_ctx* ctx, const focr_hip_deco
     //    RoPE at the chunk's positions c0 ..; 4. K / V into the stream's
     //    reference block and the chunk's causal attention over [0, c0 + cs)
     // the input norm inside qkv's quantize launch where qkv takes the tiled GEMM
-    if (linear_i8_norm_fusable(L->qkv, cs)) {
+    // (its float4 row loads need 16-byte aligned rows and norm weight)
+    if (linear_i8_norm_fusable(L->qkv, cs) && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(L->input_ln) % 16 == 0 && H % 4 == 0) {
         if ((st = linear_i8_dynamic_impl(ctx, L->qkv, x, cs, nullptr, qkv, L->input_ln, L->eps))) return st;
     } else {
         {
