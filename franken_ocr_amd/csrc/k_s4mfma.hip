@@ -479,6 +479,9 @@ constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kQRows = kPlanThreads / 256;  // token rows per quantize block
 constexpr int kPlanPre = 4;  // rounds of pairs whose expert ids the plan block loads up front
+// Up to this many rounds (8192 pairs) the counting pass keeps every (round,
+// wave, expert) count, so the scatter needs no barrier between rounds.
+constexpr int kPlanFastRounds = 8;
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane) {
     int x = v;
@@ -512,6 +515,7 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
     __shared__ int s_cnt[kMaxE];
     __shared__ int s_base[kMaxE];
     __shared__ int s_wc[kPlanWaves][kMaxE];
+    __shared__ unsigned short s_pre[kPlanFastRounds][kPlanWaves][kMaxE];  // counts, then their prefix
     __shared__ int s_err;
     __shared__ float s_red[kPlanWaves];
     const int tid = threadIdx.x;
@@ -587,18 +591,26 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         if (r >= kPlanPre) e = p < TK ? idx[p] : 127u;
         return e;
     };
+    const int rounds = (TK + kPlanThreads - 1) / kPlanThreads;
+    const bool fast = rounds <= kPlanFastRounds;  // uniform
     if (tid < kMaxE) s_cnt[tid] = 0;
     for (int i = tid; i < kPlanWaves * kMaxE; i += kPlanThreads) (&s_wc[0][0])[i] = 0;
+    if (fast)
+        for (int i = tid; i < rounds * kPlanWaves * kMaxE; i += kPlanThreads) (&s_pre[0][0][0])[i] = 0;
     if (tid == 0) s_err = 0;
     __syncthreads();
-    // counts: one LDS add per distinct expert per wave and round
+    // counts: one LDS add per distinct expert per wave and round (and, in the
+    // fast form, the wave's count of the round kept)
     for (int c0 = 0; c0 < TK; c0 += kPlanThreads) {
         const int p = c0 + tid;
         uint32_t e = expert_of(c0);
         if (p < TK && e >= static_cast<uint32_t>(E)) s_err = 1;
         if (e >= static_cast<uint32_t>(E)) e = 127u;
         const unsigned long long same = match7(e);
-        if (e < 127u && (same & ((1ull << lane) - 1ull)) == 0ull) atomicAdd(&s_cnt[e], __popcll(same));
+        if (e < 127u && (same & ((1ull << lane) - 1ull)) == 0ull) {
+            atomicAdd(&s_cnt[e], __popcll(same));
+            if (fast) s_pre[c0 / kPlanThreads][wave][e] = static_cast<unsigned short>(__popcll(same));
+        }
     }
     __syncthreads();
     // wave 0 (lane = expert): row bases and the tile list (each expert's
@@ -620,6 +632,31 @@ __global__ __launch_bounds__(kPlanThreads) void i4_prep_kernel(const float* __re
         if (lane == 0) *err = s_err;
     }
     __syncthreads();
+    if (fast) {
+        // each expert's counts in (round, wave) order turned into exclusive
+        // prefixes: pair p of round r, wave w lands at base + prefix + its
+        // rank among the wave's pairs of its expert — the stable order, with
+        // no barrier between rounds
+        if (tid < kMaxE) {
+            int run = 0;
+            for (int r = 0; r < rounds; ++r)
+                for (int w = 0; w < kPlanWaves; ++w) {
+                    const int c = s_pre[r][w][tid];
+                    s_pre[r][w][tid] = static_cast<unsigned short>(run);
+                    run += c;
+                }
+        }
+        __syncthreads();
+        for (int c0 = 0; c0 < TK; c0 += kPlanThreads) {
+            const int p = c0 + tid;
+            uint32_t e = expert_of(c0);
+            if (e >= static_cast<uint32_t>(E)) e = 127u;  // invalid: never placed
+            const unsigned long long same = match7(e);
+            const int rank = __popcll(same & ((1ull << lane) - 1ull));
+            if (e < 127u) perm[s_base[e] + s_pre[c0 / kPlanThreads][wave][e] + rank] = p;
+        }
+        return;
+    }
     // stable scatter, 1024 pairs per round: rank inside the wave by matching
     // expert ids with ballots, wave offsets from per-wave counts
     for (int c0 = 0; c0 < TK; c0 += kPlanThreads) {
