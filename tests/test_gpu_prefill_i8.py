@@ -155,6 +155,26 @@ def test_moe_prefill_i8_hot_expert_and_shared(ctx, layer_w, t):
     assert_rel(dout.numpy(), want, 1e-3)
 
 
+def test_moe_prefill_i8_plan_forms_agree(ctx, gpu_layer):
+    """1400 tokens (8400 pairs) take the plan's round-by-round scatter, 700
+    its barrier-free form for up to 8192 pairs; a token's output does not
+    depend on the other tokens of the call (exact i32 sums per row, its own
+    epilogue, its own ascending-expert combine), so one call over 1400 rows
+    equals two calls over 700 bit for bit."""
+    t = 1400
+    _say(f"moe prefill i8 plan forms t={t}")
+    x = synth.f32_normal(synth.seed_of(9600), t * H).reshape(t, H)
+    idx, gates = synth.zipf_routing(synth.seed_of(9601), t, E, K)
+    whole = ctx.empty((t, H), np.float32)
+    gpu_layer.prefill(ctx.to_device(x), ctx.to_device(idx), ctx.to_device(gates), whole)
+    halves = []
+    for a, b in ((0, t // 2), (t // 2, t)):
+        out = ctx.empty((b - a, H), np.float32)
+        gpu_layer.prefill(ctx.to_device(x[a:b]), ctx.to_device(idx[a:b]), ctx.to_device(gates[a:b]), out)
+        halves.append(out.numpy())
+    assert np.array_equal(whole.numpy(), np.concatenate(halves))
+
+
 def test_moe_prefill_i8_bad_expert_index(ctx, gpu_layer):
     from franken_ocr_amd._abi import ContractViolation
 
